@@ -1,0 +1,91 @@
+"""Seeded synthetic inputs for the VDN-H3 hot-path workloads.
+
+Every tensor k of a workload comes from its own ``torch.Generator`` seeded with
+``SEED_BASE + k`` (a fixed, documented order), is drawn in fp32 and then cast, so the
+device path and the CPU oracle see bit-identical operands (the oracle receives a host
+copy of the same cast tensor).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from .layout import VDNLayout, text_first_layout
+
+SEED_BASE = 20261201
+
+
+def generator(k: int, device="cpu") -> torch.Generator:
+    return torch.Generator(device=device).manual_seed(SEED_BASE + int(k))
+
+
+def randn(shape, k: int, device="cpu", dtype=torch.float32, scale: float = 1.0) -> torch.Tensor:
+    """``N(0, scale^2)`` drawn in fp32 from generator ``k`` on ``device``, then cast to ``dtype``."""
+    x = torch.randn(shape, generator=generator(k, device), device=device, dtype=torch.float32)
+    if scale != 1.0:
+        x.mul_(scale)
+    return x.to(dtype)
+
+
+@dataclass(frozen=True)
+class WindowWorkload:
+    """Local-window attention at a packed layout (text rows first, then video frames)."""
+
+    name: str
+    heads: int
+    head_dim: int
+    text_len: int
+    num_frames: int
+    frame_size: tuple[int, int]
+    radius: int = 1
+    chunk: int = 5
+    anchor_frames: str = "both"
+
+    @property
+    def layout(self) -> VDNLayout:
+        return text_first_layout(self.text_len, self.num_frames, self.frame_size, radius=self.radius,
+                                 chunk=self.chunk, anchor_frames=self.anchor_frames)
+
+    @property
+    def scale(self) -> float:
+        return self.head_dim ** -0.5
+
+
+# Full-shape local-window attention: 40 heads x 128, 31 frames of 48x27 tokens + 512 text rows.
+WINDOW_FULL = WindowWorkload("window_s40688_h40_d128", 40, 128, 512, 31, (48, 27))
+# CPU-plumbing shape (full cover: every frame sees every frame) and its 13-frame variant.
+WINDOW_SMALL = WindowWorkload("window_s464_h2_d64", 2, 64, 16, 7, (8, 8))
+WINDOW_SMALL_13F = WindowWorkload("window_s848_h2_d64_13f", 2, 64, 16, 13, (8, 8))
+
+
+def fused_qkv(seq: int, heads: int, head_dim: int, device="cpu", seed: int = 0) -> torch.Tensor:
+    """``[S, 3*H*D]`` bf16 ~ N(0, 1): the layout of the block's fused q/k/v projection."""
+    return randn((seq, 3 * heads * head_dim), seed, device=device, dtype=torch.bfloat16)
+
+
+def split_qkv(qkv: torch.Tensor, heads: int, head_dim: int):
+    """Strided ``[S, H, D]`` views of a fused ``[S, 3*H*D]`` buffer (row stride ``3*H*D``)."""
+    inner = heads * head_dim
+    seq = qkv.shape[0]
+    q, k, v = qkv.split(inner, dim=-1)
+    return q.view(seq, heads, head_dim), k.view(seq, heads, head_dim), v.view(seq, heads, head_dim)
+
+
+def window_inputs(w: WindowWorkload, device="cpu"):
+    """(qkv buffer, q, k, v views, layout, scale) for a window workload."""
+    lay = w.layout
+    qkv = fused_qkv(lay.seq_len, w.heads, w.head_dim, device=device, seed=0)
+    q, k, v = split_qkv(qkv, w.heads, w.head_dim)
+    return qkv, q, k, v, lay, w.scale
+
+
+def sigmoid_gate(seq: int, heads: int, device="cpu", seed: int = 10) -> torch.Tensor:
+    """Per-head gate ``sigmoid(N(0,1))`` as bf16 ``[S, H]``."""
+    return torch.sigmoid(randn((seq, heads), seed, device=device)).to(torch.bfloat16)
+
+
+def softmax_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

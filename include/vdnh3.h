@@ -1,0 +1,121 @@
+/*
+ * vdnh3.h - C ABI of libvdnh3.so, the MI355X (gfx950) VDN-H3 hybrid attention hot path.
+ *
+ * Conventions (every entry point):
+ *   - plain pointers and sizes only; device buffers are caller-owned, nothing is
+ *     allocated inside a compute entry point;
+ *   - bf16 tensors are passed as uint16_t bit patterns, fp8 as uint8_t (OCP e4m3fn);
+ *   - strides are in elements; the innermost (head_dim / K) dimension is contiguous;
+ *   - `stream` is a hipStream_t (NULL = the default stream); work is enqueued
+ *     asynchronously on it, like every op of the reference runs on the caller's
+ *     current CUDA stream;
+ *   - the return value is a VDNH3_* status; on failure vdnh3_last_error() returns a
+ *     thread-local message. The Python layer maps VDNH3_ERR_INVALID to ValueError,
+ *     VDNH3_ERR_RUNTIME to RuntimeError and VDNH3_ERR_LINALG to
+ *     torch.linalg.LinAlgError, as the reference raises them.
+ */
+#ifndef VDNH3_H
+#define VDNH3_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VDNH3_OK 0
+#define VDNH3_ERR_INVALID 1 /* geometry / shape / argument error (ValueError)    */
+#define VDNH3_ERR_RUNTIME 2 /* HIP launch or device failure (RuntimeError)       */
+#define VDNH3_ERR_LINALG 3  /* non-SPD factor reported by a host check            */
+
+/* Anchor-frame modes, in the order of ANCHOR_FRAME_MODES (vdn_h3/window.py:18). */
+#define VDNH3_ANCHOR_NONE 0
+#define VDNH3_ANCHOR_COLUMNS 1
+#define VDNH3_ANCHOR_ROWS 2
+#define VDNH3_ANCHOR_BOTH 3
+
+/* Thread-local message of the last failing call ("" if none). */
+const char *vdnh3_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int vdnh3_abi_version(void);
+
+/* ------------------------------------------------------------------------------
+ * Window attention (local-window softmax, reference vdn_h3/window.py)
+ * ------------------------------------------------------------------------------ */
+
+/*
+ * Block-sparse tile plan of the window mask. Host-only, no device access.
+ * Replaces the key-set construction of vdn_h3/window.py:248-270 (_window_runs),
+ * :233-245 (_select_keys) and the mask of :327-344 (_window_mask_mod), and the
+ * geometry validation of :162-178 (_validate_layout).
+ *
+ * `bounds` holds num_frames (lo, hi) pairs (window_bounds, vdn_h3/window.py:141-153).
+ * The plan is a list of work items, one per (<= block_m query rows of one run):
+ *   items[4*i + 0..3] = { q_start, q_end, tile_offset, tile_count }
+ * and a list of key tiles of block_n keys:
+ *   tiles[2*j + 0..1] = { key_start (multiple of block_n), valid_lo | valid_hi << 16 }
+ * Items are sorted by descending tile_count (longest work first).
+ * vdnh3_window_plan_size returns the two lengths and the number of allowed
+ * (query, key) pairs per head (the FLOP model's sum_i |A(i)|).
+ */
+int vdnh3_window_plan_size(int seq, int video_start, int video_end, int num_frames,
+                           int tokens_per_frame, const int32_t *bounds, int anchor_mode,
+                           int block_m, int block_n, int32_t *n_items, int32_t *n_tiles,
+                           int64_t *pairs_per_head);
+int vdnh3_window_plan_build(int seq, int video_start, int video_end, int num_frames,
+                            int tokens_per_frame, const int32_t *bounds, int anchor_mode,
+                            int block_m, int block_n, int32_t *items, int32_t n_items,
+                            int32_t *tiles, int32_t n_tiles);
+
+/* Query/key tile sizes the attention kernel was built for. */
+int vdnh3_window_block_m(void);
+int vdnh3_window_block_n(void);
+
+/* Device workspace (bytes) for vdnh3_window_attn_fwd: the head-major V^T copy. */
+size_t vdnh3_window_workspace_bytes(int seq, int heads, int head_dim);
+
+/*
+ * Exact local-window softmax attention, bf16 in / bf16 out, fp32 softmax and
+ * accumulation. Replaces window_softmax_grouped / _flex / _flash2 / _decomposed
+ * (vdn_h3/window.py:277-313, :694-723, :811-861) and the dense exact path
+ * (vdn_h3/hybrid.py:295-302, a plan whose every row is dense).
+ *   q, k, v  : [seq, heads, head_dim] views, element (s, h, d) at p[s*row + h*head + d]
+ *   out      : [seq, heads, head_dim], same addressing
+ *   gate     : optional bf16 [seq, heads] (element (s, h) at gate[s*gate_row + h]);
+ *              when given, out = bf16(bf16(O) * gate), the per-head softmax gate of
+ *              vdn_h3/hybrid.py:518-529 / vdn_h3/softmax_kernels.py:8-9 fused into
+ *              the epilogue.
+ *   items/tiles : the plan above (device copies), built with vdnh3_window_block_m/_n.
+ * head_dim must be 64 or 128.
+ */
+int vdnh3_window_attn_fwd(const uint16_t *q, int64_t q_row, int64_t q_head,
+                          const uint16_t *k, int64_t k_row, int64_t k_head,
+                          const uint16_t *v, int64_t v_row, int64_t v_head,
+                          uint16_t *out, int64_t o_row, int64_t o_head,
+                          const uint16_t *gate, int64_t gate_row,
+                          int seq, int heads, int head_dim, float scale,
+                          const int32_t *items, int32_t n_items, const int32_t *tiles,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * The two phases of vdnh3_window_attn_fwd, for callers that time or reuse them:
+ * vdnh3_window_vt_prepass writes the head-major V^T copy into `workspace`;
+ * vdnh3_window_attn_prepared runs the attention from q, k and that copy.
+ */
+int vdnh3_window_vt_prepass(const uint16_t *v, int64_t v_row, int64_t v_head, int seq, int heads,
+                            int head_dim, void *workspace, size_t workspace_bytes, void *stream);
+int vdnh3_window_attn_prepared(const uint16_t *q, int64_t q_row, int64_t q_head,
+                               const uint16_t *k, int64_t k_row, int64_t k_head,
+                               uint16_t *out, int64_t o_row, int64_t o_head,
+                               const uint16_t *gate, int64_t gate_row,
+                               int seq, int heads, int head_dim, float scale,
+                               const int32_t *items, int32_t n_items, const int32_t *tiles,
+                               const void *workspace, size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VDNH3_H */

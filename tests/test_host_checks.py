@@ -1,0 +1,59 @@
+"""Host-side behaviour of the product API that needs no GPU: loud failures, no CPU fallback."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+
+def test_window_op_rejects_cpu_tensors(built_lib):
+    from vdn_h3_amd import window
+
+    q = torch.zeros(8, 1, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        window.window_softmax_hip(q, q, q, 0, 8, 1, 8, [(0, 0)], 0.125)
+
+
+def test_window_op_shape_errors(built_lib):
+    from vdn_h3_amd import window
+
+    q = torch.zeros(8, 1, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="share shape"):
+        window.window_softmax_hip(q, q[:4], q, 0, 8, 1, 8, [(0, 0)], 0.125)
+
+
+def test_missing_library_is_a_hard_error(monkeypatch, tmp_path):
+    from vdn_h3_amd import _lib
+
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libvdnh3.so")
+    with pytest.raises(_lib.LibraryMissingError):
+        _lib.lib()
+
+
+def test_backend_resolution_is_hip():
+    from vdn_h3_amd import window
+
+    cache = window.WindowAttentionCache()
+    for name in window.ATTENTION_BACKENDS:
+        assert window.resolve_attention_backend(name, cache=cache) == "hip"
+    with pytest.raises(ValueError):
+        window.resolve_attention_backend("sage")
+
+
+def test_layout_mirror_matches_reference_semantics():
+    from types import SimpleNamespace
+
+    from vdn_h3_amd.layout import current_layout, from_comfy_packed_layout, publish_layout
+
+    # tests/test_layout.py:13-30 packed layout: 3 text rows, 2 audio rows, 2 frames of 2x2
+    packed = SimpleNamespace(signature=(3, 2, 4, 4, 1), segments=((0, 3, "text"), (3, 5, "audio"), (5, 13, "video")),
+                             seq_len=13)
+    lay = from_comfy_packed_layout(packed, radius=1, chunk=5, anchor_frames="both")
+    assert (lay.video_start, lay.video_end, lay.frame_size, lay.tokens_per_frame) == (5, 13, (2, 2), 4)
+    assert lay.full_cover is True
+    assert current_layout(required=False) is None
+    with publish_layout(lay):
+        assert current_layout() is lay
+    with pytest.raises(RuntimeError):
+        current_layout()

@@ -1,0 +1,118 @@
+"""Parity of the HIP window-attention kernel with the CPU oracle (GPU).
+
+Tolerance (bf16 in / bf16 out, fp32 softmax): max |got - want| <= 2e-2 and cosine >= 0.9995
+against the fp32 oracle on the same bf16 inputs; the reference's own backend parity gate
+(``vdn_h3/autotune.py:133``, ``allclose(atol=2e-2, rtol=4e-2)``) is checked as well.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import window_oracle as wo
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-2
+MIN_COS = 0.9995
+
+
+def assert_parity(got, want, atol=ATOL, min_cos=MIN_COS):
+    got = got.float().cpu()
+    want = want.float().cpu()
+    assert got.shape == want.shape
+    assert torch.isfinite(got).all()
+    err = (got - want).abs().max().item()
+    cos = torch.nn.functional.cosine_similarity(got.flatten(), want.flatten(), dim=0).item()
+    assert err <= atol and cos >= min_cos, f"max abs {err:.3e}, cosine {cos:.6f}"
+    assert torch.allclose(got, want, atol=2e-2, rtol=4e-2)
+
+
+def _run(device, seq, vs, ve, frames, per_frame, heads, dim, bounds, anchors, seed, strided=True, gate=None):
+    from vdn_h3_amd import window
+
+    gen = torch.Generator().manual_seed(seed)
+    qkv = torch.randn(seq, 3 * heads * dim, generator=gen).to(torch.bfloat16)
+    q, k, v = [t.view(seq, heads, dim) for t in qkv.split(heads * dim, dim=-1)]
+    dq = qkv.to(device)
+    gq, gk, gv = [t.view(seq, heads, dim) for t in dq.split(heads * dim, dim=-1)]
+    if not strided:
+        gq, gk, gv = gq.contiguous(), gk.contiguous(), gv.contiguous()
+    scale = dim ** -0.5
+    out = window.window_softmax_hip(gq, gk, gv, vs, ve, frames, per_frame, bounds, scale, anchors,
+                                    gate=None if gate is None else gate.to(device))
+    torch.cuda.synchronize()
+    want = wo.window_attention_grouped(q, k, v, vs, ve, frames, per_frame, bounds, scale, anchors)
+    if gate is not None:
+        want = (want.to(torch.bfloat16) * gate.reshape(seq, heads, 1)).float()
+    return out, want
+
+
+@pytest.mark.parametrize("anchors", wo.ANCHOR_FRAME_MODES)
+@pytest.mark.parametrize("chunk,radius", [(0, 2), (3, 1), (4, 2)])
+def test_small_geometry_all_anchor_modes(device, anchors, chunk, radius):
+    # the reference's window test geometry (11 frames x 3 tokens, 4 rows before, 2 after), head_dim 64
+    frames, per_frame, vs = 11, 3, 4
+    ve = vs + frames * per_frame
+    seq = ve + 2
+    bounds = wo.window_bounds(frames, radius, chunk)
+    print(f"case small anchors={anchors} chunk={chunk} radius={radius}", flush=True)
+    out, want = _run(device, seq, vs, ve, frames, per_frame, 2, 64, bounds, anchors, 1000 + 10 * chunk + radius)
+    assert_parity(out, want)
+
+
+@pytest.mark.parametrize("frames", [7, 13])
+@pytest.mark.parametrize("dim", [64, 128])
+def test_packed_layout_8x8_frames(device, frames, dim):
+    # 16 text rows + frames x 64 tokens; 7 frames is full cover (dense), 13 frames is windowed
+    per_frame, text, heads = 64, 16, 2
+    seq = text + frames * per_frame
+    bounds = wo.window_bounds(frames, 1, 5)
+    print(f"case packed frames={frames} dim={dim}", flush=True)
+    out, want = _run(device, seq, text, seq, frames, per_frame, heads, dim, bounds, "both", 7 + frames)
+    assert_parity(out, want)
+
+
+def test_ragged_tiles_and_contiguous_operands(device):
+    # frames of 100 tokens: neither query blocks (128) nor key tiles (64) align with frames
+    frames, per_frame, text, heads, dim = 12, 100, 40, 3, 128
+    seq = text + frames * per_frame + 24
+    bounds = wo.window_bounds(frames, 1, 3)
+    print("case ragged", flush=True)
+    for strided in (True, False):
+        out, want = _run(device, seq, text, text + frames * per_frame, frames, per_frame, heads, dim, bounds,
+                         "columns", 99, strided=strided)
+        assert_parity(out, want)
+
+
+def test_fused_gate(device):
+    frames, per_frame, text, heads, dim = 13, 64, 16, 2, 128
+    seq = text + frames * per_frame
+    gate = torch.sigmoid(torch.randn(seq, heads, generator=torch.Generator().manual_seed(5))).to(torch.bfloat16)
+    print("case gate", flush=True)
+    out, want = _run(device, seq, text, seq, frames, per_frame, heads, dim, wo.window_bounds(frames, 1, 5), "both",
+                     31, gate=gate)
+    assert_parity(out, want)
+
+
+def test_full_shape_sampled_rows(device):
+    """40 688 tokens x 40 heads x 128: the whole problem on the GPU, exact oracle on sampled rows."""
+    from vdn_h3_amd import synth, window
+
+    w = synth.WINDOW_FULL
+    lay = w.layout
+    print(f"case full shape S={lay.seq_len}", flush=True)
+    qkv = synth.fused_qkv(lay.seq_len, w.heads, w.head_dim, device=device, seed=0)
+    q, k, v = synth.split_qkv(qkv, w.heads, w.head_dim)
+    out = window.window_softmax_hip(q, k, v, lay.video_start, lay.video_end, lay.num_frames, lay.tokens_per_frame,
+                                    lay.bounds, w.scale, lay.anchor_frames)
+    torch.cuda.synchronize()
+    host = qkv.cpu()
+    hq, hk, hv = synth.split_qkv(host, w.heads, w.head_dim)
+    T, vs = lay.tokens_per_frame, lay.video_start
+    rows = [0, 511, vs, vs + T - 1, vs + T, vs + 2 * T + 127, vs + 2 * T + 128, vs + 5 * T - 1, vs + 5 * T,
+            vs + 12 * T + 700, vs + 25 * T, vs + 29 * T + 1295, vs + 30 * T, lay.seq_len - 1]
+    want = wo.window_attention_rows(hq, hk, hv, rows, lay.video_start, lay.video_end, lay.num_frames, T, lay.bounds,
+                                    w.scale, lay.anchor_frames)
+    assert_parity(out.cpu()[rows], want)
