@@ -29,6 +29,7 @@ namespace {
 constexpr int kBM = 128;  // query rows per workgroup
 constexpr int kBN = 64;   // keys per tile
 constexpr int kThreads = 256;
+constexpr float kLazy = 8.0f;  // log2 of the largest probability a stale running max allows
 
 // LDS position p (0..15) inside a 16-key group holds key offset kperm(p): the order in
 // which the S^T accumulator of lane group g = p / 8 enumerates its 8 keys of a k-step.
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attn_kernel(
   {
     const uint16_t *qp = q + (int64_t)qrc * q_row + (int64_t)head * q_head + 8 * g;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qf[s] = as_bf16x8(*reinterpret_cast<const uint4 *>(qp + 16 * s));
+    for (int s = 0; s < NS; ++s) qf[s] = as_bf16x8(ld16(qp + 16 * s));
   }
 
   f32x16_t oacc[NO];
@@ -113,41 +114,47 @@ __global__ __launch_bounds__(kThreads, 2) void window_attn_kernel(
 
   const uint16_t *kbase = k + (int64_t)head * k_head;
   const uint16_t *vbase = vt + (int64_t)head * D * s_pad;
-  uint4 kreg[KCH], vreg[VCH];
+  // per-thread 16-byte chunk coordinates of the K tile ([kBN][D]) and of the V^T tile ([D][kBN])
+  int k_r[KCH], k_c[KCH], v_d[VCH], v_c[VCH];
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) {
+    const int c = tid + kThreads * i;
+    k_r[i] = c / (D / 8);
+    k_c[i] = c % (D / 8);
+  }
+#pragma unroll
+  for (int i = 0; i < VCH; ++i) {
+    const int c = tid + kThreads * i;
+    v_d[i] = c >> 3;
+    v_c[i] = c & 7;
+  }
+  u32x4_t kreg[KCH], vreg[VCH];
+  {
+    const int ks = tiles[toff].x;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i)
+      kreg[i] = ld16(kbase + (int64_t)min(ks + k_r[i], seq - 1) * k_row + k_c[i] * 8);
+#pragma unroll
+    for (int i = 0; i < VCH; ++i)
+      vreg[i] = ld16(vbase + (int64_t)v_d[i] * s_pad + ks + v_c[i] * 8);
+  }
 
-  auto gload = [&](int t) {
-    const int ks = tiles[toff + t].x;
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      int c = tid + kThreads * i, r = c / (D / 8), col = c % (D / 8);
-      int kr = min(ks + r, seq - 1);
-      kreg[i] = *reinterpret_cast<const uint4 *>(kbase + (int64_t)kr * k_row + col * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      int c = tid + kThreads * i, d = c >> 3, col = c & 7;
-      vreg[i] = *reinterpret_cast<const uint4 *>(vbase + (int64_t)d * s_pad + ks + col * 8);
-    }
-  };
-  auto lstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      int c = tid + kThreads * i, r = c / (D / 8), col = c % (D / 8);
-      *reinterpret_cast<uint4 *>(&Ks[r * KP + col * 8]) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      int c = tid + kThreads * i, d = c >> 3, col = c & 7;
-      *reinterpret_cast<uint4 *>(&Vs[d * VP + col * 8]) = vreg[i];
-    }
-  };
-
-  gload(0);
   for (int t = 0; t < tcnt; ++t) {
     const int packed = tiles[toff + t].y;
-    lstore();
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) st16(&Ks[k_r[i] * KP + k_c[i] * 8], kreg[i]);
+#pragma unroll
+    for (int i = 0; i < VCH; ++i) st16(&Vs[v_d[i] * VP + v_c[i] * 8], vreg[i]);
     __syncthreads();
-    if (t + 1 < tcnt) gload(t + 1);
+    if (t + 1 < tcnt) {
+      const int ks = tiles[toff + t + 1].x;
+#pragma unroll
+      for (int i = 0; i < KCH; ++i)
+        kreg[i] = ld16(kbase + (int64_t)min(ks + k_r[i], seq - 1) * k_row + k_c[i] * 8);
+#pragma unroll
+      for (int i = 0; i < VCH; ++i)
+        vreg[i] = ld16(vbase + (int64_t)v_d[i] * s_pad + ks + v_c[i] * 8);
+    }
 
     // S^T = K Q^T : two 32-key blocks x 32 queries
     f32x16_t sacc[2];
@@ -157,7 +164,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attn_kernel(
       const uint16_t *kp = &Ks[(32 * kb + l32) * KP + 8 * g];
 #pragma unroll
       for (int s = 0; s < NS; ++s)
-        sacc[kb] = mfma_bf16_32x32x16(as_bf16x8(*reinterpret_cast<const uint4 *>(kp + 16 * s)), qf[s], sacc[kb]);
+        sacc[kb] = mfma_bf16_32x32x16(as_bf16x8(ld16(kp + 16 * s)), qf[s], sacc[kb]);
     }
     const int lo = packed & 0xffff, hi = packed >> 16;
     if (lo > 0 || hi < kBN) {
@@ -165,33 +172,40 @@ __global__ __launch_bounds__(kThreads, 2) void window_attn_kernel(
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          int ko = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
+          const int ko = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
           if (ko < lo || ko >= hi) sacc[kb][i] = -INFINITY;
         }
     }
-    // online softmax (base 2), per lane = one query
-    float mt = sacc[0][0];
+    // Online softmax in base 2, one query per lane. The running max m_run only moves when
+    // this tile's max exceeds it by more than 2^kLazy: probabilities are then bounded by
+    // 2^kLazy (exact softmax either way, since a common shift cancels in O / l), and most
+    // tiles skip rescaling the accumulators.
+    float mt = fmaxf(sacc[0][0], sacc[0][1]);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mt = fmaxf(mt, sacc[kb][i]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float m_new = fmaxf(m_run, mt * scale_log2);
-    const float corr = exp2f(m_run - m_new);
-    m_run = m_new;
+      for (int i = 0; i < 16; i += 2) mt = fmaxf(mt, fmaxf(sacc[kb][i], sacc[kb][i + 1]));
+    mt = fmaxf(mt, __shfl_xor(mt, 32)) * scale_log2;
+    const bool grow = mt > m_run + kLazy;
+    if (__any(grow)) {
+      const float m_new = grow ? mt : m_run;
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= corr;
+#pragma unroll
+      for (int m = 0; m < NO; ++m) oacc[m] *= corr;
+    }
     float rs = 0.f;
     bf16x8_t pb[4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        float p = exp2f(fmaf(sacc[kb][i], scale_log2, -m_new));
+        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i], scale_log2, -m_run));
         rs += p;
         pb[2 * kb + (i >> 3)][i & 7] = (__bf16)p;
       }
-    l_run = fmaf(l_run, corr, rs);
-#pragma unroll
-    for (int m = 0; m < NO; ++m) oacc[m] *= corr;
+    l_run += rs;
 
     // O^T += V^T P^T : NO blocks of 32 d-rows, 4 k-steps of 16 keys
 #pragma unroll
@@ -199,7 +213,7 @@ __global__ __launch_bounds__(kThreads, 2) void window_attn_kernel(
       const uint16_t *vp = &Vs[(32 * m + l32) * VP + 8 * g];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
-        oacc[m] = mfma_bf16_32x32x16(as_bf16x8(*reinterpret_cast<const uint4 *>(vp + 16 * tt)), pb[tt], oacc[m]);
+        oacc[m] = mfma_bf16_32x32x16(as_bf16x8(ld16(vp + 16 * tt)), pb[tt], oacc[m]);
     }
     __syncthreads();
   }
