@@ -36,8 +36,10 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="window", choices=["window"])
-    ap.add_argument("--cpu-sample-rows", type=int, default=192,
+    ap.add_argument("--workload", default="window", choices=["window", "hbm_copy"],
+                    help="hbm_copy: a plain 1 GiB device copy, the reference point for scaling rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE counters to bytes")
+    ap.add_argument("--cpu-sample-rows", type=int, default=2048,
                     help="query rows of the CPU-oracle baseline sample (0 disables it)")
     ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "traffic.json"),
                     help="HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE/WRITE_SIZE)")
@@ -120,6 +122,29 @@ def bench_window(args, torch, device):
     return result
 
 
+def bench_hbm_copy(args, torch, device):
+    """Copy of 2**30 bytes (bf16), timed like a step: the HBM-counter calibration kernel."""
+    n = 1 << 29
+    src = torch.ones(n, dtype=torch.bfloat16, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    gbs = 2 * (1 << 30) / (ms * 1e-3) / 1e9
+    return {"metric": "HBM copy bandwidth (counter calibration)", "value": round(gbs, 1), "unit": "GB/s",
+            "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": "hbm_copy_1GiB", "bytes_read": 1 << 30, "bytes_written": 1 << 30},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}
+
+
 def cpu_baseline_window(torch, qkv, w, lay, n_rows):
     """Time the CPU oracle (``oracle.window_oracle``) on ``n_rows`` query rows of the same problem."""
     from oracle import window_oracle as wo
@@ -159,7 +184,10 @@ def main():
         sys.exit(1)
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     device = torch.device("cuda:0")
-    result = bench_window(args, torch, device)
+    if args.workload == "hbm_copy":
+        result = bench_hbm_copy(args, torch, device)
+    else:
+        result = bench_window(args, torch, device)
     line = {
         "metric": result.pop("metric"),
         "value": result.pop("value"),
