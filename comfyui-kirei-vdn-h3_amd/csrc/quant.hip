@@ -1,0 +1,171 @@
+// Activation / weight quantisation passes for the W8A8 projections (HBM-bound).
+//
+//   rows, fp8 : scale[m] = max(amax_m / 448, 1e-12), q = e4m3fn(clamp(x / scale, +-448))
+//               (vdn_h3/fp8.py:41-54 `_quantize_rows_kernel`, :99-105)
+//   rows, int8: scale[m] = max(amax_m / 127, 1e-12), q = clamp(rne(x / scale), +-127)
+//   tensor fp8: one scale for the whole tensor, amax by a grid reduction then a cast pass
+//               (vdn_h3/fp8.py:56-71 `_absmax_kernel` + `_cast_scaled_kernel`, :114-126)
+//
+// The division is IEEE-correct and e4m3fn rounding is round-to-nearest-even, so the codes
+// equal a CPU `(x / s).clamp(...).to(torch.float8_e4m3fn)` bit for bit.
+#include <algorithm>
+
+#include "common.h"
+
+namespace vdnh3 {
+namespace {
+
+constexpr float kF8Max = 448.f;
+constexpr float kI8Max = 127.f;
+
+// fp32 (finite, |x| <= 448) -> OCP e4m3fn code, round to nearest even.
+__device__ __forceinline__ uint32_t e4m3_code(float x) {
+  const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
+  const float a = fabsf(x);
+  uint32_t code;
+  if (a < 0.015625f) {
+    // zero and subnormals: multiples of 2^-9; rounding up to 8 gives the smallest normal (0x08)
+    code = (uint32_t)rintf(a * 512.f);
+  } else {
+    uint32_t ua = __float_as_uint(a);
+    ua += 0x7ffffu + ((ua >> 20) & 1u);  // keep 3 mantissa bits, ties to even (carries into the exponent)
+    code = (((ua >> 23) - 120u) << 3) | ((ua >> 20) & 7u);
+  }
+  return sign | code;
+}
+
+__device__ __forceinline__ uint32_t i8_code(float x) {
+  return (uint32_t)(int32_t)fminf(fmaxf(rintf(x), -kI8Max), kI8Max) & 0xffu;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// One wavefront per row (4 rows per 256-thread workgroup). Two sweeps over the row: amax,
+// then quantise (the second sweep is served from L2).
+template <int KIND>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
+                                                         uint8_t *__restrict__ q, int64_t ldq,
+                                                         float *__restrict__ scale) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const uint16_t *xr = x + (int64_t)row * ldx;
+  const int chunks = K / 8;
+  float amax = 0.f;
+  for (int c = lane; c < chunks; c += 64) {
+    const u32x4_t v = ld16(xr + 8 * c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[j] << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[j] & 0xffff0000u)));
+    }
+  }
+  amax = wave_max(amax);
+  const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f);
+  if (lane == 0) scale[row] = s;
+  uint8_t *qr = q + (int64_t)row * ldq;
+  for (int c = lane; c < chunks; c += 64) {
+    const u32x4_t v = ld16(xr + 8 * c);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float e0 = __uint_as_float(v[j] << 16) / s, e1 = __uint_as_float(v[j] & 0xffff0000u) / s;
+      uint32_t c0, c1;
+      if (KIND == 1) {
+        c0 = i8_code(e0);
+        c1 = i8_code(e1);
+      } else {
+        c0 = e4m3_code(fminf(fmaxf(e0, -kF8Max), kF8Max));
+        c1 = e4m3_code(fminf(fmaxf(e1, -kF8Max), kF8Max));
+      }
+      const uint32_t pair = c0 | (c1 << 8);
+      if (j < 2)
+        lo |= pair << (16 * j);
+      else
+        hi |= pair << (16 * (j - 2));
+    }
+    *reinterpret_cast<u32x2_t *>(qr + 8 * c) = u32x2_t{lo, hi};
+  }
+}
+
+__global__ void fill_f32_kernel(float *p, float v) { *p = v; }
+
+// Grid reduction of |x| into *amax (non-negative floats order like their bit patterns).
+__global__ __launch_bounds__(256) void absmax_kernel(const uint16_t *__restrict__ x, int64_t n8,
+                                                     float *__restrict__ amax) {
+  __shared__ float red[4];
+  float m = 0.f;
+  for (int64_t c = blockIdx.x * 256 + threadIdx.x; c < n8; c += (int64_t)gridDim.x * 256) {
+    const u32x4_t v = ld16(x + 8 * c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m = fmaxf(m, fabsf(__uint_as_float(v[j] << 16)));
+      m = fmaxf(m, fabsf(__uint_as_float(v[j] & 0xffff0000u)));
+    }
+  }
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    atomicMax(reinterpret_cast<unsigned int *>(amax), __float_as_uint(m));
+  }
+}
+
+__global__ __launch_bounds__(256) void cast_tensor_f8_kernel(const uint16_t *__restrict__ x, int64_t n8,
+                                                             const float *__restrict__ amax, uint8_t *__restrict__ q,
+                                                             float *__restrict__ scale) {
+  const float s = fmaxf(*amax / kF8Max, 1e-12f);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
+  for (int64_t c = blockIdx.x * 256 + threadIdx.x; c < n8; c += (int64_t)gridDim.x * 256) {
+    const u32x4_t v = ld16(x + 8 * c);
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float e0 = fminf(fmaxf(__uint_as_float(v[j] << 16) / s, -kF8Max), kF8Max);
+      const float e1 = fminf(fmaxf(__uint_as_float(v[j] & 0xffff0000u) / s, -kF8Max), kF8Max);
+      w[j >> 1] |= (e4m3_code(e0) | (e4m3_code(e1) << 8)) << (16 * (j & 1));
+    }
+    *reinterpret_cast<u32x2_t *>(q + 8 * c) = u32x2_t{w[0], w[1]};
+  }
+}
+
+}  // namespace
+}  // namespace vdnh3
+
+extern "C" int vdnh3_quant_rows(int kind, const uint16_t *x, int64_t ldx, int M, int K, uint8_t *q, int64_t ldq,
+                                float *scale, void *stream) {
+  using namespace vdnh3;
+  VDNH3_HOST_CHECK(kind == 1 || kind == 2, VDNH3_ERR_INVALID, "quant_rows: kind must be 1 (int8) or 2 (fp8)");
+  VDNH3_HOST_CHECK(x && q && scale && M > 0 && K > 0, VDNH3_ERR_INVALID, "quant_rows: empty or null operand");
+  VDNH3_HOST_CHECK(K % 8 == 0 && ldx % 8 == 0 && ldq % 8 == 0 && ldx >= K && ldq >= K, VDNH3_ERR_INVALID,
+                   "quant_rows: K and leading dimensions must be multiples of 8 covering K");
+  VDNH3_HOST_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0,
+                   VDNH3_ERR_INVALID, "quant_rows: x must be 16-byte and q 8-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((M + 3) / 4);
+  if (kind == 1)
+    hipLaunchKernelGGL(quant_rows_kernel<1>, grid, dim3(256), 0, s, x, ldx, M, K, q, ldq, scale);
+  else
+    hipLaunchKernelGGL(quant_rows_kernel<2>, grid, dim3(256), 0, s, x, ldx, M, K, q, ldq, scale);
+  return check_launch("quant_rows");
+}
+
+extern "C" int vdnh3_quant_tensor_f8(const uint16_t *x, int64_t n, uint8_t *q, float *scale, float *amax_workspace,
+                                     void *stream) {
+  using namespace vdnh3;
+  VDNH3_HOST_CHECK(x && q && scale && amax_workspace && n > 0, VDNH3_ERR_INVALID,
+                   "quant_tensor_f8: empty or null operand");
+  VDNH3_HOST_CHECK(n % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0,
+                   VDNH3_ERR_INVALID, "quant_tensor_f8: n must be a multiple of 8, x 16-byte and q 8-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n8 = n / 8;
+  const int blocks = (int)std::min<int64_t>((n8 + 255) / 256, 4096);
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(1), dim3(1), 0, s, amax_workspace, 0.f);
+  hipLaunchKernelGGL(absmax_kernel, dim3(blocks), dim3(256), 0, s, x, n8, amax_workspace);
+  hipLaunchKernelGGL(cast_tensor_f8_kernel, dim3(blocks), dim3(256), 0, s, x, n8, amax_workspace, q, scale);
+  return check_launch("quant_tensor_f8");
+}

@@ -45,6 +45,10 @@ SIGNATURES = {
     "vdnh3_window_attn_prepared": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64,
                                             _vp, _c_i64, _c_int, _c_int, _c_int, _c_float,
                                             _vp, _c_i32, _vp, _vp, _c_size, _vp]),
+    "vdnh3_gemm": (_c_int, [_c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int,
+                            _vp, _c_int, _vp, _c_int, _c_float, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "vdnh3_quant_rows": (_c_int, [_c_int, _vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _vp]),
+    "vdnh3_quant_tensor_f8": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _vp]),
 }
 
 _lock = threading.Lock()

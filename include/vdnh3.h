@@ -114,6 +114,50 @@ int vdnh3_window_attn_prepared(const uint16_t *q, int64_t q_row, int64_t q_head,
                                const int32_t *items, int32_t n_items, const int32_t *tiles,
                                const void *workspace, size_t workspace_bytes, void *stream);
 
+/* ------------------------------------------------------------------------------
+ * Projections (reference vdn_h3/projection.py, vdn_h3/fp8.py, the block's qkv/out GEMMs)
+ * ------------------------------------------------------------------------------ */
+
+#define VDNH3_GEMM_BF16 0 /* bf16 x bf16, fp32 accumulate                         */
+#define VDNH3_GEMM_I8 1   /* int8 x int8, int32 accumulate                         */
+#define VDNH3_GEMM_F8 2   /* fp8 e4m3fn x fp8 e4m3fn, fp32 accumulate             */
+#define VDNH3_OUT_BF16 0
+#define VDNH3_OUT_F32 1
+#define VDNH3_OUT_I32 2   /* raw int32 accumulators (int8 operands only)           */
+
+/*
+ * C[m][n] = act( acc[m][n] * a_scale[m] * alpha * b_scale[n] + bias[n] ),  acc = sum_k A[m][k] B[n][k]
+ * A: [M, K] row-major (lda), B: [N, K] row-major (ldb) - the nn.Linear weight layout - so C = A B^T.
+ * a_scale / b_scale: fp32, NULL, or with 1 or M (N) entries; bias: fp32 or bf16 [N] or NULL;
+ * act: 0 none, 1 sigmoid; accumulate: C = bf16(C + bf16(result)) (bf16 out) or C += result.
+ * round_linear (bf16 out): round the linear result to bf16 before the activation, as
+ * torch.sigmoid(F.linear(x, W, b)) does in bf16. K * element size must be a multiple of 128 bytes.
+ * Replaces F.linear (vdn_h3/projection.py:259-261, vdn_h3/branch.py:736, :754-758,
+ * vdn_h3/hybrid.py:520-522), torch._scaled_mm (vdn_h3/fp8.py:254-262), comfy-kitchen
+ * ck.int8_linear (vdn_h3/projection.py:243-256, without ConvRot) and the ComfyUI qkv_proj /
+ * out_proj GEMMs (vdn_h3/hybrid.py:263, :535).
+ */
+int vdnh3_gemm(int kind, const void *A, int64_t lda, const void *B, int64_t ldb, void *C, int64_t ldc,
+               int M, int N, int K, const float *a_scale, int a_scale_n, const float *b_scale,
+               int b_scale_n, float alpha, const void *bias, int bias_bf16, int act, int out_type,
+               int accumulate, int round_linear, void *stream);
+
+/*
+ * Row-wise symmetric quantisation of a bf16 [M, K] matrix: kind 1 = int8 (scale amax/127,
+ * round half to even, clamp +-127), kind 2 = fp8 e4m3fn (scale amax/448, clamp +-448,
+ * vdn_h3/fp8.py:41-54 and :99-105). scale[m] = max(amax_m / qmax, 1e-12).
+ */
+int vdnh3_quant_rows(int kind, const uint16_t *x, int64_t ldx, int M, int K, uint8_t *q, int64_t ldq,
+                     float *scale, void *stream);
+
+/*
+ * Per-tensor fp8 quantisation of n contiguous bf16 values (vdn_h3/fp8.py:56-71, :114-126):
+ * amax by a grid reduction into amax_workspace[0] (cleared by the call), then the cast;
+ * scale[0] = max(amax / 448, 1e-12).
+ */
+int vdnh3_quant_tensor_f8(const uint16_t *x, int64_t n, uint8_t *q, float *scale, float *amax_workspace,
+                          void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,160 @@
+"""Parity of the HIP GEMM / quantisation kernels with the CPU oracle (GPU).
+
+Bars: int8 and fp8 codes and scales bit-exact; int8 int32 accumulators bit-exact; bf16
+outputs within two bf16 rounding steps of the fp32/float64 oracle (different fp32
+summation order); fp8 GEMM within 2e-2 max-abs and cosine >= 0.9995 of the dequantised
+float64 product.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import branch_oracle as bo
+from oracle import quant_oracle as qo
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(shape, seed, scale=1.0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+def assert_bf16_close(got, want, steps=2, atol=1e-6):
+    got, want = got.float().cpu(), want.float().cpu()
+    tol = steps * 2.0 ** -8 * want.abs() + atol
+    bad = (got - want).abs() > tol
+    assert not bool(bad.any()), f"{int(bad.sum())} values off; max err {(got - want).abs().max().item():.3e}"
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 200, 192), (128, 128, 64), (37, 5120, 128), (1000, 40, 5120)])
+def test_bf16_linear(device, m, n, k):
+    from vdn_h3_amd import linear
+
+    print(f"case bf16 linear {m}x{n}x{k}", flush=True)
+    x, w = _rand((m, k), 1), _rand((n, k), 2, 0.05)
+    got = linear.linear(x.to(device), w.to(device))
+    torch.cuda.synchronize()
+    assert_bf16_close(got, (x.double() @ w.double().t()).to(torch.bfloat16))
+
+
+def test_sigmoid_bias_and_accumulate_epilogues(device):
+    from vdn_h3_amd import linear
+
+    print("case epilogues", flush=True)
+    m, n, k = 257, 130, 256
+    x, w = _rand((m, k), 3), _rand((n, k), 4, 0.05)
+    b = _rand((n,), 5, 0.5)
+    got = linear.sigmoid_linear(x.to(device), w.to(device), b.to(device))
+    want = torch.sigmoid(bo.linear_bf16(x, w, b))
+    # a pre-activation one bf16 step away (fp32 summation order) moves the sigmoid by <= 2^-8
+    assert_bf16_close(got, want, steps=2, atol=2.0 ** -8)
+    base = _rand((m, n), 6)
+    out = base.to(device)
+    linear.linear(x.to(device), w.to(device), out=out, accumulate=True)
+    torch.cuda.synchronize()
+    want = (base.float() + bo.linear_bf16(x, w).float()).to(torch.bfloat16)
+    assert_bf16_close(out, want, steps=2)
+
+
+@pytest.mark.parametrize("m,k", [(257, 512), (64, 5120)])
+def test_quant_codes_bit_exact(device, m, k):
+    from vdn_h3_amd import linear
+
+    print(f"case quant codes {m}x{k}", flush=True)
+    x = _rand((m, k), 8, 3.0)
+    x[3] = 0.0
+    q8, s8 = linear.quantize_rows(x.to(device), linear.KIND_I8)
+    wq8, ws8 = qo.int8_quantize_rows(x)
+    assert torch.equal(q8.cpu(), wq8) and torch.equal(s8.cpu(), ws8)
+    qf, sf = linear.quantize_rows(x.to(device), linear.KIND_F8)
+    wqf, wsf = qo.fp8_quantize_rows(x)
+    assert torch.equal(qf.cpu().view(torch.uint8), wqf.view(torch.uint8)) and torch.equal(sf.cpu(), wsf)
+    qt, st = linear.quantize_tensor_fp8(x.to(device))
+    wqt, wst = qo.fp8_quantize_tensor(x)
+    assert torch.equal(qt.cpu().view(torch.uint8), wqt.view(torch.uint8)) and torch.equal(st.cpu(), wst)
+
+
+def test_fp8_encoder_covers_every_bf16_magnitude(device):
+    """Every finite bf16 value below 448, quantised with scale 1, matches torch's e4m3fn cast."""
+    from vdn_h3_amd import linear
+
+    print("case fp8 exhaustive", flush=True)
+    bits = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    vals = bits.float()
+    keep = torch.isfinite(vals) & (vals.abs() <= 448.0)
+    vals = vals[keep]
+    n = (vals.numel() // 8) * 8
+    row = torch.cat([vals[:n], torch.tensor([448.0] * 8)]).to(torch.bfloat16).reshape(1, -1)
+    q, s = linear.quantize_rows(row.to(device), linear.KIND_F8)
+    assert s.item() == 1.0
+    want = row.float().clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert torch.equal(q.cpu().view(torch.uint8), want)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 200, 256), (129, 257, 1024)])
+def test_int8_accumulators_bit_exact_and_scaled_output(device, m, n, k):
+    from vdn_h3_amd import linear
+
+    print(f"case int8 {m}x{n}x{k}", flush=True)
+    x, w = _rand((m, k), 9), _rand((n, k), 10, 0.02)
+    xq, xs = qo.int8_quantize_rows(x)
+    wq, ws = qo.int8_quantize_rows(w)
+    acc = linear.int8_accumulators(xq.to(device), wq.to(device))
+    assert torch.equal(acc.cpu(), qo.int8_accumulate(xq, wq))
+    out = linear.gemm_w8a8(xq.to(device), xs.to(device), wq.to(device), ws.to(device))
+    assert_bf16_close(out, qo.int8_linear(xq, xs, wq, ws), steps=1)
+
+
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_fp8_gemm(device, per_tensor):
+    from vdn_h3_amd import fp8
+
+    print(f"case fp8 gemm per_tensor={per_tensor}", flush=True)
+    m, n, k = 333, 256, 640
+    x, w = _rand((m, k), 11), _rand((n, k), 12, 0.02)
+    xq, xs = fp8.quantize_activation(x.to(device), per_tensor=per_tensor)
+    wq, ws = fp8.quantize_weight(w.to(device), per_tensor=per_tensor)
+    got = fp8.project(x.to(device), {fp8.FP8_WEIGHT_KEY: wq, fp8.FP8_SCALE_KEY: ws}).float().cpu()
+    want = qo.fp8_linear(xq.cpu(), xs.cpu(), wq.cpu(), ws.cpu()).float()
+    err = (got - want).abs().max().item()
+    cos = torch.nn.functional.cosine_similarity(got.flatten(), want.flatten(), dim=0).item()
+    assert err <= 2e-2 and cos >= 0.9995, (err, cos)
+
+
+def test_projection_dispatch(device):
+    from vdn_h3_amd import projection
+
+    print("case projection dispatch", flush=True)
+    x, w = _rand((200, 256), 13), _rand((128, 256), 14, 0.02)
+    bf = projection.project(x.to(device), {"to_out_linear.weight": w.to(device)})
+    assert_bf16_close(bf, bo.linear_bf16(x, w))
+    maps, info = projection.prepare_int8_projection_maps([{"to_out_linear.weight": w}], device)
+    assert info.quantized_blocks == 1 and maps[0]["to_out_linear.weight_fp8"].dtype == torch.int8
+    got = projection.project(x.to(device), maps[0])
+    xq, xs = qo.int8_quantize_rows(x)
+    wq, ws = qo.int8_quantize_rows(w)
+    assert_bf16_close(got, qo.int8_linear(xq, xs, wq, ws), steps=1)
+
+
+def test_full_shape_int8_qkv_accumulators_sampled(device):
+    """M=40,688, K=5,120, N=15,360 W8A8 int8: all accumulators on the GPU, sampled rows checked exactly."""
+    from vdn_h3_amd import linear, synth
+
+    print("case full-shape int8 qkv", flush=True)
+    m, k, n = 40688, 5120, 15360
+    x = synth.randn((m, k), 30, device=device, dtype=torch.bfloat16)
+    w = synth.randn((n, k), 31, device=device, dtype=torch.bfloat16, scale=0.02)
+    xq, xs = linear.quantize_rows(x, linear.KIND_I8)
+    wq, ws = linear.quantize_rows(w, linear.KIND_I8)
+    acc = linear.int8_accumulators(xq, wq)
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 1, 127, 128, 20000, 40573, 40687])
+    a = xq[rows.to(device)].cpu().numpy().astype(np.int64)
+    b = wq.cpu().numpy().astype(np.int64)
+    want = torch.from_numpy((a @ b.T).astype(np.int32))
+    assert torch.equal(acc[rows.to(device)].cpu(), want)
+    assert torch.equal(xq.cpu()[rows], qo.int8_quantize_rows(x.cpu()[rows])[0])
