@@ -1,0 +1,684 @@
+// Video Delta Attention (the VDN linear branch) on gfx950.
+//
+// Per frame f and head h, with k~ = L2(SiLU(k)), v~ = SiLU(v), q~ = L2(SiLU(q)) (vdn_h3/kernels.py:47-51):
+//   frame_stats : A = k~^T diag(beta) k~ (fp32, symmetrised), B = bf16((v~ * beta)^T k~)      (vdn_h3/branch.py:197-243)
+//   factor      : L = chol(I + A), W = L^-1, M = W^T W, Phi = diag(alpha) M, J = B M, info       (vdn_h3/branch.py:62-71, :148-160)
+//   scan        : P_f = J_f + P_{f-1} Phi_f forward, Q_f = J_f + Q_{f+1} Phi_f backward         (vdn_h3/runtime.py:118-131)
+//   readout     : L_f = decayed P[lo-1] + Q[hi+1] (bf16), r = q~ L_f^T (bf16), y = RMSNorm(r) w * gate
+//                 (vdn_h3/branch.py:372-396, vdn_h3/runtime.py:406-419, vdn_h3/branch.py:494-505)
+// plus the small per-frame pieces: frame means, the fp32 alpha projections and decay (vdn_h3/branch.py:483-491).
+//
+// The dtype contract follows the reference's bf16 model: features, beta, B, the gathered state,
+// the readout and every epilogue step are rounded to bf16 where the reference materialises a
+// bf16 tensor; A, the factor, the scans and the gather run in fp32.
+#include <algorithm>
+
+#include "common.h"
+
+namespace vdnh3 {
+namespace {
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+
+__device__ __forceinline__ f32x16_t mfma_f32_32x32x2(float a, float b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------------------
+// frame statistics. grid = frames * heads, 256 threads. Tokens are consumed in tiles of 32,
+// stored transposed ([d][t]) in LDS so both MFMA operands read 8 consecutive tokens.
+// A's operand beta*k~ (exact in fp32: a product of two bf16 values) is split into
+// hi = bf16(x) and lo = x - hi, both exact bf16, so A = hi^T k~ + lo^T k~ carries every bit.
+template <int D>
+__global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__restrict__ k,
+                                                             const uint16_t *__restrict__ v, int64_t kv_row,
+                                                             int64_t kv_head, const uint16_t *__restrict__ beta,
+                                                             int64_t beta_row, int T, int heads,
+                                                             float *__restrict__ A_out, float *__restrict__ B_out) {
+  constexpr int TT = 32, P = TT + 8, CH = D / 8, NB = D / 64;
+  constexpr int TILE = D * P;
+  constexpr int TILE_BYTES = 4 * TILE * 2, SYM_BYTES = D * (D + 1) * 4;
+  constexpr int LDS_BYTES = TILE_BYTES > SYM_BYTES ? TILE_BYTES : SYM_BYTES;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[LDS_BYTES];
+  uint16_t *Kt = reinterpret_cast<uint16_t *>(smem);
+  uint16_t *Xh = Kt + TILE;
+  uint16_t *Xl = Xh + TILE;
+  uint16_t *Vb = Xl + TILE;
+
+  const int fh = blockIdx.x, f = fh / heads, h = fh - f * heads;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int wm = (wave >> 1) * 32 * NB, wn = (wave & 1) * 32 * NB;
+  const int p = tid / CH, c = tid % CH;  // loader: token pair p, 16-byte chunk c of the row
+  const bool loader = p < TT / 2;
+  const int64_t row0 = (int64_t)f * T;
+
+  f32x16_t accA[NB][NB], accB[NB][NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) accA[i][j] = accB[i][j] = f32x16_t{};
+
+  for (int t0 = 0; t0 < T; t0 += TT) {
+    if (loader) {
+      uint32_t kk[2][8], xh[2][8], xl[2][8], vb[2][8];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int t = t0 + 2 * p + e;
+        const bool valid = t < T;
+        u32x4_t kr = u32x4_t{0, 0, 0, 0}, vr = u32x4_t{0, 0, 0, 0};
+        float b = 0.f;
+        if (valid) {
+          const int64_t off = (row0 + t) * kv_row + (int64_t)h * kv_head + 8 * c;
+          kr = ld16(k + off);
+          vr = ld16(v + off);
+          b = bf2f(beta[(row0 + t) * beta_row + h]);
+        }
+        float s[8], sumsq = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t w = kr[j >> 1];
+          const float x = __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+          s[j] = round_bf(silu_f(x));
+          sumsq += s[j] * s[j];
+        }
+#pragma unroll
+        for (int o = 1; o < CH; o <<= 1) sumsq += __shfl_xor(sumsq, o);
+        const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float kt = round_bf(s[j] / nrm);
+          const float x = kt * b;  // exact
+          const float hi = round_bf(x);
+          kk[e][j] = f2bf(kt);
+          xh[e][j] = f2bf(hi);
+          xl[e][j] = f2bf(x - hi);
+          const uint32_t w = vr[j >> 1];
+          const float vx = __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+          vb[e][j] = f2bf(round_bf(silu_f(vx)) * b);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int o = (8 * c + j) * P + 2 * p;
+        *reinterpret_cast<uint32_t *>(Kt + o) = kk[0][j] | (kk[1][j] << 16);
+        *reinterpret_cast<uint32_t *>(Xh + o) = xh[0][j] | (xh[1][j] << 16);
+        *reinterpret_cast<uint32_t *>(Xl + o) = xl[0][j] | (xl[1][j] << 16);
+        *reinterpret_cast<uint32_t *>(Vb + o) = vb[0][j] | (vb[1][j] << 16);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8_t ah[NB], al[NB], av[NB], bk[NB];
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int ro = (wm + 32 * i + l32) * P + 16 * ks + 8 * g;
+        ah[i] = as_bf16x8(ld16(Xh + ro));
+        al[i] = as_bf16x8(ld16(Xl + ro));
+        av[i] = as_bf16x8(ld16(Vb + ro));
+        bk[i] = as_bf16x8(ld16(Kt + (wn + 32 * i + l32) * P + 16 * ks + 8 * g));
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          accA[i][j] = mfma_bf16_32x32x16(ah[i], bk[j], accA[i][j]);
+          accA[i][j] = mfma_bf16_32x32x16(al[i], bk[j], accA[i][j]);
+          accB[i][j] = mfma_bf16_32x32x16(av[i], bk[j], accB[i][j]);
+        }
+    }
+    __syncthreads();
+  }
+
+  // A -> LDS, then 0.5 (A + A^T); B rounded to bf16 like the reference's bf16 matmul output
+  float *S = reinterpret_cast<float *>(smem);
+  float *Bo = B_out + (int64_t)fh * D * D;
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), n = wn + 32 * j + l32;
+        S[m * (D + 1) + n] = accA[i][j][r];
+        Bo[m * D + n] = round_bf(accB[i][j][r]);
+      }
+  __syncthreads();
+  float *Ao = A_out + (int64_t)fh * D * D;
+  for (int e = tid; e < D * D; e += 256) {
+    const int m = e / D, n = e - m * D;
+    Ao[e] = 0.5f * (S[m * (D + 1) + n] + S[n * (D + 1) + m]);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// factor. grid = n matrices, 256 threads. Each thread keeps an (D/16) x (D/16) sub-block of the
+// working matrix in registers (a 16 x 16 grid of sub-blocks); column / row j of each step is
+// broadcast through LDS. Cholesky and the triangular inverse are right-looking rank-1
+// sweeps; M = W^T W and J = B M run on v_mfma_f32_32x32x2_f32.
+template <int D>
+__global__ __launch_bounds__(256) void factor_kernel(const float *__restrict__ A, const float *__restrict__ B,
+                                                     const float *__restrict__ alpha, float *__restrict__ Phi,
+                                                     float *__restrict__ J, float j_scale, int *__restrict__ info) {
+  constexpr int SB = D / 16, PITCH = D + 1, NBW = D / 64;  // NBW: 32x32 blocks per wave side
+  __shared__ float Lb[D * PITCH];
+  __shared__ float bcast[2][D];
+  const int mat = blockIdx.x, tid = threadIdx.x;
+  const int i0 = (tid >> 4) * SB, k0 = (tid & 15) * SB;
+  const float *Am = A + (int64_t)mat * D * D;
+
+  float M[SB][SB];
+#pragma unroll
+  for (int a = 0; a < SB; ++a)
+#pragma unroll
+    for (int b = 0; b < SB; ++b) M[a][b] = Am[(i0 + a) * D + k0 + b] + ((i0 + a) == (k0 + b) ? 1.f : 0.f);
+
+  int fail = 0;
+  for (int j = 0; j < D; ++j) {
+    float *col = bcast[j & 1];
+#pragma unroll
+    for (int b = 0; b < SB; ++b)
+      if (k0 + b == j) {
+#pragma unroll
+        for (int a = 0; a < SB; ++a) col[i0 + a] = M[a][b];
+      }
+    __syncthreads();
+    const float d = col[j];
+    if (!(d > 0.f)) {
+      fail = j + 1;
+      break;
+    }
+    const float ljj = sqrtf(d);
+    float li[SB], lk[SB];
+#pragma unroll
+    for (int a = 0; a < SB; ++a) li[a] = (i0 + a > j) ? col[i0 + a] / ljj : 0.f;
+#pragma unroll
+    for (int b = 0; b < SB; ++b) lk[b] = (k0 + b > j) ? col[k0 + b] / ljj : 0.f;
+    if ((tid & 15) == 0) {
+#pragma unroll
+      for (int a = 0; a < SB; ++a) Lb[j * PITCH + i0 + a] = (i0 + a > j) ? li[a] : (i0 + a == j ? ljj : 0.f);
+    }
+#pragma unroll
+    for (int a = 0; a < SB; ++a)
+#pragma unroll
+      for (int b = 0; b < SB; ++b) M[a][b] -= li[a] * lk[b];
+  }
+  if (tid == 0) info[mat] = fail;
+  __syncthreads();
+
+  // W = L^-1 (lower): W = I; for each j: W[j,:] /= L[j][j]; W[i,:] -= L[i][j] W[j,:] for i > j
+#pragma unroll
+  for (int a = 0; a < SB; ++a)
+#pragma unroll
+    for (int b = 0; b < SB; ++b) M[a][b] = (i0 + a) == (k0 + b) ? 1.f : 0.f;
+  if (!fail) {
+    for (int j = 0; j < D; ++j) {
+      float *row = bcast[j & 1];
+      const float ljj = Lb[j * PITCH + j];
+#pragma unroll
+      for (int a = 0; a < SB; ++a)
+        if (i0 + a == j) {
+#pragma unroll
+          for (int b = 0; b < SB; ++b) {
+            M[a][b] = M[a][b] / ljj;
+            row[k0 + b] = M[a][b];
+          }
+        }
+      __syncthreads();
+      float lij[SB], wj[SB];
+#pragma unroll
+      for (int a = 0; a < SB; ++a) lij[a] = (i0 + a > j) ? Lb[j * PITCH + i0 + a] : 0.f;
+#pragma unroll
+      for (int b = 0; b < SB; ++b) wj[b] = row[k0 + b];
+#pragma unroll
+      for (int a = 0; a < SB; ++a)
+#pragma unroll
+        for (int b = 0; b < SB; ++b) M[a][b] -= lij[a] * wj[b];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int a = 0; a < SB; ++a)
+#pragma unroll
+    for (int b = 0; b < SB; ++b) Lb[(i0 + a) * PITCH + k0 + b] = M[a][b];
+  __syncthreads();
+
+  // Minv = W^T W: C[a][b] = sum_s W[s][a] W[s][b]; lane group g contracts over rows s = 2*step + g
+  const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int wm = (wave >> 1) * 32 * NBW, wn = (wave & 1) * 32 * NBW;
+  f32x16_t acc[NBW][NBW];
+#pragma unroll
+  for (int i = 0; i < NBW; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[i][j] = f32x16_t{};
+  for (int s = 0; s < D / 2; ++s) {
+    const int kappa = 2 * s + g;
+    float av[NBW], bv[NBW];
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+      av[i] = Lb[kappa * PITCH + wm + 32 * i + l32];
+      bv[i] = Lb[kappa * PITCH + wn + 32 * i + l32];
+    }
+#pragma unroll
+    for (int i = 0; i < NBW; ++i)
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) acc[i][j] = mfma_f32_32x32x2(av[i], bv[j], acc[i][j]);
+  }
+  __syncthreads();
+  float *Pm = Phi ? Phi + (int64_t)mat * D * D : nullptr;
+  const float *al = alpha ? alpha + (int64_t)mat * D : nullptr;
+#pragma unroll
+  for (int i = 0; i < NBW; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), n = wn + 32 * j + l32;
+        Lb[m * PITCH + n] = acc[i][j][r];
+        if (Pm) Pm[m * D + n] = (al ? al[m] : 1.f) * acc[i][j][r];
+      }
+  __syncthreads();
+
+  // J = B Minv: lane group g contracts over k in [g*D/2, (g+1)*D/2); B rows stream from memory
+  const float *Bm = B + (int64_t)mat * D * D;
+#pragma unroll
+  for (int i = 0; i < NBW; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) acc[i][j] = f32x16_t{};
+  for (int s0 = 0; s0 < D / 2; s0 += 4) {
+    f32x4_t brow[NBW];
+#pragma unroll
+    for (int i = 0; i < NBW; ++i)
+      brow[i] = *reinterpret_cast<const f32x4_t *>(Bm + (wm + 32 * i + l32) * D + g * (D / 2) + s0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int kappa = g * (D / 2) + s0 + e;
+      float bv[NBW];
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) bv[j] = Lb[kappa * PITCH + wn + 32 * j + l32];
+#pragma unroll
+      for (int i = 0; i < NBW; ++i)
+#pragma unroll
+        for (int j = 0; j < NBW; ++j) acc[i][j] = mfma_f32_32x32x2(brow[i][e], bv[j], acc[i][j]);
+    }
+  }
+  float *Jm = J + (int64_t)mat * D * D;
+#pragma unroll
+  for (int i = 0; i < NBW; ++i)
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), n = wn + 32 * j + l32;
+        Jm[m * D + n] = j_scale * acc[i][j][r];
+      }
+}
+
+// ---------------------------------------------------------------------------------------
+// scan. grid = heads * 2 directions * D/32 row blocks; D/32 wavefronts, wavefront w owns state
+// columns [32w, 32w+32). The state is kept transposed, X = P^T, so the 32x32 accumulator of
+// one step (lane = state row) is the next step's B operand after one LDS exchange:
+//   X_f = Phi_f^T X_{f-1} + J_f^T
+template <int D>
+__global__ __launch_bounds__(64 * (D / 32)) void scan_kernel(const float *__restrict__ Phi, const float *__restrict__ J,
+                                                             const float *__restrict__ init,
+                                                             float *__restrict__ prefix, float *__restrict__ suffix,
+                                                             int F, int heads) {
+  constexpr int NRB = D / 32, PITCH = 32 + 4;
+  __shared__ float St[2][D * PITCH];
+  const int bid = blockIdx.x;
+  const int rb = bid % NRB, dir = (bid / NRB) & 1, h = bid / (2 * NRB);
+  const int tid = threadIdx.x, cb = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int r0 = rb * 32;
+  for (int e = tid; e < D * 32; e += 64 * NRB) {
+    const int c = e >> 5, r = e & 31;
+    St[0][c * PITCH + r] = init ? init[((int64_t)h * D + r0 + r) * D + c] : 0.f;
+  }
+  __syncthreads();
+  float *out = dir == 0 ? prefix : suffix;
+  int cur = 0;
+  for (int step = 0; step < F; ++step) {
+    const int f = dir == 0 ? step : F - 1 - step;
+    const int64_t base = ((int64_t)f * heads + h) * D * D;
+    const float *Pf = Phi + base;
+    f32x16_t acc = f32x16_t{};
+#pragma unroll 16
+    for (int s = 0; s < D / 2; ++s) {
+      const int kappa = 2 * s + g;
+      acc = mfma_f32_32x32x2(Pf[kappa * D + 32 * cb + l32], St[cur][kappa * PITCH + l32], acc);
+    }
+    const float *Jr = J + base + (int64_t)(r0 + l32) * D;
+    float *Or = out + base + (int64_t)(r0 + l32) * D;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int c0 = 32 * cb + 8 * i4 + 4 * g;
+      const f32x4_t jv = *reinterpret_cast<const f32x4_t *>(Jr + c0);
+      f32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = acc[4 * i4 + e] + jv[e];
+        St[cur ^ 1][(c0 + e) * PITCH + l32] = o[e];
+      }
+      *reinterpret_cast<f32x4_t *>(Or + c0) = o;
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// readout. grid = frames * heads, 256 threads; wavefronts take 32-token tiles in turn.
+//   L_f[v][k] = bf16(before[v][k] * decay_b[k] + after[v][k] * decay_a[k])   (LDS, [v][k])
+//   r^T = L_f q~^T on bf16 MFMA (lane = token, so the RMS over v is in-lane plus one exchange)
+template <int D>
+__global__ __launch_bounds__(256, 1) void readout_kernel(
+    const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const float *__restrict__ prefix,
+    const float *__restrict__ suffix, const float *__restrict__ alpha, const float *__restrict__ text,
+    const int *__restrict__ bounds, int use_alpha, const uint16_t *__restrict__ norm_w,
+    const uint16_t *__restrict__ gate, int64_t gate_row, uint16_t *__restrict__ out, int64_t out_row, int F, int T,
+    int heads) {
+  constexpr int LP = D + 8, NS = D / 16, NO = D / 32;
+  __shared__ __attribute__((aligned(16))) uint16_t Ls[D * LP];
+  __shared__ float dec[2][D];
+  const int fh = blockIdx.x, f = fh / heads, h = fh - f * heads;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int lo = max(bounds[2 * f], 0), hi = min(bounds[2 * f + 1], F - 1);
+  const bool has_b = lo - 1 >= 0, has_a = hi + 1 < F;
+  const int bb = min(max(lo, 0), F), ba = min(max(hi + 1, 0), F);
+  if (tid < D) {
+    float lp = 0.f, lp_f = 0.f, lp_f1 = 0.f, lp_bb = 0.f, lp_ba = 0.f;
+    for (int i = 0; i <= F; ++i) {
+      if (i == f) lp_f = lp;
+      if (i == f + 1) lp_f1 = lp;
+      if (i == bb) lp_bb = lp;
+      if (i == ba) lp_ba = lp;
+      if (i < F && use_alpha) lp += logf(fmaxf(alpha[((int64_t)i * heads + h) * D + tid], 1e-12f));
+    }
+    dec[0][tid] = use_alpha ? expf(lp_f1 - lp_bb) : 1.f;
+    dec[1][tid] = use_alpha ? expf(lp_ba - lp_f) : 1.f;
+  }
+  __syncthreads();
+  const float *before = has_b ? prefix + ((int64_t)(lo - 1) * heads + h) * D * D
+                              : (text ? text + (int64_t)h * D * D : nullptr);
+  const float *after = has_a ? suffix + ((int64_t)(hi + 1) * heads + h) * D * D
+                             : (text ? text + (int64_t)h * D * D : nullptr);
+  for (int e = tid; e < D * D; e += 256) {
+    const int vv = e / D, kk = e - vv * D;
+    const float x = __fadd_rn(before ? __fmul_rn(before[e], dec[0][kk]) : 0.f,
+                              after ? __fmul_rn(after[e], dec[1][kk]) : 0.f);
+    Ls[vv * LP + kk] = f2bf(x);
+  }
+  __syncthreads();
+
+  const int ntiles = (T + 31) / 32;
+  for (int tile = wave; tile < ntiles; tile += 4) {
+    const int t = tile * 32 + l32;
+    const int64_t row = (int64_t)f * T + min(t, T - 1);
+    const uint16_t *qp = q + row * q_row + (int64_t)h * q_head + 8 * g;
+    // SiLU(q) is rounded to bf16 (the reference materialises it); it is evaluated twice, for
+    // the L2 norm and for the division, instead of keeping 64 values per lane live.
+    u32x4_t raw[NS];
+    float sumsq = 0.f;
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      raw[st] = ld16(qp + 16 * st);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t w = raw[st][j >> 1];
+        const float sv = round_bf(silu_f(__uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16))));
+        sumsq += sv * sv;
+      }
+    }
+    sumsq += __shfl_xor(sumsq, 32);
+    const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f);
+    bf16x8_t qf[NS];
+#pragma unroll
+    for (int st = 0; st < NS; ++st)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t w = raw[st][j >> 1];
+        const float sv = round_bf(silu_f(__uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16))));
+        qf[st][j] = __builtin_bit_cast(__bf16, f2bf(sv / nrm));
+      }
+    f32x16_t acc[NO];
+#pragma unroll
+    for (int mb = 0; mb < NO; ++mb) {
+      acc[mb] = f32x16_t{};
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+        acc[mb] = mfma_bf16_32x32x16(as_bf16x8(ld16(Ls + (32 * mb + l32) * LP + 16 * st + 8 * g)), qf[st], acc[mb]);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < NO; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[mb][r] = round_bf(acc[mb][r]);
+        ss += acc[mb][r] * acc[mb][r];
+      }
+    ss += __shfl_xor(ss, 32);
+    const float nv = sqrtf(ss);
+    const float inv = round_bf(1.f / sqrtf(nv * nv / (float)D + 1e-6f));
+    if (t < T) {
+      const uint16_t *gp = gate + row * gate_row + (int64_t)h * D;
+      uint16_t *op = out + row * out_row + (int64_t)h * D;
+#pragma unroll
+      for (int mb = 0; mb < NO; ++mb)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int v0 = 32 * mb + 8 * i4 + 4 * g;
+          const u32x2_t gw = *reinterpret_cast<const u32x2_t *>(gp + v0);
+          const u32x2_t nw = *reinterpret_cast<const u32x2_t *>(norm_w + v0);
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t gg = gw[e >> 1], ww = nw[e >> 1];
+            const float gv = __uint_as_float((e & 1) ? (gg & 0xffff0000u) : (gg << 16));
+            const float wv = __uint_as_float((e & 1) ? (ww & 0xffff0000u) : (ww << 16));
+            const float y = round_bf(round_bf(acc[mb][4 * i4 + e] * inv) * wv);
+            o[e] = y * gv;
+          }
+          *reinterpret_cast<u32x2_t *>(op + v0) = u32x2_t{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+__global__ void frame_mean_kernel(const uint16_t *__restrict__ x, int64_t x_row, int T, int hidden,
+                                  float *__restrict__ out) {
+  const int f = blockIdx.x, col = blockIdx.y * 256 + threadIdx.x;
+  if (col >= hidden) return;
+  const uint16_t *p = x + (int64_t)f * T * x_row + col;
+  float s = 0.f;
+  for (int t = 0; t < T; ++t) s += bf2f(p[(int64_t)t * x_row]);
+  out[(int64_t)f * hidden + col] = s / (float)T;
+}
+
+// out[m][n] = sum_k x[m][k] W[n][k] (+ bias[n]) in fp32; one thread per output element
+__global__ void linear_f32_kernel(const float *__restrict__ x, int64_t x_row, const void *__restrict__ w, int w_bf16,
+                                  int64_t w_row, const float *__restrict__ bias, float *__restrict__ out,
+                                  int64_t out_row, int M, int N, int K) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)M * N) return;
+  const int m = (int)(e / N), n = (int)(e - (int64_t)m * N);
+  const float *xr = x + (int64_t)m * x_row;
+  float s = 0.f;
+  if (w_bf16) {
+    const uint16_t *wr = static_cast<const uint16_t *>(w) + (int64_t)n * w_row;
+    for (int k = 0; k < K; ++k) s = fmaf(xr[k], bf2f(wr[k]), s);
+  } else {
+    const float *wr = static_cast<const float *>(w) + (int64_t)n * w_row;
+    for (int k = 0; k < K; ++k) s = fmaf(xr[k], wr[k], s);
+  }
+  if (bias) s = s + bias[n];
+  out[(int64_t)m * out_row + n] = s;
+}
+
+// alpha[f][h][d] = exp(-exp(a_log[h]) * softplus(delta[f][h*D + d]))  (torch softplus, threshold 20)
+__global__ void alpha_decay_kernel(const float *__restrict__ delta, const float *__restrict__ a_log,
+                                   float *__restrict__ alpha, int64_t n, int heads, int D) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int h = (int)((e / D) % heads);
+  const float x = delta[e];
+  const float sp = x > 20.f ? x : log1pf(expf(x));
+  alpha[e] = expf(-expf(a_log[h]) * sp);
+}
+
+// Sana rule: Phi = alpha[i] * (I - A / T)[i][j], J = B / sqrt(T)  (vdn_h3/branch.py:163-177)
+__global__ void sana_factor_kernel(const float *__restrict__ A, const float *__restrict__ B,
+                                   const float *__restrict__ alpha, float *__restrict__ Phi, float *__restrict__ J,
+                                   float inv_t, float inv_sqrt_t, int64_t n, int D) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int64_t mat = e / ((int64_t)D * D);
+  const int i = (int)((e / D) % D), j = (int)(e % D);
+  const float a = alpha ? alpha[mat * D + i] : 1.f;
+  Phi[e] = a * ((i == j ? 1.f : 0.f) - inv_t * A[e]);
+  J[e] = inv_sqrt_t * B[e];
+}
+
+__global__ void fill_rows_bf16_kernel(uint16_t *__restrict__ p, int64_t ld, int rows, int cols, uint16_t value) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)rows * cols) return;
+  const int64_t r = e / cols, c = e - r * cols;
+  p[r * ld + c] = value;
+}
+
+int check_dim(int head_dim) {
+  VDNH3_HOST_CHECK(head_dim == 64 || head_dim == 128, VDNH3_ERR_INVALID,
+                   "the delta-rule kernels support head_dim 64 or 128, got %d", head_dim);
+  return VDNH3_OK;
+}
+
+}  // namespace
+}  // namespace vdnh3
+
+using vdnh3::check_dim;
+using vdnh3::check_launch;
+using vdnh3::set_error;
+
+extern "C" int vdnh3_frame_stats(const uint16_t *k, const uint16_t *v, int64_t kv_row, int64_t kv_head,
+                                 const uint16_t *beta, int64_t beta_row, int frames, int tokens, int heads,
+                                 int head_dim, float *A, float *B, void *stream) {
+  int rc = check_dim(head_dim);
+  if (rc) return rc;
+  VDNH3_HOST_CHECK(k && v && beta && A && B && frames > 0 && tokens > 0 && heads > 0, VDNH3_ERR_INVALID,
+                   "frame_stats: empty or null operand");
+  VDNH3_HOST_CHECK(kv_row % 8 == 0 && kv_head % 8 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(v) % 16 == 0,
+                   VDNH3_ERR_INVALID, "frame_stats: k/v must be 16-byte aligned with strides multiple of 8");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(frames * heads);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(vdnh3::frame_stats_kernel<128>, grid, dim3(256), 0, s, k, v, kv_row, kv_head, beta, beta_row,
+                       tokens, heads, A, B);
+  else
+    hipLaunchKernelGGL(vdnh3::frame_stats_kernel<64>, grid, dim3(256), 0, s, k, v, kv_row, kv_head, beta, beta_row,
+                       tokens, heads, A, B);
+  return check_launch("frame_stats");
+}
+
+extern "C" int vdnh3_delta_factor(const float *A, const float *B, const float *alpha, float *phi, float *jay,
+                                  float jay_scale, int32_t *info, int n, int head_dim, void *stream) {
+  int rc = check_dim(head_dim);
+  if (rc) return rc;
+  VDNH3_HOST_CHECK(A && B && jay && info && n > 0, VDNH3_ERR_INVALID, "delta_factor: empty or null operand");
+  VDNH3_HOST_CHECK(reinterpret_cast<uintptr_t>(B) % 16 == 0, VDNH3_ERR_INVALID, "delta_factor: B must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(vdnh3::factor_kernel<128>, dim3(n), dim3(256), 0, s, A, B, alpha, phi, jay, jay_scale, info);
+  else
+    hipLaunchKernelGGL(vdnh3::factor_kernel<64>, dim3(n), dim3(256), 0, s, A, B, alpha, phi, jay, jay_scale, info);
+  return check_launch("delta_factor");
+}
+
+extern "C" int vdnh3_sana_factor(const float *A, const float *B, const float *alpha, float *phi, float *jay,
+                                 int tokens_per_frame, int n, int head_dim, void *stream) {
+  VDNH3_HOST_CHECK(A && B && phi && jay && n > 0 && head_dim > 0 && tokens_per_frame > 0, VDNH3_ERR_INVALID,
+                   "sana_factor: empty or null operand");
+  const int64_t total = (int64_t)n * head_dim * head_dim;
+  const float inv_t = 1.f / (float)tokens_per_frame;
+  hipLaunchKernelGGL(vdnh3::sana_factor_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), A, B, alpha, phi, jay, inv_t, sqrtf(inv_t), total, head_dim);
+  return check_launch("sana_factor");
+}
+
+extern "C" int vdnh3_delta_scan(const float *phi, const float *jay, const float *init, float *prefix, float *suffix,
+                                int frames, int heads, int head_dim, void *stream) {
+  int rc = check_dim(head_dim);
+  if (rc) return rc;
+  VDNH3_HOST_CHECK(phi && jay && prefix && suffix && frames > 0 && heads > 0, VDNH3_ERR_INVALID,
+                   "delta_scan: empty or null operand");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(heads * 2 * (head_dim / 32));
+  if (head_dim == 128)
+    hipLaunchKernelGGL(vdnh3::scan_kernel<128>, grid, dim3(256), 0, s, phi, jay, init, prefix, suffix, frames, heads);
+  else
+    hipLaunchKernelGGL(vdnh3::scan_kernel<64>, grid, dim3(128), 0, s, phi, jay, init, prefix, suffix, frames, heads);
+  return check_launch("delta_scan");
+}
+
+extern "C" int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, const float *prefix,
+                             const float *suffix, const float *alpha, const float *text_state, const int32_t *bounds,
+                             int use_alpha, const uint16_t *norm_w, const uint16_t *gate, int64_t gate_row,
+                             uint16_t *out, int64_t out_row, int frames, int tokens, int heads, int head_dim,
+                             void *stream) {
+  int rc = check_dim(head_dim);
+  if (rc) return rc;
+  VDNH3_HOST_CHECK(q && prefix && suffix && alpha && bounds && norm_w && gate && out && frames > 0 && tokens > 0,
+                   VDNH3_ERR_INVALID, "readout: empty or null operand");
+  VDNH3_HOST_CHECK(q_row % 8 == 0 && q_head % 8 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                       gate_row % 4 == 0 && out_row % 4 == 0 && reinterpret_cast<uintptr_t>(gate) % 8 == 0 &&
+                       reinterpret_cast<uintptr_t>(out) % 8 == 0 && reinterpret_cast<uintptr_t>(norm_w) % 8 == 0,
+                   VDNH3_ERR_INVALID, "readout: misaligned q / gate / out / norm weight");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(frames * heads);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(vdnh3::readout_kernel<128>, grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix, alpha,
+                       text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames, tokens, heads);
+  else
+    hipLaunchKernelGGL(vdnh3::readout_kernel<64>, grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix, alpha,
+                       text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames, tokens, heads);
+  return check_launch("readout");
+}
+
+extern "C" int vdnh3_frame_mean(const uint16_t *x, int64_t x_row, int frames, int tokens, int hidden, float *out,
+                                void *stream) {
+  VDNH3_HOST_CHECK(x && out && frames > 0 && tokens > 0 && hidden > 0, VDNH3_ERR_INVALID,
+                   "frame_mean: empty or null operand");
+  hipLaunchKernelGGL(vdnh3::frame_mean_kernel, dim3(frames, (hidden + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, x_row, tokens, hidden, out);
+  return check_launch("frame_mean");
+}
+
+extern "C" int vdnh3_linear_f32(const float *x, int64_t x_row, const void *w, int w_bf16, int64_t w_row,
+                                const float *bias, float *out, int64_t out_row, int M, int N, int K, void *stream) {
+  VDNH3_HOST_CHECK(x && w && out && M > 0 && N > 0 && K > 0, VDNH3_ERR_INVALID, "linear_f32: empty or null operand");
+  const int64_t total = (int64_t)M * N;
+  hipLaunchKernelGGL(vdnh3::linear_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, x_row, w, w_bf16, w_row, bias, out, out_row, M, N, K);
+  return check_launch("linear_f32");
+}
+
+extern "C" int vdnh3_alpha_decay(const float *delta, const float *a_log, float *alpha, int frames, int heads,
+                                 int head_dim, void *stream) {
+  VDNH3_HOST_CHECK(delta && a_log && alpha && frames > 0 && heads > 0 && head_dim > 0, VDNH3_ERR_INVALID,
+                   "alpha_decay: empty or null operand");
+  const int64_t n = (int64_t)frames * heads * head_dim;
+  hipLaunchKernelGGL(vdnh3::alpha_decay_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), delta, a_log, alpha, n, heads, head_dim);
+  return check_launch("alpha_decay");
+}
+
+extern "C" int vdnh3_fill_rows_bf16(uint16_t *p, int64_t ld, int rows, int cols, float value, void *stream) {
+  VDNH3_HOST_CHECK(p && rows >= 0 && cols >= 0 && ld >= cols, VDNH3_ERR_INVALID, "fill_rows: bad operand");
+  if (rows == 0 || cols == 0) return VDNH3_OK;
+  const int64_t n = (int64_t)rows * cols;
+  const uint32_t u = __builtin_bit_cast(uint32_t, value);
+  const uint16_t b = uint16_t((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  hipLaunchKernelGGL(vdnh3::fill_rows_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p, ld, rows, cols, b);
+  return check_launch("fill_rows_bf16");
+}

@@ -49,6 +49,18 @@ SIGNATURES = {
                             _vp, _c_int, _vp, _c_int, _c_float, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_quant_rows": (_c_int, [_c_int, _vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _vp]),
     "vdnh3_quant_tensor_f8": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _vp]),
+    "vdnh3_frame_stats": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                   _vp, _vp, _vp]),
+    "vdnh3_delta_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_float, _vp, _c_int, _c_int, _vp]),
+    "vdnh3_sana_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "vdnh3_delta_scan": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "vdnh3_readout": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_i64,
+                               _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "vdnh3_frame_mean": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _vp, _vp]),
+    "vdnh3_linear_f32": (_c_int, [_vp, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_i64, _c_int, _c_int, _c_int,
+                                  _vp]),
+    "vdnh3_alpha_decay": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "vdnh3_fill_rows_bf16": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_float, _vp]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,291 @@
+"""Video Delta Attention (the VDN linear branch) on MI355X: functional ops.
+
+Mirrors the inference pieces of ``vdn_h3/branch.py`` with HIP kernels behind each:
+
+* ``cholesky_runtime_scope`` / deferred SPD validation (``:24-71``): factor statuses are
+  collected on the device and checked once when the scope exits, raising
+  ``torch.linalg.LinAlgError`` with the reference's message;
+* ``frame_statistics_raw`` - ``frame_statistics`` (``:197-282``) with the feature map of
+  ``vdn_h3/kernels.py:47-51`` fused into the loads;
+* ``VdnDelta`` / ``SanaDelta`` ``.factor_apply`` (``:144-180``);
+* ``run_scans_inference`` (``:315-333``);
+* ``alpha_gate`` (``:483-491``), ``frame_mean``;
+* ``readout_epilogue`` - ``gather_linear_state`` + readout matmul + ``linear_epilogue``
+  (``:372-396``, ``:494-530``, ``vdn_h3/runtime.py:406-419``) as one kernel.
+
+Every op takes and returns device tensors; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+from contextlib import contextmanager
+from contextvars import ContextVar
+from typing import Any
+
+import torch
+
+from . import _lib
+
+TEXT_STATE_SCALE = 0.5
+_CHOLESKY_CHECKS: ContextVar[Any] = ContextVar("vdn_h3_amd_cholesky_checks", default=None)
+
+
+class _CholeskyChecks:
+    """Factor statuses of one forward, validated with a single host read."""
+
+    def __init__(self):
+        self.statuses: list[torch.Tensor] = []
+        self.factor_calls = 0
+
+    def validate(self):
+        if not self.statuses:
+            return
+        info = torch.cat([s.reshape(-1) for s in self.statuses])
+        bad = torch.nonzero(info != 0)
+        if bad.numel():
+            failed = int(bad[0, 0])
+            for index, status in enumerate(self.statuses):
+                if failed < status.numel():
+                    minor = int(status.reshape(-1)[failed])
+                    raise torch.linalg.LinAlgError(
+                        f"VDN-H3 Cholesky factor {index}, batch {failed}: "
+                        f"leading minor of order {minor} is not positive-definite")
+                failed -= status.numel()
+
+
+@contextmanager
+def cholesky_runtime_scope(diagnostics=None):
+    """Collect factor statuses inside the scope; validate them once on exit."""
+    del diagnostics
+    checks = _CholeskyChecks()
+    token = _CHOLESKY_CHECKS.set(checks)
+    try:
+        yield checks
+        checks.validate()
+    finally:
+        checks.statuses.clear()
+        _CHOLESKY_CHECKS.reset(token)
+
+
+def _record_status(info: torch.Tensor):
+    checks = _CHOLESKY_CHECKS.get()
+    if checks is None:
+        scope = _CholeskyChecks()
+        scope.statuses.append(info)
+        scope.validate()
+        return
+    checks.statuses.append(info)
+    checks.factor_calls += 1
+
+
+def _dim(head_dim: int):
+    if head_dim not in (64, 128):
+        raise ValueError(f"the HIP delta-rule kernels support head_dim 64 or 128, got {head_dim}")
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """A ``[rows, heads, D]`` view whose D is contiguous and whose strides are 16-byte multiples."""
+    if t.stride(-1) != 1 or t.stride(0) % 8 or t.stride(1) % 8 or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def frame_statistics_raw(k_raw: torch.Tensor, v_raw: torch.Tensor, beta: torch.Tensor, num_frames: int,
+                         tokens_per_frame: int):
+    """``A, B`` ``[F, H, D, D]`` fp32 from raw ``k``/``v`` rows ``[F*T, H, D]`` and ``beta`` ``[F*T, H]``."""
+    if k_raw.shape != v_raw.shape or k_raw.ndim != 3:
+        raise ValueError("key and value must share shape [rows, heads, dim]")
+    rows, heads, dim = k_raw.shape
+    if rows != num_frames * tokens_per_frame:
+        raise ValueError("rows must equal num_frames * tokens_per_frame")
+    if beta.shape != (rows, heads):
+        raise ValueError("beta must have shape [rows, heads]")
+    _dim(dim)
+    device = _lib.require_device(k_raw, v_raw, beta)
+    k_raw, v_raw = _rows(k_raw), _rows(v_raw)
+    if k_raw.stride() != v_raw.stride():
+        v_raw = v_raw.contiguous()
+        k_raw = k_raw.contiguous()
+    beta = beta.to(torch.bfloat16)
+    if beta.stride(1) != 1:
+        beta = beta.contiguous()
+    a = torch.empty((num_frames, heads, dim, dim), dtype=torch.float32, device=device)
+    b = torch.empty_like(a)
+    rc = _lib.lib().vdnh3_frame_stats(_lib.ptr(k_raw), _lib.ptr(v_raw), k_raw.stride(0), k_raw.stride(1),
+                                      _lib.ptr(beta), beta.stride(0), num_frames, tokens_per_frame, heads, dim,
+                                      _lib.ptr(a), _lib.ptr(b), _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_frame_stats")
+    return a, b
+
+
+class VdnDelta:
+    """``Phi = diag(alpha) (I + A)^-1``, ``J = B (I + A)^-1`` by Cholesky, with deferred SPD checks."""
+
+    def __init__(self, tokens_per_frame: int | None = None):
+        del tokens_per_frame
+
+    def factor_apply(self, alpha, a_raw, b_raw, *, jay_scale: float = 1.0, need_phi: bool = True):
+        if a_raw.shape != b_raw.shape or a_raw.shape[-1] != a_raw.shape[-2]:
+            raise ValueError("A and B must share a square [..., D, D] shape")
+        if alpha is not None and alpha.shape != a_raw.shape[:-1]:
+            raise ValueError("alpha must have shape A.shape[:-1]")
+        dim = a_raw.shape[-1]
+        _dim(dim)
+        device = _lib.require_device(a_raw, b_raw, alpha)
+        a32, b32 = a_raw.float().contiguous(), b_raw.float().contiguous()
+        n = a32.numel() // (dim * dim)
+        phi = torch.empty_like(a32) if need_phi else None
+        jay = torch.empty_like(a32)
+        info = torch.empty(a32.shape[:-2], dtype=torch.int32, device=device)
+        al = None if alpha is None else alpha.float().contiguous()
+        rc = _lib.lib().vdnh3_delta_factor(_lib.ptr(a32), _lib.ptr(b32), _lib.ptr(al), _lib.ptr(phi), _lib.ptr(jay),
+                                           float(jay_scale), _lib.ptr(info), n, dim, _lib.stream_handle(device))
+        _lib.check(rc, "vdnh3_delta_factor")
+        _record_status(info)
+        return phi, jay
+
+
+class SanaDelta:
+    """``Phi = alpha (I - A/T)``, ``J = B / sqrt(T)``."""
+
+    def __init__(self, tokens_per_frame: int):
+        if tokens_per_frame <= 0:
+            raise ValueError("tokens_per_frame must be positive")
+        self.tokens = int(tokens_per_frame)
+
+    def factor_apply(self, alpha, a_raw, b_raw, *, jay_scale: float = 1.0, need_phi: bool = True):
+        if a_raw.shape != b_raw.shape or a_raw.shape[-1] != a_raw.shape[-2]:
+            raise ValueError("A and B must share a square [..., D, D] shape")
+        dim = a_raw.shape[-1]
+        device = _lib.require_device(a_raw, b_raw, alpha)
+        a32, b32 = a_raw.float().contiguous(), b_raw.float().contiguous()
+        phi, jay = torch.empty_like(a32), torch.empty_like(a32)
+        al = None if alpha is None else alpha.float().contiguous()
+        rc = _lib.lib().vdnh3_sana_factor(_lib.ptr(a32), _lib.ptr(b32), _lib.ptr(al), _lib.ptr(phi), _lib.ptr(jay),
+                                          self.tokens, a32.numel() // (dim * dim), dim, _lib.stream_handle(device))
+        _lib.check(rc, "vdnh3_sana_factor")
+        if jay_scale != 1.0:
+            jay.mul_(jay_scale)
+        return phi, jay
+
+
+DELTA_BACKENDS = {"vdn_solve": VdnDelta, "sana_scaled": SanaDelta}
+
+
+def run_scans_from_factors(transitions, injections, initial=None):
+    """Prefix / suffix scans from already factored ``Phi``/``J`` ``[F, H, D, D]``."""
+    frames, heads, dim, _ = transitions.shape
+    _dim(dim)
+    device = _lib.require_device(transitions, injections, initial)
+    transitions, injections = transitions.contiguous(), injections.contiguous()
+    if initial is not None:
+        if initial.shape != (heads, dim, dim):
+            raise ValueError("text_state must have shape [heads, D, D]")
+        initial = initial.float().contiguous()
+    prefix = torch.empty_like(transitions)
+    suffix = torch.empty_like(transitions)
+    rc = _lib.lib().vdnh3_delta_scan(_lib.ptr(transitions), _lib.ptr(injections), _lib.ptr(initial),
+                                     _lib.ptr(prefix), _lib.ptr(suffix), frames, heads, dim,
+                                     _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_delta_scan")
+    return prefix, suffix
+
+
+def run_scans_inference(backend, alpha, a_raw, b_raw, text_state=None):
+    """Factor all frames, then the bidirectional recurrence (``vdn_h3/branch.py:315-333``)."""
+    if a_raw.ndim != 4 or a_raw.shape != b_raw.shape or a_raw.shape[0] == 0:
+        raise ValueError("A and B must share non-empty [frames, heads, D, D] shape")
+    phi, jay = backend.factor_apply(alpha, a_raw, b_raw)
+    return run_scans_from_factors(phi, jay, text_state)
+
+
+def frame_mean(xv: torch.Tensor, num_frames: int, tokens_per_frame: int) -> torch.Tensor:
+    """``xv.reshape(F, T, -1).mean(1, dtype=float32)``."""
+    device = _lib.require_device(xv)
+    if xv.stride(1) != 1:
+        xv = xv.contiguous()
+    out = torch.empty((num_frames, xv.shape[1]), dtype=torch.float32, device=device)
+    rc = _lib.lib().vdnh3_frame_mean(_lib.ptr(xv), xv.stride(0), num_frames, tokens_per_frame, xv.shape[1],
+                                     _lib.ptr(out), _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_frame_mean")
+    return out
+
+
+def linear_f32(x: torch.Tensor, weight: torch.Tensor, bias=None) -> torch.Tensor:
+    """fp32 ``F.linear(x, weight.float(), bias)`` (small projections)."""
+    device = _lib.require_device(x, weight, bias)
+    x = x.float().contiguous()
+    if weight.dtype == torch.bfloat16:
+        w, w_bf16 = weight.contiguous(), 1
+    else:
+        w, w_bf16 = weight.float().contiguous(), 0
+    b = None if bias is None else bias.float().contiguous()
+    m, k = x.shape
+    n = w.shape[0]
+    out = torch.empty((m, n), dtype=torch.float32, device=device)
+    rc = _lib.lib().vdnh3_linear_f32(_lib.ptr(x), x.stride(0), _lib.ptr(w), w_bf16, w.stride(0), _lib.ptr(b),
+                                     _lib.ptr(out), out.stride(0), m, n, k, _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_linear_f32")
+    return out
+
+
+def alpha_gate(frame_mean_f32, weight_down, weight_up, dt_bias, a_log, num_heads, head_dim):
+    """``exp(-exp(A_log) * softplus(W_up W_down m + dt_bias))`` as ``[F, H, D]`` fp32."""
+    d1 = linear_f32(frame_mean_f32, weight_down)
+    d2 = linear_f32(d1, weight_up, dt_bias)
+    if d2.shape[-1] != num_heads * head_dim or a_log.numel() != num_heads:
+        raise ValueError("alpha weights are incompatible with head geometry")
+    device = d2.device
+    alpha = torch.empty((d2.shape[0], num_heads, head_dim), dtype=torch.float32, device=device)
+    a_log = a_log.float().contiguous()
+    rc = _lib.lib().vdnh3_alpha_decay(_lib.ptr(d2), _lib.ptr(a_log), _lib.ptr(alpha), d2.shape[0], num_heads,
+                                      head_dim, _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_alpha_decay")
+    return alpha
+
+
+def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *, text_state=None,
+                     bridge="alpha", num_frames, tokens_per_frame, out=None):
+    """Gather, readout and RMSNorm/gate epilogue: ``[F*T, H*D]`` bf16."""
+    if bridge not in ("alpha", "none"):
+        raise ValueError("bridge must be 'alpha' or 'none'")
+    rows, heads, dim = q_raw.shape
+    _dim(dim)
+    if len(bounds) != num_frames:
+        raise ValueError("bounds must contain one entry per frame")
+    for frame, (lo, hi) in enumerate(bounds):
+        if lo > frame or hi < frame or lo > hi:
+            raise ValueError(f"bounds[{frame}] does not contain its query frame")
+    device = _lib.require_device(q_raw, prefix, suffix, alpha, gate, text_state, out)
+    q_raw = _rows(q_raw)
+    bounds_t = torch.tensor([int(x) for pair in bounds for x in pair], dtype=torch.int32).to(device)
+    norm_w = norm_weight.to(torch.bfloat16).contiguous()
+    gate = gate.to(torch.bfloat16)
+    if gate.stride(1) != 1:
+        gate = gate.contiguous()
+    text = None if text_state is None else text_state.float().contiguous()
+    if out is None:
+        out = torch.empty((rows, heads * dim), dtype=torch.bfloat16, device=device)
+    rc = _lib.lib().vdnh3_readout(_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), _lib.ptr(prefix),
+                                  _lib.ptr(suffix), _lib.ptr(alpha.contiguous()), _lib.ptr(text), _lib.ptr(bounds_t),
+                                  int(bridge == "alpha"), _lib.ptr(norm_w), _lib.ptr(gate), gate.stride(0),
+                                  _lib.ptr(out), out.stride(0), num_frames, tokens_per_frame, heads, dim,
+                                  _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_readout")
+    return out
+
+
+def fill_rows(t: torch.Tensor, value: float = 0.0):
+    """Fill a bf16 ``[rows, cols]`` view (contiguous rows) with ``value`` on the device."""
+    if t.numel() == 0:
+        return t
+    device = _lib.require_device(t)
+    rc = _lib.lib().vdnh3_fill_rows_bf16(_lib.ptr(t), t.stride(0), t.shape[0], t.shape[1], float(value),
+                                         _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_fill_rows_bf16")
+    return t
+
+
+__all__ = ["DELTA_BACKENDS", "SanaDelta", "TEXT_STATE_SCALE", "VdnDelta", "alpha_gate", "cholesky_runtime_scope",
+           "fill_rows", "frame_mean", "frame_statistics_raw", "linear_f32", "readout_epilogue",
+           "run_scans_from_factors", "run_scans_inference"]

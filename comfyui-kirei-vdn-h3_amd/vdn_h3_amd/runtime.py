@@ -1,0 +1,160 @@
+"""The VDN linear branch the hybrid block calls: ``OptimizedLinearBranch.projected_delta``.
+
+Mirrors ``vdn_h3/runtime.py`` (``OptimizedLinearBranch`` ``:237-607``, ``projected_delta``
+``:545-607``) and ``LinearBranch.readout`` (``vdn_h3/branch.py:672-722``): same arguments, the
+same anchor-frame handling (``skip_ends`` slices frames 0 and F-1 off before any branch work
+and leaves their rows zero), the text state (``vdn_h3/branch.py:649-670``) and the projector
+hook. The inference spelling only: the device path runs under ``torch.no_grad()``.
+
+Per call, on the caller's current stream:
+  beta (GEMM + sigmoid) -> frame statistics (features fused) -> frame means -> alpha
+  -> text state (statistics + factor, J scaled by 1/2) -> factor of every frame
+  -> bidirectional scans -> output gate (two GEMMs + sigmoid)
+  -> gather + readout + RMSNorm epilogue -> projector (bf16 / fp8 / int8 GEMM).
+"""
+
+from __future__ import annotations
+
+from typing import Mapping
+
+import torch
+
+from . import branch as _b
+from . import linear as _linear
+from . import projection as _projection
+
+
+class OptimizedLinearBranch:
+    """One block's VDN branch (weights are passed per call, as in the reference)."""
+
+    def __init__(self, weights: Mapping[str, torch.Tensor] | None, num_heads: int, head_dim: int,
+                 delta_rule: str = "vdn_solve", bridge: str = "alpha", a_fp32: bool = True, short_conv=(),
+                 enable_text_state: bool = True, **_runtime):
+        if delta_rule not in _b.DELTA_BACKENDS:
+            raise ValueError(f"unknown delta rule: {delta_rule!r}")
+        if bridge not in ("alpha", "none"):
+            raise ValueError("bridge must be 'alpha' or 'none'")
+        targets = tuple(short_conv)
+        if len(set(targets)) != len(targets) or any(t not in ("q", "k", "v") for t in targets):
+            raise ValueError("short_conv must be a distinct subset of ('q', 'k', 'v')")
+        if targets:
+            raise NotImplementedError("the HIP branch does not implement the K/V short convolutions yet; "
+                                      "use short_conv=()")
+        if not a_fp32:
+            raise NotImplementedError("the HIP branch computes A at full fp32 accuracy (a_fp32=True)")
+        self.w = weights
+        self.num_heads = int(num_heads)
+        self.head_dim = int(head_dim)
+        self.delta_rule = delta_rule
+        self.bridge = bridge
+        self.a_fp32 = True
+        self.short_conv = targets
+        self.enable_text_state = bool(enable_text_state)
+
+    def _backend(self, tokens):
+        return _b.DELTA_BACKENDS[self.delta_rule](tokens)
+
+    def _text_state(self, weights, text_x, text_k_raw, text_v_raw):
+        if not self.enable_text_state or text_x is None:
+            return None
+        if text_k_raw is None or text_v_raw is None:
+            raise ValueError("text state needs both raw text key and value")
+        length = text_x.shape[0]
+        if length <= 0 or text_k_raw.shape[0] != length or text_v_raw.shape[0] != length:
+            raise ValueError("text tensors must share a positive sequence length")
+        beta = _linear.sigmoid_linear(text_x, weights["beta_proj.weight"])
+        a, b = _b.frame_statistics_raw(text_k_raw, text_v_raw, beta, 1, length)
+        _, jay = self._backend(length).factor_apply(None, a, b, jay_scale=_b.TEXT_STATE_SCALE, need_phi=False)
+        return jay[0]
+
+    def _readout_flat(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, text_x,
+                      text_k_raw, text_v_raw, out=None):
+        heads, dim = self.num_heads, self.head_dim
+        beta = _linear.sigmoid_linear(xv, weights["beta_proj.weight"])
+        a, b = _b.frame_statistics_raw(k_raw, v_raw, beta, num_frames, tokens_per_frame)
+        mean = _b.frame_mean(xv, num_frames, tokens_per_frame)
+        alpha = _b.alpha_gate(mean, weights["alpha.down.weight"], weights["alpha.up.weight"],
+                              weights["alpha.dt_bias"], weights["alpha.A_log"], heads, dim)
+        text_state = self._text_state(weights, text_x, text_k_raw, text_v_raw)
+        prefix, suffix = _b.run_scans_inference(self._backend(tokens_per_frame), alpha, a, b, text_state)
+        del a, b
+        hidden = _linear.linear(xv, weights["output_gate.down.weight"])
+        gate = _linear.sigmoid_linear(hidden, weights["output_gate.up.weight"], weights.get("output_gate.up.bias"))
+        return _b.readout_epilogue(q_raw, prefix, suffix, alpha, bounds, weights["norm.weight"], gate,
+                                   text_state=text_state, bridge=self.bridge, num_frames=num_frames,
+                                   tokens_per_frame=tokens_per_frame, out=out)
+
+    def _check(self, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds):
+        if torch.is_grad_enabled():
+            raise RuntimeError("VDN-H3 inference linear branch requires no_grad/inference_mode")
+        rows = num_frames * tokens_per_frame
+        if xv.ndim != 2 or xv.shape[0] != rows:
+            raise ValueError("xv rows must equal num_frames * tokens_per_frame")
+        expected = (rows, self.num_heads, self.head_dim)
+        if q_raw.shape != expected or k_raw.shape != expected or v_raw.shape != expected:
+            raise ValueError("raw q/k/v have incompatible video row/head geometry")
+        if len(bounds) != num_frames:
+            raise ValueError("bounds must contain one entry per frame")
+
+    def readout(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, frame_size=None,
+                text_x=None, text_k_raw=None, text_v_raw=None, skip_ends=False, *, inference=True):
+        """Branch readout before ``to_out_linear``: ``[F*T, H*D]`` bf16, anchor rows zero with ``skip_ends``."""
+        del frame_size, inference
+        self._check(xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds)
+        rows = num_frames * tokens_per_frame
+        if not skip_ends:
+            return self._readout_flat(weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds,
+                                      text_x, text_k_raw, text_v_raw)
+        out = torch.empty((rows, self.num_heads * self.head_dim), dtype=torch.bfloat16, device=xv.device)
+        if num_frames <= 2:
+            return _b.fill_rows(out)
+        t = tokens_per_frame
+        inner = slice(t, (num_frames - 1) * t)
+        _b.fill_rows(out[:t])
+        _b.fill_rows(out[(num_frames - 1) * t:])
+        self._readout_flat(weights, xv[inner], q_raw[inner], k_raw[inner], v_raw[inner], num_frames - 2, t,
+                           [(lo - 1, hi - 1) for lo, hi in bounds[1:-1]], text_x, text_k_raw, text_v_raw,
+                           out=out[inner])
+        return out
+
+    def projected_delta(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, *,
+                        frame_size=None, text_x=None, text_k_raw=None, text_v_raw=None, skip_ends=False,
+                        inference=True, projector=None, tile_frames=None, out=None, accumulate=False):
+        """Branch output after ``to_out_linear``, ``[F*T, hidden]`` bf16, anchor rows zero.
+
+        ``out``/``accumulate``: write (or add, ``out += delta``) straight into an existing
+        ``[F*T, hidden]`` bf16 view, e.g. the video rows of the block output; with
+        ``accumulate`` the anchor rows of ``out`` are left untouched (their delta is zero).
+        ``projector(rows, out=..., accumulate=...)`` defaults to ``projection.project``.
+        """
+        del frame_size, inference, tile_frames
+        self._check(xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds)
+        proj = projector or (lambda rows, **kw: _projection.project(rows, weights, **kw))
+        hidden = _projection.projection_out_features(weights)
+        original_rows = num_frames * tokens_per_frame
+        if out is None:
+            if accumulate:
+                raise ValueError("accumulate needs an existing output")
+            out = torch.empty((original_rows, hidden), dtype=torch.bfloat16, device=xv.device)
+        elif out.shape != (original_rows, hidden):
+            raise ValueError(f"out must be [{original_rows}, {hidden}]")
+        t = tokens_per_frame
+        if skip_ends:
+            if num_frames <= 2:
+                return out if accumulate else _b.fill_rows(out)
+            inner = slice(t, (num_frames - 1) * t)
+            if not accumulate:
+                _b.fill_rows(out[:t])
+                _b.fill_rows(out[(num_frames - 1) * t:])
+            flat = self._readout_flat(weights, xv[inner], q_raw[inner], k_raw[inner], v_raw[inner],
+                                      num_frames - 2, t, [(lo - 1, hi - 1) for lo, hi in bounds[1:-1]], text_x,
+                                      text_k_raw, text_v_raw)
+            proj(flat, out=out[inner], accumulate=accumulate)
+            return out
+        flat = self._readout_flat(weights, xv, q_raw, k_raw, v_raw, num_frames, t, bounds, text_x, text_k_raw,
+                                  text_v_raw)
+        proj(flat, out=out, accumulate=accumulate)
+        return out
+
+
+__all__ = ["OptimizedLinearBranch"]

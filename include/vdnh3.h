@@ -158,6 +158,76 @@ int vdnh3_quant_rows(int kind, const uint16_t *x, int64_t ldx, int M, int K, uin
 int vdnh3_quant_tensor_f8(const uint16_t *x, int64_t n, uint8_t *q, float *scale, float *amax_workspace,
                           void *stream);
 
+/* ------------------------------------------------------------------------------
+ * Video Delta Attention branch (reference vdn_h3/branch.py, vdn_h3/runtime.py)
+ * All head_dim arguments must be 64 or 128. fp32 matrices are [n][D][D] row-major.
+ * ------------------------------------------------------------------------------ */
+
+/*
+ * Frame statistics with the feature map fused in: for frame f and head h (tokens t of the
+ * frame at rows f*tokens + t of k/v, element d at p[row*kv_row + h*kv_head + d]):
+ *   k~ = L2(SiLU(k)), v~ = SiLU(v) (vdn_h3/kernels.py:47-51), b = beta[row*beta_row + h] (bf16),
+ *   A[f][h] = 0.5 (S + S^T), S = (k~ b)^T k~ in fp32        (vdn_h3/branch.py:197-241)
+ *   B[f][h] = bf16((v~ * b)^T k~)                             (vdn_h3/branch.py:242)
+ * A and B are [frames][heads][D][D] fp32.
+ */
+int vdnh3_frame_stats(const uint16_t *k, const uint16_t *v, int64_t kv_row, int64_t kv_head,
+                      const uint16_t *beta, int64_t beta_row, int frames, int tokens, int heads,
+                      int head_dim, float *A, float *B, void *stream);
+
+/*
+ * VdnDelta.factor_apply (vdn_h3/branch.py:148-160) over n matrices with the status of
+ * torch.linalg.cholesky_ex (vdn_h3/branch.py:62-71): L = chol(I + A), M = L^-T L^-1,
+ * phi = alpha[i] * M[i][j] (phi may be NULL; alpha NULL means ones), jay = jay_scale * (B M),
+ * info[i] = 0 or the order of the first non-positive leading minor.
+ */
+int vdnh3_delta_factor(const float *A, const float *B, const float *alpha, float *phi, float *jay,
+                       float jay_scale, int32_t *info, int n, int head_dim, void *stream);
+
+/* SanaDelta.factor_apply (vdn_h3/branch.py:163-177): phi = alpha (I - A/T), jay = B / sqrt(T). */
+int vdnh3_sana_factor(const float *A, const float *B, const float *alpha, float *phi, float *jay,
+                      int tokens_per_frame, int n, int head_dim, void *stream);
+
+/*
+ * Bidirectional scans (vdn_h3/runtime.py:118-131, vdn_h3/branch.py:315-333) over
+ * phi/jay [frames][heads][D][D]: prefix[f] = jay[f] + prefix[f-1] phi[f] (prefix[-1] = init),
+ * suffix[f] = jay[f] + suffix[f+1] phi[f] (suffix[frames] = init); init [heads][D][D] or NULL (zeros).
+ */
+int vdnh3_delta_scan(const float *phi, const float *jay, const float *init, float *prefix, float *suffix,
+                     int frames, int heads, int head_dim, void *stream);
+
+/*
+ * Gather + readout + epilogue (vdn_h3/branch.py:372-396, vdn_h3/runtime.py:406-419,
+ * vdn_h3/branch.py:494-505), q~ = L2(SiLU(q)) fused in. For frame f with bounds
+ * lo = max(bounds[2f], 0), hi = min(bounds[2f+1], frames-1):
+ *   L_f = bf16(before * decay_b + after * decay_a)  (before = prefix[lo-1] or text_state or 0,
+ *         after = suffix[hi+1] or text_state or 0, decays from cumulated log(alpha) when use_alpha)
+ *   r = bf16(q~ L_f^T);  out[row][h*D + v] = bf16(RMSNorm(r)[v] * norm_w[v]) * gate[row][h*D + v]
+ * alpha: [frames][heads][D] fp32; out and gate: [frames*tokens, heads*D] bf16.
+ */
+int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, const float *prefix,
+                  const float *suffix, const float *alpha, const float *text_state, const int32_t *bounds,
+                  int use_alpha, const uint16_t *norm_w, const uint16_t *gate, int64_t gate_row,
+                  uint16_t *out, int64_t out_row, int frames, int tokens, int heads, int head_dim,
+                  void *stream);
+
+/* Per-frame mean over tokens in fp32: out[f][c] = mean_t x[(f*tokens + t)*x_row + c]
+ * (vdn_h3/branch.py:743-745). */
+int vdnh3_frame_mean(const uint16_t *x, int64_t x_row, int frames, int tokens, int hidden, float *out,
+                     void *stream);
+
+/* fp32 F.linear for the small alpha projections: out = x W^T (+ bias); W fp32 or bf16
+ * (vdn_h3/branch.py:485-486). */
+int vdnh3_linear_f32(const float *x, int64_t x_row, const void *w, int w_bf16, int64_t w_row,
+                     const float *bias, float *out, int64_t out_row, int M, int N, int K, void *stream);
+
+/* alpha = exp(-exp(a_log[h]) * softplus(delta)) over [frames][heads][D] (vdn_h3/branch.py:489-491). */
+int vdnh3_alpha_decay(const float *delta, const float *a_log, float *alpha, int frames, int heads,
+                      int head_dim, void *stream);
+
+/* Fill rows x cols of a bf16 matrix with a constant (anchor-frame rows of the branch output). */
+int vdnh3_fill_rows_bf16(uint16_t *p, int64_t ld, int rows, int cols, float value, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -121,7 +121,7 @@ def test_fp8_gemm(device, per_tensor):
     got = fp8.project(x.to(device), {fp8.FP8_WEIGHT_KEY: wq, fp8.FP8_SCALE_KEY: ws}).float().cpu()
     want = qo.fp8_linear(xq.cpu(), xs.cpu(), wq.cpu(), ws.cpu()).float()
     err = (got - want).abs().max().item()
-    cos = torch.nn.functional.cosine_similarity(got.flatten(), want.flatten(), dim=0).item()
+    cos = torch.nn.functional.cosine_similarity(got.double().flatten(), want.double().flatten(), dim=0).item()
     assert err <= 2e-2 and cos >= 0.9995, (err, cos)
 
 

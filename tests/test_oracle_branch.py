@@ -175,6 +175,6 @@ def test_branch_oracle_matches_reference_golden(name):
     # the oracle reproduces the reference's bf16 values; a few differ by one rounding step
     assert err <= 4e-3 * max(1.0, scale), (err, scale)
     assert (delta.float() == want).float().mean().item() >= 0.999
-    cos = F.cosine_similarity(delta.float().flatten(), want.flatten(), dim=0).item()
+    cos = F.cosine_similarity(delta.double().flatten(), want.double().flatten(), dim=0).item()
     assert cos >= 0.99999, cos
     assert torch.count_nonzero(delta[:tpf]) == 0 and torch.count_nonzero(delta[-tpf:]) == 0

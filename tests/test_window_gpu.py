@@ -24,7 +24,7 @@ def assert_parity(got, want, atol=ATOL, min_cos=MIN_COS):
     assert got.shape == want.shape
     assert torch.isfinite(got).all()
     err = (got - want).abs().max().item()
-    cos = torch.nn.functional.cosine_similarity(got.flatten(), want.flatten(), dim=0).item()
+    cos = torch.nn.functional.cosine_similarity(got.double().flatten(), want.double().flatten(), dim=0).item()
     assert err <= atol and cos >= min_cos, f"max abs {err:.3e}, cosine {cos:.6f}"
     assert torch.allclose(got, want, atol=2e-2, rtol=4e-2)
 
