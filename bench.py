@@ -1,15 +1,24 @@
 #!/usr/bin/env python3
 """Benchmark of the VDN-H3 hybrid attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload window]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload block]
 
-Prints one JSON line. Workload ``window``: exact local-window softmax attention at the
-full shape (512 text rows + 31 frames x 1296 tokens = 40 688 rows, 40 heads x 128,
-chunk 5, radius 1, anchors both), inputs resident in HBM before timing. A step is one
-call of the op (V^T pre-pass + attention kernel). ``value`` is algorithmic TFLOP/s of
-the step (``4 * D * H * allowed pairs``, masked tile work and exp not counted);
-``roofline`` is the attention kernel alone, timed with HIP events on the stream it
-runs on; ``cpu_baseline`` times the CPU oracle on a bounded sample of query rows.
+Prints one JSON line. Inputs and weights are resident in HBM before timing; synthetic
+seeded data, random-init weights.
+
+Workload ``block`` (default): one hybrid attention block, the patched ``attn.forward``, at the
+full shape: 512 text rows + 31 frames x 1296 tokens = 40 688 rows, hidden 5120, 40 heads x
+128, chunk 5, radius 1, anchors both. A step is one block forward: W8A8 int8 qkv projection,
+q/k RMSNorm, softmax gate, window attention (gate fused), W8A8 out projection, and the VDN
+branch (29 inner frames) with its int8 to_out_linear accumulated into the output.
+``value`` is the block's algorithmic work per second (int8 OPs + bf16/fp32 FLOPs, listed per
+stage in ``config.work_per_step``); ``roofline`` is the window attention kernel (the dominant
+kernel), timed with HIP events on the stream it runs on; ``stages_ms`` are per-stage event
+timings of the same timed steps.
+
+Other workloads: ``window`` (attention alone), ``branch`` (VDN branch alone),
+``gemm_{i8,f8}_{qkv,out}`` (W8A8 GEMMs alone), ``hbm_copy`` (counter calibration).
+``cpu_baseline`` times the CPU oracle on a bounded sample of query rows.
 """
 
 from __future__ import annotations
@@ -29,14 +38,17 @@ sys.path.insert(0, str(ROOT))
 METRIC = "VDN hybrid block ms + TFLOP/s (% MFMA peak) at 40,688 tok x 40 heads, 1 GPU"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+PEAK_I8_TOPS = 5000.0       # dense int8 MFMA
+PEAK_F8_TFLOPS = 5000.0     # dense fp8 MFMA
 
 
 def _parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="window", choices=["window", "hbm_copy"],
+    ap.add_argument("--workload", default="block", choices=["block", "window", "hbm_copy", "branch", "gemm_i8_qkv",
+                                                             "gemm_i8_out", "gemm_f8_qkv", "gemm_f8_out"],
                     help="hbm_copy: a plain 1 GiB device copy, the reference point for scaling rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes")
     ap.add_argument("--cpu-sample-rows", type=int, default=2048,
@@ -145,6 +157,194 @@ def bench_hbm_copy(args, torch, device):
                          "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}
 
 
+def _time_steps(torch, stream, steps, warmup, fn):
+    """Mean ms per call of ``fn`` over ``steps`` timed calls (HIP events on ``stream``)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        fn()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def block_flops(lay, heads, dim, hidden, pairs_per_head):
+    """Algorithmic work of one hybrid block (int8 OPs of the W8A8 GEMMs + bf16/fp32 FLOPs), by stage."""
+    s, inner = lay.seq_len, heads * dim
+    fi = lay.num_frames - 2 if lay.anchor_frames == "both" else lay.num_frames
+    r, t = fi * lay.tokens_per_frame, lay.tokens_per_frame
+    return {
+        "qkv_proj": 2.0 * s * hidden * 3 * inner,
+        "softmax_gate": 2.0 * s * hidden * heads,
+        "window_attention": 4.0 * dim * heads * pairs_per_head,
+        "out_proj": 2.0 * s * inner * hidden,
+        "branch_core": fi * heads * (6.0 * t * dim * dim + (11.0 / 3.0) * dim ** 3 + 4.0 * dim ** 3),
+        "branch_gates": 2.0 * r * hidden * dim + 2.0 * r * dim * inner + 2.0 * r * hidden * heads,
+        "branch_text_state": heads * (4.0 * lay.text_len * dim * dim + (11.0 / 3.0) * dim ** 3)
+                             + 2.0 * lay.text_len * hidden * heads,
+        "to_out_linear": 2.0 * r * inner * hidden,
+    }
+
+
+def bench_block(args, torch, device):
+    """One VDN-H3 hybrid attention block at the full shape (the patched attn.forward)."""
+    from types import SimpleNamespace
+
+    from vdn_h3_amd import projection, synth
+    from vdn_h3_amd.hybrid import VDNState, forward_scope, make_vdn_forward
+    from vdn_h3_amd.linear import HipLinear
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+
+    w = synth.WINDOW_FULL
+    lay = w.layout
+    heads, dim, hidden = w.heads, w.head_dim, 5120
+    x = synth.randn((lay.seq_len, hidden), 0, device=device, dtype=torch.bfloat16)
+    attn = SimpleNamespace(
+        heads=heads, head_dim=dim, forward=None,
+        qkv_proj=HipLinear(synth.randn((3 * heads * dim, hidden), 1, device, torch.bfloat16, 0.02), "int8"),
+        out_proj=HipLinear(synth.randn((hidden, heads * dim), 2, device, torch.bfloat16, 0.02), "int8"),
+        q_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), 3, device)).to(torch.bfloat16), eps=1e-6),
+        k_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), 4, device)).to(torch.bfloat16), eps=1e-6))
+    (bw,), _ = projection.prepare_projection_maps([synth.branch_weights(heads, dim, hidden, device=device)],
+                                                  device, "int8")
+    branch = OptimizedLinearBranch(bw, heads, dim)
+    state = VDNState("bench", {"enable_softmax_gate": True, "linear_enabled": True, "enable_text_state": True},
+                     [branch], heads, dim, projection_precision="int8", diagnostics=True)
+    forward = make_vdn_forward(attn, state, 0)
+    stream = torch.cuda.current_stream(device)
+    with torch.no_grad(), forward_scope(lay):
+        for _ in range(args.warmup):
+            forward(x)
+        torch.cuda.synchronize()
+        state.diagnostics.clear()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(args.steps):
+            forward(x)
+        t1.record(stream)
+        torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    stages = {k: v["mean_ms"] for k, v in state.diagnostics.snapshot()["stages"].items()}
+    plan = state.window_cache.plan(lay.seq_len, lay.video_start, lay.video_end, lay.num_frames,
+                                   lay.tokens_per_frame, lay.bounds, lay.anchor_frames, device)
+    work = block_flops(lay, heads, dim, hidden, plan.pairs_per_head)
+    total = sum(work.values())
+    attn_ms = stages["attention.softmax.kernel"]
+    attn_tflops = work["window_attention"] / (attn_ms * 1e-3) / 1e12
+    qkv_tops = work["qkv_proj"] / (stages["attention.qkv"] * 1e-3) / 1e12
+    out_tops = work["out_proj"] / (stages["attention.out_proj"] * 1e-3) / 1e12
+    return {
+        "metric": METRIC,
+        "value": round(total / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 4),
+        "dtype": "int8+bf16",
+        "config": {"workload": "hybrid_block_s40688_h40_d128_hidden5120_int8proj", "seq_len": lay.seq_len,
+                   "heads": heads, "head_dim": dim, "hidden": hidden, "frames": lay.num_frames,
+                   "tokens_per_frame": lay.tokens_per_frame, "text_rows": lay.text_len, "chunk": w.chunk,
+                   "radius": w.radius, "anchor_frames": lay.anchor_frames,
+                   "projections": "W8A8 int8 qkv/out/to_out_linear (per-token x per-channel)",
+                   "allowed_pairs_per_head": plan.pairs_per_head, "work_per_step": work,
+                   "work_total": total},
+        "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128>", "achieved": round(attn_tflops, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+                     "kernel_ms": round(attn_ms, 4), "traffic": _traffic(args.traffic_json, "window_attn_kernel")},
+        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
+        "stage_rooflines": {
+            "qkv_proj (quant + int8 GEMM)": {"achieved_TOPs": round(qkv_tops, 1),
+                                             "frac_int8_peak": round(qkv_tops / PEAK_I8_TOPS, 4)},
+            "out_proj (quant + int8 GEMM)": {"achieved_TOPs": round(out_tops, 1),
+                                             "frac_int8_peak": round(out_tops / PEAK_I8_TOPS, 4)},
+            "window_attention": {"achieved_TFLOPs": round(attn_tflops, 1),
+                                 "frac_bf16_peak": round(attn_tflops / PEAK_BF16_TFLOPS, 4)},
+        },
+        "linear_to_softmax_ratio": round(stages["attention.linear_branch"] / stages["attention.softmax"], 4),
+    }
+
+
+def bench_gemm(args, torch, device):
+    """W8A8 projection GEMM at the block's shapes: M=40,688 tokens, K=5,120, N=15,360 (qkv) or 5,120 (out)."""
+    from vdn_h3_amd import linear, synth
+
+    kind_name, which = args.workload.split("_")[1:]
+    m, k = 40688, 5120
+    n = 15360 if which == "qkv" else 5120
+    x = synth.randn((m, k), 30, device=device, dtype=torch.bfloat16)
+    w = synth.randn((n, k), 31, device=device, dtype=torch.bfloat16, scale=0.02)
+    if kind_name == "i8":
+        wq, ws = linear.quantize_rows(w, linear.KIND_I8)
+        quant = lambda: linear.quantize_rows(x, linear.KIND_I8)  # noqa: E731
+        peak, dtype = PEAK_I8_TOPS, "int8"
+    else:
+        wq, ws = linear.quantize_tensor_fp8(w)
+        quant = lambda: linear.quantize_tensor_fp8(x)  # noqa: E731
+        peak, dtype = PEAK_F8_TFLOPS, "fp8_e4m3"
+    xq, xs = quant()
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    stream = torch.cuda.current_stream(device)
+    gemm_ms = _time_steps(torch, stream, args.steps, args.warmup,
+                          lambda: linear.gemm_w8a8(xq, xs, wq, ws, out=out))
+    quant_ms = _time_steps(torch, stream, args.steps, args.warmup, quant)
+    ops = 2.0 * m * n * k
+    tops = ops / (gemm_ms * 1e-3) / 1e12
+    qbytes = m * k * 2 + m * k + 4 * m
+    return {
+        "metric": f"W8A8 {which} projection GEMM TOP/s ({dtype} MFMA)",
+        "value": round(tops, 2), "unit": "TOP/s", "ms_per_step": round(gemm_ms, 4), "dtype": dtype,
+        "config": {"workload": f"gemm_{kind_name}_{which}_m{m}_k{k}_n{n}", "M": m, "N": n, "K": k,
+                   "scales": "per-token x per-channel" if kind_name == "i8" else "per-tensor", "ops_per_step": ops},
+        "roofline": {"bound": "mfma", "kernel": f"gemm_nt_kernel<{kind_name}>", "achieved": round(tops, 2),
+                     "peak": peak, "unit": "TOP/s", "frac": round(tops / peak, 4), "kernel_ms": round(gemm_ms, 4),
+                     "traffic": None},
+        "breakdown_ms": {"activation_quant": round(quant_ms, 4), "gemm": round(gemm_ms, 4),
+                         "activation_quant_GBs": round(qbytes / (quant_ms * 1e-3) / 1e9, 1)},
+    }
+
+
+def bench_branch(args, torch, device):
+    """Video Delta Attention branch at the full shape: projected_delta over 31 frames x 1296 tokens, 40 x 128."""
+    from vdn_h3_amd import synth
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+    from vdn_h3_amd.window import window_bounds
+
+    frames, tpf, text, heads, dim, hidden = 31, 1296, 512, 40, 128, 5120
+    seq = text + frames * tpf
+    qkv = synth.fused_qkv(seq, heads, dim, device=device, seed=40)
+    x = synth.randn((seq, hidden), 41, device=device, dtype=torch.bfloat16)
+    w = synth.branch_weights(heads, dim, hidden, device=device)
+    q, k, v = synth.split_qkv(qkv, heads, dim)
+    bounds = window_bounds(frames, 1, 5)
+    br = OptimizedLinearBranch(w, heads, dim)
+    out = torch.empty((frames * tpf, hidden), dtype=torch.bfloat16, device=device)
+    kw = dict(text_x=x[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True, out=out)
+    stream = torch.cuda.current_stream(device)
+
+    def step():
+        br.projected_delta(w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, **kw)
+
+    with torch.no_grad():
+        ms = _time_steps(torch, stream, args.steps, args.warmup, step)
+    fi, r = frames - 2, (frames - 2) * tpf
+    core = fi * heads * (6.0 * tpf * dim * dim + (11.0 / 3.0) * dim ** 3 + 4.0 * dim ** 3)
+    gates = 2.0 * r * hidden * dim + 2.0 * r * dim * heads * dim + 2.0 * r * hidden * heads
+    proj = 2.0 * r * heads * dim * hidden
+    flops = core + gates + proj
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "VDN delta-rule branch ms + TFLOP/s at 29 inner frames x 1296 tok x 40 heads, 1 GPU",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+        "config": {"workload": "branch_f31_t1296_h40_d128", "frames": frames, "inner_frames": fi,
+                   "tokens_per_frame": tpf, "text_rows": text, "heads": heads, "head_dim": dim, "hidden": hidden,
+                   "flop_core": core, "flop_gates": gates, "flop_to_out_linear": proj},
+        "roofline": {"bound": "mfma", "kernel": "projected_delta (all kernels)", "achieved": round(tflops, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+    }
+
+
 def cpu_baseline_window(torch, qkv, w, lay, n_rows):
     """Time the CPU oracle (``oracle.window_oracle``) on ``n_rows`` query rows of the same problem."""
     from oracle import window_oracle as wo
@@ -184,8 +384,22 @@ def main():
         sys.exit(1)
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     device = torch.device("cuda:0")
-    if args.workload == "hbm_copy":
+    if args.workload == "block":
+        result = bench_block(args, torch, device)
+        if args.cpu_sample_rows > 0:
+            from vdn_h3_amd import synth
+
+            w = synth.WINDOW_FULL
+            qkv = synth.fused_qkv(w.layout.seq_len, w.heads, w.head_dim, device=device, seed=0)
+            result["cpu_baseline"] = cpu_baseline_window(torch, qkv, w, w.layout, args.cpu_sample_rows)
+            result["cpu_baseline"]["sample"] += (" - the window attention stage, 63% of the block's work; "
+                                                 "the value is that stage's CPU throughput")
+    elif args.workload == "hbm_copy":
         result = bench_hbm_copy(args, torch, device)
+    elif args.workload == "branch":
+        result = bench_branch(args, torch, device)
+    elif args.workload.startswith("gemm_"):
+        result = bench_gemm(args, torch, device)
     else:
         result = bench_window(args, torch, device)
     line = {

@@ -1,0 +1,144 @@
+// Pointwise passes of the hybrid attention block on gfx950 (HBM-bound):
+//
+//   qk_rmsnorm : the block's q_norm / k_norm over the head dim (vdn_h3/hybrid.py:271-273 with
+//                rope_freqs=None), y = bf16(x * rsqrt(mean(x^2) + eps) * w), fp32 statistics,
+//                written to separate normalised copies (the VDN branch reads the raw q / k);
+//   head_gate  : apply_softmax_gate (vdn_h3/softmax_kernels.py:8-9), out = bf16(O * g) per
+//                (row, head), flattened to [S, H*D].
+//
+// Both kernels give each head vector to 16 lanes x 16 bytes (D = 128) or 8 lanes (D = 64): a
+// wavefront covers 4 (8) head vectors of one row with fully coalesced 16-byte accesses, and the
+// sum of squares is reduced with lane shuffles inside the lane group.
+#include "common.h"
+
+namespace vdnh3 {
+namespace {
+
+__device__ __forceinline__ void unpack8(u32x4_t w, float *x) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t u = w[j >> 1];
+    x[j] = __uint_as_float((j & 1) ? (u & 0xffff0000u) : (u << 16));
+  }
+}
+
+__device__ __forceinline__ u32x4_t pack8(const float *y) {
+  return u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])};
+}
+
+// One thread = 8 consecutive channels of one head vector. vec indexes (row, which, head) with
+// which = 0 for q, 1 for k; grid covers seq * 2 * heads vectors.
+template <int D>
+__global__ __launch_bounds__(256) void qk_rmsnorm_kernel(const uint16_t *__restrict__ q, int64_t q_row,
+                                                         int64_t q_head, const uint16_t *__restrict__ k,
+                                                         int64_t k_row, int64_t k_head,
+                                                         const uint16_t *__restrict__ wq,
+                                                         const uint16_t *__restrict__ wk, float eps,
+                                                         uint16_t *__restrict__ qo, int64_t qo_row, int64_t qo_head,
+                                                         uint16_t *__restrict__ ko, int64_t ko_row, int64_t ko_head,
+                                                         int64_t n_vec, int heads) {
+  constexpr int LANES = D / 8;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t vec = t / LANES;
+  const int c = (int)(t % LANES);
+  if (vec >= n_vec) return;  // lane groups are aligned: a group is wholly in range or wholly out
+  const int head = (int)(vec % heads);
+  const int which = (int)((vec / heads) & 1);
+  const int64_t row = vec / (2 * heads);
+  const uint16_t *src = which ? k + row * k_row + head * k_head : q + row * q_row + head * q_head;
+  uint16_t *dst = which ? ko + row * ko_row + head * ko_head : qo + row * qo_row + head * qo_head;
+  const uint16_t *w = which ? wk : wq;
+  float x[8], wf[8], y[8];
+  unpack8(ld16(src + 8 * c), x);
+  unpack8(ld16(w + 8 * c), wf);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss = fmaf(x[j], x[j], ss);
+#pragma unroll
+  for (int o = 1; o < LANES; o <<= 1) ss += __shfl_xor(ss, o);
+  const float r = 1.f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = x[j] * r * wf[j];
+  st16(dst + 8 * c, pack8(y));
+}
+
+// out[s][h*D + d] = bf16(O[s][h][d] * g[s][h])
+template <int D>
+__global__ __launch_bounds__(256) void head_gate_kernel(const uint16_t *__restrict__ o, int64_t o_row,
+                                                        int64_t o_head, const uint16_t *__restrict__ gate,
+                                                        int64_t g_row, uint16_t *__restrict__ out, int64_t out_row,
+                                                        int64_t n_vec, int heads) {
+  constexpr int LANES = D / 8;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t vec = t / LANES;
+  const int c = (int)(t % LANES);
+  if (vec >= n_vec) return;
+  const int head = (int)(vec % heads);
+  const int64_t row = vec / heads;
+  float x[8], y[8];
+  unpack8(ld16(o + row * o_row + head * o_head + 8 * c), x);
+  const float g = bf2f(gate[row * g_row + head]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = x[j] * g;
+  st16(out + row * out_row + (int64_t)head * D + 8 * c, pack8(y));
+}
+
+int check_rows(const void *p, int64_t row, int64_t head, const char *name) {
+  VDNH3_HOST_CHECK(p != nullptr, VDNH3_ERR_INVALID, "%s is null", name);
+  VDNH3_HOST_CHECK(row % 8 == 0 && head % 8 == 0 && reinterpret_cast<uintptr_t>(p) % 16 == 0, VDNH3_ERR_INVALID,
+                   "%s must be 16-byte aligned with row and head strides that are multiples of 8 elements", name);
+  return VDNH3_OK;
+}
+
+}  // namespace
+}  // namespace vdnh3
+
+extern "C" int vdnh3_qk_rmsnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
+                                int64_t k_head, const uint16_t *q_weight, const uint16_t *k_weight, float eps,
+                                uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
+                                int64_t ko_head, int seq, int heads, int head_dim, void *stream) {
+  using namespace vdnh3;
+  VDNH3_HOST_CHECK(head_dim == 64 || head_dim == 128, VDNH3_ERR_INVALID,
+                   "qk_rmsnorm supports head_dim 64 or 128, got %d", head_dim);
+  VDNH3_HOST_CHECK(seq > 0 && heads > 0, VDNH3_ERR_INVALID, "qk_rmsnorm: seq and heads must be positive");
+  int rc = check_rows(q, q_row, q_head, "q");
+  if (!rc) rc = check_rows(k, k_row, k_head, "k");
+  if (!rc) rc = check_rows(q_out, qo_row, qo_head, "q_out");
+  if (!rc) rc = check_rows(k_out, ko_row, ko_head, "k_out");
+  if (!rc) rc = check_rows(q_weight, 0, 0, "q_weight");
+  if (!rc) rc = check_rows(k_weight, 0, 0, "k_weight");
+  if (rc) return rc;
+  const int64_t n_vec = (int64_t)seq * 2 * heads;
+  const int64_t threads = n_vec * (head_dim / 8);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(qk_rmsnorm_kernel<128>, grid, dim3(256), 0, s, q, q_row, q_head, k, k_row, k_head, q_weight,
+                       k_weight, eps, q_out, qo_row, qo_head, k_out, ko_row, ko_head, n_vec, heads);
+  else
+    hipLaunchKernelGGL(qk_rmsnorm_kernel<64>, grid, dim3(256), 0, s, q, q_row, q_head, k, k_row, k_head, q_weight,
+                       k_weight, eps, q_out, qo_row, qo_head, k_out, ko_row, ko_head, n_vec, heads);
+  return check_launch("qk_rmsnorm");
+}
+
+extern "C" int vdnh3_head_gate(const uint16_t *o, int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row,
+                               uint16_t *out, int64_t out_row, int seq, int heads, int head_dim, void *stream) {
+  using namespace vdnh3;
+  VDNH3_HOST_CHECK(head_dim == 64 || head_dim == 128, VDNH3_ERR_INVALID,
+                   "head_gate supports head_dim 64 or 128, got %d", head_dim);
+  VDNH3_HOST_CHECK(seq > 0 && heads > 0 && gate != nullptr, VDNH3_ERR_INVALID, "head_gate: empty or null operand");
+  int rc = check_rows(o, o_row, o_head, "o");
+  if (!rc) rc = check_rows(out, out_row, head_dim, "out");
+  if (rc) return rc;
+  const int64_t n_vec = (int64_t)seq * heads;
+  const int64_t threads = n_vec * (head_dim / 8);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(head_gate_kernel<128>, grid, dim3(256), 0, s, o, o_row, o_head, gate, gate_row, out, out_row,
+                       n_vec, heads);
+  else
+    hipLaunchKernelGGL(head_gate_kernel<64>, grid, dim3(256), 0, s, o, o_row, o_head, gate, gate_row, out, out_row,
+                       n_vec, heads);
+  return check_launch("head_gate");
+}

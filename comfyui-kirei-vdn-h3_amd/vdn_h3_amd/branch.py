@@ -244,6 +244,21 @@ def alpha_gate(frame_mean_f32, weight_down, weight_up, dt_bias, a_log, num_heads
     return alpha
 
 
+_BOUNDS_CACHE: dict[tuple, torch.Tensor] = {}
+
+
+def _device_bounds(bounds, device) -> torch.Tensor:
+    """The ``(lo, hi)`` pairs as a device int32 tensor, copied once per geometry and device."""
+    key = (tuple((int(lo), int(hi)) for lo, hi in bounds), device.type, device.index)
+    cached = _BOUNDS_CACHE.get(key)
+    if cached is None:
+        if len(_BOUNDS_CACHE) > 64:
+            _BOUNDS_CACHE.clear()
+        cached = torch.tensor([x for pair in key[0] for x in pair], dtype=torch.int32).to(device)
+        _BOUNDS_CACHE[key] = cached
+    return cached
+
+
 def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *, text_state=None,
                      bridge="alpha", num_frames, tokens_per_frame, out=None):
     """Gather, readout and RMSNorm/gate epilogue: ``[F*T, H*D]`` bf16."""
@@ -258,7 +273,7 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
             raise ValueError(f"bounds[{frame}] does not contain its query frame")
     device = _lib.require_device(q_raw, prefix, suffix, alpha, gate, text_state, out)
     q_raw = _rows(q_raw)
-    bounds_t = torch.tensor([int(x) for pair in bounds for x in pair], dtype=torch.int32).to(device)
+    bounds_t = _device_bounds(bounds, device)
     norm_w = norm_weight.to(torch.bfloat16).contiguous()
     gate = gate.to(torch.bfloat16)
     if gate.stride(1) != 1:

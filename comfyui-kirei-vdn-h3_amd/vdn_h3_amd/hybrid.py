@@ -1,0 +1,274 @@
+"""The VDN-H3 hybrid attention block on MI355X: the patched ``attn.forward``.
+
+Mirrors ``vdn_h3/hybrid.py``: ``VDNState`` (``:33-213``), ``make_vdn_forward``
+(``:409-579``) and ``apply_vdn`` (``:606-641``), with the same call signature
+``vdn_forward(x, rope_freqs=None, transformer_options=None) -> [S, hidden]``, the same
+layout contract (the request-local ``VDNLayout``; without one the original forward runs)
+and the same exception types. Per call, on the caller's current stream:
+
+  qkv = attn.qkv_proj(x)                         raw q / k / v views [S, H, D]
+  q, k = q_norm(q_raw), k_norm(k_raw)            one HIP pass into a separate buffer
+  g = sigmoid(x W_g^T + b_g)                     [S, H], GEMM with a sigmoid epilogue
+  flat = bf16(window_attention(q, k, v) * g)     one HIP kernel, the gate in its epilogue
+  out = attn.out_proj(flat)
+  out[video] += to_out_linear(branch(x, q_raw, k_raw, v))   GEMM epilogue accumulates into out
+
+The branch runs after ``out_proj`` here (the reference computes it first and adds it last):
+the sum is the same bf16 addition, ``bf16(out + bf16(delta))``. A full-cover layout runs
+dense attention and no branch (``:422``, ``:495-499``). The path is inference-only
+(``torch.no_grad`` / ``inference_mode``); RoPE (``rope_freqs`` not ``None``) is not
+implemented on the HIP path and raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import logging
+from collections.abc import Mapping, Sequence
+from contextlib import contextmanager
+from typing import Any
+
+import torch
+
+from . import _lib
+from . import linear as _linear
+from . import projection as _projection
+from . import window as _window
+from .branch import cholesky_runtime_scope
+from .diagnostics import DiagnosticsRecorder
+from .layout import current_layout, publish_layout
+
+_LOG = logging.getLogger("vdn_h3_amd")
+_STATE_PATCH = "diffusion_model._vdn_h3_state"
+
+
+class VDNState:
+    """Runtime state of one patched model: config, per-block branches and weights, plan cache."""
+
+    def __init__(self, name: str, config: Mapping[str, Any], branches: Sequence[Any], num_heads: int,
+                 head_dim: int, *, attention_backend: str = "hip", weight_maps=None, inference: bool = True,
+                 projection_precision: str = "bf16", projection_info: Any = None, diagnostics: bool = False,
+                 **_runtime):
+        if attention_backend not in _window.ATTENTION_BACKENDS:
+            raise ValueError(f"unsupported attention backend {attention_backend!r}")
+        if projection_precision not in _projection.PROJECTION_PRECISIONS:
+            raise ValueError(f"unsupported projection precision {projection_precision!r}")
+        self.name = str(name)
+        self.config = dict(config)
+        self.cfg = self.config
+        self.num_heads = int(num_heads)
+        self.head_dim = int(head_dim)
+        self.attention_backend = attention_backend
+        self.inference = bool(inference)
+        self.projection_precision = projection_precision
+        self.projection_info = projection_info
+        self.branches = list(branches)
+        self.window_cache = _window.WindowAttentionCache(limit=24)
+        self.forwards = 0
+        self.last_attention_backend = None
+        self.last_layout = None
+        self.branch_execution = "serial"
+        self.diagnostics = DiagnosticsRecorder(diagnostics)
+        if weight_maps is None:
+            maps = []
+            for index, branch in enumerate(self.branches):
+                if branch is None:
+                    raise ValueError(f"branch {index} is None")
+                mapping = branch if isinstance(branch, Mapping) else getattr(branch, "w", None)
+                if not isinstance(mapping, Mapping):
+                    raise TypeError(f"branch {index} does not expose a weight mapping as .w")
+                maps.append(mapping)
+        else:
+            maps = list(weight_maps)
+            if len(maps) != len(self.branches):
+                raise ValueError("weight_maps must match branch count")
+        self._maps = maps
+        self._resident: dict[tuple[int, Any], dict[str, torch.Tensor]] = {}
+
+    # Weights are resident in HBM (a block's branch weights are ~55 MB at hidden 5120; all
+    # 50 blocks fit many times over in 288 GB), so prefetch / consume are bookkeeping only.
+    def prefetch_weights(self, index, device, dtype, keys=None):
+        del keys
+        self.weights_on(index, device, dtype)
+
+    def weights_on(self, index, device, dtype, keys=None):
+        device = torch.device(device)
+        key = (int(index), device)
+        cached = self._resident.get(key)
+        if cached is None:
+            cached = {}
+            for name, value in self._maps[index].items():
+                if not isinstance(value, torch.Tensor):
+                    cached[name] = value
+                    continue
+                keep_fp32 = name in ("alpha.A_log", "alpha.dt_bias") or value.dtype in (
+                    torch.int8, torch.float8_e4m3fn) or name.endswith("weight_scale")
+                cached[name] = value.to(device=device, dtype=value.dtype if keep_fp32 else dtype)
+            self._resident[key] = cached
+        if keys is None:
+            return cached
+        return {k: cached[k] for k in keys if k in cached}
+
+    def mark_weights_consumed(self, index, device, dtype):
+        del index, device, dtype
+
+    def projection_view(self, weights):
+        """Branch-visible weights plus the ``to_out_linear`` projector (``vdn_h3/hybrid.py:185-196``)."""
+        if _projection.BF16_WEIGHT_KEY not in weights and _projection.FP8_WEIGHT_KEY not in weights:
+            raise RuntimeError("VDN projection state contains neither BF16 nor quantized weight")
+        return weights, lambda rows, **kw: _projection.project(rows, weights, **kw)
+
+    def release(self):
+        self._resident.clear()
+        self.window_cache.release()
+        return self
+
+    close = release
+
+
+def normalise_qk(q_raw: torch.Tensor, k_raw: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                 eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
+    """``attn.q_norm(q), attn.k_norm(k)`` (RMSNorm over the head dim) into one new ``[S, 2, H, D]`` buffer."""
+    if q_raw.shape != k_raw.shape or q_raw.ndim != 3:
+        raise ValueError("q and k must share shape [sequence, heads, dim]")
+    device = _lib.require_device(q_raw, k_raw, q_weight, k_weight)
+    seq, heads, dim = q_raw.shape
+    q_raw, k_raw = _window._kernel_operand(q_raw), _window._kernel_operand(k_raw)
+    wq = q_weight.to(torch.bfloat16).contiguous()
+    wk = k_weight.to(torch.bfloat16).contiguous()
+    if wq.numel() != dim or wk.numel() != dim:
+        raise ValueError(f"q/k norm weights must have {dim} entries")
+    buf = torch.empty((seq, 2, heads, dim), dtype=torch.bfloat16, device=device)
+    qn, kn = buf[:, 0], buf[:, 1]
+    rc = _lib.lib().vdnh3_qk_rmsnorm(_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), _lib.ptr(k_raw),
+                                     k_raw.stride(0), k_raw.stride(1), _lib.ptr(wq), _lib.ptr(wk), float(eps),
+                                     _lib.ptr(qn), qn.stride(0), qn.stride(1), _lib.ptr(kn), kn.stride(0),
+                                     kn.stride(1), seq, heads, dim, _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_qk_rmsnorm")
+    return qn, kn
+
+
+def _norm_weight_eps(module, dim, device):
+    weight = getattr(module, "weight", None)
+    if weight is None:
+        weight = torch.ones(dim, dtype=torch.bfloat16)
+    eps = getattr(module, "eps", None)
+    return weight.to(device), 1e-6 if eps is None else float(eps)
+
+
+def _qkv(attn: Any, x: torch.Tensor):
+    heads, head_dim = int(attn.heads), int(attn.head_dim)
+    inner = heads * head_dim
+    projected = attn.qkv_proj(x)
+    if projected.shape[-1] != inner * 3:
+        raise RuntimeError(f"H3 qkv_proj returned {projected.shape[-1]} features; expected {inner * 3}")
+    q, k, v = projected.split(inner, dim=-1)
+    seq = x.shape[0]
+    return q.view(seq, heads, head_dim), k.view(seq, heads, head_dim), v.view(seq, heads, head_dim)
+
+
+def make_vdn_forward(attn: Any, state: VDNState, block_index: int):
+    """The patched ``attn.forward`` of block ``block_index``."""
+    original_forward = attn.forward
+    heads, head_dim = int(attn.heads), int(attn.head_dim)
+    config = state.config
+    branch = state.branches[block_index]
+
+    def vdn_forward(x, rope_freqs=None, transformer_options=None):
+        layout = current_layout(required=False)
+        if layout is None:
+            return original_forward(x, rope_freqs=rope_freqs, transformer_options=transformer_options or {})
+        if int(x.shape[0]) != layout.seq_len:
+            raise RuntimeError(f"VDN layout has {layout.seq_len} rows but attention received {x.shape[0]}")
+        if torch.is_grad_enabled():
+            raise RuntimeError("the MI355X VDN-H3 block is inference-only; run it under torch.no_grad()")
+        if rope_freqs is not None:
+            raise RuntimeError("RoPE execution is not implemented on the MI355X VDN-H3 path (rope_freqs must be None)")
+        linear_active = bool(config.get("linear_enabled", True)) and not layout.full_cover
+        gate_enabled = bool(config.get("enable_softmax_gate", True))
+        device = x.device
+        weights = state.weights_on(block_index, device, x.dtype)
+
+        scope = state.diagnostics.scope
+        with scope("attention.qkv", device):
+            q_raw, k_raw, value = _qkv(attn, x)
+        qw, q_eps = _norm_weight_eps(attn.q_norm, head_dim, device)
+        kw, _ = _norm_weight_eps(attn.k_norm, head_dim, device)
+        with scope("attention.rope_norm", device):
+            query, key = normalise_qk(q_raw, k_raw, qw, kw, q_eps)
+
+        gate = None
+        if gate_enabled:
+            try:
+                with scope("attention.gate", device):
+                    gate = _linear.sigmoid_linear(x, weights["softmax_gate.up.weight"],
+                                                  weights.get("softmax_gate.up.bias"))
+            except KeyError as exc:
+                raise RuntimeError(f"VDN branch block {block_index} is missing softmax gate tensor "
+                                   f"{exc.args[0]!r}") from exc
+        cache = state.window_cache
+        if layout.full_cover:
+            plan = cache.plan(layout.seq_len, 0, layout.seq_len, 1, layout.seq_len, [(0, 0)], "none", device)
+            state.last_attention_backend = "dense_exact"
+        else:
+            plan = cache.plan(layout.seq_len, layout.video_start, layout.video_end, layout.num_frames,
+                              layout.tokens_per_frame, layout.bounds, layout.anchor_frames, device)
+            state.last_attention_backend = _window.resolve_attention_backend(state.attention_backend, cache=cache)
+        with scope("attention.softmax", device):
+            attended = _window.window_softmax_hip(
+                query, key, value, layout.video_start, layout.video_end, layout.num_frames,
+                layout.tokens_per_frame, layout.bounds, head_dim ** -0.5, layout.anchor_frames, gate=gate, plan=plan,
+                diagnostics=state.diagnostics if state.diagnostics.enabled else None)
+        del query, key
+        flat = attended.view(layout.seq_len, heads * head_dim)
+        with scope("attention.out_proj", device):
+            out = attn.out_proj(flat)
+        del flat, attended
+        if linear_active:
+            va, vb = layout.video_start, layout.video_end
+            ta, tb = layout.text_start, layout.text_start + layout.text_len
+            text_enabled = bool(getattr(branch, "enable_text_state", config.get("enable_text_state", False)))
+            branch_weights, projector = state.projection_view(weights)
+            with scope("attention.linear_branch", device):
+                branch.projected_delta(
+                    branch_weights, x[va:vb], q_raw[va:vb], k_raw[va:vb], value[va:vb], layout.num_frames,
+                    layout.tokens_per_frame, layout.bounds, frame_size=layout.frame_size,
+                    text_x=x[ta:tb] if text_enabled else None,
+                    text_k_raw=k_raw[ta:tb] if text_enabled else None,
+                    text_v_raw=value[ta:tb] if text_enabled else None, skip_ends=(layout.anchor_frames == "both"),
+                    inference=True, projector=projector, out=out[va:vb], accumulate=True)
+        state.forwards += 1
+        state.last_layout = layout
+        return out
+
+    vdn_forward._vdn_h3_forward = True
+    vdn_forward._vdn_h3_original = original_forward
+    return vdn_forward
+
+
+@contextmanager
+def forward_scope(layout):
+    """What the reference's DIFFUSION_MODEL wrapper does per model call (``vdn_h3/hybrid.py:216-241``):
+    publish the layout and validate every Cholesky status of the call once at its end."""
+    with publish_layout(layout), cholesky_runtime_scope():
+        yield layout
+
+
+def apply_vdn(model_patcher: Any, state: VDNState):
+    """Install ``make_vdn_forward`` on every block (``vdn_h3/hybrid.py:606-641``, object patches only).
+
+    ``model_patcher`` needs ``get_model_object`` and ``add_object_patch``; the caller publishes
+    the layout around each model call with ``forward_scope`` (the reference installs a ComfyUI
+    DIFFUSION_MODEL wrapper for that).
+    """
+    dm = model_patcher.get_model_object("diffusion_model")
+    blocks = dm.blocks
+    if len(blocks) != len(state.branches):
+        raise RuntimeError(f"VDN state has {len(state.branches)} blocks but the model has {len(blocks)}")
+    model_patcher.add_object_patch(_STATE_PATCH, state)
+    for index, block in enumerate(blocks):
+        model_patcher.add_object_patch(f"diffusion_model.blocks.{index}.attn.forward",
+                                       make_vdn_forward(block.attn, state, index))
+    return model_patcher
+
+
+__all__ = ["VDNState", "apply_vdn", "forward_scope", "make_vdn_forward", "normalise_qk"]

@@ -124,3 +124,58 @@ def gemm_w8a8(a_q, a_scale, b_q, b_scale, *, out_dtype=torch.bfloat16, bias=None
 def int8_accumulators(a_q: torch.Tensor, b_q: torch.Tensor) -> torch.Tensor:
     """Raw int32 accumulators ``a_q b_q^T`` of two int8 matrices."""
     return gemm(KIND_I8, a_q, b_q, out_dtype=torch.int32)
+
+
+LINEAR_PRECISIONS = ("bf16", "int8", "fp8")
+
+
+class HipLinear(torch.nn.Module):
+    """``nn.Linear`` (no bias) on MI355X MFMA with bf16, W8A8 int8 or fp8 e4m3fn weights.
+
+    The host model's ``attn.qkv_proj`` / ``attn.out_proj`` (``vdn_h3/hybrid.py:263``, ``:535``)
+    and the VDN ``to_out_linear`` run through it. ``int8`` stores symmetric per-output-channel
+    codes and quantises activations per token at call time (int32 accumulation, both scales in
+    the epilogue); ``fp8`` stores e4m3fn codes with a per-tensor or per-channel scale and
+    quantises activations the same way (per tensor / per token). Output is bf16.
+    """
+
+    def __init__(self, weight: torch.Tensor, precision: str = "bf16", *, per_tensor: bool = False):
+        super().__init__()
+        if precision not in LINEAR_PRECISIONS:
+            raise ValueError(f"unknown precision {precision!r}; expected one of {LINEAR_PRECISIONS}")
+        if weight.ndim != 2:
+            raise ValueError("weight must be [out_features, in_features]")
+        _lib.require_device(weight)
+        self.precision = precision
+        self.per_tensor = bool(per_tensor)
+        self.out_features, self.in_features = int(weight.shape[0]), int(weight.shape[1])
+        w = weight.to(torch.bfloat16).contiguous()
+        if precision == "bf16":
+            self.register_buffer("weight", w)
+            self.register_buffer("weight_scale", None)
+        elif precision == "int8":
+            q, s = quantize_rows(w, KIND_I8)
+            self.register_buffer("weight", q)
+            self.register_buffer("weight_scale", s.reshape(1, -1))
+        else:
+            q, s = quantize_tensor_fp8(w) if per_tensor else quantize_rows(w, KIND_F8)
+            self.register_buffer("weight", q)
+            self.register_buffer("weight_scale", s.reshape(1, -1))
+
+    def forward(self, x: torch.Tensor, *, out: torch.Tensor | None = None, accumulate: bool = False):
+        if x.ndim != 2 or x.shape[1] != self.in_features:
+            raise ValueError(f"expected [rows, {self.in_features}] input, got {tuple(x.shape)}")
+        if x.dtype != torch.bfloat16:
+            x = x.to(torch.bfloat16)
+        if self.precision == "bf16":
+            return linear(x, self.weight, out=out, accumulate=accumulate)
+        if self.precision == "int8":
+            xq, xs = quantize_rows(x, KIND_I8)
+        elif self.per_tensor:
+            xq, xs = quantize_tensor_fp8(x)
+        else:
+            xq, xs = quantize_rows(x, KIND_F8)
+        return gemm_w8a8(xq, xs, self.weight, self.weight_scale, out=out, accumulate=accumulate)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, precision={self.precision}"

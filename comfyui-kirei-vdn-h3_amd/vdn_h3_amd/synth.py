@@ -89,3 +89,26 @@ def sigmoid_gate(seq: int, heads: int, device="cpu", seed: int = 10) -> torch.Te
 
 def softmax_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
+
+
+def branch_weights(heads: int, head_dim: int, hidden: int, device="cpu", seed: int = 42) -> dict:
+    """Random-init VDN branch weights of one block (shapes of ``vdn_h3/spec.py:471-486``).
+
+    Matrices ~ N(0, 0.02); ``alpha.dt_bias`` / ``alpha.A_log`` ~ N(0, 0.5^2) kept in fp32 (the
+    reference stores them in fp32); ``norm.weight`` = 1 + 0.1 N(0, 1); gate biases N(0, 0.5^2).
+    """
+    bf = torch.bfloat16
+    return {
+        "beta_proj.weight": randn((heads, hidden), seed, device, bf, 0.02),
+        "alpha.down.weight": randn((head_dim, hidden), seed + 1, device, bf, 0.02),
+        "alpha.up.weight": randn((heads * head_dim, head_dim), seed + 2, device, bf, 0.02),
+        "alpha.dt_bias": randn((heads * head_dim,), seed + 3, device, scale=0.5),
+        "alpha.A_log": randn((heads,), seed + 4, device, scale=0.5),
+        "output_gate.down.weight": randn((head_dim, hidden), seed + 5, device, bf, 0.02),
+        "output_gate.up.weight": randn((heads * head_dim, head_dim), seed + 6, device, bf, 0.02),
+        "output_gate.up.bias": randn((heads * head_dim,), seed + 7, device, bf, 0.5),
+        "norm.weight": (1 + 0.1 * randn((head_dim,), seed + 8, device)).to(bf),
+        "to_out_linear.weight": randn((hidden, heads * head_dim), seed + 9, device, bf, 0.02),
+        "softmax_gate.up.weight": randn((heads, hidden), seed + 10, device, bf, 0.02),
+        "softmax_gate.up.bias": randn((heads,), seed + 11, device, bf, 0.5),
+    }

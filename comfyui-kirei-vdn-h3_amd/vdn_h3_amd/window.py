@@ -163,11 +163,13 @@ def _kernel_operand(t: torch.Tensor) -> torch.Tensor:
 
 def window_softmax_hip(query, key, value, video_start, video_end, num_frames, tokens_per_frame, bounds, scale,
                        anchor_frames="none", cache: WindowAttentionCache | None = None, *, gate=None,
-                       out: torch.Tensor | None = None, plan: WindowPlan | None = None):
+                       out: torch.Tensor | None = None, plan: WindowPlan | None = None, diagnostics=None):
     """Exact window softmax attention on the GPU; returns a new ``[S, H, D]`` bf16 tensor.
 
     ``gate`` (optional, ``[S, H]`` or ``[S, H, 1]``) fuses the per-head softmax gate into the
     epilogue: the result is then ``bf16(bf16(O) * gate)``. Inputs are not modified.
+    ``diagnostics`` (a ``DiagnosticsRecorder``) times the V^T pre-pass and the attention kernel
+    as the stages ``attention.softmax.vt_prepass`` / ``attention.softmax.kernel``.
     """
     if query.ndim != 3 or query.shape != key.shape or query.shape != value.shape:
         raise ValueError("query, key and value must share shape [sequence, heads, dim]")
@@ -199,12 +201,24 @@ def window_softmax_hip(query, key, value, video_start, video_end, num_frames, to
     lib = _lib.lib()
     ws_bytes = lib.vdnh3_window_workspace_bytes(seq, heads, dim)
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
-    rc = lib.vdnh3_window_attn_fwd(
-        _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
-        _lib.ptr(v), v.stride(0), v.stride(1), _lib.ptr(out), out.stride(0), out.stride(1),
-        _lib.ptr(gate), g_row, seq, heads, dim, float(scale),
-        _lib.ptr(plan.items), plan.n_items, _lib.ptr(plan.tiles), _lib.ptr(workspace), ws_bytes,
-        _lib.stream_handle(device))
+    sh = _lib.stream_handle(device)
+    if diagnostics is None:
+        rc = lib.vdnh3_window_attn_fwd(
+            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
+            _lib.ptr(v), v.stride(0), v.stride(1), _lib.ptr(out), out.stride(0), out.stride(1),
+            _lib.ptr(gate), g_row, seq, heads, dim, float(scale),
+            _lib.ptr(plan.items), plan.n_items, _lib.ptr(plan.tiles), _lib.ptr(workspace), ws_bytes, sh)
+        _lib.check(rc, "window_softmax_hip")
+        return out
+    with diagnostics.scope("attention.softmax.vt_prepass", device):
+        rc = lib.vdnh3_window_vt_prepass(_lib.ptr(v), v.stride(0), v.stride(1), seq, heads, dim,
+                                         _lib.ptr(workspace), ws_bytes, sh)
+    _lib.check(rc, "window_softmax_hip")
+    with diagnostics.scope("attention.softmax.kernel", device):
+        rc = lib.vdnh3_window_attn_prepared(
+            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
+            _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(gate), g_row, seq, heads, dim, float(scale),
+            _lib.ptr(plan.items), plan.n_items, _lib.ptr(plan.tiles), _lib.ptr(workspace), ws_bytes, sh)
     _lib.check(rc, "window_softmax_hip")
     return out
 

@@ -225,6 +225,30 @@ int vdnh3_linear_f32(const float *x, int64_t x_row, const void *w, int w_bf16, i
 int vdnh3_alpha_decay(const float *delta, const float *a_log, float *alpha, int frames, int heads,
                       int head_dim, void *stream);
 
+/* ------------------------------------------------------------------------------
+ * Hybrid block pointwise passes (reference vdn_h3/hybrid.py, vdn_h3/softmax_kernels.py)
+ * ------------------------------------------------------------------------------ */
+
+/*
+ * q_norm / k_norm of the block (vdn_h3/hybrid.py:271-273, rope_freqs=None: the attention's
+ * RMSNorm modules over the head dim): y = bf16(x * rsqrt(mean(x^2) + eps) * w), fp32 statistics.
+ * q / k are [seq, heads, head_dim] views (element (s, h, d) at p[s*row + h*head + d]); the
+ * results go to separate views q_out / k_out (the raw q / k stay intact for the VDN branch).
+ * Weights are bf16 [head_dim]. All pointers 16-byte aligned, strides multiples of 8.
+ */
+int vdnh3_qk_rmsnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
+                     int64_t k_head, const uint16_t *q_weight, const uint16_t *k_weight, float eps,
+                     uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
+                     int64_t ko_head, int seq, int heads, int head_dim, void *stream);
+
+/*
+ * apply_softmax_gate (vdn_h3/softmax_kernels.py:8-9): out[s][h*D + d] = bf16(O[s][h][d] * gate[s][h])
+ * with O a [seq, heads, head_dim] bf16 view and gate bf16 (element (s, h) at gate[s*gate_row + h]).
+ * The window attention kernel fuses the same gate into its epilogue; this is the standalone op.
+ */
+int vdnh3_head_gate(const uint16_t *o, int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row,
+                    uint16_t *out, int64_t out_row, int seq, int heads, int head_dim, void *stream);
+
 /* Fill rows x cols of a bf16 matrix with a constant (anchor-frame rows of the branch output). */
 int vdnh3_fill_rows_bf16(uint16_t *p, int64_t ld, int rows, int cols, float value, void *stream);
 

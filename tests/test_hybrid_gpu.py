@@ -1,0 +1,193 @@
+"""Parity of the HIP hybrid attention block (``make_vdn_forward``) with the reference (GPU).
+
+Bars (north star): max-abs 2e-2 and cosine >= 0.9995 against the reference's own
+``make_vdn_forward`` output (golden vector) and against the CPU oracle of the block; the
+q/k RMSNorm pass and the standalone softmax gate within one bf16 rounding step.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+from types import SimpleNamespace
+
+import pytest
+import torch
+import torch.nn.functional as F
+from safetensors import safe_open
+
+from oracle import hybrid_oracle as ho
+from oracle import quant_oracle as qo
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _parity(got, want, what, atol=2e-2, min_cos=0.9995):
+    got, want = got.float().cpu().flatten(), want.float().cpu().flatten()
+    err = (got - want).abs().max().item()
+    cos = F.cosine_similarity(got.double(), want.double(), dim=0).item()
+    print(f"{what}: max abs {err:.3e}, cosine {cos:.7f}", flush=True)
+    assert torch.isfinite(got).all(), what
+    assert err <= atol and cos >= min_cos, f"{what}: max abs {err:.3e}, cosine {cos:.7f}"
+
+
+def _attn(aw, heads, dim, device, precision="bf16"):
+    from vdn_h3_amd.linear import HipLinear
+
+    def forward(*args, **kwargs):  # the original forward must not run while a layout is published
+        raise AssertionError("original attention forward called")
+
+    return SimpleNamespace(
+        heads=heads, head_dim=dim, forward=forward,
+        qkv_proj=HipLinear(aw["qkv_proj.weight"].to(device), precision),
+        out_proj=HipLinear(aw["out_proj.weight"].to(device), precision),
+        q_norm=SimpleNamespace(weight=aw["q_norm.weight"].to(device), eps=1e-6),
+        k_norm=SimpleNamespace(weight=aw["k_norm.weight"].to(device), eps=1e-6))
+
+
+def _block(aw, bw, heads, dim, device, precision="bf16", config=None):
+    from vdn_h3_amd.hybrid import VDNState, make_vdn_forward
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+
+    attn = _attn(aw, heads, dim, device, precision)
+    branch = OptimizedLinearBranch(bw, heads, dim, short_conv=(), enable_text_state=True)
+    cfg = {"enable_softmax_gate": True, "linear_enabled": True, "enable_text_state": True}
+    cfg.update(config or {})
+    state = VDNState("test", cfg, [branch], heads, dim)
+    return make_vdn_forward(attn, state, 0), state
+
+
+def _run(forward, x, layout):
+    from vdn_h3_amd.hybrid import forward_scope
+
+    with torch.no_grad(), forward_scope(layout):
+        out = forward(x)
+    torch.cuda.synchronize()
+    return out
+
+
+def _golden():
+    from vdn_h3_amd.layout import text_first_layout
+
+    with safe_open(str(GOLDEN / "hybrid_13f.safetensors"), "pt") as f:
+        t, meta = {k: f.get_tensor(k) for k in f.keys()}, f.metadata()
+    frames, text, heads, dim = int(meta["frames"]), int(meta["text"]), int(meta["heads"]), int(meta["dim"])
+    grid = tuple(map(int, meta["grid"].split("x")))
+    layout = text_first_layout(text, frames, grid, anchor_frames=meta["anchor_frames"])
+    bw = {k[2:]: v for k, v in t.items() if k.startswith("w.")}
+    aw = {k[5:]: v for k, v in t.items() if k.startswith("attn.")}
+    return t, layout, aw, bw, heads, dim
+
+
+def test_block_matches_reference_golden(device):
+    print("case hybrid block golden (13 frames, 2 x 64)", flush=True)
+    t, layout, aw, bw, heads, dim = _golden()
+    forward, state = _block(aw, {k: v.to(device) for k, v in bw.items()}, heads, dim, device)
+    out = _run(forward, t["x"].to(device), layout)
+    assert state.last_attention_backend == "hip"
+    _parity(out, t["out"], "block vs reference make_vdn_forward")
+    _parity(out, ho.vdn_forward(t["x"], layout, aw, bw, heads, dim), "block vs oracle")
+
+
+def _synthetic(frames, grid, text, heads, dim, hidden, seed=0):
+    from vdn_h3_amd import synth
+    from vdn_h3_amd.layout import text_first_layout
+
+    layout = text_first_layout(text, frames, grid)
+    x = synth.randn((layout.seq_len, hidden), seed, dtype=torch.bfloat16)
+    bw = synth.branch_weights(heads, dim, hidden, seed=seed + 100)
+    aw = {"qkv_proj.weight": synth.randn((3 * heads * dim, hidden), seed + 1, dtype=torch.bfloat16, scale=0.05),
+          "out_proj.weight": synth.randn((hidden, heads * dim), seed + 2, dtype=torch.bfloat16, scale=0.05),
+          "q_norm.weight": (1 + 0.1 * synth.randn((dim,), seed + 3)).to(torch.bfloat16),
+          "k_norm.weight": (1 + 0.1 * synth.randn((dim,), seed + 4)).to(torch.bfloat16)}
+    return layout, x, aw, bw
+
+
+@pytest.mark.parametrize("frames", [7, 13])
+def test_block_d128_vs_oracle(device, frames):
+    """4 heads x 128, hidden 512, 16x16-token frames; 7 frames is full cover (dense, no branch)."""
+    print(f"case hybrid block d128 frames={frames}", flush=True)
+    heads, dim, hidden = 4, 128, 512
+    layout, x, aw, bw = _synthetic(frames, (16, 16), 64, heads, dim, hidden)
+    forward, state = _block(aw, {k: v.to(device) for k, v in bw.items()}, heads, dim, device)
+    out = _run(forward, x.to(device), layout)
+    assert state.last_attention_backend == ("dense_exact" if layout.full_cover else "hip")
+    torch.set_num_threads(16)
+    _parity(out, ho.vdn_forward(x, layout, aw, bw, heads, dim), f"block d128 {frames} frames vs oracle")
+
+
+def test_block_int8_projections_vs_oracle(device):
+    """W8A8 int8 qkv / out projections (per-token x per-channel) and an int8 to_out_linear."""
+    from vdn_h3_amd import projection
+
+    print("case hybrid block int8 projections", flush=True)
+    heads, dim, hidden = 4, 128, 512
+    layout, x, aw, bw = _synthetic(13, (16, 16), 64, heads, dim, hidden, seed=7)
+    dbw = {k: v.to(device) for k, v in bw.items()}
+    (qbw,), _ = projection.prepare_projection_maps([dbw], device, "int8")
+    forward, _ = _block(aw, qbw, heads, dim, device, precision="int8")
+    out = _run(forward, x.to(device), layout)
+
+    def int8_project(weight):
+        wq, ws = qo.int8_quantize_rows(weight)
+        return lambda rows: qo.int8_linear(*qo.int8_quantize_rows(rows), wq, ws.reshape(1, -1))
+
+    want = ho.vdn_forward(x, layout, aw, bw, heads, dim, project_qkv=int8_project(aw["qkv_proj.weight"]),
+                          project_out=int8_project(aw["out_proj.weight"]),
+                          branch_projector=int8_project(bw["to_out_linear.weight"]))
+    _parity(out, want, "block int8 vs oracle")
+
+
+def test_gate_off_and_branch_off(device):
+    print("case hybrid block config switches", flush=True)
+    t, layout, aw, bw, heads, dim = _golden()
+    dbw = {k: v.to(device) for k, v in bw.items()}
+    for cfg, kw in (({"enable_softmax_gate": False}, dict(gate_enabled=False)),
+                    ({"linear_enabled": False}, dict(linear_enabled=False))):
+        forward, _ = _block(aw, dbw, heads, dim, device, config=cfg)
+        out = _run(forward, t["x"].to(device), layout)
+        _parity(out, ho.vdn_forward(t["x"], layout, aw, bw, heads, dim, **kw), f"block {cfg} vs oracle")
+
+
+def test_without_layout_calls_original_and_grad_is_rejected(device):
+    from vdn_h3_amd.hybrid import VDNState, make_vdn_forward
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+
+    t, layout, aw, bw, heads, dim = _golden()
+    attn = _attn(aw, heads, dim, device)
+    attn.forward = lambda x, rope_freqs=None, transformer_options=None: "original"
+    state = VDNState("t", {}, [OptimizedLinearBranch({}, heads, dim)], heads, dim)
+    forward = make_vdn_forward(attn, state, 0)
+    x = t["x"].to(device)
+    assert forward(x) == "original"
+    from vdn_h3_amd.hybrid import forward_scope
+
+    with forward_scope(layout), pytest.raises(RuntimeError, match="inference-only"):
+        forward(x)
+    with torch.no_grad(), forward_scope(layout), pytest.raises(RuntimeError, match="rows"):
+        forward(x[:-1])
+
+
+def test_qk_rmsnorm_and_softmax_gate_ops(device):
+    from vdn_h3_amd import synth
+    from vdn_h3_amd.hybrid import normalise_qk
+    from vdn_h3_amd.softmax_kernels import apply_softmax_gate
+
+    print("case qk rmsnorm + softmax gate", flush=True)
+    for dim in (64, 128):
+        seq, heads = 1000, 5
+        qkv = (3 * synth.randn((seq, 3 * heads * dim), 60)).to(torch.bfloat16)
+        q, k, _ = synth.split_qkv(qkv, heads, dim)
+        wq = (1 + 0.1 * synth.randn((dim,), 61)).to(torch.bfloat16)
+        wk = (1 + 0.1 * synth.randn((dim,), 62)).to(torch.bfloat16)
+        dq, dk, _ = synth.split_qkv(qkv.to(device), heads, dim)
+        qn, kn = normalise_qk(dq, dk, wq.to(device), wk.to(device))
+        for got, x, w in ((qn, q, wq), (kn, k, wk)):
+            want = F.rms_norm(x, (dim,), w, 1e-6).float()
+            ulp = torch.ldexp(torch.ones_like(want), torch.frexp(want)[1] - 8)   # bf16 spacing at want
+            ulps = (got.cpu().float() - want).abs() / ulp
+            assert ulps.max().item() <= 1.0, ulps.max().item()
+        o = synth.randn((seq, heads, dim), 63, dtype=torch.bfloat16)
+        g = torch.sigmoid(synth.randn((seq, heads), 64)).to(torch.bfloat16)
+        got = apply_softmax_gate(o.to(device), g.to(device).unsqueeze(-1))
+        assert torch.equal(got.cpu(), (o * g.unsqueeze(-1)).reshape(seq, heads * dim))
