@@ -112,7 +112,7 @@ class VDNState:
         del index, device, dtype
 
     def projection_view(self, weights):
-        """Branch-visible weights plus the ``to_out_linear`` projector (``vdn_h3/hybrid.py:185-196``)."""
+        """Branch-visible weights plus the ``to_out_linear`` projector (``vdn_h3/hybrid.py:168-181``)."""
         if _projection.BF16_WEIGHT_KEY not in weights and _projection.FP8_WEIGHT_KEY not in weights:
             raise RuntimeError("VDN projection state contains neither BF16 nor quantized weight")
         return weights, lambda rows, **kw: _projection.project(rows, weights, **kw)
