@@ -26,9 +26,10 @@
 namespace vdnh3 {
 namespace {
 
-constexpr int kBM = 128;  // query rows per workgroup
+constexpr int kBM = 256;  // query rows per workgroup (8 wavefronts x 32)
 constexpr int kBN = 64;   // keys per tile
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
+constexpr int kRing = 4;  // LDS slots per K and V^T ring: tile loads are issued kRing - 1 tiles ahead
 constexpr float kLazy = 8.0f;  // log2 of the largest probability a stale running max allows
 
 // LDS position p (0..15) inside a 16-key group holds key offset kperm(p): the order in
@@ -73,30 +74,102 @@ __global__ __launch_bounds__(kThreads) void vt_prepass_kernel(const uint16_t *__
 }
 
 // ---------------------------------------------------------------------------------
+// LDS slots of the staged tiles. Each tile row is split into 16-byte chunks; chunk c of row r
+// is stored at slot c ^ swizzle(r), so that the 16 lanes of one MFMA fragment read (16
+// consecutive rows, one chunk column) hit 16 different 16-byte bank groups.
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void window_attn_kernel(
+__device__ __forceinline__ int k_slot(int r, int c) {
+  if constexpr (D == 128) return c ^ (r & 15);  // 16 chunks per 256-byte row
+  else return c ^ ((r >> 1) & 7);               // 8 chunks per 128-byte row
+}
+__device__ __forceinline__ int v_slot(int d, int c) { return c ^ ((d >> 1) & 7); }  // 8 chunks per row
+
+// s_waitcnt with vmcnt <= N, lgkmcnt = 0 (expcnt left alone), gfx9 encoding of the immediate.
+template <int N>
+__device__ __forceinline__ void wait_vm_lds() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier without the fence of __syncthreads (which would also wait for every
+// in-flight tile load); the empty asm statements keep the compiler from moving memory
+// accesses across it. The waits the step needs are issued explicitly before it.
+__device__ __forceinline__ void bare_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane i of the
+// wave writes lds_wave_base + 16 i; lds_wave_base must be the same for the whole wave. Issued
+// as inline assembly so that the compiler does not add its own conservative "wait for every
+// LDS DMA" before each LDS read: the kernel orders these loads itself, with an explicit vmcnt
+// wait and a barrier at the top of every step.
+__device__ __forceinline__ void global_to_lds16(const uint16_t *src, uint16_t *lds_wave_base) {
+  const uint32_t lds = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)(lds_wave_base)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "m0");
+}
+
+// The value of lane (l + 32) mod 64, via v_permlane32_swap (gfx950).
+__device__ __forceinline__ float other_half(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const uint32_t lane = __lane_id();
+  return __uint_as_float(lane < 32 ? r[1] : r[0]);
+}
+
+// Order of one MFMA phase (32 LDS fragment reads, 32 MFMAs): eight reads ahead, then one read
+// per MFMA, so each MFMA's operand was requested about eight MFMAs (~250 cycles) earlier.
+__device__ __forceinline__ void mfma_phase_schedule() {
+  constexpr int kMfma = 0x008, kDsRead = 0x100;
+  __builtin_amdgcn_sched_group_barrier(kDsRead, 8, 0);
+#pragma unroll
+  for (int i = 0; i < 24; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
+}
+
+// ---------------------------------------------------------------------------------
+// Two-group ping-pong over the key tiles t = 0..T-1 of a work item (256 query rows of one head).
+// Waves 0-3 (group A) and 4-7 (group B) each own 32 query rows; wave w and w + 4 share a SIMD.
+// The item runs in barrier-separated phases p = 0 .. 2T+1; in each phase one group works on the
+// matrix cores and the other on the VALU, so the two waves of every SIMD alternate:
+//   MFMA phase of tile t :  O^T += V(t-1)^T P(t-1)^T   and   S(t)^T = K(t) Q^T      (32 MFMAs)
+//   VALU phase of tile t :  P(t) = exp2(scale S(t) - m), row max / sum, O rescale   (softmax)
+// Group A runs tile t's MFMA phase in phase 2t and its VALU phase in 2t+1; group B one phase
+// later. K(t) and V(t-1) are read in phases 2t and 2t+1 only; tiles are loaded (direct to LDS,
+// every thread) into four-slot rings three tiles ahead, which hides HBM latency for the tiles
+// that miss L2.
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
     const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const uint16_t *__restrict__ k, int64_t k_row,
     int64_t k_head, const uint16_t *__restrict__ vt, int s_pad, uint16_t *__restrict__ out, int64_t o_row,
     int64_t o_head, const uint16_t *__restrict__ gate, int64_t g_row, int seq, float scale_log2,
     const int4 *__restrict__ items, int n_items, const int2 *__restrict__ tiles, int per_xcd, int total) {
-  constexpr int KP = D + 8;    // K tile row pitch (elements): 16-byte pad -> conflict-free 16-row reads
-  constexpr int VP = kBN + 8;  // V^T tile row pitch
+  constexpr int KC = D / 8;    // 16-byte chunks per K row
   constexpr int NS = D / 16;   // k-steps of the QK^T contraction
   constexpr int NO = D / 32;   // 32-row blocks of O^T
-  constexpr int KCH = kBN * D / 8 / kThreads;  // 16-byte K chunks per thread
-  constexpr int VCH = D * kBN / 8 / kThreads;  // 16-byte V^T chunks per thread
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[D * VP];
+  constexpr int KCH = kBN * KC / kThreads;  // 16-byte K chunks per thread and tile
+  constexpr int VCH = D * 8 / kThreads;     // 16-byte V^T chunks per thread and tile
+  constexpr int KT = kBN * D, VT = D * kBN;  // elements per tile
+  static_assert(KCH >= 1 && VCH >= 1, "every thread loads at least one chunk of each tile");
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kRing][KT];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kRing][VT];
 
   const int bid = blockIdx.x;
   const int L = (bid & 7) * per_xcd + (bid >> 3);
   if (L >= total) return;
   const int head = L / n_items;
   const int4 item = items[L - head * n_items];
-  const int q0 = item.x, q1 = item.y, toff = item.z, tcnt = item.w;
+  const int q0 = item.x, q1 = item.y, toff = item.z, T = item.w;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, g = lane >> 5;
+  const int group = wave >> 2;
   const int qr = q0 + wave * 32 + l32;
   const int qrc = min(qr, q1 - 1);
 
@@ -107,118 +180,161 @@ __global__ __launch_bounds__(kThreads, 2) void window_attn_kernel(
     for (int s = 0; s < NS; ++s) qf[s] = as_bf16x8(ld16(qp + 16 * s));
   }
 
-  f32x16_t oacc[NO];
-#pragma unroll
-  for (int m = 0; m < NO; ++m) oacc[m] = f32x16_t{};
-  float m_run = -INFINITY, l_run = 0.f;
-
   const uint16_t *kbase = k + (int64_t)head * k_head;
   const uint16_t *vbase = vt + (int64_t)head * D * s_pad;
-  // per-thread 16-byte chunk coordinates of the K tile ([kBN][D]) and of the V^T tile ([D][kBN])
-  int k_r[KCH], k_c[KCH], v_d[VCH], v_c[VCH];
-#pragma unroll
-  for (int i = 0; i < KCH; ++i) {
-    const int c = tid + kThreads * i;
-    k_r[i] = c / (D / 8);
-    k_c[i] = c % (D / 8);
-  }
-#pragma unroll
-  for (int i = 0; i < VCH; ++i) {
-    const int c = tid + kThreads * i;
-    v_d[i] = c >> 3;
-    v_c[i] = c & 7;
-  }
-  u32x4_t kreg[KCH], vreg[VCH];
-  {
-    const int ks = tiles[toff].x;
-#pragma unroll
-    for (int i = 0; i < KCH; ++i)
-      kreg[i] = ld16(kbase + (int64_t)min(ks + k_r[i], seq - 1) * k_row + k_c[i] * 8);
-#pragma unroll
-    for (int i = 0; i < VCH; ++i)
-      vreg[i] = ld16(vbase + (int64_t)v_d[i] * s_pad + ks + v_c[i] * 8);
-  }
-
-  for (int t = 0; t < tcnt; ++t) {
-    const int packed = tiles[toff + t].y;
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) st16(&Ks[k_r[i] * KP + k_c[i] * 8], kreg[i]);
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) st16(&Vs[v_d[i] * VP + v_c[i] * 8], vreg[i]);
-    __syncthreads();
-    if (t + 1 < tcnt) {
-      const int ks = tiles[toff + t + 1].x;
+  // Tile loads: LDS position P of a K tile is (row P / KC, slot P % KC) and holds chunk
+  // slot ^ swizzle(row) of that key row (likewise for V^T with 8 chunks per d-row). Thread chunk
+  // i covers row kr0 + i * kBN / KCH; the swizzle depends on the row only through bits that are
+  // the same for every i, so one 32-bit lane offset serves all chunks.
+  const int kr0 = tid / KC, vd0 = tid >> 3;
+  const uint32_t koff = (uint32_t)(kr0 * k_row + k_slot<D>(kr0, tid % KC) * 8);
+  const uint32_t voff = (uint32_t)(vd0 * s_pad + v_slot(vd0, tid & 7) * 8);
+  auto load_k = [&](int t, uint16_t *dst) __device__ {
+    const int ks = tiles[toff + t].x;
+    if (ks + kBN <= seq) {
+      const uint16_t *src = kbase + (int64_t)ks * k_row;
 #pragma unroll
       for (int i = 0; i < KCH; ++i)
-        kreg[i] = ld16(kbase + (int64_t)min(ks + k_r[i], seq - 1) * k_row + k_c[i] * 8);
+        global_to_lds16(src + (int64_t)i * (kBN / KCH) * k_row + koff, dst + (i * kThreads + wave * 64) * 8);
+    } else {  // last tile of the sequence: clamp rows to seq - 1 (their scores are masked)
 #pragma unroll
-      for (int i = 0; i < VCH; ++i)
-        vreg[i] = ld16(vbase + (int64_t)v_d[i] * s_pad + ks + v_c[i] * 8);
+      for (int i = 0; i < KCH; ++i) {
+        const int r = kr0 + i * (kBN / KCH);
+        global_to_lds16(kbase + (int64_t)min(ks + r, seq - 1) * k_row + k_slot<D>(r, tid % KC) * 8,
+                        dst + (i * kThreads + wave * 64) * 8);
+      }
     }
+  };
+  auto load_v = [&](int t, uint16_t *dst) __device__ {
+    const uint16_t *src = vbase + tiles[toff + t].x;
+#pragma unroll
+    for (int i = 0; i < VCH; ++i)
+      global_to_lds16(src + (int64_t)i * (D / VCH) * s_pad + voff, dst + (i * kThreads + wave * 64) * 8);
+  };
 
-    // S^T = K Q^T : two 32-key blocks x 32 queries
-    f32x16_t sacc[2];
+  // Fragment offsets inside a tile (elements). The swizzles depend on the row only through
+  // l32 (r = 32 kb + l32, d = 32 m + l32), so the 32-row blocks differ by constant offsets.
+  int kfo[NS], vfo[4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sacc[kb] = f32x16_t{};
-      const uint16_t *kp = &Ks[(32 * kb + l32) * KP + 8 * g];
+  for (int st = 0; st < NS; ++st) kfo[st] = (l32 * KC + k_slot<D>(l32, 2 * st + g)) * 8;
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
-        sacc[kb] = mfma_bf16_32x32x16(as_bf16x8(ld16(kp + 16 * s)), qf[s], sacc[kb]);
+  for (int tt = 0; tt < 4; ++tt) vfo[tt] = (l32 * 8 + v_slot(l32, 2 * tt + g)) * 8;
+
+  f32x16_t oacc[NO], sacc[2];
+#pragma unroll
+  for (int m = 0; m < NO; ++m) oacc[m] = f32x16_t{};
+  bf16x8_t pb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) pb[j] = bf16x8_t{};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // Rings: K(tau) and V(tau) live in slot tau % kRing. K(t) and V(t-1) are read in phases 2t
+  // and 2t+1. Phase 2t issues K(t+kRing-1) (over K(t-1)) and V(t+kRing-2) (over V(t-2)), both
+  // last read in phase 2t-1, so each load has 2(kRing-1) phases to land. Past the end the tile
+  // index is clamped to T-1: such loads rewrite slots that no real tile reads any more, and
+  // every even phase issues the same number of loads, which keeps the vmcnt wait exact.
+  constexpr int kLoadsPerIssue = KCH + VCH;
+  // prologue: K(0..kRing-2), V(0..kRing-3) landed; V(-1), the V^T slot read by the PV of tile 0
+  // (with P(-1) = 0), is zeroed so that product is exactly zero
+#pragma unroll
+  for (int j = 0; j < kRing - 1; ++j) load_k(min(j, T - 1), Ks[j]);
+#pragma unroll
+  for (int j = 0; j < kRing - 2; ++j) load_v(min(j, T - 1), Vs[j]);
+#pragma unroll
+  for (int i = 0; i < VT / 8 / kThreads; ++i)
+    st16(Vs[kRing - 1] + (i * kThreads + tid) * 8, u32x4_t{0, 0, 0, 0});
+  wait_vm_lds<0>();
+  bare_barrier();
+
+  const int phases = 2 * T + 2;
+  for (int p = 0; p < phases; ++p) {
+    if ((p & 1) == 0) {  // all threads: issue K(t+kRing-1), V(t+kRing-2) for t = p / 2
+      const int t = p >> 1;
+      load_k(min(t + kRing - 1, T - 1), Ks[(t + kRing - 1) % kRing]);
+      load_v(min(t + kRing - 2, T - 1), Vs[(t + kRing - 2) % kRing]);
     }
-    const int lo = packed & 0xffff, hi = packed >> 16;
-    if (lo > 0 || hi < kBN) {
+    // Group A (B) works on the matrix cores in even (odd) phases. Both tile indices depend on
+    // p only, so tile descriptors are scalar loads: a per-lane load would make the compiler
+    // wait for every in-flight tile load before using it.
+    const int t_mfma = p >> 1;            // A: p = 2t; B: p = 2t + 1
+    const int t_valu = (p - 1) >> 1;      // A: p = 2t + 1 (odd); B: p = 2t + 2 (even)
+    if (group == (p & 1)) {
+      // MFMA phase of tile t
+      const int t = t_mfma;
+      // t = 0 has no PV and t = T no QK: those phases run on a zero tile / discard the scores,
+      // so the phase is one branch-free block whose LDS reads can run well ahead of the MFMAs
+      {
+        const uint16_t *vtile = Vs[(t + kRing - 1) % kRing];
+#pragma unroll
+        for (int m = 0; m < NO; ++m)
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            oacc[m] = mfma_bf16_32x32x16(as_bf16x8(ld16(vtile + m * 32 * kBN + vfo[tt])), pb[tt], oacc[m]);
+      }
+      {
+        const uint16_t *ktile = Ks[t % kRing];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          sacc[kb] = f32x16_t{};
+#pragma unroll
+          for (int st = 0; st < NS; ++st)
+            sacc[kb] = mfma_bf16_32x32x16(as_bf16x8(ld16(ktile + kb * 32 * D + kfo[st])), qf[st], sacc[kb]);
+        }
+      }
+      mfma_phase_schedule();
+    } else if (p >= 1 + group && t_valu < T) {
+      // VALU phase of tile t: softmax in base 2, one query per lane. The running max m_run moves
+      // only when this tile's max exceeds it by more than 2^kLazy: probabilities stay below
+      // 2^kLazy (exact softmax either way, a common shift cancels in O / l) and most tiles skip
+      // the rescale.
+      const int packed = tiles[toff + t_valu].y;
+      const int lo = packed & 0xffff, hi = packed >> 16;
+      if (lo > 0 || hi < kBN) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int ko = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
+            if (ko < lo || ko >= hi) sacc[kb][i] = -INFINITY;
+          }
+      }
+      // tile row max: a balanced tree over the lane's 32 scores (depth 5 instead of a 32-long
+      // chain), then the other half-wave's value through v_permlane32_swap (no LDS round trip)
+      float mx[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx[i] = fmaxf(sacc[0][i], sacc[1][i]);
+#pragma unroll
+      for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) mx[i] = fmaxf(mx[i], mx[i + w]);
+      float mt = fmaxf(mx[0], other_half(mx[0])) * scale_log2;
+      const bool grow = mt > m_run + kLazy;
+      if (__any(grow)) {
+        const float m_new = grow ? mt : m_run;
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= corr;
+#pragma unroll
+        for (int m = 0; m < NO; ++m) oacc[m] *= corr;
+      }
+      float rs[4] = {0.f, 0.f, 0.f, 0.f};  // four partial sums: short dependency chains
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int ko = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
-          if (ko < lo || ko >= hi) sacc[kb][i] = -INFINITY;
+          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i], scale_log2, -m_run));
+          rs[i & 3] += pv;
+          pb[2 * kb + (i >> 3)][i & 7] = (__bf16)pv;
         }
+      l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
     }
-    // Online softmax in base 2, one query per lane. The running max m_run only moves when
-    // this tile's max exceeds it by more than 2^kLazy: probabilities are then bounded by
-    // 2^kLazy (exact softmax either way, since a common shift cancels in O / l), and most
-    // tiles skip rescaling the accumulators.
-    float mt = fmaxf(sacc[0][0], sacc[0][1]);
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) mt = fmaxf(mt, fmaxf(sacc[kb][i], sacc[kb][i + 1]));
-    mt = fmaxf(mt, __shfl_xor(mt, 32)) * scale_log2;
-    const bool grow = mt > m_run + kLazy;
-    if (__any(grow)) {
-      const float m_new = grow ? mt : m_run;
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
-      l_run *= corr;
-#pragma unroll
-      for (int m = 0; m < NO; ++m) oacc[m] *= corr;
-    }
-    float rs = 0.f;
-    bf16x8_t pb[4];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i], scale_log2, -m_run));
-        rs += p;
-        pb[2 * kb + (i >> 3)][i & 7] = (__bf16)p;
-      }
-    l_run += rs;
-
-    // O^T += V^T P^T : NO blocks of 32 d-rows, 4 k-steps of 16 keys
-#pragma unroll
-    for (int m = 0; m < NO; ++m) {
-      const uint16_t *vp = &Vs[(32 * m + l32) * VP + 8 * g];
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-        oacc[m] = mfma_bf16_32x32x16(as_bf16x8(ld16(vp + 16 * tt)), pb[tt], oacc[m]);
-    }
-    __syncthreads();
+    // before an even phase 2(t+1): K(t+1) and V(t) (issued kRing - 1 issue phases ago) have
+    // landed; the loads of the last kRing - 2 issue phases may still be in flight
+    if (p & 1) wait_vm_lds<(kRing - 2) * kLoadsPerIssue>();
+    bare_barrier();
   }
 
-  l_run += __shfl_xor(l_run, 32);
+  l_run += other_half(l_run);
   const float inv = 1.f / l_run;
   if (qr < q1) {
     float gv = 1.f;
