@@ -28,19 +28,17 @@ int check_launch(const char *what);
 // ---- bf16 <-> fp32 (device) ---------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
 
-// Round to nearest even; NaN stays a quiet NaN.
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
-}
+// Round to nearest even (v_cvt_pk_bf16_f32 in the default rounding mode); NaN stays a NaN.
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // bf16 rounding of an fp32 value, returned as fp32.
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// two values rounded to bf16 by one packed conversion; `lo` in the low half
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return uint32_t(f2bf(lo)) | (uint32_t(f2bf(hi)) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
 // ---- MFMA wrappers ------------------------------------------------------------------
@@ -55,6 +53,43 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_
 // 16-byte vector load / store (addresses must be 16-byte aligned).
 __device__ __forceinline__ u32x4_t ld16(const void *p) { return *reinterpret_cast<const u32x4_t *>(p); }
 __device__ __forceinline__ void st16(void *p, u32x4_t v) { *reinterpret_cast<u32x4_t *>(p) = v; }
+
+// ---- direct-to-LDS tile loads and explicit waits ---------------------------------------
+// s_waitcnt with vmcnt <= N, lgkmcnt = 0 (expcnt left alone), gfx9 encoding of the immediate.
+template <int N>
+__device__ __forceinline__ void wait_vm_lds() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier without the fence of __syncthreads (which would also wait for every
+// in-flight tile load); the empty asm statements keep the compiler from moving memory
+// accesses across it. The waits the step needs are issued explicitly before it.
+__device__ __forceinline__ void bare_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane i of the
+// wave writes lds_wave_base + 16 i; lds_wave_base must be the same for the whole wave. Issued
+// as inline assembly so that the compiler does not add its own conservative "wait for every
+// LDS DMA" before each LDS read: the kernel orders these loads itself, with explicit vmcnt
+// waits and barriers. M0 is a reserved register the compiler does not preserve around the
+// statement; no kernel of this library uses M0 otherwise (the generated code has no other M0
+// access).
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(p)));
+}
+// the same with the wave's LDS byte address given directly (wave-uniform)
+__device__ __forceinline__ void global_to_lds16_at(const void *src, uint32_t lds_wave_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
+               "s"(__builtin_amdgcn_readfirstlane(lds_wave_addr))
+               : "m0");
+}
+__device__ __forceinline__ void global_to_lds16(const void *src, void *lds_wave_base) {
+  global_to_lds16_at(src, lds_address(lds_wave_base));
+}
 
 }  // namespace vdnh3
 

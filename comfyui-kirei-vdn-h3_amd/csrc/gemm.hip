@@ -8,16 +8,22 @@
 // (vdn_h3/fp8.py:254-262) and the W8A8 int8 projection with per-token x per-channel scales
 // (the ComfyUI-native qkv_proj / out_proj of vdn_h3/hybrid.py:263, :535).
 //
-// Tiling: a workgroup of 4 wavefronts computes a 128x128 tile of C, each wavefront a 64x64
-// quadrant as 2x2 blocks of 32x32 MFMA accumulators. K advances in tiles of 128 bytes per row
-// (64 bf16, 128 int8 or 128 fp8 elements); both operand tiles are staged in LDS with a
-// 16-byte row pad (conflict-free 16-row reads) and the next tile is prefetched into
-// registers while the current one is multiplied.
-//   bf16: v_mfma_f32_32x32x16_bf16, 4 k-steps of 16 B per lane per tile
-//   int8: v_mfma_i32_32x32x32_i8,   4 k-steps of 16 B per lane per tile
-//   fp8 : v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales), 2 k-steps of 32 B per lane
+// Tiling: a workgroup of 4 wavefronts (one per SIMD) computes a 256x256 tile of C; wavefront w
+// owns rows 128 * (w / 2) .. +128 and columns 128 * (w % 2) .. +128 as 4 x 4 blocks of 32x32
+// MFMA accumulators (eight 16-byte LDS fragment reads feed sixteen independent MFMAs per
+// k-step; the accumulators live in AGPRs). K advances in
+// stages of 64 bytes per row (32 bf16, 64 int8 or 64 fp8 elements):
+//   bf16: v_mfma_f32_32x32x16_bf16, 2 k-steps of 32 bytes per stage
+//   int8: v_mfma_i32_32x32x32_i8,   2 k-steps of 32 bytes
+//   fp8 : v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales), 1 k-step of 64 bytes
 // Every lane reads its A and B k-slices at the same byte offsets, so the products pair the
 // same k whatever order the instruction assigns to the lane's bytes.
+// Stages are loaded straight into LDS (global_load_lds) in a four-slot ring and consumed in
+// pairs, one barrier per pair, while the next pair loads (its loads are spread between the
+// MFMAs); 16-byte chunk c of stage row r is stored at slot c ^ ((r >> 2) & 3), which makes the
+// 16-lane fragment reads conflict-free.
+// Tiles are ordered so that the workgroups resident on one XCD cover an 8 x 4 block of
+// tiles and share their A and B panels in that XCD's L2.
 #include <type_traits>
 
 #include "common.h"
@@ -25,9 +31,12 @@
 namespace vdnh3 {
 namespace {
 
-constexpr int kGemmBM = 128, kGemmBN = 128, kGemmKB = 128;  // tile rows, cols, bytes of K per tile
+constexpr int kGemmBM = 256, kGemmBN = 256;
+constexpr int kGemmKB = 128;    // K bytes per row that the host requires K * element size to be a multiple of
+constexpr int kGemmSK = 128;    // K bytes per row of one pipeline stage
+constexpr int kGemmStages = 2;  // LDS ring slots
 constexpr int kGemmThreads = 256;
-constexpr int kGemmPitch = kGemmKB + 16;  // LDS row pitch in bytes
+constexpr int kGemmGroupM = 8;                             // tile rows per grouping band
 
 enum GemmKind { kBF16 = 0, kI8 = 1, kF8 = 2 };
 enum OutType { kOutBF16 = 0, kOutF32 = 1, kOutI32 = 2 };
@@ -44,143 +53,349 @@ struct GemmEpi {
   int out_type;       // OutType
   int accumulate;     // C += epi(acc)
   int round_linear;   // bf16 output: round the linear result to bf16 before the activation
+  int vec;            // N % 4 == 0, ldc % 4 == 0 and C aligned for 4-element stores
 };
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
 
+// LDS slot of 16-byte chunk c of stage row r (8 chunks per 128-byte row): 16 consecutive rows
+// read at one chunk column hit 16 different 16-byte bank groups (row parity x 8 slots)
+__host__ __device__ constexpr int gemm_slot(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+// MFMA operand reads: one k-step = 32 bytes per row (bf16 / int8, one 16-byte chunk per lane
+// group) or 64 bytes (fp8, two chunks per lane group)
 template <int KIND>
-__global__ __launch_bounds__(kGemmThreads, 2) void gemm_nt_kernel(const uint8_t *__restrict__ A, int64_t lda_b,
+struct Frag {
+  using type = typename std::conditional<KIND == kF8, i32x8_t, u32x4_t>::type;
+};
+
+// Epilogue. Each wavefront stages its 128 x 128 block of C through LDS 32 rows at a time
+// (row-major, kEpiStride words per row: rows r and r + 4, written by the two lane halves of
+// one MFMA register, land 32 banks apart) and reads it back as row segments: lane
+// (h = lane / 32, c = lane % 32) takes columns 4c .. 4c+3 of row 2 it + h, so each row of the
+// block leaves as one contiguous run. The staged words are the raw accumulator bits (int32
+// for int8 operands, fp32 otherwise). ACT (sigmoid) and ACCUM are not combined by any caller
+// (the launcher keeps them apart).
+constexpr int kEpiStride = 136;
+constexpr int kEpiWaveWords = 32 * kEpiStride;
+
+// Per-lane epilogue operands, loaded at the start of the kernel so that their latency hides
+// behind the main loop: the scales of rows mb + lane and mb + 64 + lane of the wavefront's
+// block, and the column scale (times alpha) and bias of the lane's four columns nb + 4 (lane % 32) + k.
+struct EpiOperands {
+  float row_scale[2];
+  float col_scale[4];
+  float bias[4];
+};
+
+__device__ __forceinline__ EpiOperands load_epi_operands(const GemmEpi &epi, int M, int N, int mb, int nb, int lane) {
+  EpiOperands o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int m = min(mb + 64 * h + lane, M - 1);
+    o.row_scale[h] = epi.a_scale ? epi.a_scale[epi.a_scale_n == 1 ? 0 : m] : 1.f;
+  }
+  const int n = nb + 4 * (lane & 31);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int nk = min(n + k, N - 1);
+    o.col_scale[k] = epi.b_scale ? epi.alpha * epi.b_scale[epi.b_scale_n == 1 ? 0 : nk] : epi.alpha;
+    o.bias[k] = !epi.bias ? 0.f
+                : epi.bias_bf16 ? bf2f(static_cast<const uint16_t *>(epi.bias)[nk])
+                                : static_cast<const float *>(epi.bias)[nk];
+  }
+  return o;
+}
+
+template <int OUT, bool ACT, bool ACCUM, bool INT_ACC, typename Acc>
+__device__ __forceinline__ void store_block(const Acc (&acc)[4][4], uint32_t *stage, const GemmEpi &epi,
+                                            const EpiOperands &eo, void *C, int64_t ldc, int M, int N, int mb,
+                                            int nb, int lane) {
+  const int l32 = lane & 31, g = lane >> 5;
+  const int c0 = 4 * l32, n = nb + c0;
+  const bool vec = epi.vec && n < N;  // the host sets vec only when N % 4 == 0 and C allows 4-wide stores
+  using old_t = typename std::conditional<OUT == kOutF32, f32x4_t, u32x2_t>::type;
+  const bool round_linear = epi.round_linear;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // stage rows 32 i .. +32 of the block
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        // element copied out first: __builtin_bit_cast of a vector-element lvalue reads
+        // element 0 whatever the index
+        const auto e = acc[i][j][r];
+        const uint32_t w = __builtin_bit_cast(uint32_t, e);
+        stage[(8 * (r >> 2) + 4 * g + (r & 3)) * kEpiStride + 32 * j + l32] = w;
+      }
+    asm volatile("" ::: "memory");  // LDS operations of one wavefront complete in order
+    // rows 2 it + g of the round in chunks of four; when accumulating, a chunk's old values
+    // are loaded together before any of its stores
+#pragma unroll 1
+    for (int c4 = 0; c4 < 4; ++c4) {
+      old_t old[4];
+      if constexpr (ACCUM) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = mb + 32 * i + 2 * (4 * c4 + q) + g;
+          old[q] = old_t{};
+          if (vec && m < M) {
+            const int64_t off = (int64_t)m * ldc + n;
+            if constexpr (OUT == kOutF32) old[q] = *reinterpret_cast<const f32x4_t *>(static_cast<float *>(C) + off);
+            else old[q] = *reinterpret_cast<const u32x2_t *>(static_cast<uint16_t *>(C) + off);
+          }
+        }
+      }
+      // the chunk's staged rows and row scales (row 32 i + 2 it + g of the block: scale held by
+      // lane (32 i + 2 it + g) % 64, entry i / 2), read before any of its arithmetic
+      u32x4_t wq[4];
+      float asq[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = 2 * (4 * c4 + q) + g;
+        wq[q] = *reinterpret_cast<const u32x4_t *>(stage + row * kEpiStride + c0);
+        asq[q] = __shfl(eo.row_scale[i >> 1], 32 * (i & 1) + row);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = mb + 32 * i + 2 * (4 * c4 + q) + g;
+        if (m >= M || n >= N) continue;
+        const int64_t off = (int64_t)m * ldc + n;
+        const u32x4_t w = wq[q];
+        const uint32_t wk[4] = {w.x, w.y, w.z, w.w};
+        if constexpr (OUT == kOutI32) {
+          if (vec) {
+            *reinterpret_cast<u32x4_t *>(static_cast<int32_t *>(C) + off) = w;
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              if (n + k < N) static_cast<uint32_t *>(C)[off + k] = wk[k];
+          }
+        } else {
+          float v[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            float x = INT_ACC ? (float)__builtin_bit_cast(int32_t, wk[k]) : __builtin_bit_cast(float, wk[k]);
+            x *= asq[q];  // 1 without row scales
+            x = x * eo.col_scale[k] + eo.bias[k];
+            // bf16 output: rounding the linear value first only matters before the sigmoid (a
+            // second rounding of a bf16 value, or the accumulation's own rounding, is exact)
+            if constexpr (OUT == kOutBF16 && ACT) x = round_linear ? round_bf(x) : x;
+            if constexpr (ACT) x = sigmoidf_(x);
+            v[k] = x;
+          }
+          if constexpr (OUT == kOutF32) {
+            float *cp = static_cast<float *>(C) + off;
+            if (vec) {
+              f32x4_t o = {v[0], v[1], v[2], v[3]};
+              if constexpr (ACCUM) o += old[q];
+              *reinterpret_cast<f32x4_t *>(cp) = o;
+            } else {
+#pragma unroll
+              for (int k = 0; k < 4; ++k)
+                if (n + k < N) cp[k] = ACCUM ? cp[k] + v[k] : v[k];
+            }
+          } else {
+            uint16_t *cp = static_cast<uint16_t *>(C) + off;
+            if (vec) {
+              uint32_t lo, hi;
+              if constexpr (ACCUM) {
+                const u32x2_t o = old[q];
+                lo = pack_bf2(bf2f(o.x & 0xffff) + round_bf(v[0]), bf2f(o.x >> 16) + round_bf(v[1]));
+                hi = pack_bf2(bf2f(o.y & 0xffff) + round_bf(v[2]), bf2f(o.y >> 16) + round_bf(v[3]));
+              } else {
+                lo = pack_bf2(v[0], v[1]);
+                hi = pack_bf2(v[2], v[3]);
+              }
+              *reinterpret_cast<u32x2_t *>(cp) = u32x2_t{lo, hi};
+            } else {
+#pragma unroll
+              for (int k = 0; k < 4; ++k)
+                if (n + k < N) cp[k] = f2bf(ACCUM ? bf2f(cp[k]) + round_bf(v[k]) : v[k]);
+            }
+          }
+        }
+      }
+    }
+    asm volatile("" ::: "memory");
+  }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t *__restrict__ A, int64_t lda_b,
                                                                    const uint8_t *__restrict__ B, int64_t ldb_b,
                                                                    void *__restrict__ C, int64_t ldc, int M, int N,
-                                                                   int nkt, GemmEpi epi, int tiles_n) {
-  __shared__ __attribute__((aligned(16))) uint8_t As[kGemmBM * kGemmPitch];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[kGemmBN * kGemmPitch];
-  const int tile = blockIdx.x;
-  const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
-  const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+                                                                   int nkt, GemmEpi epi, int tiles_m, int tiles_n,
+                                                                   int per_xcd, int total) {
+  constexpr int STAGE_BYTES = kGemmBM * kGemmSK;  // one 256-row x 128-byte stage of A or B (32 KB)
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2][kGemmStages][STAGE_BYTES];
+  static_assert(4 * kEpiWaveWords * 4 <= (int)sizeof(smem), "epilogue staging must fit the ring");
+  auto &As = smem[0];
+  auto &Bs = smem[1];
 
-  // 4 x 16-byte chunks of each operand tile per thread: row = c >> 3, byte column = (c & 7) * 16
-  const uint8_t *a_src[4];
-  const uint8_t *b_src[4];
-  int lds_off[4];
+  // XCD-aware tile order: workgroups are dealt round-robin over the 8 XCDs, so logical tile L
+  // of XCD x is bid = 8 (L - x per_xcd) + x. Logical tiles walk bands of kGemmGroupM tile rows,
+  // column by column, so concurrently resident workgroups share A rows and B columns.
+  const int bid = blockIdx.x;
+  const int L = (bid & 7) * per_xcd + (bid >> 3);
+  if (L >= total) return;
+  const int band = L / (kGemmGroupM * tiles_n);
+  const int first_m = band * kGemmGroupM;
+  const int band_m = min(kGemmGroupM, tiles_m - first_m);
+  const int in_band = L - band * kGemmGroupM * tiles_n;
+  const int tm = first_m + in_band % band_m, tn = in_band / band_m;
+  const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
+
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+  const int mb = m0 + wm, nb = n0 + wn;
+  const EpiOperands eo = load_epi_operands(epi, M, N, mb, nb, lane);
+
+  // Stage loads. A stage is 128 bytes of K for the tile's 256 A rows and 256 B rows (32 KB
+  // each); LDS position P (16-byte units) of an operand's stage is row P / 8, slot P % 8 and
+  // holds chunk slot ^ swz(row) of that row. Load instruction q (0..7) of a wavefront covers
+  // positions 256 q + tid, i.e. rows 32 q + tid / 8, so each row is read as one whole
+  // 128-byte line. Rows past M (N) read the last row; their results are not stored.
+  const int lrow = tid >> 3;
+  const int lchunk = gemm_slot(lrow, tid & 7);
+  const uint8_t *a_src[8], *b_src[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = tid + kGemmThreads * i, r = c >> 3, col = (c & 7) * 16;
-    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda_b + col;
-    b_src[i] = B + (int64_t)min(n0 + r, N - 1) * ldb_b + col;
-    lds_off[i] = r * kGemmPitch + col;
+  for (int q = 0; q < 8; ++q) {
+    a_src[q] = A + (int64_t)min(m0 + 32 * q + lrow, M - 1) * lda_b + lchunk * 16;
+    b_src[q] = B + (int64_t)min(n0 + 32 * q + lrow, N - 1) * ldb_b + lchunk * 16;
   }
-  u32x4_t areg[4], breg[4];
+  // load q (0..15) of stage st into ring slot `slot`: A rows 32 q .. +32 (q < 8), else B rows
+  // 32 (q - 8) .. +32
+  const uint32_t lds_wave = lds_address(&smem[0][0][0]) + wave * 64 * 16;
+  auto load_part = [&](int st, int slot, int q) __device__ {
+    const int64_t off = (int64_t)st * kGemmSK;
+    const int i = q & 7;
+    const uint32_t dst = lds_wave + (uint32_t)(((q >> 3) * kGemmStages + slot) * STAGE_BYTES + i * kGemmThreads * 16);
+    global_to_lds16_at((q >= 8 ? b_src[i] : a_src[i]) + off, dst);
+  };
+
+  // fragment byte offsets inside an operand's stage (rows 32 i + l32 share l32's swizzle):
+  // bf16 / int8 k-step ks reads chunk 2 ks + g (foff[ks]); fp8 k-step ks reads chunks
+  // 4 ks + 2 g and 4 ks + 2 g + 1 (foff[2 ks], foff[2 ks + 1])
+  int foff[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    areg[i] = ld16(a_src[i]);
-    breg[i] = ld16(b_src[i]);
+  for (int c = 0; c < 4; ++c) {
+    const int chunk = KIND == kF8 ? 4 * (c >> 1) + 2 * g + (c & 1) : 2 * c + g;
+    foff[c] = l32 * kGemmSK + gemm_slot(l32, chunk) * 16;
   }
 
   using acc_t = typename std::conditional<KIND == kI8, i32x16_t, f32x16_t>::type;
-  acc_t acc[2][2];
+  acc_t acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
+    for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
 
-  for (int kt = 0; kt < nkt; ++kt) {
+  // k-steps per stage: 32 bytes per lane group for bf16 / int8, 64 for fp8
+  constexpr int KS = KIND == kF8 ? 2 : 4;
+  using frag_t = typename Frag<KIND>::type;
+  frag_t fa[2][4], fb[2][4];
+  // fragments of k-step ks of the stage in `slot` into buffer `buf`
+  auto read_frags = [&](int slot, int ks, int buf) __device__ {
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t *at = smem[0][slot] + wm * kGemmSK;
+    const uint8_t *bt = smem[1][slot] + wn * kGemmSK;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      st16(As + lds_off[i], areg[i]);
-      st16(Bs + lds_off[i], breg[i]);
-    }
-    __syncthreads();
-    if (kt + 1 < nkt) {
-      const int64_t off = (int64_t)(kt + 1) * kGemmKB;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        areg[i] = ld16(a_src[i] + off);
-        breg[i] = ld16(b_src[i] + off);
+      if constexpr (KIND == kF8) {
+        const u32x4_t alo = ld16(at + i * 32 * kGemmSK + foff[2 * ks]);
+        const u32x4_t ahi = ld16(at + i * 32 * kGemmSK + foff[2 * ks + 1]);
+        const u32x4_t blo = ld16(bt + i * 32 * kGemmSK + foff[2 * ks]);
+        const u32x4_t bhi = ld16(bt + i * 32 * kGemmSK + foff[2 * ks + 1]);
+        fa[buf][i] = i32x8_t{(int)alo.x, (int)alo.y, (int)alo.z, (int)alo.w, (int)ahi.x, (int)ahi.y, (int)ahi.z, (int)ahi.w};
+        fb[buf][i] = i32x8_t{(int)blo.x, (int)blo.y, (int)blo.z, (int)blo.w, (int)bhi.x, (int)bhi.y, (int)bhi.z, (int)bhi.w};
+      } else {
+        fa[buf][i] = ld16(at + i * 32 * kGemmSK + foff[ks]);
+        fb[buf][i] = ld16(bt + i * 32 * kGemmSK + foff[ks]);
       }
     }
-    if constexpr (KIND == kF8) {
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // the 16 MFMAs of one k-step; `dma` issues one stage load before each MFMA of A row block
+  // i = 0..3 (4 per block: 16 per k-step)
+  auto mfmas = [&](int buf, int ld_st, int ld_slot, bool dma) __device__ {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        i32x8_t av[2], bv[2];
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const uint8_t *pa = As + (wm + 32 * i + l32) * kGemmPitch + 64 * ks + 32 * g;
-          const uint8_t *pb = Bs + (wn + 32 * i + l32) * kGemmPitch + 64 * ks + 32 * g;
-          u32x4_t a0 = ld16(pa), a1 = ld16(pa + 16), b0 = ld16(pb), b1 = ld16(pb + 16);
-          av[i] = i32x8_t{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-          bv[i] = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+      for (int j = 0; j < 4; ++j) {
+        if (dma) load_part(ld_st, ld_slot, 4 * i + j);
+        // fixed issue order: each stage load sits between two MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (KIND == kF8)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0, 127,
+                                                                     0, 127);
+        else if constexpr (KIND == kBF16)
+          acc[i][j] = mfma_bf16_32x32x16(as_bf16x8(fa[buf][i]), as_bf16x8(fb[buf][j]), acc[i][j]);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, fa[buf][i]),
+                                                            __builtin_bit_cast(i32x4_t, fb[buf][j]), acc[i][j], 0, 0, 0);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Stage s (ring slot s % 2). Its first k-step's fragments were read before the call. Before
+  // its last k-step, once its own reads are done and stage s + 1 has landed, one barrier frees
+  // slot s % 2 (stage s + 2 loads into it during the last k-step) and makes stage s + 1
+  // readable (its first fragments are read during the last k-step).
+  auto run_stage = [&](int s, bool next, bool dma) __device__ {
+    const int slot = s & 1;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) {
+        read_frags(slot, ks + 1, (ks + 1) & 1);
+        mfmas(ks & 1, 0, 0, false);
+      } else {
+        if (next) {
+          wait_vm_lds<0>();  // stage s + 1 has landed (nothing later is in flight)
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of slot s are done
+          bare_barrier();
+          read_frags(slot ^ 1, 0, 0);
         }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[i], bv[j], acc[i][j], 0, 0, 0, 127, 0,
-                                                                        127);
-      }
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        u32x4_t av[2], bv[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          av[i] = ld16(As + (wm + 32 * i + l32) * kGemmPitch + 32 * ks + 16 * g);
-          bv[i] = ld16(Bs + (wn + 32 * i + l32) * kGemmPitch + 32 * ks + 16 * g);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            if constexpr (KIND == kBF16)
-              acc[i][j] = mfma_bf16_32x32x16(as_bf16x8(av[i]), as_bf16x8(bv[j]), acc[i][j]);
-            else
-              acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, av[i]),
-                                                                __builtin_bit_cast(i32x4_t, bv[j]), acc[i][j], 0, 0,
-                                                                0);
-          }
+        mfmas(ks & 1, s + 2, slot, dma);
       }
     }
-    __syncthreads();
-  }
+  };
 
-  // epilogue: lane holds C[m = 8*(r/4) + 4*g + r%4][n = l32] of each 32x32 block
+  const int nst = nkt;  // stages of 128 bytes of K
+  // prologue: stages 0 and 1 in flight, stage 0's first fragments read
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + wn + 32 * j + l32;
-    if (n >= N) continue;
-    float bs = epi.alpha;
-    if (epi.b_scale) bs *= epi.b_scale[epi.b_scale_n == 1 ? 0 : n];
-    float bias = 0.f;
-    if (epi.bias) bias = epi.bias_bf16 ? bf2f(static_cast<const uint16_t *>(epi.bias)[n])
-                                       : static_cast<const float *>(epi.bias)[n];
+  for (int q = 0; q < 16; ++q) load_part(0, 0, q);
+  if (nst > 1) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (m >= M) continue;
-        const int64_t off = (int64_t)m * ldc + n;
-        if (epi.out_type == kOutI32) {
-          static_cast<int32_t *>(C)[off] = (int32_t)acc[i][j][r];
-          continue;
-        }
-        float v = (float)acc[i][j][r];
-        if (epi.a_scale) v *= epi.a_scale[epi.a_scale_n == 1 ? 0 : m];
-        v = v * bs + bias;
-        if (epi.out_type == kOutF32) {
-          if (epi.act == 1) v = sigmoidf_(v);
-          float *cp = static_cast<float *>(C) + off;
-          *cp = epi.accumulate ? *cp + v : v;
-        } else {
-          if (epi.round_linear) v = round_bf(v);
-          if (epi.act == 1) v = sigmoidf_(v);
-          uint16_t *cp = static_cast<uint16_t *>(C) + off;
-          if (epi.accumulate) v = bf2f(*cp) + round_bf(v);
-          *cp = f2bf(v);
-        }
-      }
+    for (int q = 0; q < 16; ++q) load_part(1, 1, q);
+    wait_vm_lds<16>();
+  } else {
+    wait_vm_lds<0>();
+  }
+  bare_barrier();
+  read_frags(0, 0, 0);
+  int s = 0;
+  for (; s + 2 < nst; ++s) run_stage(s, true, true);
+  if (s + 1 < nst) run_stage(s++, true, false);
+  run_stage(s, false, false);
+
+  // epilogue, specialised on the output type, activation and accumulation (one uniform
+  // branch here instead of per-element tests); the ring's LDS is reused for staging
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  bare_barrier();  // every wave is done reading the last stage
+  uint32_t *stage = reinterpret_cast<uint32_t *>(&smem[0][0][0]) + wave * kEpiWaveWords;
+  constexpr bool kInt = KIND == kI8;
+  if (epi.out_type == kOutI32) {
+    store_block<kOutI32, false, false, kInt>(acc, stage, epi, eo, C, ldc, M, N, mb, nb, lane);
+  } else if (epi.out_type == kOutF32) {
+    if (epi.act) store_block<kOutF32, true, false, kInt>(acc, stage, epi, eo, C, ldc, M, N, mb, nb, lane);
+    else if (epi.accumulate) store_block<kOutF32, false, true, kInt>(acc, stage, epi, eo, C, ldc, M, N, mb, nb, lane);
+    else store_block<kOutF32, false, false, kInt>(acc, stage, epi, eo, C, ldc, M, N, mb, nb, lane);
+  } else {
+    if (epi.act) store_block<kOutBF16, true, false, kInt>(acc, stage, epi, eo, C, ldc, M, N, mb, nb, lane);
+    else if (epi.accumulate) store_block<kOutBF16, false, true, kInt>(acc, stage, epi, eo, C, ldc, M, N, mb, nb, lane);
+    else store_block<kOutBF16, false, false, kInt>(acc, stage, epi, eo, C, ldc, M, N, mb, nb, lane);
   }
 }
 
@@ -198,9 +413,10 @@ int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
   VDNH3_HOST_CHECK(reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0,
                    VDNH3_ERR_INVALID, "gemm: A and B must be 16-byte aligned");
   const int tiles_m = (M + kGemmBM - 1) / kGemmBM, tiles_n = (N + kGemmBN - 1) / kGemmBN;
-  hipLaunchKernelGGL(gemm_nt_kernel<KIND>, dim3(tiles_m * tiles_n), dim3(kGemmThreads), 0, stream,
+  const int total = tiles_m * tiles_n, per_xcd = (total + 7) / 8;
+  hipLaunchKernelGGL(gemm_nt_kernel<KIND>, dim3(per_xcd * 8), dim3(kGemmThreads), 0, stream,
                      static_cast<const uint8_t *>(A), lda * eb, static_cast<const uint8_t *>(B), ldb * eb, C, ldc, M,
-                     N, int(kb / kGemmKB), epi, tiles_n);
+                     N, int(kb / kGemmKB), epi, tiles_m, tiles_n, per_xcd, total);
   return check_launch("gemm_nt");
 }
 
@@ -216,11 +432,15 @@ extern "C" int vdnh3_gemm(int kind, const void *A, int64_t lda, const void *B, i
   VDNH3_HOST_CHECK(out_type >= kOutBF16 && out_type <= kOutI32, VDNH3_ERR_INVALID, "gemm: bad out_type %d", out_type);
   VDNH3_HOST_CHECK(out_type != kOutI32 || kind == kI8, VDNH3_ERR_INVALID, "gemm: int32 output needs int8 operands");
   VDNH3_HOST_CHECK(act == 0 || act == 1, VDNH3_ERR_INVALID, "gemm: bad activation %d", act);
+  VDNH3_HOST_CHECK(!(act && accumulate), VDNH3_ERR_INVALID, "gemm: a sigmoid epilogue cannot accumulate");
   VDNH3_HOST_CHECK(!a_scale || a_scale_n == 1 || a_scale_n == M, VDNH3_ERR_INVALID,
                    "gemm: a_scale must have 1 or M entries");
   VDNH3_HOST_CHECK(!b_scale || b_scale_n == 1 || b_scale_n == N, VDNH3_ERR_INVALID,
                    "gemm: b_scale must have 1 or N entries");
-  GemmEpi epi{a_scale, b_scale, b_scale_n, a_scale_n, alpha, bias, bias_bf16, act, out_type, accumulate, round_linear};
+  const int esize = out_type == kOutBF16 ? 2 : 4;
+  const int vec = N % 4 == 0 && ldc % 4 == 0 && reinterpret_cast<uintptr_t>(C) % (4 * esize) == 0;
+  GemmEpi epi{a_scale, b_scale, b_scale_n, a_scale_n, alpha, bias, bias_bf16, act, out_type, accumulate, round_linear,
+              vec};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (kind) {
     case kBF16:

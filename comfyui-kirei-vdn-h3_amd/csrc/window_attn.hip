@@ -84,34 +84,6 @@ __device__ __forceinline__ int k_slot(int r, int c) {
 }
 __device__ __forceinline__ int v_slot(int d, int c) { return c ^ ((d >> 1) & 7); }  // 8 chunks per row
 
-// s_waitcnt with vmcnt <= N, lgkmcnt = 0 (expcnt left alone), gfx9 encoding of the immediate.
-template <int N>
-__device__ __forceinline__ void wait_vm_lds() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier without the fence of __syncthreads (which would also wait for every
-// in-flight tile load); the empty asm statements keep the compiler from moving memory
-// accesses across it. The waits the step needs are issued explicitly before it.
-__device__ __forceinline__ void bare_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane i of the
-// wave writes lds_wave_base + 16 i; lds_wave_base must be the same for the whole wave. Issued
-// as inline assembly so that the compiler does not add its own conservative "wait for every
-// LDS DMA" before each LDS read: the kernel orders these loads itself, with an explicit vmcnt
-// wait and a barrier at the top of every step.
-__device__ __forceinline__ void global_to_lds16(const uint16_t *src, uint16_t *lds_wave_base) {
-  const uint32_t lds = static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void *)(lds_wave_base)));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
-               "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "m0");
-}
 
 // The value of lane (l + 32) mod 64, via v_permlane32_swap (gfx950).
 __device__ __forceinline__ float other_half(float x) {
