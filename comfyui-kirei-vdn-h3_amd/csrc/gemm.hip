@@ -18,10 +18,13 @@
 //   fp8 : v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales), 1 k-step of 64 bytes
 // Every lane reads its A and B k-slices at the same byte offsets, so the products pair the
 // same k whatever order the instruction assigns to the lane's bytes.
-// Stages are loaded straight into LDS (global_load_lds) in a four-slot ring and consumed in
-// pairs, one barrier per pair, while the next pair loads (its loads are spread between the
-// MFMAs); 16-byte chunk c of stage row r is stored at slot c ^ ((r >> 2) & 3), which makes the
-// 16-lane fragment reads conflict-free.
+// Stages are loaded straight into LDS (global_load_lds) through a five-slot ring (160 KB, all
+// of the CU's LDS): each stage's k-steps issue the loads of the stage four ahead, evenly spaced
+// between their MFMAs, so the loads have three to four stages of MFMA time to land and the
+// address unit sees a steady stream instead of bursts. One barrier per stage, placed before
+// its last k-step, frees a slot and publishes the next stage; fragments are double-buffered
+// in registers one k-step ahead, across that barrier too. 16-byte chunk c of stage row r is
+// stored at slot c ^ ((r >> 2) & 3), which makes the 16-lane fragment reads conflict-free.
 // Tiles are ordered so that the workgroups resident on one XCD cover an 8 x 4 block of
 // tiles and share their A and B panels in that XCD's L2.
 #include <type_traits>
@@ -33,8 +36,8 @@ namespace {
 
 constexpr int kGemmBM = 256, kGemmBN = 256;
 constexpr int kGemmKB = 128;    // K bytes per row that the host requires K * element size to be a multiple of
-constexpr int kGemmSK = 128;    // K bytes per row of one pipeline stage
-constexpr int kGemmStages = 2;  // LDS ring slots
+constexpr int kGemmSK = 64;     // K bytes per row of one pipeline stage
+constexpr int kGemmStages = 5;  // LDS ring slots (5 x 32 KB: all 160 KB)
 constexpr int kGemmThreads = 256;
 constexpr int kGemmGroupM = 8;                             // tile rows per grouping band
 
@@ -58,9 +61,9 @@ struct GemmEpi {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
 
-// LDS slot of 16-byte chunk c of stage row r (8 chunks per 128-byte row): 16 consecutive rows
-// read at one chunk column hit 16 different 16-byte bank groups (row parity x 8 slots)
-__host__ __device__ constexpr int gemm_slot(int r, int c) { return c ^ ((r >> 1) & 7); }
+// LDS slot of 16-byte chunk c of stage row r (4 chunks per 64-byte row): 16 consecutive rows
+// read at one chunk column hit 16 different 16-byte bank groups (row % 4 x 4 slots)
+__host__ __device__ constexpr int gemm_slot(int r, int c) { return c ^ ((r >> 2) & 3); }
 
 // MFMA operand reads: one k-step = 32 bytes per row (bf16 / int8, one 16-byte chunk per lane
 // group) or 64 bytes (fp8, two chunks per lane group)
@@ -228,7 +231,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
                                                                    void *__restrict__ C, int64_t ldc, int M, int N,
                                                                    int nkt, GemmEpi epi, int tiles_m, int tiles_n,
                                                                    int per_xcd, int total) {
-  constexpr int STAGE_BYTES = kGemmBM * kGemmSK;  // one 256-row x 128-byte stage of A or B (32 KB)
+  constexpr int STAGE_BYTES = kGemmBM * kGemmSK;  // one 256-row x 64-byte stage of A or B (16 KB)
   __shared__ __attribute__((aligned(16))) uint8_t smem[2][kGemmStages][STAGE_BYTES];
   static_assert(4 * kEpiWaveWords * 4 <= (int)sizeof(smem), "epilogue staging must fit the ring");
   auto &As = smem[0];
@@ -253,36 +256,36 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
   const int mb = m0 + wm, nb = n0 + wn;
   const EpiOperands eo = load_epi_operands(epi, M, N, mb, nb, lane);
 
-  // Stage loads. A stage is 128 bytes of K for the tile's 256 A rows and 256 B rows (32 KB
-  // each); LDS position P (16-byte units) of an operand's stage is row P / 8, slot P % 8 and
-  // holds chunk slot ^ swz(row) of that row. Load instruction q (0..7) of a wavefront covers
-  // positions 256 q + tid, i.e. rows 32 q + tid / 8, so each row is read as one whole
-  // 128-byte line. Rows past M (N) read the last row; their results are not stored.
-  const int lrow = tid >> 3;
-  const int lchunk = gemm_slot(lrow, tid & 7);
-  const uint8_t *a_src[8], *b_src[8];
+  // Stage loads. A stage is 64 bytes of K for the tile's 256 A rows and 256 B rows (16 KB
+  // each); LDS position P (16-byte units) of an operand's stage is row P / 4, slot P % 4 and
+  // holds chunk slot ^ swz(row) of that row. Load instruction q (0..3) of a wavefront covers
+  // positions 256 q + tid, i.e. rows 64 q + tid / 4. Rows past M (N) read the last row; their
+  // results are not stored.
+  const int lrow = tid >> 2;
+  const int lchunk = gemm_slot(lrow, tid & 3);
+  const uint8_t *a_src[4], *b_src[4];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    a_src[q] = A + (int64_t)min(m0 + 32 * q + lrow, M - 1) * lda_b + lchunk * 16;
-    b_src[q] = B + (int64_t)min(n0 + 32 * q + lrow, N - 1) * ldb_b + lchunk * 16;
+  for (int q = 0; q < 4; ++q) {
+    a_src[q] = A + (int64_t)min(m0 + 64 * q + lrow, M - 1) * lda_b + lchunk * 16;
+    b_src[q] = B + (int64_t)min(n0 + 64 * q + lrow, N - 1) * ldb_b + lchunk * 16;
   }
-  // load q (0..15) of stage st into ring slot `slot`: A rows 32 q .. +32 (q < 8), else B rows
-  // 32 (q - 8) .. +32
+  // load q (0..7) of stage st into ring slot `slot`: A rows 64 q .. +64 (q < 4), else B rows
+  // 64 (q - 4) .. +64
   const uint32_t lds_wave = lds_address(&smem[0][0][0]) + wave * 64 * 16;
   auto load_part = [&](int st, int slot, int q) __device__ {
     const int64_t off = (int64_t)st * kGemmSK;
-    const int i = q & 7;
-    const uint32_t dst = lds_wave + (uint32_t)(((q >> 3) * kGemmStages + slot) * STAGE_BYTES + i * kGemmThreads * 16);
-    global_to_lds16_at((q >= 8 ? b_src[i] : a_src[i]) + off, dst);
+    const int i = q & 3;
+    const uint32_t dst = lds_wave + (uint32_t)(((q >> 2) * kGemmStages + slot) * STAGE_BYTES + i * kGemmThreads * 16);
+    global_to_lds16_at((q >= 4 ? b_src[i] : a_src[i]) + off, dst);
   };
 
   // fragment byte offsets inside an operand's stage (rows 32 i + l32 share l32's swizzle):
-  // bf16 / int8 k-step ks reads chunk 2 ks + g (foff[ks]); fp8 k-step ks reads chunks
-  // 4 ks + 2 g and 4 ks + 2 g + 1 (foff[2 ks], foff[2 ks + 1])
-  int foff[4];
+  // bf16 / int8 k-step ks reads chunk 2 ks + g (foff[ks]); fp8 reads chunks 2 g and 2 g + 1
+  // (foff[0], foff[1])
+  int foff[2];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int chunk = KIND == kF8 ? 4 * (c >> 1) + 2 * g + (c & 1) : 2 * c + g;
+  for (int c = 0; c < 2; ++c) {
+    const int chunk = KIND == kF8 ? 2 * g + c : 2 * c + g;
     foff[c] = l32 * kGemmSK + gemm_slot(l32, chunk) * 16;
   }
 
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
     for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
 
   // k-steps per stage: 32 bytes per lane group for bf16 / int8, 64 for fp8
-  constexpr int KS = KIND == kF8 ? 2 : 4;
+  constexpr int KS = KIND == kF8 ? 1 : 2;
   using frag_t = typename Frag<KIND>::type;
   frag_t fa[2][4], fb[2][4];
   // fragments of k-step ks of the stage in `slot` into buffer `buf`
@@ -305,10 +308,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (KIND == kF8) {
-        const u32x4_t alo = ld16(at + i * 32 * kGemmSK + foff[2 * ks]);
-        const u32x4_t ahi = ld16(at + i * 32 * kGemmSK + foff[2 * ks + 1]);
-        const u32x4_t blo = ld16(bt + i * 32 * kGemmSK + foff[2 * ks]);
-        const u32x4_t bhi = ld16(bt + i * 32 * kGemmSK + foff[2 * ks + 1]);
+        const u32x4_t alo = ld16(at + i * 32 * kGemmSK + foff[0]);
+        const u32x4_t ahi = ld16(at + i * 32 * kGemmSK + foff[1]);
+        const u32x4_t blo = ld16(bt + i * 32 * kGemmSK + foff[0]);
+        const u32x4_t bhi = ld16(bt + i * 32 * kGemmSK + foff[1]);
         fa[buf][i] = i32x8_t{(int)alo.x, (int)alo.y, (int)alo.z, (int)alo.w, (int)ahi.x, (int)ahi.y, (int)ahi.z, (int)ahi.w};
         fb[buf][i] = i32x8_t{(int)blo.x, (int)blo.y, (int)blo.z, (int)blo.w, (int)bhi.x, (int)bhi.y, (int)bhi.z, (int)bhi.w};
       } else {
@@ -318,14 +321,17 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // the 16 MFMAs of one k-step; `dma` issues one stage load before each MFMA of A row block
-  // i = 0..3 (4 per block: 16 per k-step)
-  auto mfmas = [&](int buf, int ld_st, int ld_slot, bool dma) __device__ {
+  // the 16 MFMAs of one k-step; with `dma`, stage loads q0 .. q0 + 8 / KS - 1 of stage ld_st
+  // sit between them, evenly spaced; `reads` (the next k-step's fragment reads) follows the
+  // second MFMA, so that any LDS wait before the first ones covers only older reads
+  auto mfmas = [&](int buf, bool dma, int ld_st, int ld_slot, int q0, auto reads) __device__ {
+    constexpr int kLoads = 8 / KS, kEvery = 16 / kLoads;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (dma) load_part(ld_st, ld_slot, 4 * i + j);
+        if (i == 0 && j == 2) reads();
+        if (dma && (4 * i + j) % kEvery == 0) load_part(ld_st, ld_slot, q0 + (4 * i + j) / kEvery);
         // fixed issue order: each stage load sits between two MFMAs
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (KIND == kF8)
@@ -339,46 +345,70 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
       }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // Stage s (ring slot s % 2). Its first k-step's fragments were read before the call. Before
-  // its last k-step, once its own reads are done and stage s + 1 has landed, one barrier frees
-  // slot s % 2 (stage s + 2 loads into it during the last k-step) and makes stage s + 1
-  // readable (its first fragments are read during the last k-step).
-  auto run_stage = [&](int s, bool next, bool dma) __device__ {
-    const int slot = s & 1;
+
+  // Ring of kGemmStages = 5 slots; stage s lives in slot s % 5. Stage s's first k-step
+  // fragments are read before it starts (buffer (KS s) % 2). Its k-steps issue the loads of
+  // stage s + 4 into slot (s + 4) % 5, which every wave finished reading before the barrier of
+  // stage s - 1. Before its last k-step, once this wave's reads of stage s are done and stage
+  // s + 1 has landed, one barrier lets stage s + 1 be read (its first fragments are read
+  // during the last k-step) and frees slot s % 5. At that barrier the loads issued after
+  // stage s + 1's are those of stages s + 2, s + 3 and the first KS - 1 k-steps of stage s + 4.
+  const int nst = nkt * (kGemmKB / kGemmSK);  // even
+  auto run_stage = [&](int s, int slot, auto parity, auto dma, auto next) __device__ {
+    constexpr int P = decltype(parity)::value;
+    const int ld_slot = slot == 0 ? kGemmStages - 1 : slot - 1;
+    const int nslot = slot == kGemmStages - 1 ? 0 : slot + 1;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
+      const int buf = (P * KS + ks) & 1;
+      const int q0 = ks * (8 / KS);
       if (ks + 1 < KS) {
-        read_frags(slot, ks + 1, (ks + 1) & 1);
-        mfmas(ks & 1, 0, 0, false);
+        mfmas(buf, decltype(dma)::value, s + 4, ld_slot, q0, [&]() __device__ { read_frags(slot, ks + 1, buf ^ 1); });
+      } else if constexpr (decltype(next)::value) {
+        if (decltype(dma)::value) wait_vm_lds<16 + 4 * (KS - 1)>();
+        else wait_vm_lds<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of stage s are done
+        bare_barrier();
+        mfmas(buf, decltype(dma)::value, s + 4, ld_slot, q0, [&]() __device__ { read_frags(nslot, 0, buf ^ 1); });
       } else {
-        if (next) {
-          wait_vm_lds<0>();  // stage s + 1 has landed (nothing later is in flight)
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of slot s are done
-          bare_barrier();
-          read_frags(slot ^ 1, 0, 0);
-        }
-        mfmas(ks & 1, s + 2, slot, dma);
+        mfmas(buf, decltype(dma)::value, s + 4, ld_slot, q0, []() __device__ {});
       }
     }
   };
+  using T = std::true_type;
+  using F = std::false_type;
 
-  const int nst = nkt;  // stages of 128 bytes of K
-  // prologue: stages 0 and 1 in flight, stage 0's first fragments read
+  // prologue: stages 0..3 in flight, stage 0's first fragments read
 #pragma unroll
-  for (int q = 0; q < 16; ++q) load_part(0, 0, q);
-  if (nst > 1) {
+  for (int st = 0; st < 4; ++st) {
+    if (st < nst) {
 #pragma unroll
-    for (int q = 0; q < 16; ++q) load_part(1, 1, q);
-    wait_vm_lds<16>();
-  } else {
-    wait_vm_lds<0>();
+      for (int q = 0; q < 8; ++q) load_part(st, st, q);
+    }
   }
+  if (nst >= 4) wait_vm_lds<24>();
+  else wait_vm_lds<0>();
   bare_barrier();
   read_frags(0, 0, 0);
-  int s = 0;
-  for (; s + 2 < nst; ++s) run_stage(s, true, true);
-  if (s + 1 < nst) run_stage(s++, true, false);
-  run_stage(s, false, false);
+  // stages in pairs (so that the fragment buffer parity is static); the last two pairs issue
+  // no loads and the very last stage has no successor
+  int s = 0, slot = 0;
+  auto adv = [&]() __device__ { slot = slot == kGemmStages - 1 ? 0 : slot + 1; ++s; };
+  for (; s + 4 < nst;) {
+    run_stage(s, slot, std::integral_constant<int, 0>{}, T{}, T{});
+    adv();
+    run_stage(s, slot, std::integral_constant<int, 1>{}, T{}, T{});
+    adv();
+  }
+  for (; s + 2 < nst;) {
+    run_stage(s, slot, std::integral_constant<int, 0>{}, F{}, T{});
+    adv();
+    run_stage(s, slot, std::integral_constant<int, 1>{}, F{}, T{});
+    adv();
+  }
+  run_stage(s, slot, std::integral_constant<int, 0>{}, F{}, T{});
+  adv();
+  run_stage(s, slot, std::integral_constant<int, 1>{}, F{}, F{});
 
   // epilogue, specialised on the output type, activation and accumulation (one uniform
   // branch here instead of per-element tests); the ring's LDS is reused for staging
