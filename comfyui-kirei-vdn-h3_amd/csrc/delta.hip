@@ -152,132 +152,90 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
 }
 
 // ---------------------------------------------------------------------------------------
-// factor. grid = n matrices, 256 threads. Each thread keeps an (D/16) x (D/16) sub-block of the
-// working matrix in registers (a 16 x 16 grid of sub-blocks); column / row j of each step is
-// broadcast through LDS. Cholesky and the triangular inverse are right-looking rank-1
-// sweeps; M = W^T W and J = B M run on v_mfma_f32_32x32x2_f32.
+// factor. grid = n matrices, 256 threads. M = (I + A)^-1 by the symmetric sweep operator: the
+// working matrix S starts as I + A and is swept on pivots k = 0 .. D-1,
+//   d = S[k][k];  S[i][l] -= S[i][k] S[k][l] / d;  S[i][k] = S[k][i] = S[i][k] / d;  S[k][k] = -1 / d
+// (i, l != k), which leaves S = -(I + A)^-1 and keeps S symmetric throughout. Pivot k is the
+// k-th leading Schur complement - the square of Cholesky's L[k][k] - so the first pivot that
+// is not positive marks the leading minor of order k + 1 that is not positive-definite, the
+// condition the reference's Cholesky reports. Each thread keeps a (D/16) x (D/16) sub-block of
+// S in registers (a 16 x 16 grid of sub-blocks); column k of each step is broadcast through a
+// double-buffered LDS line (one barrier per pivot). Then Phi = diag(alpha) M from registers and
+// J = B M on v_mfma_f32_32x32x2_f32.
 template <int D>
 __global__ __launch_bounds__(256) void factor_kernel(const float *__restrict__ A, const float *__restrict__ B,
                                                      const float *__restrict__ alpha, float *__restrict__ Phi,
                                                      float *__restrict__ J, float j_scale, int *__restrict__ info) {
   constexpr int SB = D / 16, PITCH = D + 1, NBW = D / 64;  // NBW: 32x32 blocks per wave side
   __shared__ float Lb[D * PITCH];
-  __shared__ float bcast[2][D];
+  __shared__ __attribute__((aligned(16))) float bcast[2][D];
   const int mat = blockIdx.x, tid = threadIdx.x;
-  const int i0 = (tid >> 4) * SB, k0 = (tid & 15) * SB;
+  const int ib = tid >> 4, kb0 = tid & 15;  // sub-block row / column of this thread
+  const int i0 = ib * SB, k0 = kb0 * SB;
   const float *Am = A + (int64_t)mat * D * D;
 
-  float M[SB][SB];
+  float S[SB][SB];
 #pragma unroll
   for (int a = 0; a < SB; ++a)
 #pragma unroll
-    for (int b = 0; b < SB; ++b) M[a][b] = Am[(i0 + a) * D + k0 + b] + ((i0 + a) == (k0 + b) ? 1.f : 0.f);
+    for (int b = 0; b < SB; ++b) S[a][b] = Am[(i0 + a) * D + k0 + b] + ((i0 + a) == (k0 + b) ? 1.f : 0.f);
 
   int fail = 0;
-  for (int j = 0; j < D; ++j) {
-    float *col = bcast[j & 1];
+  for (int kb = 0; kb < 16 && !fail; ++kb) {
 #pragma unroll
-    for (int b = 0; b < SB; ++b)
-      if (k0 + b == j) {
+    for (int b = 0; b < SB; ++b) {
+      const int k = kb * SB + b;
+      float *col = bcast[k & 1];
+      if (kb0 == kb) {
 #pragma unroll
-        for (int a = 0; a < SB; ++a) col[i0 + a] = M[a][b];
+        for (int a = 0; a < SB; ++a) col[i0 + a] = S[a][b];
       }
-    __syncthreads();
-    const float d = col[j];
-    if (!(d > 0.f)) {
-      fail = j + 1;
-      break;
+      __syncthreads();
+      const float d = col[k];
+      if (!(d > 0.f)) {  // uniform: every thread reads the same pivot
+        fail = k + 1;
+        break;
+      }
+      const float rd = 1.f / d;
+      float ci[SB], ck[SB];
+#pragma unroll
+      for (int a = 0; a < SB; ++a) ci[a] = col[i0 + a] * rd;
+#pragma unroll
+      for (int c = 0; c < SB; ++c) ck[c] = col[k0 + c];
+#pragma unroll
+      for (int a = 0; a < SB; ++a)
+#pragma unroll
+        for (int c = 0; c < SB; ++c) S[a][c] = fmaf(-ci[a], ck[c], S[a][c]);
+      // row and column k: S[i][k] = S[k][i] = S[i][k] / d, S[k][k] = -1 / d
+      if (kb0 == kb) {
+#pragma unroll
+        for (int a = 0; a < SB; ++a) S[a][b] = ci[a];
+      }
+      if (ib == kb) {
+#pragma unroll
+        for (int c = 0; c < SB; ++c) S[b][c] = ck[c] * rd;
+        if (kb0 == kb) S[b][b] = -rd;
+      }
     }
-    const float ljj = sqrtf(d);
-    float li[SB], lk[SB];
-#pragma unroll
-    for (int a = 0; a < SB; ++a) li[a] = (i0 + a > j) ? col[i0 + a] / ljj : 0.f;
-#pragma unroll
-    for (int b = 0; b < SB; ++b) lk[b] = (k0 + b > j) ? col[k0 + b] / ljj : 0.f;
-    if ((tid & 15) == 0) {
-#pragma unroll
-      for (int a = 0; a < SB; ++a) Lb[j * PITCH + i0 + a] = (i0 + a > j) ? li[a] : (i0 + a == j ? ljj : 0.f);
-    }
-#pragma unroll
-    for (int a = 0; a < SB; ++a)
-#pragma unroll
-      for (int b = 0; b < SB; ++b) M[a][b] -= li[a] * lk[b];
   }
   if (tid == 0) info[mat] = fail;
-  __syncthreads();
 
-  // W = L^-1 (lower): W = I; for each j: W[j,:] /= L[j][j]; W[i,:] -= L[i][j] W[j,:] for i > j
-#pragma unroll
-  for (int a = 0; a < SB; ++a)
-#pragma unroll
-    for (int b = 0; b < SB; ++b) M[a][b] = (i0 + a) == (k0 + b) ? 1.f : 0.f;
-  if (!fail) {
-    for (int j = 0; j < D; ++j) {
-      float *row = bcast[j & 1];
-      const float ljj = Lb[j * PITCH + j];
-#pragma unroll
-      for (int a = 0; a < SB; ++a)
-        if (i0 + a == j) {
-#pragma unroll
-          for (int b = 0; b < SB; ++b) {
-            M[a][b] = M[a][b] / ljj;
-            row[k0 + b] = M[a][b];
-          }
-        }
-      __syncthreads();
-      float lij[SB], wj[SB];
-#pragma unroll
-      for (int a = 0; a < SB; ++a) lij[a] = (i0 + a > j) ? Lb[j * PITCH + i0 + a] : 0.f;
-#pragma unroll
-      for (int b = 0; b < SB; ++b) wj[b] = row[k0 + b];
-#pragma unroll
-      for (int a = 0; a < SB; ++a)
-#pragma unroll
-        for (int b = 0; b < SB; ++b) M[a][b] -= lij[a] * wj[b];
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int a = 0; a < SB; ++a)
-#pragma unroll
-    for (int b = 0; b < SB; ++b) Lb[(i0 + a) * PITCH + k0 + b] = M[a][b];
-  __syncthreads();
-
-  // Minv = W^T W: C[a][b] = sum_s W[s][a] W[s][b]; lane group g contracts over rows s = 2*step + g
-  const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
-  const int wm = (wave >> 1) * 32 * NBW, wn = (wave & 1) * 32 * NBW;
-  f32x16_t acc[NBW][NBW];
-#pragma unroll
-  for (int i = 0; i < NBW; ++i)
-#pragma unroll
-    for (int j = 0; j < NBW; ++j) acc[i][j] = f32x16_t{};
-  for (int s = 0; s < D / 2; ++s) {
-    const int kappa = 2 * s + g;
-    float av[NBW], bv[NBW];
-#pragma unroll
-    for (int i = 0; i < NBW; ++i) {
-      av[i] = Lb[kappa * PITCH + wm + 32 * i + l32];
-      bv[i] = Lb[kappa * PITCH + wn + 32 * i + l32];
-    }
-#pragma unroll
-    for (int i = 0; i < NBW; ++i)
-#pragma unroll
-      for (int j = 0; j < NBW; ++j) acc[i][j] = mfma_f32_32x32x2(av[i], bv[j], acc[i][j]);
-  }
-  __syncthreads();
+  // M = -S: Phi = diag(alpha) M straight from registers, M into LDS for J = B M
   float *Pm = Phi ? Phi + (int64_t)mat * D * D : nullptr;
   const float *al = alpha ? alpha + (int64_t)mat * D : nullptr;
 #pragma unroll
-  for (int i = 0; i < NBW; ++i)
+  for (int a = 0; a < SB; ++a) {
+    const float sa = al ? -al[i0 + a] : -1.f;
 #pragma unroll
-    for (int j = 0; j < NBW; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), n = wn + 32 * j + l32;
-        Lb[m * PITCH + n] = acc[i][j][r];
-        if (Pm) Pm[m * D + n] = (al ? al[m] : 1.f) * acc[i][j][r];
-      }
+    for (int c = 0; c < SB; ++c) {
+      Lb[(i0 + a) * PITCH + k0 + c] = -S[a][c];
+      if (Pm) Pm[(i0 + a) * D + k0 + c] = sa * S[a][c];
+    }
+  }
   __syncthreads();
+  const int wave = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int wm = (wave >> 1) * 32 * NBW, wn = (wave & 1) * 32 * NBW;
+  f32x16_t acc[NBW][NBW];
 
   // J = B Minv: lane group g contracts over k in [g*D/2, (g+1)*D/2); B rows stream from memory
   const float *Bm = B + (int64_t)mat * D * D;
@@ -485,34 +443,77 @@ __global__ __launch_bounds__(256, 1) void readout_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
-__global__ void frame_mean_kernel(const uint16_t *__restrict__ x, int64_t x_row, int T, int hidden,
-                                  float *__restrict__ out) {
-  const int f = blockIdx.x, col = blockIdx.y * 256 + threadIdx.x;
-  if (col >= hidden) return;
-  const uint16_t *p = x + (int64_t)f * T * x_row + col;
-  float s = 0.f;
-  for (int t = 0; t < T; ++t) s += bf2f(p[(int64_t)t * x_row]);
-  out[(int64_t)f * hidden + col] = s / (float)T;
+// frame means: grid (frames, hidden / 256), 256 threads = 32 column groups of 8 columns x 8
+// token lanes; token lane l sums tokens l, l + 8, ... with 16-byte loads, the 8 partial sums
+// of a column are added in LDS. hidden and the row stride are multiples of 8 (host check).
+__global__ __launch_bounds__(256) void frame_mean_kernel(const uint16_t *__restrict__ x, int64_t x_row, int T,
+                                                         int hidden, float *__restrict__ out) {
+  __shared__ float part[8][257];
+  const int f = blockIdx.x, tid = threadIdx.x, cg = tid & 31, tl = tid >> 5;
+  const int col = blockIdx.y * 256 + cg * 8;
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (col < hidden) {
+    const uint16_t *p = x + (int64_t)f * T * x_row + col;
+    int t = tl;
+    for (; t + 24 < T; t += 32) {
+      u32x4_t r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) r[u] = ld16(p + (int64_t)(t + 8 * u) * x_row);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s[j] += bf2f(uint16_t((j & 1) ? (r[u][j >> 1] >> 16) : (r[u][j >> 1] & 0xffffu)));
+    }
+    for (; t < T; t += 8) {
+      const u32x4_t r = ld16(p + (int64_t)t * x_row);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[j] += bf2f(uint16_t((j & 1) ? (r[j >> 1] >> 16) : (r[j >> 1] & 0xffffu)));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) part[tl][cg * 8 + j] = s[j];
+  __syncthreads();
+  const int c = blockIdx.y * 256 + tid;
+  if (c < hidden) {
+    float v = 0.f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) v += part[l][tid];
+    out[(int64_t)f * hidden + c] = v / (float)T;
+  }
 }
 
-// out[m][n] = sum_k x[m][k] W[n][k] (+ bias[n]) in fp32; one thread per output element
-__global__ void linear_f32_kernel(const float *__restrict__ x, int64_t x_row, const void *__restrict__ w, int w_bf16,
-                                  int64_t w_row, const float *__restrict__ bias, float *__restrict__ out,
-                                  int64_t out_row, int M, int N, int K) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= (int64_t)M * N) return;
-  const int m = (int)(e / N), n = (int)(e - (int64_t)m * N);
-  const float *xr = x + (int64_t)m * x_row;
-  float s = 0.f;
-  if (w_bf16) {
-    const uint16_t *wr = static_cast<const uint16_t *>(w) + (int64_t)n * w_row;
-    for (int k = 0; k < K; ++k) s = fmaf(xr[k], bf2f(wr[k]), s);
-  } else {
-    const float *wr = static_cast<const float *>(w) + (int64_t)n * w_row;
-    for (int k = 0; k < K; ++k) s = fmaf(xr[k], wr[k], s);
+// out[m][n] = sum_k x[m][k] W[n][k] (+ bias[n]) in fp32 (the small alpha projections: few rows,
+// K up to the hidden size). One wavefront per output column n: lanes stride K so that the rows
+// of x and W are read coalesced, eight rows of x at a time, then a butterfly sum over lanes.
+template <bool WBF16>
+__global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict__ x, int64_t x_row,
+                                                         const void *__restrict__ w, int64_t w_row,
+                                                         const float *__restrict__ bias, float *__restrict__ out,
+                                                         int64_t out_row, int M, int N, int K) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (n >= N) return;  // the whole wavefront leaves; no workgroup barrier follows
+  const float bn = bias ? bias[n] : 0.f;
+  for (int m0 = 0; m0 < M; m0 += 8) {
+    const float *xr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xr[i] = x + (int64_t)min(m0 + i, M - 1) * x_row;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k = lane; k < K; k += 64) {
+      const float wk = WBF16 ? bf2f(static_cast<const uint16_t *>(w)[(int64_t)n * w_row + k])
+                             : static_cast<const float *>(w)[(int64_t)n * w_row + k];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = fmaf(xr[i][k], wk, acc[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) acc[i] += __shfl_xor(acc[i], o);
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (m0 + i < M) out[(int64_t)(m0 + i) * out_row + n] = acc[i] + bn;
+    }
   }
-  if (bias) s = s + bias[n];
-  out[(int64_t)m * out_row + n] = s;
 }
 
 // alpha[f][h][d] = exp(-exp(a_log[h]) * softplus(delta[f][h*D + d]))  (torch softplus, threshold 20)
@@ -648,6 +649,8 @@ extern "C" int vdnh3_frame_mean(const uint16_t *x, int64_t x_row, int frames, in
                                 void *stream) {
   VDNH3_HOST_CHECK(x && out && frames > 0 && tokens > 0 && hidden > 0, VDNH3_ERR_INVALID,
                    "frame_mean: empty or null operand");
+  VDNH3_HOST_CHECK(hidden % 8 == 0 && x_row % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, VDNH3_ERR_INVALID,
+                   "frame_mean: hidden and the row stride must be multiples of 8, x 16-byte aligned");
   hipLaunchKernelGGL(vdnh3::frame_mean_kernel, dim3(frames, (hidden + 255) / 256), dim3(256), 0,
                      static_cast<hipStream_t>(stream), x, x_row, tokens, hidden, out);
   return check_launch("frame_mean");
@@ -656,9 +659,13 @@ extern "C" int vdnh3_frame_mean(const uint16_t *x, int64_t x_row, int frames, in
 extern "C" int vdnh3_linear_f32(const float *x, int64_t x_row, const void *w, int w_bf16, int64_t w_row,
                                 const float *bias, float *out, int64_t out_row, int M, int N, int K, void *stream) {
   VDNH3_HOST_CHECK(x && w && out && M > 0 && N > 0 && K > 0, VDNH3_ERR_INVALID, "linear_f32: empty or null operand");
-  const int64_t total = (int64_t)M * N;
-  hipLaunchKernelGGL(vdnh3::linear_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, x_row, w, w_bf16, w_row, bias, out, out_row, M, N, K);
+  const dim3 grid((unsigned)((N + 3) / 4));
+  if (w_bf16)
+    hipLaunchKernelGGL(vdnh3::linear_f32_kernel<true>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x, x_row,
+                       w, w_row, bias, out, out_row, M, N, K);
+  else
+    hipLaunchKernelGGL(vdnh3::linear_f32_kernel<false>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x,
+                       x_row, w, w_row, bias, out, out_row, M, N, K);
   return check_launch("linear_f32");
 }
 
