@@ -20,13 +20,42 @@ namespace {
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
 
+// True when fp32 value y lies within 32 ulp of a bf16 rounding midpoint (its low 16 bits
+// near 0x8000): only there can an approximation with a smaller error round differently.
+__device__ __forceinline__ bool near_bf16_midpoint(float y) {
+  return ((__float_as_uint(y) & 0xffffu) - 0x7fe0u) < 0x40u;
+}
+
+// bf16(SiLU(x)) as fp32, bit-identical to round_bf(silu_f(x)): the hardware exp2 / reciprocal
+// form is within ~15 ulp of x / (1 + e^-x) for |x| <= 16 (argument rounding of -x log2(e),
+// v_exp_f32, 1 + e, v_rcp_f32, the product), so it rounds to the same bf16 value unless it
+// lies near a midpoint; those values and |x| > 16 take the exact expression.
+__device__ __forceinline__ float silu_bf(float x) {
+  const float y = x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+  if (__builtin_expect(fabsf(x) > 16.f || near_bf16_midpoint(y), 0)) return round_bf(silu_f(x));
+  return round_bf(y);
+}
+
+// bf16(s / n) as fp32, bit-identical to round_bf(s / n); rn = 1 / n (correctly rounded), so
+// s * rn is within 1.5 ulp of the quotient.
+__device__ __forceinline__ float div_bf(float s, float n, float rn) {
+  const float y = s * rn;
+  if (__builtin_expect(near_bf16_midpoint(y), 0)) return round_bf(s / n);
+  return round_bf(y);
+}
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 __device__ __forceinline__ f32x16_t mfma_f32_32x32x2(float a, float b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------------------
 // frame statistics. grid = frames * heads, 256 threads. Tokens are consumed in tiles of 32,
-// stored transposed ([d][t]) in LDS so both MFMA operands read 8 consecutive tokens.
+// stored transposed ([d][t]) in LDS so both MFMA operands read 8 consecutive tokens; the LDS
+// tiles are double-buffered (one barrier per tile) and each tile's raw k / v / beta are loaded
+// into registers while the previous tile's features are formed and multiplied.
 // A's operand beta*k~ (exact in fp32: a product of two bf16 values) is split into
 // hi = bf16(x) and lo = x - hi, both exact bf16, so A = hi^T k~ + lo^T k~ carries every bit.
 template <int D>
@@ -37,13 +66,9 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
                                                              float *__restrict__ A_out, float *__restrict__ B_out) {
   constexpr int TT = 32, P = TT + 8, CH = D / 8, NB = D / 64;
   constexpr int TILE = D * P;
-  constexpr int TILE_BYTES = 4 * TILE * 2, SYM_BYTES = D * (D + 1) * 4;
-  constexpr int LDS_BYTES = TILE_BYTES > SYM_BYTES ? TILE_BYTES : SYM_BYTES;
+  constexpr int BUF_BYTES = 4 * TILE * 2, SYM_BYTES = D * (D + 1) * 4;
+  constexpr int LDS_BYTES = 2 * BUF_BYTES > SYM_BYTES ? 2 * BUF_BYTES : SYM_BYTES;
   __shared__ __attribute__((aligned(16))) uint8_t smem[LDS_BYTES];
-  uint16_t *Kt = reinterpret_cast<uint16_t *>(smem);
-  uint16_t *Xh = Kt + TILE;
-  uint16_t *Xl = Xh + TILE;
-  uint16_t *Vb = Xl + TILE;
 
   const int fh = blockIdx.x, f = fh / heads, h = fh - f * heads;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
@@ -58,45 +83,60 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
 #pragma unroll
     for (int j = 0; j < NB; ++j) accA[i][j] = accB[i][j] = f32x16_t{};
 
-  for (int t0 = 0; t0 < T; t0 += TT) {
+  // raw operands of one tile for this loader thread: tokens t0 + 2p, t0 + 2p + 1
+  u32x4_t kr[2], vr[2];
+  float br[2];
+  auto load_raw = [&](int t0) __device__ {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int t = t0 + 2 * p + e;
+      kr[e] = vr[e] = u32x4_t{0, 0, 0, 0};
+      br[e] = 0.f;
+      if (loader && t < T) {
+        const int64_t off = (row0 + t) * kv_row + (int64_t)h * kv_head + 8 * c;
+        kr[e] = ld16(k + off);
+        vr[e] = ld16(v + off);
+        br[e] = bf2f(beta[(row0 + t) * beta_row + h]);
+      }
+    }
+  };
+
+  load_raw(0);
+  int buf = 0;
+  for (int t0 = 0; t0 < T; t0 += TT, buf ^= 1) {
+    uint16_t *Kt = reinterpret_cast<uint16_t *>(smem + buf * BUF_BYTES);
+    uint16_t *Xh = Kt + TILE;
+    uint16_t *Xl = Xh + TILE;
+    uint16_t *Vb = Xl + TILE;
     if (loader) {
+      // features of this tile from the registers, then the next tile's loads
       uint32_t kk[2][8], xh[2][8], xl[2][8], vb[2][8];
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        const int t = t0 + 2 * p + e;
-        const bool valid = t < T;
-        u32x4_t kr = u32x4_t{0, 0, 0, 0}, vr = u32x4_t{0, 0, 0, 0};
-        float b = 0.f;
-        if (valid) {
-          const int64_t off = (row0 + t) * kv_row + (int64_t)h * kv_head + 8 * c;
-          kr = ld16(k + off);
-          vr = ld16(v + off);
-          b = bf2f(beta[(row0 + t) * beta_row + h]);
-        }
-        float s[8], sumsq = 0.f;
+        float sv[8], sumsq = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const uint32_t w = kr[j >> 1];
-          const float x = __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
-          s[j] = round_bf(silu_f(x));
-          sumsq += s[j] * s[j];
+          const uint32_t w = kr[e][j >> 1];
+          sv[j] = silu_bf((j & 1) ? bf_hi(w) : bf_lo(w));
+          sumsq += sv[j] * sv[j];
         }
 #pragma unroll
         for (int o = 1; o < CH; o <<= 1) sumsq += __shfl_xor(sumsq, o);
-        const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f);
+        const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f), rn = 1.f / nrm;
+        const float b = br[e];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float kt = round_bf(s[j] / nrm);
+          const float kt = div_bf(sv[j], nrm, rn);
           const float x = kt * b;  // exact
           const float hi = round_bf(x);
           kk[e][j] = f2bf(kt);
           xh[e][j] = f2bf(hi);
           xl[e][j] = f2bf(x - hi);
-          const uint32_t w = vr[j >> 1];
-          const float vx = __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
-          vb[e][j] = f2bf(round_bf(silu_f(vx)) * b);
+          const uint32_t w = vr[e][j >> 1];
+          vb[e][j] = f2bf(silu_bf((j & 1) ? bf_hi(w) : bf_lo(w)) * b);
         }
       }
+      if (t0 + TT < T) load_raw(t0 + TT);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int o = (8 * c + j) * P + 2 * p;
@@ -106,6 +146,8 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
         *reinterpret_cast<uint32_t *>(Vb + o) = vb[0][j] | (vb[1][j] << 16);
       }
     }
+    // one barrier: this tile is complete, and every wave is done with the buffer the next
+    // tile will overwrite (it was read two tiles ago, before the previous barrier)
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -127,8 +169,8 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
           accB[i][j] = mfma_bf16_32x32x16(av[i], bk[j], accB[i][j]);
         }
     }
-    __syncthreads();
   }
+  __syncthreads();  // the symmetrisation below reuses the tile buffers
 
   // A -> LDS, then 0.5 (A + A^T); B rounded to bf16 like the reference's bf16 matmul output
   float *S = reinterpret_cast<float *>(smem);
@@ -325,78 +367,129 @@ __global__ __launch_bounds__(64 * (D / 32)) void scan_kernel(const float *__rest
 }
 
 // ---------------------------------------------------------------------------------------
+// Running sums of log(alpha) over frames: out[i][h][d] = sum_{j < i} log(max(alpha[j][h][d],
+// 1e-12)), i = 0 .. F, summed in frame order (the decay factors of the readout are
+// differences of these). One thread per (h, d).
+__global__ void alpha_logsum_kernel(const float *__restrict__ alpha, float *__restrict__ out, int F, int hd) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= hd) return;
+  float lp = 0.f;
+  out[e] = 0.f;
+  for (int i = 0; i < F; ++i) {
+    lp += logf(fmaxf(alpha[(int64_t)i * hd + e], 1e-12f));
+    out[(int64_t)(i + 1) * hd + e] = lp;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // readout. grid = frames * heads, 256 threads; wavefronts take 32-token tiles in turn.
 //   L_f[v][k] = bf16(before[v][k] * decay_b[k] + after[v][k] * decay_a[k])   (LDS, [v][k])
 //   r^T = L_f q~^T on bf16 MFMA (lane = token, so the RMS over v is in-lane plus one exchange)
+// The normalised, weighted tile y (bf16) goes through a per-wavefront LDS stage so that the
+// gate is read and the output written as row-contiguous 16-byte pieces; the tile's gate rows
+// are loaded before its MFMAs, the next tile's q after its features.
 template <int D>
-__global__ __launch_bounds__(256, 1) void readout_kernel(
+__global__ __launch_bounds__(256, 2) void readout_kernel(
     const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const float *__restrict__ prefix,
-    const float *__restrict__ suffix, const float *__restrict__ alpha, const float *__restrict__ text,
+    const float *__restrict__ suffix, const float *__restrict__ logsum, const float *__restrict__ text,
     const int *__restrict__ bounds, int use_alpha, const uint16_t *__restrict__ norm_w,
     const uint16_t *__restrict__ gate, int64_t gate_row, uint16_t *__restrict__ out, int64_t out_row, int F, int T,
     int heads) {
-  constexpr int LP = D + 8, NS = D / 16, NO = D / 32;
+  constexpr int LP = D + 8, NS = D / 16, NO = D / 32, YP = D + 8, CPR = D / 8;  // CPR: 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;                                                  // rows per wave instruction
   __shared__ __attribute__((aligned(16))) uint16_t Ls[D * LP];
+  __shared__ __attribute__((aligned(16))) uint16_t Ys[4][32 * YP];
   __shared__ float dec[2][D];
+  __shared__ __attribute__((aligned(16))) uint16_t Wn[D];
   const int fh = blockIdx.x, f = fh / heads, h = fh - f * heads;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int lo = max(bounds[2 * f], 0), hi = min(bounds[2 * f + 1], F - 1);
   const bool has_b = lo - 1 >= 0, has_a = hi + 1 < F;
   const int bb = min(max(lo, 0), F), ba = min(max(hi + 1, 0), F);
   if (tid < D) {
-    float lp = 0.f, lp_f = 0.f, lp_f1 = 0.f, lp_bb = 0.f, lp_ba = 0.f;
-    for (int i = 0; i <= F; ++i) {
-      if (i == f) lp_f = lp;
-      if (i == f + 1) lp_f1 = lp;
-      if (i == bb) lp_bb = lp;
-      if (i == ba) lp_ba = lp;
-      if (i < F && use_alpha) lp += logf(fmaxf(alpha[((int64_t)i * heads + h) * D + tid], 1e-12f));
-    }
-    dec[0][tid] = use_alpha ? expf(lp_f1 - lp_bb) : 1.f;
-    dec[1][tid] = use_alpha ? expf(lp_ba - lp_f) : 1.f;
+    const int64_t hd = (int64_t)heads * D, e = (int64_t)h * D + tid;
+    dec[0][tid] = use_alpha ? expf(logsum[(f + 1) * hd + e] - logsum[bb * hd + e]) : 1.f;
+    dec[1][tid] = use_alpha ? expf(logsum[ba * hd + e] - logsum[f * hd + e]) : 1.f;
   }
-  __syncthreads();
   const float *before = has_b ? prefix + ((int64_t)(lo - 1) * heads + h) * D * D
                               : (text ? text + (int64_t)h * D * D : nullptr);
   const float *after = has_a ? suffix + ((int64_t)(hi + 1) * heads + h) * D * D
                              : (text ? text + (int64_t)h * D * D : nullptr);
-  for (int e = tid; e < D * D; e += 256) {
-    const int vv = e / D, kk = e - vv * D;
-    const float x = __fadd_rn(before ? __fmul_rn(before[e], dec[0][kk]) : 0.f,
-                              after ? __fmul_rn(after[e], dec[1][kk]) : 0.f);
-    Ls[vv * LP + kk] = f2bf(x);
+  // the two states in halves, each half's loads issued before any of its use (D * D / 4
+  // float4 per state, N4 per thread)
+  constexpr int N4 = D * D / 4 / 256, H4 = N4 > 8 ? 8 : N4;
+#pragma unroll
+  for (int u0 = 0; u0 < N4; u0 += H4) {
+    f32x4_t bv[H4], av[H4];
+#pragma unroll
+    for (int u = 0; u < H4; ++u) {
+      const int i4 = tid + 256 * (u0 + u);
+      bv[u] = before ? reinterpret_cast<const f32x4_t *>(before)[i4] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      av[u] = after ? reinterpret_cast<const f32x4_t *>(after)[i4] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    if (u0 == 0) __syncthreads();  // dec
+#pragma unroll
+    for (int u = 0; u < H4; ++u) {
+      const int e0 = 4 * (tid + 256 * (u0 + u)), vv = e0 / D, kk = e0 - vv * D;
+      float x[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        x[e] = __fadd_rn(before ? __fmul_rn(bv[u][e], dec[0][kk + e]) : 0.f,
+                         after ? __fmul_rn(av[u][e], dec[1][kk + e]) : 0.f);
+      *reinterpret_cast<u32x2_t *>(Ls + vv * LP + kk) = u32x2_t{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3])};
+    }
   }
+  if (tid < D / 4) *reinterpret_cast<u32x2_t *>(Wn + 4 * tid) = *reinterpret_cast<const u32x2_t *>(norm_w + 4 * tid);
   __syncthreads();
 
+  // q tiles: lane = token; the next tile's raw q is loaded after this tile's features
   const int ntiles = (T + 31) / 32;
+  auto q_ptr = [&](int tile) __device__ {
+    const int64_t row = (int64_t)f * T + min(tile * 32 + l32, T - 1);
+    return q + row * q_row + (int64_t)h * q_head + 8 * g;
+  };
+  u32x4_t raw[NS];
+  if (wave < ntiles) {
+    const uint16_t *qp = q_ptr(wave);
+#pragma unroll
+    for (int st = 0; st < NS; ++st) raw[st] = ld16(qp + 16 * st);
+  }
+  uint16_t *Yw = Ys[wave];
+  const int orow = lane / CPR, ochunk = lane % CPR;  // row-major pass: row it * RPI + orow, chunk ochunk
   for (int tile = wave; tile < ntiles; tile += 4) {
-    const int t = tile * 32 + l32;
-    const int64_t row = (int64_t)f * T + min(t, T - 1);
-    const uint16_t *qp = q + row * q_row + (int64_t)h * q_head + 8 * g;
-    // SiLU(q) is rounded to bf16 (the reference materialises it); it is evaluated twice, for
-    // the L2 norm and for the division, instead of keeping 64 values per lane live.
-    u32x4_t raw[NS];
+    // this tile's gate rows, row-major (used at the end of the tile)
+    u32x4_t gv[32 / RPI];
+#pragma unroll
+    for (int it = 0; it < 32 / RPI; ++it) {
+      const int t = min(tile * 32 + it * RPI + orow, T - 1);
+      gv[it] = ld16(gate + ((int64_t)f * T + t) * gate_row + (int64_t)h * D + 8 * ochunk);
+    }
+    // SiLU(q) rounded to bf16 (the reference materialises it), packed in pairs; its L2 norm
+    u32x4_t sq[NS];
     float sumsq = 0.f;
 #pragma unroll
-    for (int st = 0; st < NS; ++st) {
-      raw[st] = ld16(qp + 16 * st);
+    for (int st = 0; st < NS; ++st)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t w = raw[st][j >> 1];
-        const float sv = round_bf(silu_f(__uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16))));
-        sumsq += sv * sv;
+      for (int w = 0; w < 4; ++w) {
+        const float lo_ = silu_bf(bf_lo(raw[st][w])), hi_ = silu_bf(bf_hi(raw[st][w]));
+        sumsq += lo_ * lo_;
+        sumsq += hi_ * hi_;
+        sq[st][w] = pack_bf2(lo_, hi_);
       }
+    if (tile + 4 < ntiles) {
+      const uint16_t *qp = q_ptr(tile + 4);
+#pragma unroll
+      for (int st = 0; st < NS; ++st) raw[st] = ld16(qp + 16 * st);
     }
     sumsq += __shfl_xor(sumsq, 32);
-    const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f);
+    const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f), rn = 1.f / nrm;
     bf16x8_t qf[NS];
 #pragma unroll
     for (int st = 0; st < NS; ++st)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t w = raw[st][j >> 1];
-        const float sv = round_bf(silu_f(__uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16))));
-        qf[st][j] = __builtin_bit_cast(__bf16, f2bf(sv / nrm));
+      for (int w = 0; w < 4; ++w) {
+        qf[st][2 * w] = __builtin_bit_cast(__bf16, f2bf(div_bf(bf_lo(sq[st][w]), nrm, rn)));
+        qf[st][2 * w + 1] = __builtin_bit_cast(__bf16, f2bf(div_bf(bf_hi(sq[st][w]), nrm, rn)));
       }
     f32x16_t acc[NO];
 #pragma unroll
@@ -411,34 +504,44 @@ __global__ __launch_bounds__(256, 1) void readout_kernel(
     for (int mb = 0; mb < NO; ++mb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        acc[mb][r] = round_bf(acc[mb][r]);
-        ss += acc[mb][r] * acc[mb][r];
+        const float e = acc[mb][r];
+        const float rb = round_bf(e);
+        acc[mb][r] = rb;
+        ss += rb * rb;
       }
     ss += __shfl_xor(ss, 32);
     const float nv = sqrtf(ss);
     const float inv = round_bf(1.f / sqrtf(nv * nv / (float)D + 1e-6f));
-    if (t < T) {
-      const uint16_t *gp = gate + row * gate_row + (int64_t)h * D;
-      uint16_t *op = out + row * out_row + (int64_t)h * D;
+    // y = bf16(bf16(r * inv) * w) into the stage, row = token l32
 #pragma unroll
-      for (int mb = 0; mb < NO; ++mb)
+    for (int mb = 0; mb < NO; ++mb)
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const int v0 = 32 * mb + 8 * i4 + 4 * g;
-          const u32x2_t gw = *reinterpret_cast<const u32x2_t *>(gp + v0);
-          const u32x2_t nw = *reinterpret_cast<const u32x2_t *>(norm_w + v0);
-          float o[4];
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int v0 = 32 * mb + 8 * i4 + 4 * g;
+        const u32x2_t nw = *reinterpret_cast<const u32x2_t *>(Wn + v0);
+        float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t gg = gw[e >> 1], ww = nw[e >> 1];
-            const float gv = __uint_as_float((e & 1) ? (gg & 0xffff0000u) : (gg << 16));
-            const float wv = __uint_as_float((e & 1) ? (ww & 0xffff0000u) : (ww << 16));
-            const float y = round_bf(round_bf(acc[mb][4 * i4 + e] * inv) * wv);
-            o[e] = y * gv;
-          }
-          *reinterpret_cast<u32x2_t *>(op + v0) = u32x2_t{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t ww = nw[e >> 1];
+          y[e] = round_bf(acc[mb][4 * i4 + e] * inv) * ((e & 1) ? bf_hi(ww) : bf_lo(ww));
         }
+        *reinterpret_cast<u32x2_t *>(Yw + l32 * YP + v0) = u32x2_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
+      }
+    asm volatile("" ::: "memory");  // LDS operations of one wavefront complete in order
+    // out = y * gate, row-major 16-byte pieces
+#pragma unroll
+    for (int it = 0; it < 32 / RPI; ++it) {
+      const int tt = it * RPI + orow, t = tile * 32 + tt;
+      const u32x4_t yv = *reinterpret_cast<const u32x4_t *>(Yw + tt * YP + 8 * ochunk);
+      if (t < T) {
+        u32x4_t o;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          o[w] = pack_bf2(bf_lo(yv[w]) * bf_lo(gv[it][w]), bf_hi(yv[w]) * bf_hi(gv[it][w]));
+        *reinterpret_cast<u32x4_t *>(out + ((int64_t)f * T + t) * out_row + (int64_t)h * D + 8 * ochunk) = o;
+      }
     }
+    asm volatile("" ::: "memory");
   }
 }
 
@@ -621,27 +724,42 @@ extern "C" int vdnh3_delta_scan(const float *phi, const float *jay, const float 
   return check_launch("delta_scan");
 }
 
+extern "C" int vdnh3_alpha_logsum(const float *alpha, int frames, int heads, int head_dim, float *out, void *stream) {
+  VDNH3_HOST_CHECK(alpha && out && frames > 0 && heads > 0 && head_dim > 0, VDNH3_ERR_INVALID,
+                   "alpha_logsum: empty or null operand");
+  const int hd = heads * head_dim;
+  hipLaunchKernelGGL(vdnh3::alpha_logsum_kernel, dim3((hd + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     alpha, out, frames, hd);
+  return check_launch("alpha_logsum");
+}
+
 extern "C" int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, const float *prefix,
-                             const float *suffix, const float *alpha, const float *text_state, const int32_t *bounds,
+                             const float *suffix, const float *alpha_logsum, const float *text_state,
+                             const int32_t *bounds,
                              int use_alpha, const uint16_t *norm_w, const uint16_t *gate, int64_t gate_row,
                              uint16_t *out, int64_t out_row, int frames, int tokens, int heads, int head_dim,
                              void *stream) {
   int rc = check_dim(head_dim);
   if (rc) return rc;
-  VDNH3_HOST_CHECK(q && prefix && suffix && alpha && bounds && norm_w && gate && out && frames > 0 && tokens > 0,
+  VDNH3_HOST_CHECK(q && prefix && suffix && (alpha_logsum || !use_alpha) && bounds && norm_w && gate && out &&
+                       frames > 0 && tokens > 0,
                    VDNH3_ERR_INVALID, "readout: empty or null operand");
   VDNH3_HOST_CHECK(q_row % 8 == 0 && q_head % 8 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
-                       gate_row % 4 == 0 && out_row % 4 == 0 && reinterpret_cast<uintptr_t>(gate) % 8 == 0 &&
-                       reinterpret_cast<uintptr_t>(out) % 8 == 0 && reinterpret_cast<uintptr_t>(norm_w) % 8 == 0,
-                   VDNH3_ERR_INVALID, "readout: misaligned q / gate / out / norm weight");
+                       gate_row % 8 == 0 && out_row % 8 == 0 && reinterpret_cast<uintptr_t>(gate) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(out) % 16 == 0 && reinterpret_cast<uintptr_t>(norm_w) % 8 == 0 &&
+                       reinterpret_cast<uintptr_t>(prefix) % 16 == 0 && reinterpret_cast<uintptr_t>(suffix) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(text_state) % 16 == 0,
+                   VDNH3_ERR_INVALID, "readout: misaligned q / gate / out / norm weight / states");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(frames * heads);
   if (head_dim == 128)
-    hipLaunchKernelGGL(vdnh3::readout_kernel<128>, grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix, alpha,
-                       text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames, tokens, heads);
+    hipLaunchKernelGGL(vdnh3::readout_kernel<128>, grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix,
+                       alpha_logsum, text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames,
+                       tokens, heads);
   else
-    hipLaunchKernelGGL(vdnh3::readout_kernel<64>, grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix, alpha,
-                       text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames, tokens, heads);
+    hipLaunchKernelGGL(vdnh3::readout_kernel<64>, grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix,
+                       alpha_logsum, text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames,
+                       tokens, heads);
   return check_launch("readout");
 }
 

@@ -60,6 +60,7 @@ SIGNATURES = {
     "vdnh3_linear_f32": (_c_int, [_vp, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_i64, _c_int, _c_int, _c_int,
                                   _vp]),
     "vdnh3_alpha_decay": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "vdnh3_alpha_logsum": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "vdnh3_fill_rows_bf16": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_float, _vp]),
     "vdnh3_qk_rmsnorm": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _c_float,
                                   _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp]),

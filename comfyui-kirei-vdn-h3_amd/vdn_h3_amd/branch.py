@@ -281,8 +281,19 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
     text = None if text_state is None else text_state.float().contiguous()
     if out is None:
         out = torch.empty((rows, heads * dim), dtype=torch.bfloat16, device=device)
-    rc = _lib.lib().vdnh3_readout(_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), _lib.ptr(prefix),
-                                  _lib.ptr(suffix), _lib.ptr(alpha.contiguous()), _lib.ptr(text), _lib.ptr(bounds_t),
+    if out.stride(-1) != 1 or out.stride(0) % 8 or out.data_ptr() % 16:
+        raise ValueError("out must have contiguous, 16-byte aligned rows")
+    if gate.stride(0) % 8 or gate.data_ptr() % 16:
+        gate = gate.contiguous()
+    logsum = None
+    if bridge == "alpha":
+        alpha = alpha.float().contiguous()
+        logsum = torch.empty((num_frames + 1, heads, dim), dtype=torch.float32, device=device)
+        rc = _lib.lib().vdnh3_alpha_logsum(_lib.ptr(alpha), num_frames, heads, dim, _lib.ptr(logsum),
+                                           _lib.stream_handle(device))
+        _lib.check(rc, "vdnh3_alpha_logsum")
+    rc = _lib.lib().vdnh3_readout(_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), _lib.ptr(prefix.contiguous()),
+                                  _lib.ptr(suffix.contiguous()), _lib.ptr(logsum), _lib.ptr(text), _lib.ptr(bounds_t),
                                   int(bridge == "alpha"), _lib.ptr(norm_w), _lib.ptr(gate), gate.stride(0),
                                   _lib.ptr(out), out.stride(0), num_frames, tokens_per_frame, heads, dim,
                                   _lib.stream_handle(device))

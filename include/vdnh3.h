@@ -198,16 +198,26 @@ int vdnh3_delta_scan(const float *phi, const float *jay, const float *init, floa
                      int frames, int heads, int head_dim, void *stream);
 
 /*
+ * Running sums of the log decay over frames (vdn_h3/branch.py:372-396, the cumulative
+ * log(alpha) of the bridge): out[i][h][d] = sum_{j<i} log(max(alpha[j][h][d], 1e-12)), i = 0..frames,
+ * summed in frame order. alpha: [frames][heads][D] fp32; out: [frames+1][heads][D] fp32.
+ */
+int vdnh3_alpha_logsum(const float *alpha, int frames, int heads, int head_dim, float *out, void *stream);
+
+/*
  * Gather + readout + epilogue (vdn_h3/branch.py:372-396, vdn_h3/runtime.py:406-419,
  * vdn_h3/branch.py:494-505), q~ = L2(SiLU(q)) fused in. For frame f with bounds
  * lo = max(bounds[2f], 0), hi = min(bounds[2f+1], frames-1):
  *   L_f = bf16(before * decay_b + after * decay_a)  (before = prefix[lo-1] or text_state or 0,
- *         after = suffix[hi+1] or text_state or 0, decays from cumulated log(alpha) when use_alpha)
+ *         after = suffix[hi+1] or text_state or 0; when use_alpha, decay_b = exp(S[f+1] - S[lo])
+ *         and decay_a = exp(S[hi+1] - S[f]) with S = alpha_logsum)
  *   r = bf16(q~ L_f^T);  out[row][h*D + v] = bf16(RMSNorm(r)[v] * norm_w[v]) * gate[row][h*D + v]
- * alpha: [frames][heads][D] fp32; out and gate: [frames*tokens, heads*D] bf16.
+ * alpha_logsum: [frames+1][heads][D] fp32 from vdnh3_alpha_logsum (may be NULL without use_alpha);
+ * out and gate: [frames*tokens, heads*D] bf16 with 16-byte aligned rows; prefix, suffix and
+ * text_state 16-byte aligned.
  */
 int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, const float *prefix,
-                  const float *suffix, const float *alpha, const float *text_state, const int32_t *bounds,
+                  const float *suffix, const float *alpha_logsum, const float *text_state, const int32_t *bounds,
                   int use_alpha, const uint16_t *norm_w, const uint16_t *gate, int64_t gate_row,
                   uint16_t *out, int64_t out_row, int frames, int tokens, int heads, int head_dim,
                   void *stream);
