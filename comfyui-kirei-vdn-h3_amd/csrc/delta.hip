@@ -84,26 +84,27 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
     for (int j = 0; j < NB; ++j) accA[i][j] = accB[i][j] = f32x16_t{};
 
   // raw operands of one tile for this loader thread: tokens t0 + 2p, t0 + 2p + 1
-  u32x4_t kr[2], vr[2];
-  float br[2];
-  auto load_raw = [&](int t0) __device__ {
+  struct Raw {
+    u32x4_t k[2], v[2];
+    float b[2];
+  };
+  auto load_raw = [&](Raw &r, int t0) __device__ {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int t = t0 + 2 * p + e;
-      kr[e] = vr[e] = u32x4_t{0, 0, 0, 0};
-      br[e] = 0.f;
+      r.k[e] = r.v[e] = u32x4_t{0, 0, 0, 0};
+      r.b[e] = 0.f;
       if (loader && t < T) {
         const int64_t off = (row0 + t) * kv_row + (int64_t)h * kv_head + 8 * c;
-        kr[e] = ld16(k + off);
-        vr[e] = ld16(v + off);
-        br[e] = bf2f(beta[(row0 + t) * beta_row + h]);
+        r.k[e] = ld16(k + off);
+        r.v[e] = ld16(v + off);
+        r.b[e] = bf2f(beta[(row0 + t) * beta_row + h]);
       }
     }
   };
-
-  load_raw(0);
-  int buf = 0;
-  for (int t0 = 0; t0 < T; t0 += TT, buf ^= 1) {
+  // LDS tile layout [d][token]: 8-token group tg of row d sits at group slot tg ^ ((d / 8) % 4),
+  // which spreads the transposed writes of one instruction over 4x more banks
+  auto tile_step = [&](Raw &r, int t0, int buf) __device__ {
     uint16_t *Kt = reinterpret_cast<uint16_t *>(smem + buf * BUF_BYTES);
     uint16_t *Xh = Kt + TILE;
     uint16_t *Xl = Xh + TILE;
@@ -116,14 +117,14 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
         float sv[8], sumsq = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const uint32_t w = kr[e][j >> 1];
+          const uint32_t w = r.k[e][j >> 1];
           sv[j] = silu_bf((j & 1) ? bf_hi(w) : bf_lo(w));
           sumsq += sv[j] * sv[j];
         }
 #pragma unroll
         for (int o = 1; o < CH; o <<= 1) sumsq += __shfl_xor(sumsq, o);
         const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f), rn = 1.f / nrm;
-        const float b = br[e];
+        const float b = r.b[e];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float kt = div_bf(sv[j], nrm, rn);
@@ -132,14 +133,15 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
           kk[e][j] = f2bf(kt);
           xh[e][j] = f2bf(hi);
           xl[e][j] = f2bf(x - hi);
-          const uint32_t w = vr[e][j >> 1];
+          const uint32_t w = r.v[e][j >> 1];
           vb[e][j] = f2bf(silu_bf((j & 1) ? bf_hi(w) : bf_lo(w)) * b);
         }
       }
-      if (t0 + TT < T) load_raw(t0 + TT);
+      if (t0 + TT < T) load_raw(r, t0 + TT);
+      const int col = 8 * ((p >> 2) ^ (c & 3)) + 2 * (p & 3);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int o = (8 * c + j) * P + 2 * p;
+        const int o = (8 * c + j) * P + col;
         *reinterpret_cast<uint32_t *>(Kt + o) = kk[0][j] | (kk[1][j] << 16);
         *reinterpret_cast<uint32_t *>(Xh + o) = xh[0][j] | (xh[1][j] << 16);
         *reinterpret_cast<uint32_t *>(Xl + o) = xl[0][j] | (xl[1][j] << 16);
@@ -149,16 +151,18 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
     // one barrier: this tile is complete, and every wave is done with the buffer the next
     // tile will overwrite (it was read two tiles ago, before the previous barrier)
     __syncthreads();
+    const int sw = (l32 >> 3) & 3;  // rows 32 i + l32 share (row / 8) % 4
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
+      const int slot = 8 * ((2 * ks + g) ^ sw);
       bf16x8_t ah[NB], al[NB], av[NB], bk[NB];
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
-        const int ro = (wm + 32 * i + l32) * P + 16 * ks + 8 * g;
+        const int ro = (wm + 32 * i + l32) * P + slot;
         ah[i] = as_bf16x8(ld16(Xh + ro));
         al[i] = as_bf16x8(ld16(Xl + ro));
         av[i] = as_bf16x8(ld16(Vb + ro));
-        bk[i] = as_bf16x8(ld16(Kt + (wn + 32 * i + l32) * P + 16 * ks + 8 * g));
+        bk[i] = as_bf16x8(ld16(Kt + (wn + 32 * i + l32) * P + slot));
       }
 #pragma unroll
       for (int i = 0; i < NB; ++i)
@@ -169,7 +173,12 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
           accB[i][j] = mfma_bf16_32x32x16(av[i], bk[j], accB[i][j]);
         }
     }
-  }
+  };
+
+  Raw r;
+  load_raw(r, 0);
+  int buf = 0;
+  for (int t0 = 0; t0 < T; t0 += TT, buf ^= 1) tile_step(r, t0, buf);
   __syncthreads();  // the symmetrisation below reuses the tile buffers
 
   // A -> LDS, then 0.5 (A + A^T); B rounded to bf16 like the reference's bf16 matmul output
