@@ -92,19 +92,6 @@ __device__ __forceinline__ float other_half(float x) {
   return __uint_as_float(lane < 32 ? r[1] : r[0]);
 }
 
-// Order of one MFMA phase (32 LDS fragment reads, 32 MFMAs): eight reads ahead, then one read
-// per MFMA, so each MFMA's operand was requested about eight MFMAs (~250 cycles) earlier.
-__device__ __forceinline__ void mfma_phase_schedule() {
-  constexpr int kMfma = 0x008, kDsRead = 0x100;
-  __builtin_amdgcn_sched_group_barrier(kDsRead, 8, 0);
-#pragma unroll
-  for (int i = 0; i < 24; ++i) {
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
-}
-
 // ---------------------------------------------------------------------------------
 // Two-group ping-pong over the key tiles t = 0..T-1 of a work item (256 query rows of one head).
 // Waves 0-3 (group A) and 4-7 (group B) each own 32 query rows; wave w and w + 4 share a SIMD.
@@ -113,9 +100,10 @@ __device__ __forceinline__ void mfma_phase_schedule() {
 //   MFMA phase of tile t :  O^T += V(t-1)^T P(t-1)^T   and   S(t)^T = K(t) Q^T      (32 MFMAs)
 //   VALU phase of tile t :  P(t) = exp2(scale S(t) - m), row max / sum, O rescale   (softmax)
 // Group A runs tile t's MFMA phase in phase 2t and its VALU phase in 2t+1; group B one phase
-// later. K(t) and V(t-1) are read in phases 2t and 2t+1 only; tiles are loaded (direct to LDS,
-// every thread) into four-slot rings three tiles ahead, which hides HBM latency for the tiles
-// that miss L2.
+// later. K(t) and V(t-1) are read in phases 2t and 2t+1 only; tiles are loaded direct to LDS
+// into four-slot rings, K tiles by group A three tiles ahead and V^T tiles by group B two tiles
+// ahead, each between the MFMAs of the issuing group's MFMA phase (the VALU group issues no
+// memory operations), which hides HBM latency for the tiles that miss L2.
 template <int D>
 __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
     const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const uint16_t *__restrict__ k, int64_t k_row,
@@ -125,10 +113,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   constexpr int KC = D / 8;    // 16-byte chunks per K row
   constexpr int NS = D / 16;   // k-steps of the QK^T contraction
   constexpr int NO = D / 32;   // 32-row blocks of O^T
-  constexpr int KCH = kBN * KC / kThreads;  // 16-byte K chunks per thread and tile
-  constexpr int VCH = D * 8 / kThreads;     // 16-byte V^T chunks per thread and tile
   constexpr int KT = kBN * D, VT = D * kBN;  // elements per tile
-  static_assert(KCH >= 1 && VCH >= 1, "every thread loads at least one chunk of each tile");
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kRing][KT];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kRing][VT];
 
@@ -154,34 +139,44 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
 
   const uint16_t *kbase = k + (int64_t)head * k_head;
   const uint16_t *vbase = vt + (int64_t)head * D * s_pad;
-  // Tile loads: LDS position P of a K tile is (row P / KC, slot P % KC) and holds chunk
-  // slot ^ swizzle(row) of that key row (likewise for V^T with 8 chunks per d-row). Thread chunk
-  // i covers row kr0 + i * kBN / KCH; the swizzle depends on the row only through bits that are
-  // the same for every i, so one 32-bit lane offset serves all chunks.
-  const int kr0 = tid / KC, vd0 = tid >> 3;
-  const uint32_t koff = (uint32_t)(kr0 * k_row + k_slot<D>(kr0, tid % KC) * 8);
-  const uint32_t voff = (uint32_t)(vd0 * s_pad + v_slot(vd0, tid & 7) * 8);
-  auto load_k = [&](int t, uint16_t *dst) __device__ {
-    const int ks = tiles[toff + t].x;
-    if (ks + kBN <= seq) {
-      const uint16_t *src = kbase + (int64_t)ks * k_row;
+  // Tile loads, by one group of 256 threads: LDS position P of a K tile is (row P / KC, slot
+  // P % KC) and holds chunk slot ^ swizzle(row) of that key row (likewise for V^T with 8 chunks
+  // per d-row). Thread chunk i covers row kr0 + i * kBN / KCG; the swizzle depends on the row
+  // only through bits that are the same for every i. Rows past seq read row seq - 1 (their
+  // scores are masked).
+  constexpr int KCG = kBN * KC / 256, VCG = D * 8 / 256;  // 16-byte chunks per thread and tile
+  static_assert(KCG >= 1 && VCG >= 1 && KCG == VCG, "both groups issue the same number of loads");
+  const int gtid = tid & 255, gw = wave & 3;
+  const int kr0 = gtid / KC, vd0 = gtid >> 3;
+  const int kslot = k_slot<D>(kr0, gtid % KC) * 8;
+  // per-lane element offsets of this group's chunks inside a tile's source rows (K rows for
+  // group A, V^T rows for group B), the tile's LDS base of this wavefront, and the per-tile
+  // source stride: the issue inside the MFMA stream is one 64-bit add, a scalar M0 and the load
+  int doff[KCG];
 #pragma unroll
-      for (int i = 0; i < KCH; ++i)
-        global_to_lds16(src + (int64_t)i * (kBN / KCH) * k_row + koff, dst + (i * kThreads + wave * 64) * 8);
-    } else {  // last tile of the sequence: clamp rows to seq - 1 (their scores are masked)
+  for (int i = 0; i < KCG; ++i)
+    doff[i] = group == 0 ? (kr0 + i * (kBN / KCG)) * (int)k_row + kslot
+                         : (vd0 + i * (D / VCG)) * s_pad + v_slot(vd0, gtid & 7) * 8;
+  const uint32_t lds_dma = __builtin_amdgcn_readfirstlane(
+      (group == 0 ? lds_address(&Ks[0][0]) : lds_address(&Vs[0][0])) + gw * 64 * 16);
+  constexpr uint32_t kTileBytes = KT * 2;
+  static_assert(KT == VT, "K and V^T tiles have the same size");
+  // sources of this thread's chunks of the tile whose first key is ks; the last K tile of the
+  // sequence reads rows past seq as row seq - 1 (their scores are masked)
+  auto tile_srcs = [&](int ks, const uint16_t *(&src)[KCG]) __device__ {
+    const uint16_t *base = group == 0 ? kbase + (int64_t)ks * k_row : vbase + ks;
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) {
-        const int r = kr0 + i * (kBN / KCH);
-        global_to_lds16(kbase + (int64_t)min(ks + r, seq - 1) * k_row + k_slot<D>(r, tid % KC) * 8,
-                        dst + (i * kThreads + wave * 64) * 8);
+    for (int i = 0; i < KCG; ++i) src[i] = base + doff[i];
+    if (__builtin_amdgcn_readfirstlane(ks + kBN > seq)) {  // uniform: skipped except for the last tile
+      if (group == 0) {
+#pragma unroll
+        for (int i = 0; i < KCG; ++i)
+          src[i] = kbase + (int64_t)min(ks + kr0 + i * (kBN / KCG), seq - 1) * k_row + kslot;
       }
     }
   };
-  auto load_v = [&](int t, uint16_t *dst) __device__ {
-    const uint16_t *src = vbase + tiles[toff + t].x;
-#pragma unroll
-    for (int i = 0; i < VCH; ++i)
-      global_to_lds16(src + (int64_t)i * (D / VCH) * s_pad + voff, dst + (i * kThreads + wave * 64) * 8);
+  auto dma_kv = [&](const uint16_t *src, int slot, int i) __device__ {
+    global_to_lds16_at(src, lds_dma + (uint32_t)slot * kTileBytes + (uint32_t)(i * 256 * 16));
   };
 
   // Fragment offsets inside a tile (elements). The swizzles depend on the row only through
@@ -201,111 +196,142 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   float m_run = -INFINITY, l_run = 0.f;
 
   // Rings: K(tau) and V(tau) live in slot tau % kRing. K(t) and V(t-1) are read in phases 2t
-  // and 2t+1. Phase 2t issues K(t+kRing-1) (over K(t-1)) and V(t+kRing-2) (over V(t-2)), both
-  // last read in phase 2t-1, so each load has 2(kRing-1) phases to land. Past the end the tile
-  // index is clamped to T-1: such loads rewrite slots that no real tile reads any more, and
-  // every even phase issues the same number of loads, which keeps the vmcnt wait exact.
-  constexpr int kLoadsPerIssue = KCH + VCH;
-  // prologue: K(0..kRing-2), V(0..kRing-3) landed; V(-1), the V^T slot read by the PV of tile 0
-  // (with P(-1) = 0), is zeroed so that product is exactly zero
+  // (group A) and 2t+1 (group B). Group A issues K(t+kRing-1) in phase 2t, over K(t-1); group
+  // B issues V(t+kRing-2) in phase 2t+1, over V(t-2); both slots were last read before the
+  // barrier that ended phase 2t-1. Past the end the tile index is clamped to T-1: such loads
+  // rewrite slots that no real tile reads any more, and every issue has the same count, so
+  // each group's vmcnt wait at the end of odd phases is exact.
+  // prologue: K(0..kRing-2) by group A, V(0..kRing-3) by group B, all landed; V(-1), the V^T
+  // slot read by the PV of tile 0 (with P(-1) = 0), is zeroed so that product is exactly zero
 #pragma unroll
-  for (int j = 0; j < kRing - 1; ++j) load_k(min(j, T - 1), Ks[j]);
+  for (int j = 0; j < kRing - 1; ++j) {
+    if (j < kRing - 2 || group == 0) {
+      const uint16_t *src[KCG];
+      tile_srcs(tiles[toff + min(j, T - 1)].x, src);
 #pragma unroll
-  for (int j = 0; j < kRing - 2; ++j) load_v(min(j, T - 1), Vs[j]);
+      for (int i = 0; i < KCG; ++i) dma_kv(src[i], j, i);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < VT / 8 / kThreads; ++i)
     st16(Vs[kRing - 1] + (i * kThreads + tid) * 8, u32x4_t{0, 0, 0, 0});
   wait_vm_lds<0>();
   bare_barrier();
 
+  // Tile descriptors are scalar loads made one or two phases before their use: the DMA key
+  // start of this group's next issue and the mask bounds of its next VALU phase.
+  // (readfirstlane: a provably uniform index keeps the descriptor loads scalar)
+  const int dma_ahead = __builtin_amdgcn_readfirstlane(group == 0 ? kRing - 1 : kRing - 2);
+  int dma_ks = tiles[toff + min(dma_ahead, T - 1)].x;
+  int mask = 0;
+
   const int phases = 2 * T + 2;
   for (int p = 0; p < phases; ++p) {
-    if ((p & 1) == 0) {  // all threads: issue K(t+kRing-1), V(t+kRing-2) for t = p / 2
-      const int t = p >> 1;
-      load_k(min(t + kRing - 1, T - 1), Ks[(t + kRing - 1) % kRing]);
-      load_v(min(t + kRing - 2, T - 1), Vs[(t + kRing - 2) % kRing]);
-    }
     // Group A (B) works on the matrix cores in even (odd) phases. Both tile indices depend on
-    // p only, so tile descriptors are scalar loads: a per-lane load would make the compiler
-    // wait for every in-flight tile load before using it.
+    // p only, so tile descriptors are scalar loads.
     const int t_mfma = p >> 1;            // A: p = 2t; B: p = 2t + 1
     const int t_valu = (p - 1) >> 1;      // A: p = 2t + 1 (odd); B: p = 2t + 2 (even)
     if (group == (p & 1)) {
-      // MFMA phase of tile t
-      const int t = t_mfma;
+      // MFMA phase of tile t: O^T += V(t-1)^T P(t-1)^T, S(t)^T = K(t) Q^T (16 + 16 MFMAs at D = 128).
       // t = 0 has no PV and t = T no QK: those phases run on a zero tile / discard the scores,
-      // so the phase is one branch-free block whose LDS reads can run well ahead of the MFMAs
-      {
-        const uint16_t *vtile = Vs[(t + kRing - 1) % kRing];
+      // so the phase is one branch-free block. Fragment reads run eight MFMAs ahead; this
+      // group's tile loads sit between the MFMAs.
+      const int t = t_mfma;
+      const int ld_slot = (t + dma_ahead) & (kRing - 1);
+      const uint16_t *src[KCG];
+      tile_srcs(dma_ks, src);
+      const uint16_t *vtile = Vs[(t + kRing - 1) & (kRing - 1)];
+      const uint16_t *ktile = Ks[t & (kRing - 1)];
+      // MFMA i < NP: PV block m = i % NO, k-step tt = i / NO; i >= NP: QK block kb = (i - NP) % 2,
+      // k-step st = (i - NP) / 2. Consecutive MFMAs update different accumulators, so none waits
+      // for the result of the one before it.
+      constexpr int NP = NO * 4, NM = NP + 2 * NS, EVERY = NM / KCG;
+      auto frag = [&](int i) __device__ {
+        return i < NP ? ld16(vtile + (i % NO) * 32 * kBN + vfo[i / NO])
+                      : ld16(ktile + ((i - NP) & 1) * 32 * D + kfo[(i - NP) >> 1]);
+      };
+      // the MFMA wave of each SIMD issues ahead of the VALU wave sharing it
+      __builtin_amdgcn_s_setprio(1);
+      u32x4_t fr[8];
 #pragma unroll
-        for (int m = 0; m < NO; ++m)
+      for (int i = 0; i < 8; ++i) fr[i] = frag(i);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
-            oacc[m] = mfma_bf16_32x32x16(as_bf16x8(ld16(vtile + m * 32 * kBN + vfo[tt])), pb[tt], oacc[m]);
-      }
-      {
-        const uint16_t *ktile = Ks[t % kRing];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          sacc[kb] = f32x16_t{};
-#pragma unroll
-          for (int st = 0; st < NS; ++st)
-            sacc[kb] = mfma_bf16_32x32x16(as_bf16x8(ld16(ktile + kb * 32 * D + kfo[st])), qf[st], sacc[kb]);
+      for (int i = 0; i < NM; ++i) {
+        const u32x4_t a = fr[i & 7];
+        if (i < NP) {
+          oacc[i % NO] = mfma_bf16_32x32x16(as_bf16x8(a), pb[i / NO], oacc[i % NO]);
+        } else {
+          const int kb = (i - NP) & 1, st = (i - NP) >> 1;
+          if (st == 0) sacc[kb] = f32x16_t{};
+          sacc[kb] = mfma_bf16_32x32x16(as_bf16x8(a), qf[st], sacc[kb]);
         }
+        if (i + 8 < NM) fr[i & 7] = frag(i + 8);
+        if (i % EVERY == EVERY / 2) dma_kv(src[i / EVERY], ld_slot, i / EVERY);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      mfma_phase_schedule();
-    } else if (p >= 1 + group && t_valu < T) {
+      __builtin_amdgcn_s_setprio(0);
+      // descriptors for this group's next issue (two phases on) and next VALU phase
+      dma_ks = tiles[toff + min(t + 1 + dma_ahead, T - 1)].x;
+      mask = t < T ? tiles[toff + t].y : 0;
+    } else {
       // VALU phase of tile t: softmax in base 2, one query per lane. The running max m_run moves
       // only when this tile's max exceeds it by more than 2^kLazy: probabilities stay below
       // 2^kLazy (exact softmax either way, a common shift cancels in O / l) and most tiles skip
       // the rescale.
-      const int packed = tiles[toff + t_valu].y;
-      const int lo = packed & 0xffff, hi = packed >> 16;
-      if (lo > 0 || hi < kBN) {
+      const bool work = p >= 1 + group && t_valu < T;
+      float mt = 0.f;
+      if (work) {
+        const int lo = mask & 0xffff, hi = mask >> 16;
+        if (lo > 0 || hi < kBN) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int ko = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
+              if (ko < lo || ko >= hi) sacc[kb][i] = -INFINITY;
+            }
+        }
+        // tile row max: a balanced tree over the lane's 32 scores (depth 5 instead of a 32-long
+        // chain), then the other half-wave's value through v_permlane32_swap (no LDS round trip)
+        float mx[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx[i] = fmaxf(sacc[0][i], sacc[1][i]);
+#pragma unroll
+        for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+          for (int i = 0; i < w; ++i) mx[i] = fmaxf(mx[i], mx[i + w]);
+        mt = fmaxf(mx[0], other_half(mx[0])) * scale_log2;
+      }
+      if (work) {
+        const bool grow = mt > m_run + kLazy;
+        if (__any(grow)) {
+          const float m_new = grow ? mt : m_run;
+          const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+          m_run = m_new;
+          l_run *= corr;
+#pragma unroll
+          for (int m = 0; m < NO; ++m) oacc[m] *= corr;
+        }
+        float rs[4] = {0.f, 0.f, 0.f, 0.f};  // four partial sums: short dependency chains
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            const int ko = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
-            if (ko < lo || ko >= hi) sacc[kb][i] = -INFINITY;
+            const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i], scale_log2, -m_run));
+            rs[i & 3] += pv;
+            pb[2 * kb + (i >> 3)][i & 7] = (__bf16)pv;
           }
+        l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
       }
-      // tile row max: a balanced tree over the lane's 32 scores (depth 5 instead of a 32-long
-      // chain), then the other half-wave's value through v_permlane32_swap (no LDS round trip)
-      float mx[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx[i] = fmaxf(sacc[0][i], sacc[1][i]);
-#pragma unroll
-      for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-        for (int i = 0; i < w; ++i) mx[i] = fmaxf(mx[i], mx[i + w]);
-      float mt = fmaxf(mx[0], other_half(mx[0])) * scale_log2;
-      const bool grow = mt > m_run + kLazy;
-      if (__any(grow)) {
-        const float m_new = grow ? mt : m_run;
-        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        l_run *= corr;
-#pragma unroll
-        for (int m = 0; m < NO; ++m) oacc[m] *= corr;
-      }
-      float rs[4] = {0.f, 0.f, 0.f, 0.f};  // four partial sums: short dependency chains
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i], scale_log2, -m_run));
-          rs[i & 3] += pv;
-          pb[2 * kb + (i >> 3)][i & 7] = (__bf16)pv;
-        }
-      l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
     }
-    // before an even phase 2(t+1): K(t+1) and V(t) (issued kRing - 1 issue phases ago) have
-    // landed; the loads of the last kRing - 2 issue phases may still be in flight
-    if (p & 1) wait_vm_lds<(kRing - 2) * kLoadsPerIssue>();
+    // before an even phase 2(t+1): K(t+1) and V(t) (issued kRing - 1 issues ago by their group)
+    // have landed; each group's two latest issues may still be in flight
+    if (p & 1) wait_vm_lds<(kRing - 2) * KCG>();
     bare_barrier();
   }
 
+  wait_vm_lds<0>();  // no tile load may land in LDS after the workgroup ends
   l_run += other_half(l_run);
   const float inv = 1.f / l_run;
   if (qr < q1) {
