@@ -298,7 +298,7 @@ def bench_gemm(args, torch, device):
                    "scales": "per-token x per-channel" if kind_name == "i8" else "per-tensor", "ops_per_step": ops},
         "roofline": {"bound": "mfma", "kernel": f"gemm_nt_kernel<{kind_name}>", "achieved": round(tops, 2),
                      "peak": peak, "unit": "TOP/s", "frac": round(tops / peak, 4), "kernel_ms": round(gemm_ms, 4),
-                     "traffic": None},
+                     "traffic": _traffic(args.traffic_json, f"gemm_nt_kernel<{kind_name}>:{which}")},
         "breakdown_ms": {"activation_quant": round(quant_ms, 4), "gemm": round(gemm_ms, 4),
                          "activation_quant_GBs": round(qbytes / (quant_ms * 1e-3) / 1e9, 1)},
     }

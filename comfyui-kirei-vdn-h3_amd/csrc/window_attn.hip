@@ -5,7 +5,7 @@
 // optional fused per-head sigmoid gate (vdn_h3/hybrid.py:518-529).
 //
 // Work decomposition
-//   one workgroup = 4 wavefronts = 128 query rows of one head x the key tiles of its run;
+//   one workgroup = 8 wavefronts = 256 query rows of one head x the key tiles of its run;
 //   each wavefront owns 32 query rows and keeps its Q fragment in registers.
 //   Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16: every lane
 //   then owns one query column (lane % 32) and 16+16 of the 64 keys of a tile, so the row
@@ -13,12 +13,14 @@
 //   MFMA (O^T += V^T P^T) straight from registers, without an LDS round trip.
 //   V^T is read from a head-major copy made by a pre-pass (one extra 2*S*H*D-byte sweep),
 //   stored with keys interleaved in 16-key groups so that each lane's 8 MFMA k-values are
-//   one 16-byte LDS read.
+//   one 16-byte LDS read. K and V^T tiles go straight from HBM/L2 to LDS rings
+//   (global_load_lds_dwordx4); the two halves of the workgroup alternate between the matrix
+//   cores and the VALU (see window_attn_kernel).
 //
 // Scheduling
 //   work items (query block, head) are ordered longest-first per head, and the flat
 //   workgroup index is remapped so that each XCD (workgroups are dealt round-robin over
-//   the 8 XCDs) runs a contiguous slice of that order: the ~64 resident workgroups of an
+//   the 8 XCDs) runs a contiguous slice of that order: the resident workgroups of an
 //   XCD work on the same head and neighbouring query blocks, so their K/V tiles are
 //   shared in that XCD's L2.
 #include "common.h"
