@@ -51,6 +51,9 @@ def _parse():
                                                              "gemm_i8_out", "gemm_f8_qkv", "gemm_f8_out"],
                     help="hbm_copy: a plain 1 GiB device copy, the reference point for scaling rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes")
+    ap.add_argument("--short-conv", default="k,v",
+                    help="branch short-convolution targets of the block / branch workloads (the released "
+                         "checkpoints convolve k and v); '' for none")
     ap.add_argument("--cpu-sample-rows", type=int, default=2048,
                     help="query rows of the CPU-oracle baseline sample (0 disables it)")
     ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "traffic.json"),
@@ -171,12 +174,17 @@ def _time_steps(torch, stream, steps, warmup, fn):
     return t0.elapsed_time(t1) / steps
 
 
-def block_flops(lay, heads, dim, hidden, pairs_per_head):
+def _short_conv(args):
+    return tuple(t for t in args.short_conv.split(",") if t)
+
+
+def block_flops(lay, heads, dim, hidden, pairs_per_head, short_conv=()):
     """Algorithmic work of one hybrid block (int8 OPs of the W8A8 GEMMs + bf16/fp32 FLOPs), by stage."""
     s, inner = lay.seq_len, heads * dim
     fi = lay.num_frames - 2 if lay.anchor_frames == "both" else lay.num_frames
     r, t = fi * lay.tokens_per_frame, lay.tokens_per_frame
     return {
+        "branch_short_conv": len(short_conv) * 2.0 * (25 + 5) * r * inner,
         "qkv_proj": 2.0 * s * hidden * 3 * inner,
         "softmax_gate": 2.0 * s * hidden * heads,
         "window_attention": 4.0 * dim * heads * pairs_per_head,
@@ -208,9 +216,10 @@ def bench_block(args, torch, device):
         out_proj=HipLinear(synth.randn((hidden, heads * dim), 2, device, torch.bfloat16, 0.02), "int8"),
         q_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), 3, device)).to(torch.bfloat16), eps=1e-6),
         k_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), 4, device)).to(torch.bfloat16), eps=1e-6))
-    (bw,), _ = projection.prepare_projection_maps([synth.branch_weights(heads, dim, hidden, device=device)],
-                                                  device, "int8")
-    branch = OptimizedLinearBranch(bw, heads, dim)
+    conv = _short_conv(args)
+    (bw,), _ = projection.prepare_projection_maps(
+        [synth.branch_weights(heads, dim, hidden, device=device, short_conv=conv)], device, "int8")
+    branch = OptimizedLinearBranch(bw, heads, dim, short_conv=conv)
     state = VDNState("bench", {"enable_softmax_gate": True, "linear_enabled": True, "enable_text_state": True},
                      [branch], heads, dim, projection_precision="int8", diagnostics=True)
     forward = make_vdn_forward(attn, state, 0)
@@ -230,7 +239,7 @@ def bench_block(args, torch, device):
     stages = {k: v["mean_ms"] for k, v in state.diagnostics.snapshot()["stages"].items()}
     plan = state.window_cache.plan(lay.seq_len, lay.video_start, lay.video_end, lay.num_frames,
                                    lay.tokens_per_frame, lay.bounds, lay.anchor_frames, device)
-    work = block_flops(lay, heads, dim, hidden, plan.pairs_per_head)
+    work = block_flops(lay, heads, dim, hidden, plan.pairs_per_head, conv)
     total = sum(work.values())
     attn_ms = stages["attention.softmax.kernel"]
     attn_tflops = work["window_attention"] / (attn_ms * 1e-3) / 1e12
@@ -247,6 +256,7 @@ def bench_block(args, torch, device):
                    "tokens_per_frame": lay.tokens_per_frame, "text_rows": lay.text_len, "chunk": w.chunk,
                    "radius": w.radius, "anchor_frames": lay.anchor_frames,
                    "projections": "W8A8 int8 qkv/out/to_out_linear (per-token x per-channel)",
+                   "branch_short_conv": ",".join(conv) or "none",
                    "allowed_pairs_per_head": plan.pairs_per_head, "work_per_step": work,
                    "work_total": total},
         "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128>", "achieved": round(attn_tflops, 2),
@@ -314,12 +324,14 @@ def bench_branch(args, torch, device):
     seq = text + frames * tpf
     qkv = synth.fused_qkv(seq, heads, dim, device=device, seed=40)
     x = synth.randn((seq, hidden), 41, device=device, dtype=torch.bfloat16)
-    w = synth.branch_weights(heads, dim, hidden, device=device)
+    conv = _short_conv(args)
+    w = synth.branch_weights(heads, dim, hidden, device=device, short_conv=conv)
     q, k, v = synth.split_qkv(qkv, heads, dim)
     bounds = window_bounds(frames, 1, 5)
-    br = OptimizedLinearBranch(w, heads, dim)
+    br = OptimizedLinearBranch(w, heads, dim, short_conv=conv)
     out = torch.empty((frames * tpf, hidden), dtype=torch.bfloat16, device=device)
-    kw = dict(text_x=x[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True, out=out)
+    kw = dict(frame_size=(48, 27), text_x=x[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True,
+              out=out)
     stream = torch.cuda.current_stream(device)
 
     def step():
@@ -331,14 +343,16 @@ def bench_branch(args, torch, device):
     core = fi * heads * (6.0 * tpf * dim * dim + (11.0 / 3.0) * dim ** 3 + 4.0 * dim ** 3)
     gates = 2.0 * r * hidden * dim + 2.0 * r * dim * heads * dim + 2.0 * r * hidden * heads
     proj = 2.0 * r * heads * dim * hidden
-    flops = core + gates + proj
+    conv_flops = len(conv) * 2.0 * (25 + 5) * r * heads * dim
+    flops = core + gates + proj + conv_flops
     tflops = flops / (ms * 1e-3) / 1e12
     return {
         "metric": "VDN delta-rule branch ms + TFLOP/s at 29 inner frames x 1296 tok x 40 heads, 1 GPU",
         "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
         "config": {"workload": "branch_f31_t1296_h40_d128", "frames": frames, "inner_frames": fi,
                    "tokens_per_frame": tpf, "text_rows": text, "heads": heads, "head_dim": dim, "hidden": hidden,
-                   "flop_core": core, "flop_gates": gates, "flop_to_out_linear": proj},
+                   "short_conv": ",".join(conv) or "none", "flop_core": core, "flop_gates": gates,
+                   "flop_short_conv": conv_flops, "flop_to_out_linear": proj},
         "roofline": {"bound": "mfma", "kernel": "projected_delta (all kernels)", "achieved": round(tflops, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": None},

@@ -58,12 +58,15 @@ __device__ __forceinline__ f32x16_t mfma_f32_32x32x2(float a, float b, f32x16_t 
 // into registers while the previous tile's features are formed and multiplied.
 // A's operand beta*k~ (exact in fp32: a product of two bf16 values) is split into
 // hi = bf16(x) and lo = x - hi, both exact bf16, so A = hi^T k~ + lo^T k~ carries every bit.
-template <int D>
-__global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__restrict__ k,
-                                                             const uint16_t *__restrict__ v, int64_t kv_row,
-                                                             int64_t kv_head, const uint16_t *__restrict__ beta,
-                                                             int64_t beta_row, int T, int heads,
-                                                             float *__restrict__ A_out, float *__restrict__ B_out) {
+// KF / VF: k / v already hold the features k~ / v~ (the output of the short convolutions),
+// so the feature map is not applied on load.
+template <int D, bool KF, bool VF>
+__global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__restrict__ k, int64_t k_row,
+                                                             int64_t k_head, const uint16_t *__restrict__ v,
+                                                             int64_t v_row, int64_t v_head,
+                                                             const uint16_t *__restrict__ beta, int64_t beta_row,
+                                                             int T, int heads, float *__restrict__ A_out,
+                                                             float *__restrict__ B_out) {
   constexpr int TT = 32, P = TT + 8, CH = D / 8, NB = D / 64;
   constexpr int TILE = D * P;
   constexpr int BUF_BYTES = 4 * TILE * 2, SYM_BYTES = D * (D + 1) * 4;
@@ -95,9 +98,8 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
       r.k[e] = r.v[e] = u32x4_t{0, 0, 0, 0};
       r.b[e] = 0.f;
       if (loader && t < T) {
-        const int64_t off = (row0 + t) * kv_row + (int64_t)h * kv_head + 8 * c;
-        r.k[e] = ld16(k + off);
-        r.v[e] = ld16(v + off);
+        r.k[e] = ld16(k + (row0 + t) * k_row + (int64_t)h * k_head + 8 * c);
+        r.v[e] = ld16(v + (row0 + t) * v_row + (int64_t)h * v_head + 8 * c);
         r.b[e] = bf2f(beta[(row0 + t) * beta_row + h]);
       }
     }
@@ -118,23 +120,29 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const uint32_t w = r.k[e][j >> 1];
-          sv[j] = silu_bf((j & 1) ? bf_hi(w) : bf_lo(w));
+          const float raw = (j & 1) ? bf_hi(w) : bf_lo(w);
+          sv[j] = KF ? raw : silu_bf(raw);
           sumsq += sv[j] * sv[j];
         }
+        float nrm = 1.f, rn = 1.f;
+        if (!KF) {
 #pragma unroll
-        for (int o = 1; o < CH; o <<= 1) sumsq += __shfl_xor(sumsq, o);
-        const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f), rn = 1.f / nrm;
+          for (int o = 1; o < CH; o <<= 1) sumsq += __shfl_xor(sumsq, o);
+          nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f);
+          rn = 1.f / nrm;
+        }
         const float b = r.b[e];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float kt = div_bf(sv[j], nrm, rn);
+          const float kt = KF ? sv[j] : div_bf(sv[j], nrm, rn);
           const float x = kt * b;  // exact
           const float hi = round_bf(x);
           kk[e][j] = f2bf(kt);
           xh[e][j] = f2bf(hi);
           xl[e][j] = f2bf(x - hi);
           const uint32_t w = r.v[e][j >> 1];
-          vb[e][j] = f2bf(silu_bf((j & 1) ? bf_hi(w) : bf_lo(w)) * b);
+          const float vr = (j & 1) ? bf_hi(w) : bf_lo(w);
+          vb[e][j] = f2bf((VF ? vr : silu_bf(vr)) * b);
         }
       }
       if (t0 + TT < T) load_raw(r, t0 + TT);
@@ -397,7 +405,8 @@ __global__ void alpha_logsum_kernel(const float *__restrict__ alpha, float *__re
 // The normalised, weighted tile y (bf16) goes through a per-wavefront LDS stage so that the
 // gate is read and the output written as row-contiguous 16-byte pieces; the tile's gate rows
 // are loaded before its MFMAs, the next tile's q after its features.
-template <int D>
+// QF: q already holds the features q~ (the output of a short convolution).
+template <int D, bool QF>
 __global__ __launch_bounds__(256, 2) void readout_kernel(
     const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const float *__restrict__ prefix,
     const float *__restrict__ suffix, const float *__restrict__ logsum, const float *__restrict__ text,
@@ -473,33 +482,43 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
       const int t = min(tile * 32 + it * RPI + orow, T - 1);
       gv[it] = ld16(gate + ((int64_t)f * T + t) * gate_row + (int64_t)h * D + 8 * ochunk);
     }
-    // SiLU(q) rounded to bf16 (the reference materialises it), packed in pairs; its L2 norm
-    u32x4_t sq[NS];
-    float sumsq = 0.f;
-#pragma unroll
-    for (int st = 0; st < NS; ++st)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float lo_ = silu_bf(bf_lo(raw[st][w])), hi_ = silu_bf(bf_hi(raw[st][w]));
-        sumsq += lo_ * lo_;
-        sumsq += hi_ * hi_;
-        sq[st][w] = pack_bf2(lo_, hi_);
-      }
-    if (tile + 4 < ntiles) {
-      const uint16_t *qp = q_ptr(tile + 4);
-#pragma unroll
-      for (int st = 0; st < NS; ++st) raw[st] = ld16(qp + 16 * st);
-    }
-    sumsq += __shfl_xor(sumsq, 32);
-    const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f), rn = 1.f / nrm;
     bf16x8_t qf[NS];
+    if (QF) {
 #pragma unroll
-    for (int st = 0; st < NS; ++st)
+      for (int st = 0; st < NS; ++st) qf[st] = as_bf16x8(raw[st]);
+      if (tile + 4 < ntiles) {
+        const uint16_t *qp = q_ptr(tile + 4);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        qf[st][2 * w] = __builtin_bit_cast(__bf16, f2bf(div_bf(bf_lo(sq[st][w]), nrm, rn)));
-        qf[st][2 * w + 1] = __builtin_bit_cast(__bf16, f2bf(div_bf(bf_hi(sq[st][w]), nrm, rn)));
+        for (int st = 0; st < NS; ++st) raw[st] = ld16(qp + 16 * st);
       }
+    } else {
+      // SiLU(q) rounded to bf16 (the reference materialises it), packed in pairs; its L2 norm
+      u32x4_t sq[NS];
+      float sumsq = 0.f;
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float lo_ = silu_bf(bf_lo(raw[st][w])), hi_ = silu_bf(bf_hi(raw[st][w]));
+          sumsq += lo_ * lo_;
+          sumsq += hi_ * hi_;
+          sq[st][w] = pack_bf2(lo_, hi_);
+        }
+      if (tile + 4 < ntiles) {
+        const uint16_t *qp = q_ptr(tile + 4);
+#pragma unroll
+        for (int st = 0; st < NS; ++st) raw[st] = ld16(qp + 16 * st);
+      }
+      sumsq += __shfl_xor(sumsq, 32);
+      const float nrm = fmaxf(round_bf(sqrtf(sumsq)), 1e-6f), rn = 1.f / nrm;
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          qf[st][2 * w] = __builtin_bit_cast(__bf16, f2bf(div_bf(bf_lo(sq[st][w]), nrm, rn)));
+          qf[st][2 * w + 1] = __builtin_bit_cast(__bf16, f2bf(div_bf(bf_hi(sq[st][w]), nrm, rn)));
+        }
+    }
     f32x16_t acc[NO];
 #pragma unroll
     for (int mb = 0; mb < NO; ++mb) {
@@ -672,24 +691,33 @@ using vdnh3::check_dim;
 using vdnh3::check_launch;
 using vdnh3::set_error;
 
-extern "C" int vdnh3_frame_stats(const uint16_t *k, const uint16_t *v, int64_t kv_row, int64_t kv_head,
-                                 const uint16_t *beta, int64_t beta_row, int frames, int tokens, int heads,
-                                 int head_dim, float *A, float *B, void *stream) {
+extern "C" int vdnh3_frame_stats(const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *v,
+                                 int64_t v_row, int64_t v_head, int features, const uint16_t *beta,
+                                 int64_t beta_row, int frames, int tokens, int heads, int head_dim, float *A,
+                                 float *B, void *stream) {
   int rc = check_dim(head_dim);
   if (rc) return rc;
   VDNH3_HOST_CHECK(k && v && beta && A && B && frames > 0 && tokens > 0 && heads > 0, VDNH3_ERR_INVALID,
                    "frame_stats: empty or null operand");
-  VDNH3_HOST_CHECK(kv_row % 8 == 0 && kv_head % 8 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
-                       reinterpret_cast<uintptr_t>(v) % 16 == 0,
+  VDNH3_HOST_CHECK(k_row % 8 == 0 && k_head % 8 == 0 && v_row % 8 == 0 && v_head % 8 == 0 &&
+                       reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0,
                    VDNH3_ERR_INVALID, "frame_stats: k/v must be 16-byte aligned with strides multiple of 8");
+  VDNH3_HOST_CHECK((features & ~3) == 0, VDNH3_ERR_INVALID, "frame_stats: unknown feature flags %d", features);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(frames * heads);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(vdnh3::frame_stats_kernel<128>, grid, dim3(256), 0, s, k, v, kv_row, kv_head, beta, beta_row,
-                       tokens, heads, A, B);
-  else
-    hipLaunchKernelGGL(vdnh3::frame_stats_kernel<64>, grid, dim3(256), 0, s, k, v, kv_row, kv_head, beta, beta_row,
-                       tokens, heads, A, B);
+#define VDNH3_FS(D, KF, VF)                                                                                    \
+  if (head_dim == D && (features & 1) == KF && ((features >> 1) & 1) == VF)                                   \
+    hipLaunchKernelGGL((vdnh3::frame_stats_kernel<D, KF, VF>), grid, dim3(256), 0, s, k, k_row, k_head, v, \
+                       v_row, v_head, beta, beta_row, tokens, heads, A, B);
+  VDNH3_FS(128, 0, 0)
+  VDNH3_FS(128, 1, 0)
+  VDNH3_FS(128, 0, 1)
+  VDNH3_FS(128, 1, 1)
+  VDNH3_FS(64, 0, 0)
+  VDNH3_FS(64, 1, 0)
+  VDNH3_FS(64, 0, 1)
+  VDNH3_FS(64, 1, 1)
+#undef VDNH3_FS
   return check_launch("frame_stats");
 }
 
@@ -742,12 +770,11 @@ extern "C" int vdnh3_alpha_logsum(const float *alpha, int frames, int heads, int
   return check_launch("alpha_logsum");
 }
 
-extern "C" int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, const float *prefix,
-                             const float *suffix, const float *alpha_logsum, const float *text_state,
-                             const int32_t *bounds,
-                             int use_alpha, const uint16_t *norm_w, const uint16_t *gate, int64_t gate_row,
-                             uint16_t *out, int64_t out_row, int frames, int tokens, int heads, int head_dim,
-                             void *stream) {
+extern "C" int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, int q_features,
+                             const float *prefix, const float *suffix, const float *alpha_logsum,
+                             const float *text_state, const int32_t *bounds, int use_alpha, const uint16_t *norm_w,
+                             const uint16_t *gate, int64_t gate_row, uint16_t *out, int64_t out_row, int frames,
+                             int tokens, int heads, int head_dim, void *stream) {
   int rc = check_dim(head_dim);
   if (rc) return rc;
   VDNH3_HOST_CHECK(q && prefix && suffix && (alpha_logsum || !use_alpha) && bounds && norm_w && gate && out &&
@@ -759,16 +786,19 @@ extern "C" int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, c
                        reinterpret_cast<uintptr_t>(prefix) % 16 == 0 && reinterpret_cast<uintptr_t>(suffix) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(text_state) % 16 == 0,
                    VDNH3_ERR_INVALID, "readout: misaligned q / gate / out / norm weight / states");
+  VDNH3_HOST_CHECK(q_features == 0 || q_features == 1, VDNH3_ERR_INVALID, "readout: q_features must be 0 or 1");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(frames * heads);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(vdnh3::readout_kernel<128>, grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix,
-                       alpha_logsum, text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames,
+#define VDNH3_RO(D, QF)                                                                                        \
+  if (head_dim == D && q_features == QF)                                                                       \
+    hipLaunchKernelGGL((vdnh3::readout_kernel<D, QF>), grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix, \
+                       alpha_logsum, text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames,  \
                        tokens, heads);
-  else
-    hipLaunchKernelGGL(vdnh3::readout_kernel<64>, grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix,
-                       alpha_logsum, text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames,
-                       tokens, heads);
+  VDNH3_RO(128, 0)
+  VDNH3_RO(128, 1)
+  VDNH3_RO(64, 0)
+  VDNH3_RO(64, 1)
+#undef VDNH3_RO
   return check_launch("readout");
 }
 

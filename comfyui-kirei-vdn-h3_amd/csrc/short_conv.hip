@@ -1,0 +1,239 @@
+// K/V short convolutions of the VDN branch features on gfx950 (vdn_h3/runtime.py:319-341,
+// vdn_h3/branch.py:443-480, the fused temporal kernel of vdn_h3/kernels.py:100-129):
+//   s[f][y][x][c] = bf16( sum_{dy,dx} x[f][y+dy-P][x+dx-P][c] * w_sp[c][dy][dx] )  zero padded, fp32 sum
+//   a[f][p][c]    = sum_{dt} s[f+dt-PT][p][c] * w_tm[c][dt]                        zero padded over frames, fp32
+//   y = a * sigmoid(a);  with l2norm y /= max(||y||, 1e-6) over the head's D channels;  out = bf16(y)
+// The spatial sum is rounded to bf16 because the reference materialises the depthwise Conv2d
+// output as a bf16 tensor; the temporal sum, SiLU and norm stay in fp32 up to the one final
+// rounding, as in the reference's fused temporal kernel.
+//
+// One workgroup owns the D channels of one head on a TX x TY tile of the frame grid and walks
+// the frames in order. Per frame it stages the raw tile with its halo in LDS (the next frame's
+// loads are in flight during the arithmetic), forms the spatial sums, keeps the last KT of them
+// per position in registers (bf16 pairs) and emits the temporal output of frame f - KT/2.
+// D/4 lanes share one position, 4 channels (8 bytes) each, so the norm over the head is a
+// lane reduction; the filter taps of a lane's 4 channels live in registers.
+#include "common.h"
+
+namespace vdnh3 {
+namespace {
+
+constexpr int SC_THREADS = 512;
+constexpr int SC_MAX_POS = 64;     // positions of one tile (TX * TY)
+constexpr int SC_MAX_STAGE = 160;  // staged positions, tile plus halo ((TX + 2P) * (TY + 2P))
+
+__device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+template <int D, int KS, int KT>
+__global__ __launch_bounds__(SC_THREADS) void short_conv_kernel(
+    const uint16_t *__restrict__ x, int64_t x_row, int64_t x_head, const uint16_t *__restrict__ w_sp,
+    const uint16_t *__restrict__ w_tm, int F, int gh, int gw, int TX, int TY, int nx, int n_tiles, int l2norm,
+    uint16_t *__restrict__ out, int64_t o_row, int64_t o_head) {
+  constexpr int P = KS / 2, PT = KT / 2;
+  constexpr int LPP = D / 4;                      // lanes per position
+  constexpr int PPP = SC_THREADS / LPP;           // positions per pass
+  constexpr int NPASS = SC_MAX_POS / PPP;         // passes over a tile
+  constexpr int CPP = D / 8;                      // 16-byte chunks per staged position
+  constexpr int MAXL = (SC_MAX_STAGE * CPP + SC_THREADS - 1) / SC_THREADS;
+  __shared__ __attribute__((aligned(16))) uint16_t tile[SC_MAX_STAGE * D];
+
+  const int h = blockIdx.x / n_tiles, ti = blockIdx.x - h * n_tiles;
+  const int y0 = (ti / nx) * TY, x0 = (ti % nx) * TX;
+  const int tid = threadIdx.x, cl = tid % LPP, ps = tid / LPP;
+  const int SX = TX + 2 * P, SY = TY + 2 * P, n_stage = SX * SY * CPP;
+  const int T = gh * gw;
+
+  // filter taps of this lane's 4 channels, fp32
+  float wsp[KS * KS][4], wtm[KT][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t c = (int64_t)h * D + 4 * cl + j;
+#pragma unroll
+    for (int t = 0; t < KS * KS; ++t) wsp[t][j] = bf2f(w_sp[c * KS * KS + t]);
+#pragma unroll
+    for (int t = 0; t < KT; ++t) wtm[t][j] = bf2f(w_tm[c * KT + t]);
+  }
+
+  // this thread's tile positions (one per pass); slots past the tile read position 0
+  int lbase[NPASS];
+  int64_t obase[NPASS];
+  bool valid[NPASS];
+#pragma unroll
+  for (int i = 0; i < NPASS; ++i) {
+    const int pi = i * PPP + ps;
+    const bool in_tile = pi < TX * TY;
+    const int py = in_tile ? pi / TX : 0, px = in_tile ? pi % TX : 0;
+    valid[i] = in_tile && y0 + py < gh && x0 + px < gw;
+    lbase[i] = (py * SX + px) * D + 4 * cl;
+    obase[i] = valid[i] ? (int64_t)((y0 + py) * gw + x0 + px) * o_row + (int64_t)h * o_head + 4 * cl : 0;
+  }
+
+  // staging of frame f: chunk e = position (ly, lx) of the tile plus halo, 16-byte piece e % CPP
+  u32x4_t pre[MAXL];
+  auto stage_load = [&](int f) __device__ {
+#pragma unroll
+    for (int u = 0; u < MAXL; ++u) {
+      const int e = tid + u * SC_THREADS;
+      pre[u] = u32x4_t{0, 0, 0, 0};
+      if (e < n_stage) {
+        const int sp = e / CPP, ch = e - sp * CPP, ly = sp / SX, lx = sp - ly * SX;
+        const int gy = y0 + ly - P, gx = x0 + lx - P;
+        if (gy >= 0 && gy < gh && gx >= 0 && gx < gw)
+          pre[u] = ld16(x + ((int64_t)f * T + gy * gw + gx) * x_row + (int64_t)h * x_head + 8 * ch);
+      }
+    }
+  };
+  auto stage_store = [&]() __device__ {
+#pragma unroll
+    for (int u = 0; u < MAXL; ++u) {
+      const int e = tid + u * SC_THREADS;
+      if (e < n_stage) st16(tile + 8 * e, pre[u]);
+    }
+  };
+
+  uint32_t ring[NPASS][KT][2];
+#pragma unroll
+  for (int i = 0; i < NPASS; ++i)
+#pragma unroll
+    for (int t = 0; t < KT; ++t) ring[i][t][0] = ring[i][t][1] = 0u;
+
+  stage_load(0);
+  for (int f = 0; f < F + PT; ++f) {
+    uint32_t fresh[NPASS][2];
+    if (f < F) {
+      __syncthreads();  // every lane is done reading the previous frame's tile
+      stage_store();
+      __syncthreads();
+      if (f + 1 < F) stage_load(f + 1);
+#pragma unroll
+      for (int i = 0; i < NPASS; ++i) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dy = 0; dy < KS; ++dy)
+#pragma unroll
+          for (int dx = 0; dx < KS; ++dx) {
+            const u32x2_t v = *reinterpret_cast<const u32x2_t *>(tile + lbase[i] + (dy * SX + dx) * D);
+            const int t = dy * KS + dx;
+            acc[0] = fmaf(lo_f(v[0]), wsp[t][0], acc[0]);
+            acc[1] = fmaf(hi_f(v[0]), wsp[t][1], acc[1]);
+            acc[2] = fmaf(lo_f(v[1]), wsp[t][2], acc[2]);
+            acc[3] = fmaf(hi_f(v[1]), wsp[t][3], acc[3]);
+          }
+        fresh[i][0] = pack_bf2(acc[0], acc[1]);
+        fresh[i][1] = pack_bf2(acc[2], acc[3]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NPASS; ++i) fresh[i][0] = fresh[i][1] = 0u;
+    }
+    // ring[i][t] holds the spatial sum of frame f - KT + 1 + t
+#pragma unroll
+    for (int i = 0; i < NPASS; ++i) {
+#pragma unroll
+      for (int t = 0; t + 1 < KT; ++t) {
+        ring[i][t][0] = ring[i][t + 1][0];
+        ring[i][t][1] = ring[i][t + 1][1];
+      }
+      ring[i][KT - 1][0] = fresh[i][0];
+      ring[i][KT - 1][1] = fresh[i][1];
+    }
+    const int fo = f - PT;  // output frame: its taps are frames fo - PT .. fo + PT = ring[0 .. KT-1]
+    if (fo < 0) continue;
+#pragma unroll
+    for (int i = 0; i < NPASS; ++i) {
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        a[0] = fmaf(lo_f(ring[i][t][0]), wtm[t][0], a[0]);
+        a[1] = fmaf(hi_f(ring[i][t][0]), wtm[t][1], a[1]);
+        a[2] = fmaf(lo_f(ring[i][t][1]), wtm[t][2], a[2]);
+        a[3] = fmaf(hi_f(ring[i][t][1]), wtm[t][3], a[3]);
+      }
+      float y[4], ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        y[j] = a[j] / (1.f + expf(-a[j]));
+        ss = fmaf(y[j], y[j], ss);
+      }
+      if (l2norm) {
+#pragma unroll
+        for (int o = 1; o < LPP; o <<= 1) ss += __shfl_xor(ss, o);
+        const float nrm = fmaxf(sqrtf(ss), 1e-6f);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] = y[j] / nrm;
+      }
+      if (valid[i])
+        *reinterpret_cast<u32x2_t *>(out + obase[i] + (int64_t)fo * T * o_row) =
+            u32x2_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3])};
+    }
+  }
+}
+
+// Tile shape of the frame grid: the fewest tiles with TX * TY <= 64 positions, TX, TY <= 16
+// and the tile plus its halo within the LDS stage.
+void pick_tile(int gh, int gw, int P, int *TX, int *TY, int *nx, int *ny) {
+  int best = -1;
+  for (int tx = 1; tx <= 16; ++tx) {
+    const int cx = (gw + tx - 1) / tx, txr = (gw + cx - 1) / cx;
+    int ty = SC_MAX_POS / txr;
+    if (ty > 16) ty = 16;
+    while (ty > 1 && (txr + 2 * P) * (ty + 2 * P) > SC_MAX_STAGE) --ty;
+    if ((txr + 2 * P) * (ty + 2 * P) > SC_MAX_STAGE) continue;
+    const int cy = (gh + ty - 1) / ty, tyr = (gh + cy - 1) / cy;
+    const int cost = cx * cy;
+    if (best < 0 || cost < best) {
+      best = cost;
+      *TX = txr;
+      *TY = tyr;
+      *nx = cx;
+      *ny = cy;
+    }
+  }
+}
+
+template <int D, int KS, int KT>
+void launch(const uint16_t *x, int64_t x_row, int64_t x_head, const uint16_t *w_sp, const uint16_t *w_tm, int F,
+            int gh, int gw, int heads, int l2norm, uint16_t *out, int64_t o_row, int64_t o_head, hipStream_t s) {
+  int TX = 1, TY = 1, nx = gw, ny = gh;
+  pick_tile(gh, gw, KS / 2, &TX, &TY, &nx, &ny);
+  const int n_tiles = nx * ny;
+  hipLaunchKernelGGL((short_conv_kernel<D, KS, KT>), dim3(heads * n_tiles), dim3(SC_THREADS), 0, s, x, x_row,
+                     x_head, w_sp, w_tm, F, gh, gw, TX, TY, nx, n_tiles, l2norm, out, o_row, o_head);
+}
+
+}  // namespace
+}  // namespace vdnh3
+
+extern "C" int vdnh3_short_conv(const uint16_t *x, int64_t x_row, int64_t x_head, const uint16_t *w_spatial,
+                                int kernel_h, int kernel_w, const uint16_t *w_temporal, int kernel_t, int frames,
+                                int grid_h, int grid_w, int heads, int head_dim, int l2norm, uint16_t *out,
+                                int64_t out_row, int64_t out_head, void *stream) {
+  VDNH3_HOST_CHECK(head_dim == 64 || head_dim == 128, VDNH3_ERR_INVALID,
+                   "short_conv: head_dim must be 64 or 128, got %d", head_dim);
+  VDNH3_HOST_CHECK(kernel_h == kernel_w && (kernel_h == 3 || kernel_h == 5) && (kernel_t == 3 || kernel_t == 5),
+                   VDNH3_ERR_INVALID,
+                   "short_conv: supported kernels are 3x3 or 5x5 spatial and 3 or 5 temporal taps, got %dx%d and %d",
+                   kernel_h, kernel_w, kernel_t);
+  VDNH3_HOST_CHECK(x && w_spatial && w_temporal && out && frames > 0 && grid_h > 0 && grid_w > 0 && heads > 0,
+                   VDNH3_ERR_INVALID, "short_conv: empty or null operand");
+  VDNH3_HOST_CHECK(x_row % 8 == 0 && x_head % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0,
+                   VDNH3_ERR_INVALID, "short_conv: x must be 16-byte aligned with strides multiple of 8");
+  VDNH3_HOST_CHECK(out_row % 4 == 0 && out_head % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0,
+                   VDNH3_ERR_INVALID, "short_conv: out must be 8-byte aligned with strides multiple of 4");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define VDNH3_SC(D, KS, KT)                                                                                  \
+  if (head_dim == D && kernel_h == KS && kernel_t == KT)                                                     \
+    vdnh3::launch<D, KS, KT>(x, x_row, x_head, w_spatial, w_temporal, frames, grid_h, grid_w, heads, l2norm, \
+                             out, out_row, out_head, s);
+  VDNH3_SC(128, 5, 5)
+  VDNH3_SC(128, 5, 3)
+  VDNH3_SC(128, 3, 5)
+  VDNH3_SC(128, 3, 3)
+  VDNH3_SC(64, 5, 5)
+  VDNH3_SC(64, 5, 3)
+  VDNH3_SC(64, 3, 5)
+  VDNH3_SC(64, 3, 3)
+#undef VDNH3_SC
+  return vdnh3::check_launch("short_conv");
+}

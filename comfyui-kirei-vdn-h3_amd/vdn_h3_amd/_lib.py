@@ -49,12 +49,14 @@ SIGNATURES = {
                             _vp, _c_int, _vp, _c_int, _c_float, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_quant_rows": (_c_int, [_c_int, _vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _vp]),
     "vdnh3_quant_tensor_f8": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _vp]),
-    "vdnh3_frame_stats": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int,
-                                   _vp, _vp, _vp]),
+    "vdnh3_frame_stats": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _c_i64, _c_int,
+                                   _c_int, _c_int, _c_int, _vp, _vp, _vp]),
+    "vdnh3_short_conv": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
+                                  _c_int, _c_int, _c_int, _vp, _c_i64, _c_i64, _vp]),
     "vdnh3_delta_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_float, _vp, _c_int, _c_int, _vp]),
     "vdnh3_sana_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_delta_scan": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
-    "vdnh3_readout": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_i64,
+    "vdnh3_readout": (_c_int, [_vp, _c_i64, _c_i64, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_i64,
                                _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_frame_mean": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _vp, _vp]),
     "vdnh3_linear_f32": (_c_int, [_vp, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_i64, _c_int, _c_int, _c_int,

@@ -7,6 +7,8 @@ Mirrors the inference pieces of ``vdn_h3/branch.py`` with HIP kernels behind eac
   ``torch.linalg.LinAlgError`` with the reference's message;
 * ``frame_statistics_raw`` - ``frame_statistics`` (``:197-282``) with the feature map of
   ``vdn_h3/kernels.py:47-51`` fused into the loads;
+* ``conv_features`` - the short convolutions (``:443-480``, ``vdn_h3/runtime.py:319-341``) as
+  one kernel;
 * ``VdnDelta`` / ``SanaDelta`` ``.factor_apply`` (``:144-180``);
 * ``run_scans_inference`` (``:315-333``);
 * ``alpha_gate`` (``:483-491``), ``frame_mean``;
@@ -91,8 +93,12 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
 
 
 def frame_statistics_raw(k_raw: torch.Tensor, v_raw: torch.Tensor, beta: torch.Tensor, num_frames: int,
-                         tokens_per_frame: int):
-    """``A, B`` ``[F, H, D, D]`` fp32 from raw ``k``/``v`` rows ``[F*T, H, D]`` and ``beta`` ``[F*T, H]``."""
+                         tokens_per_frame: int, *, k_features: bool = False, v_features: bool = False):
+    """``A, B`` ``[F, H, D, D]`` fp32 from ``k``/``v`` rows ``[F*T, H, D]`` and ``beta`` ``[F*T, H]``.
+
+    ``k``/``v`` are raw projections (the feature map is applied on load) unless
+    ``k_features``/``v_features`` say they already hold the features (short-convolution output).
+    """
     if k_raw.shape != v_raw.shape or k_raw.ndim != 3:
         raise ValueError("key and value must share shape [rows, heads, dim]")
     rows, heads, dim = k_raw.shape
@@ -103,19 +109,59 @@ def frame_statistics_raw(k_raw: torch.Tensor, v_raw: torch.Tensor, beta: torch.T
     _dim(dim)
     device = _lib.require_device(k_raw, v_raw, beta)
     k_raw, v_raw = _rows(k_raw), _rows(v_raw)
-    if k_raw.stride() != v_raw.stride():
-        v_raw = v_raw.contiguous()
-        k_raw = k_raw.contiguous()
     beta = beta.to(torch.bfloat16)
     if beta.stride(1) != 1:
         beta = beta.contiguous()
     a = torch.empty((num_frames, heads, dim, dim), dtype=torch.float32, device=device)
     b = torch.empty_like(a)
-    rc = _lib.lib().vdnh3_frame_stats(_lib.ptr(k_raw), _lib.ptr(v_raw), k_raw.stride(0), k_raw.stride(1),
-                                      _lib.ptr(beta), beta.stride(0), num_frames, tokens_per_frame, heads, dim,
-                                      _lib.ptr(a), _lib.ptr(b), _lib.stream_handle(device))
+    flags = int(bool(k_features)) | (int(bool(v_features)) << 1)
+    rc = _lib.lib().vdnh3_frame_stats(_lib.ptr(k_raw), k_raw.stride(0), k_raw.stride(1), _lib.ptr(v_raw),
+                                      v_raw.stride(0), v_raw.stride(1), flags, _lib.ptr(beta), beta.stride(0),
+                                      num_frames, tokens_per_frame, heads, dim, _lib.ptr(a), _lib.ptr(b),
+                                      _lib.stream_handle(device))
     _lib.check(rc, "vdnh3_frame_stats")
     return a, b
+
+
+def conv_features(tokens: torch.Tensor, spatial_weight: torch.Tensor, temporal_weight: torch.Tensor,
+                  num_frames: int, frame_size, l2norm: bool, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Short-convolution features ``[F*T, H, D]`` bf16 (``vdn_h3/branch.py:443-480``, ``vdn_h3/runtime.py:319-341``).
+
+    Depthwise ``kh x kw`` spatial convolution per frame (rounded to bf16), depthwise temporal
+    convolution over the ``num_frames`` frames (zero padded), SiLU, and with ``l2norm`` a unit
+    L2 norm over each head's ``D`` channels, as one kernel.
+    """
+    if tokens.ndim != 3 or frame_size is None:
+        raise ValueError("conv features need [rows, heads, dim] and frame_size")
+    heads, head_dim = tokens.shape[-2:]
+    gh, gw = (int(v) for v in frame_size)
+    if gh <= 0 or gw <= 0:
+        raise ValueError("frame_size dimensions must be positive")
+    channels = heads * head_dim
+    if tokens.shape[0] != num_frames * gh * gw:
+        raise ValueError("token rows do not match num_frames * frame area")
+    if spatial_weight.ndim != 4 or spatial_weight.shape[0] != channels or spatial_weight.shape[1] != 1:
+        raise ValueError("spatial convolution must have one depthwise filter per channel")
+    kh, kw = spatial_weight.shape[-2:]
+    if kh % 2 == 0 or kw % 2 == 0:
+        raise ValueError("spatial kernels must have odd dimensions")
+    kt = temporal_weight.shape[-1]
+    if temporal_weight.numel() != channels * kt or kt <= 0 or kt % 2 == 0:
+        raise ValueError("temporal kernel must be positive, odd and symmetrically padded")
+    _dim(head_dim)
+    device = _lib.require_device(tokens, spatial_weight, temporal_weight, out)
+    tokens = _rows(tokens)
+    sp = spatial_weight.to(torch.bfloat16).reshape(channels, kh * kw).contiguous()
+    tm = temporal_weight.to(torch.bfloat16).reshape(channels, kt).contiguous()
+    if out is None:
+        out = torch.empty((tokens.shape[0], heads, head_dim), dtype=torch.bfloat16, device=device)
+    elif out.shape != tokens.shape or out.dtype != torch.bfloat16 or out.stride(-1) != 1:
+        raise ValueError("out must be a bf16 [rows, heads, dim] view with contiguous dim")
+    rc = _lib.lib().vdnh3_short_conv(_lib.ptr(tokens), tokens.stride(0), tokens.stride(1), _lib.ptr(sp), kh, kw,
+                                     _lib.ptr(tm), kt, num_frames, gh, gw, heads, head_dim, int(bool(l2norm)),
+                                     _lib.ptr(out), out.stride(0), out.stride(1), _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_short_conv")
+    return out
 
 
 class VdnDelta:
@@ -260,8 +306,12 @@ def _device_bounds(bounds, device) -> torch.Tensor:
 
 
 def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *, text_state=None,
-                     bridge="alpha", num_frames, tokens_per_frame, out=None):
-    """Gather, readout and RMSNorm/gate epilogue: ``[F*T, H*D]`` bf16."""
+                     bridge="alpha", num_frames, tokens_per_frame, out=None, q_features=False):
+    """Gather, readout and RMSNorm/gate epilogue: ``[F*T, H*D]`` bf16.
+
+    ``q_raw`` is the raw query (``L2(SiLU(q))`` is applied on load) unless ``q_features`` says it
+    already holds the query features (short-convolution output).
+    """
     if bridge not in ("alpha", "none"):
         raise ValueError("bridge must be 'alpha' or 'none'")
     rows, heads, dim = q_raw.shape
@@ -292,7 +342,8 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
         rc = _lib.lib().vdnh3_alpha_logsum(_lib.ptr(alpha), num_frames, heads, dim, _lib.ptr(logsum),
                                            _lib.stream_handle(device))
         _lib.check(rc, "vdnh3_alpha_logsum")
-    rc = _lib.lib().vdnh3_readout(_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), _lib.ptr(prefix.contiguous()),
+    rc = _lib.lib().vdnh3_readout(_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), int(bool(q_features)),
+                                  _lib.ptr(prefix.contiguous()),
                                   _lib.ptr(suffix.contiguous()), _lib.ptr(logsum), _lib.ptr(text), _lib.ptr(bounds_t),
                                   int(bridge == "alpha"), _lib.ptr(norm_w), _lib.ptr(gate), gate.stride(0),
                                   _lib.ptr(out), out.stride(0), num_frames, tokens_per_frame, heads, dim,
@@ -313,5 +364,5 @@ def fill_rows(t: torch.Tensor, value: float = 0.0):
 
 
 __all__ = ["DELTA_BACKENDS", "SanaDelta", "TEXT_STATE_SCALE", "VdnDelta", "alpha_gate", "cholesky_runtime_scope",
-           "fill_rows", "frame_mean", "frame_statistics_raw", "linear_f32", "readout_epilogue",
+           "conv_features", "fill_rows", "frame_mean", "frame_statistics_raw", "linear_f32", "readout_epilogue",
            "run_scans_from_factors", "run_scans_inference"]

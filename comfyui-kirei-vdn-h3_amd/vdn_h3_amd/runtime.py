@@ -7,7 +7,8 @@ and leaves their rows zero), the text state (``vdn_h3/branch.py:649-670``) and t
 hook. The inference spelling only: the device path runs under ``torch.no_grad()``.
 
 Per call, on the caller's current stream:
-  beta (GEMM + sigmoid) -> frame statistics (features fused) -> frame means -> alpha
+  beta (GEMM + sigmoid) -> [short convolutions of the short_conv targets] -> frame statistics
+  (features fused) -> frame means -> alpha
   -> text state (statistics + factor, J scaled by 1/2) -> factor of every frame
   -> bidirectional scans -> output gate (two GEMMs + sigmoid)
   -> gather + readout + RMSNorm epilogue -> projector (bf16 / fp8 / int8 GEMM).
@@ -37,9 +38,6 @@ class OptimizedLinearBranch:
         targets = tuple(short_conv)
         if len(set(targets)) != len(targets) or any(t not in ("q", "k", "v") for t in targets):
             raise ValueError("short_conv must be a distinct subset of ('q', 'k', 'v')")
-        if targets:
-            raise NotImplementedError("the HIP branch does not implement the K/V short convolutions yet; "
-                                      "use short_conv=()")
         if not a_fp32:
             raise NotImplementedError("the HIP branch computes A at full fp32 accuracy (a_fp32=True)")
         self.w = weights
@@ -67,11 +65,26 @@ class OptimizedLinearBranch:
         _, jay = self._backend(length).factor_apply(None, a, b, jay_scale=_b.TEXT_STATE_SCALE, need_phi=False)
         return jay[0]
 
+    def _features(self, weights, name, raw, num_frames, frame_size):
+        """Short-convolution features of ``q``/``k``/``v`` (``vdn_h3/runtime.py:311-341``), or the raw
+        rows when ``name`` has no short convolution (its feature map is fused into the consumer)."""
+        if name not in self.short_conv:
+            return raw, False
+        if frame_size is None:
+            raise ValueError("short convolution requires frame_size")
+        feats = _b.conv_features(raw, weights[f"short_conv.{name}_sp.weight"], weights[f"short_conv.{name}_tm.weight"],
+                                 num_frames, frame_size, name != "v")
+        return feats, True
+
     def _readout_flat(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, text_x,
-                      text_k_raw, text_v_raw, out=None):
+                      text_k_raw, text_v_raw, frame_size=None, out=None):
         heads, dim = self.num_heads, self.head_dim
         beta = _linear.sigmoid_linear(xv, weights["beta_proj.weight"])
-        a, b = _b.frame_statistics_raw(k_raw, v_raw, beta, num_frames, tokens_per_frame)
+        k_in, k_feat = self._features(weights, "k", k_raw, num_frames, frame_size)
+        v_in, v_feat = self._features(weights, "v", v_raw, num_frames, frame_size)
+        a, b = _b.frame_statistics_raw(k_in, v_in, beta, num_frames, tokens_per_frame, k_features=k_feat,
+                                       v_features=v_feat)
+        del k_in, v_in
         mean = _b.frame_mean(xv, num_frames, tokens_per_frame)
         alpha = _b.alpha_gate(mean, weights["alpha.down.weight"], weights["alpha.up.weight"],
                               weights["alpha.dt_bias"], weights["alpha.A_log"], heads, dim)
@@ -80,9 +93,10 @@ class OptimizedLinearBranch:
         del a, b
         hidden = _linear.linear(xv, weights["output_gate.down.weight"])
         gate = _linear.sigmoid_linear(hidden, weights["output_gate.up.weight"], weights.get("output_gate.up.bias"))
-        return _b.readout_epilogue(q_raw, prefix, suffix, alpha, bounds, weights["norm.weight"], gate,
+        q_in, q_feat = self._features(weights, "q", q_raw, num_frames, frame_size)
+        return _b.readout_epilogue(q_in, prefix, suffix, alpha, bounds, weights["norm.weight"], gate,
                                    text_state=text_state, bridge=self.bridge, num_frames=num_frames,
-                                   tokens_per_frame=tokens_per_frame, out=out)
+                                   tokens_per_frame=tokens_per_frame, out=out, q_features=q_feat)
 
     def _check(self, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds):
         if torch.is_grad_enabled():
@@ -99,12 +113,12 @@ class OptimizedLinearBranch:
     def readout(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, frame_size=None,
                 text_x=None, text_k_raw=None, text_v_raw=None, skip_ends=False, *, inference=True):
         """Branch readout before ``to_out_linear``: ``[F*T, H*D]`` bf16, anchor rows zero with ``skip_ends``."""
-        del frame_size, inference
+        del inference
         self._check(xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds)
         rows = num_frames * tokens_per_frame
         if not skip_ends:
             return self._readout_flat(weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds,
-                                      text_x, text_k_raw, text_v_raw)
+                                      text_x, text_k_raw, text_v_raw, frame_size)
         out = torch.empty((rows, self.num_heads * self.head_dim), dtype=torch.bfloat16, device=xv.device)
         if num_frames <= 2:
             return _b.fill_rows(out)
@@ -114,7 +128,7 @@ class OptimizedLinearBranch:
         _b.fill_rows(out[(num_frames - 1) * t:])
         self._readout_flat(weights, xv[inner], q_raw[inner], k_raw[inner], v_raw[inner], num_frames - 2, t,
                            [(lo - 1, hi - 1) for lo, hi in bounds[1:-1]], text_x, text_k_raw, text_v_raw,
-                           out=out[inner])
+                           frame_size, out=out[inner])
         return out
 
     def projected_delta(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, *,
@@ -127,7 +141,7 @@ class OptimizedLinearBranch:
         ``accumulate`` the anchor rows of ``out`` are left untouched (their delta is zero).
         ``projector(rows, out=..., accumulate=...)`` defaults to ``projection.project``.
         """
-        del frame_size, inference, tile_frames
+        del inference, tile_frames
         self._check(xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds)
         proj = projector or (lambda rows, **kw: _projection.project(rows, weights, **kw))
         hidden = _projection.projection_out_features(weights)
@@ -148,11 +162,11 @@ class OptimizedLinearBranch:
                 _b.fill_rows(out[(num_frames - 1) * t:])
             flat = self._readout_flat(weights, xv[inner], q_raw[inner], k_raw[inner], v_raw[inner],
                                       num_frames - 2, t, [(lo - 1, hi - 1) for lo, hi in bounds[1:-1]], text_x,
-                                      text_k_raw, text_v_raw)
+                                      text_k_raw, text_v_raw, frame_size)
             proj(flat, out=out[inner], accumulate=accumulate)
             return out
         flat = self._readout_flat(weights, xv, q_raw, k_raw, v_raw, num_frames, t, bounds, text_x, text_k_raw,
-                                  text_v_raw)
+                                  text_v_raw, frame_size)
         proj(flat, out=out, accumulate=accumulate)
         return out
 

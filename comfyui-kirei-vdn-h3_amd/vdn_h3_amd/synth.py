@@ -91,14 +91,22 @@ def softmax_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
 
 
-def branch_weights(heads: int, head_dim: int, hidden: int, device="cpu", seed: int = 42) -> dict:
+def branch_weights(heads: int, head_dim: int, hidden: int, device="cpu", seed: int = 42,
+                   short_conv=()) -> dict:
     """Random-init VDN branch weights of one block (shapes of ``vdn_h3/spec.py:471-486``).
 
     Matrices ~ N(0, 0.02); ``alpha.dt_bias`` / ``alpha.A_log`` ~ N(0, 0.5^2) kept in fp32 (the
-    reference stores them in fp32); ``norm.weight`` = 1 + 0.1 N(0, 1); gate biases N(0, 0.5^2).
+    reference stores them in fp32); ``norm.weight`` = 1 + 0.1 N(0, 1); gate biases N(0, 0.5^2);
+    for each ``short_conv`` target a depthwise 5x5 spatial filter ~ N(0, 0.2^2) and a 5-tap
+    temporal filter ~ N(0, 0.4^2) per channel.
     """
     bf = torch.bfloat16
+    conv = {}
+    for i, name in enumerate(short_conv):
+        conv[f"short_conv.{name}_sp.weight"] = randn((heads * head_dim, 1, 5, 5), seed + 12 + 2 * i, device, bf, 0.2)
+        conv[f"short_conv.{name}_tm.weight"] = randn((heads * head_dim, 1, 5), seed + 13 + 2 * i, device, bf, 0.4)
     return {
+        **conv,
         "beta_proj.weight": randn((heads, hidden), seed, device, bf, 0.02),
         "alpha.down.weight": randn((head_dim, hidden), seed + 1, device, bf, 0.02),
         "alpha.up.weight": randn((heads * head_dim, head_dim), seed + 2, device, bf, 0.02),

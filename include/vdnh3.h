@@ -166,15 +166,33 @@ int vdnh3_quant_tensor_f8(const uint16_t *x, int64_t n, uint8_t *q, float *scale
 
 /*
  * Frame statistics with the feature map fused in: for frame f and head h (tokens t of the
- * frame at rows f*tokens + t of k/v, element d at p[row*kv_row + h*kv_head + d]):
+ * frame at rows f*tokens + t; element d of k at k[row*k_row + h*k_head + d], of v likewise):
  *   k~ = L2(SiLU(k)), v~ = SiLU(v) (vdn_h3/kernels.py:47-51), b = beta[row*beta_row + h] (bf16),
  *   A[f][h] = 0.5 (S + S^T), S = (k~ b)^T k~ in fp32        (vdn_h3/branch.py:197-241)
  *   B[f][h] = bf16((v~ * b)^T k~)                             (vdn_h3/branch.py:242)
+ * `features` bit 0: k already holds k~; bit 1: v already holds v~ (the outputs of
+ * vdnh3_short_conv, vdn_h3/runtime.py:319-341), so the feature map is not applied to it.
  * A and B are [frames][heads][D][D] fp32.
  */
-int vdnh3_frame_stats(const uint16_t *k, const uint16_t *v, int64_t kv_row, int64_t kv_head,
-                      const uint16_t *beta, int64_t beta_row, int frames, int tokens, int heads,
-                      int head_dim, float *A, float *B, void *stream);
+int vdnh3_frame_stats(const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *v, int64_t v_row,
+                      int64_t v_head, int features, const uint16_t *beta, int64_t beta_row, int frames,
+                      int tokens, int heads, int head_dim, float *A, float *B, void *stream);
+
+/*
+ * K/V (or Q) short convolutions of the branch features (vdn_h3/runtime.py:319-341,
+ * vdn_h3/branch.py:443-480, vdn_h3/kernels.py:100-129). x holds frames * grid_h * grid_w rows
+ * (frame-major, then row-major over the grid), element (r, h, d) at x[r*x_row + h*x_head + d]:
+ *   s = bf16(depthwise kernel_h x kernel_w spatial conv per frame, zero padded)   (F.conv2d, groups=C)
+ *   a = depthwise kernel_t-tap temporal conv of s over frames, zero padded, fp32 (temporal kernel)
+ *   out = bf16(SiLU(a) / max(||SiLU(a)||_head, 1e-6)) with l2norm, else bf16(SiLU(a))
+ * w_spatial: bf16 [heads*head_dim][kernel_h*kernel_w] (the [C,1,kh,kw] Conv2d weight);
+ * w_temporal: bf16 [heads*head_dim][kernel_t] (the [C,1,kt] weight). Supported: 3x3 or 5x5 and
+ * 3 or 5 taps. out: element (r, h, d) at out[r*out_row + h*out_head + d], 8-byte aligned.
+ */
+int vdnh3_short_conv(const uint16_t *x, int64_t x_row, int64_t x_head, const uint16_t *w_spatial, int kernel_h,
+                     int kernel_w, const uint16_t *w_temporal, int kernel_t, int frames, int grid_h, int grid_w,
+                     int heads, int head_dim, int l2norm, uint16_t *out, int64_t out_row, int64_t out_head,
+                     void *stream);
 
 /*
  * VdnDelta.factor_apply (vdn_h3/branch.py:148-160) over n matrices with the status of
@@ -206,7 +224,8 @@ int vdnh3_alpha_logsum(const float *alpha, int frames, int heads, int head_dim, 
 
 /*
  * Gather + readout + epilogue (vdn_h3/branch.py:372-396, vdn_h3/runtime.py:406-419,
- * vdn_h3/branch.py:494-505), q~ = L2(SiLU(q)) fused in. For frame f with bounds
+ * vdn_h3/branch.py:494-505), q~ = L2(SiLU(q)) fused in (q_features = 1: q already holds q~,
+ * the output of vdnh3_short_conv). For frame f with bounds
  * lo = max(bounds[2f], 0), hi = min(bounds[2f+1], frames-1):
  *   L_f = bf16(before * decay_b + after * decay_a)  (before = prefix[lo-1] or text_state or 0,
  *         after = suffix[hi+1] or text_state or 0; when use_alpha, decay_b = exp(S[f+1] - S[lo])
@@ -216,7 +235,7 @@ int vdnh3_alpha_logsum(const float *alpha, int frames, int heads, int head_dim, 
  * out and gate: [frames*tokens, heads*D] bf16 with 16-byte aligned rows; prefix, suffix and
  * text_state 16-byte aligned.
  */
-int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, const float *prefix,
+int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, int q_features, const float *prefix,
                   const float *suffix, const float *alpha_logsum, const float *text_state, const int32_t *bounds,
                   int use_alpha, const uint16_t *norm_w, const uint16_t *gate, int64_t gate_row,
                   uint16_t *out, int64_t out_row, int frames, int tokens, int heads, int head_dim,

@@ -8,7 +8,10 @@ statistics, factor, scans and gather in fp32):
 
 * ``activate``           -> ``vdn_h3/kernels.py:47-51``
 * ``temporal_shift``     -> ``vdn_h3/kernels.py:59-68``
-* ``conv_features``      -> ``vdn_h3/runtime.py:319-341`` / ``vdn_h3/branch.py:443-480``
+* ``conv_features``      -> ``vdn_h3/runtime.py:319-341`` / ``vdn_h3/branch.py:443-480`` (eager
+  bf16 temporal sum, the reference's CPU spelling)
+* ``conv_features_fused``-> the same with the fused temporal kernel of ``vdn_h3/kernels.py:100-129``
+  (fp32 temporal sum, SiLU and norm; the reference's CUDA spelling)
 * ``frame_statistics``   -> ``vdn_h3/branch.py:197-243``
 * ``vdn_factor``         -> ``vdn_h3/branch.py:62-71``, ``:148-160`` (``VdnDelta.factor_apply``)
 * ``sana_factor``        -> ``vdn_h3/branch.py:163-177``
@@ -34,6 +37,9 @@ Pinning (``tests/test_oracle_branch.py``):
 * ``alpha_gate`` / ``rms_norm`` / ``activate``: closed forms (``exp(-e^A softplus)``,
   ``x / sqrt(mean x^2 + eps)``, ``silu`` then unit norm).
 * ``conv_features``: unit norm and ``F.conv3d`` with a (1,kh,kw) then (kt,1,1) kernel.
+* ``conv_features_fused``: ``F.conv3d`` in float64 with the bf16 rounding of the spatial output,
+  then SiLU / unit norm in float64 (within one bf16 step), and the branch golden with short
+  convolutions (``tests/golden/branch_13f_conv.safetensors``) end to end.
 * ``readout`` / ``projected_delta`` composites: golden vectors written by
   ``tests/golden/make_golden.py`` from the reference implementation itself
   (``tests/golden/branch_*.safetensors``).
@@ -92,6 +98,46 @@ def conv_features(tokens, spatial_weight, temporal_weight, num_frames, frame_siz
     temporal = temporal_weight.squeeze(1).to(flat.dtype)
     raw = temporal_shift(flat, temporal, temporal.shape[-1])
     return activate(raw.reshape(-1, heads, head_dim), l2norm)
+
+
+def temporal_conv_act_fused(flat, weight, heads, head_dim, l2norm):
+    """The reference's fused temporal kernel (``vdn_h3/kernels.py:100-129``) on ``[F, T, C]`` bf16.
+
+    ``acc = sum_dt x[f + dt - kt//2] * w[:, dt]`` in fp32 (zero padded over frames), then
+    ``y = acc * sigmoid(acc)``, with ``l2norm`` ``y * 1/sqrt(max(sum_head y^2, 1e-12))``, one
+    rounding to bf16 at the end.
+    """
+    frames, tokens, channels = flat.shape
+    kt = weight.shape[-1]
+    pad = kt // 2
+    xp = F.pad(flat.float(), (0, 0, 0, 0, pad, pad))
+    w = weight.reshape(channels, kt).to(flat.dtype).float()
+    acc = torch.zeros((frames, tokens, channels), dtype=torch.float32)
+    for dt in range(kt):
+        acc = acc + xp[dt:dt + frames] * w[:, dt]
+    y = acc * torch.sigmoid(acc)
+    y = y.reshape(frames, tokens, heads, head_dim)
+    if l2norm:
+        y = y * (1.0 / torch.sqrt(torch.clamp((y * y).sum(-1, keepdim=True), min=1e-12)))
+    return y.to(flat.dtype).reshape(frames * tokens, heads, head_dim)
+
+
+def conv_features_fused(tokens, spatial_weight, temporal_weight, num_frames, frame_size, l2norm):
+    """Short-convolution features as the reference's CUDA path computes them.
+
+    ``vdn_h3/runtime.py:319-341``: the depthwise ``Conv2d`` output is a bf16 tensor (fp32
+    accumulation, one rounding), then the fused temporal kernel (``temporal_conv_act_fused``).
+    Returns ``[F*T, H, D]`` bf16.
+    """
+    heads, head_dim = tokens.shape[-2:]
+    gh, gw = frame_size
+    channels = heads * head_dim
+    kh, kw = spatial_weight.shape[-2:]
+    volume = tokens.reshape(num_frames, gh, gw, channels).permute(0, 3, 1, 2).float()
+    sp = spatial_weight.to(tokens.dtype).float()
+    volume = F.conv2d(volume, sp, padding=(kh // 2, kw // 2), groups=channels).to(tokens.dtype)
+    flat = volume.permute(0, 2, 3, 1).reshape(num_frames, gh * gw, channels)
+    return temporal_conv_act_fused(flat, temporal_weight, heads, head_dim, l2norm)
 
 
 def frame_statistics(key_by_frame, value_by_frame, beta, a_fp32=True):
@@ -245,15 +291,19 @@ def text_state(weights, text_x, text_k_raw, text_v_raw, num_heads, head_dim, del
     return TEXT_STATE_SCALE * injection[0], info
 
 
-def features(weights, q_raw, k_raw, v_raw, num_frames, frame_size, short_conv=()):
-    """q, k, v features in FHSD layout (``vdn_h3/runtime.py:311-359``)."""
+def features(weights, q_raw, k_raw, v_raw, num_frames, frame_size, short_conv=(), fused_conv=False):
+    """q, k, v features in FHSD layout (``vdn_h3/runtime.py:311-359``).
+
+    ``fused_conv`` selects the CUDA spelling of the short convolutions (``conv_features_fused``).
+    """
     heads, head_dim = q_raw.shape[-2:]
     out = []
+    conv = conv_features_fused if fused_conv else conv_features
     for name, raw in (("q", q_raw), ("k", k_raw), ("v", v_raw)):
         l2 = name != "v"
         if name in short_conv:
-            rows = conv_features(raw, weights[f"short_conv.{name}_sp.weight"],
-                                 weights[f"short_conv.{name}_tm.weight"], num_frames, frame_size, l2)
+            rows = conv(raw, weights[f"short_conv.{name}_sp.weight"],
+                        weights[f"short_conv.{name}_tm.weight"], num_frames, frame_size, l2)
         else:
             rows = activate(raw, l2)
         out.append(to_fhsd(rows, num_frames, heads, head_dim))
@@ -262,7 +312,7 @@ def features(weights, q_raw, k_raw, v_raw, num_frames, frame_size, short_conv=()
 
 def readout(weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, *, frame_size=None,
             text_x=None, text_k_raw=None, text_v_raw=None, short_conv=(), delta_rule="vdn_solve",
-            bridge="alpha", a_fp32=True, return_parts=False):
+            bridge="alpha", a_fp32=True, return_parts=False, fused_conv=False):
     """Inference readout before ``to_out_linear`` (``vdn_h3/runtime.py:361-419``).
 
     Returns ``[F*T, H*D]`` in the activation dtype (and the intermediate tensors with
@@ -270,7 +320,7 @@ def readout(weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, boun
     """
     heads, head_dim = q_raw.shape[-2:]
     rows = num_frames * tokens_per_frame
-    qf, kf, vf = features(weights, q_raw, k_raw, v_raw, num_frames, frame_size, short_conv)
+    qf, kf, vf = features(weights, q_raw, k_raw, v_raw, num_frames, frame_size, short_conv, fused_conv)
     beta = torch.sigmoid(linear_bf16(xv, weights["beta_proj.weight"]))
     beta = beta.reshape(num_frames, tokens_per_frame, heads).permute(0, 2, 1)
     matrix_a, matrix_b = frame_statistics(kf, vf, beta, a_fp32)

@@ -123,6 +123,32 @@ def test_readout_epilogue(device, text, bridge):
     _close(got, want, 4 * 2.0 ** -8, 4 * 2.0 ** -8, "readout")
 
 
+@pytest.mark.parametrize("dim,ks,kt,l2,grid,frames", [
+    (128, 5, 5, True, (48, 27), 4), (128, 5, 5, False, (48, 27), 3), (128, 5, 5, True, (8, 8), 1),
+    (64, 3, 3, True, (7, 5), 6), (64, 5, 3, False, (2, 2), 5), (128, 3, 5, True, (17, 40), 3)])
+def test_short_conv_kernel(device, dim, ks, kt, l2, grid, frames):
+    """vdnh3_short_conv vs the CUDA spelling of the oracle (bf16 spatial sum, fp32 temporal / SiLU / norm)."""
+    from vdn_h3_amd import branch
+
+    print(f"case short conv D={dim} k={ks}x{ks}x{kt} l2={l2} grid={grid} frames={frames}", flush=True)
+    heads = 2
+    gh, gw = grid
+    rows, ch = frames * gh * gw, heads * dim
+    fused = _rand((rows, 3 * ch), 60, dtype=torch.bfloat16)          # the kernel reads a strided q/k/v view
+    x = fused[:, ch:2 * ch].reshape(rows, heads, dim)
+    sp = _rand((ch, 1, ks, ks), 61, 0.2, torch.bfloat16)
+    tm = _rand((ch, 1, kt), 62, 0.4, torch.bfloat16)
+    dx = fused.to(device)[:, ch:2 * ch].view(rows, heads, dim)
+    got = branch.conv_features(dx, sp.to(device), tm.to(device), frames, grid, l2)
+    torch.cuda.synchronize()
+    want = bo.conv_features_fused(x, sp, tm, frames, grid, l2)
+    g32, w32 = got.float().cpu(), want.float()
+    step = 2.0 ** -7 * w32.abs() + 2.0 ** -30
+    assert ((g32 - w32).abs() <= step).all(), f"max err {(g32 - w32).abs().max().item():.3e}"
+    exact = (g32 == w32).float().mean().item()
+    assert exact >= 0.99, exact
+
+
 def _load(name):
     with safe_open(str(GOLDEN / name), "pt") as f:
         return {k: f.get_tensor(k) for k in f.keys()}, f.metadata()
@@ -152,6 +178,74 @@ def test_projected_delta_matches_reference_golden(device):
     assert torch.count_nonzero(got[:tpf]) == 0 and torch.count_nonzero(got[-tpf:]) == 0
     _parity(got, t["delta"], "projected_delta vs reference")
     _parity(readout, t["readout"], "readout vs reference")
+
+
+def test_projected_delta_short_conv_matches_reference_golden(device):
+    """The branch with K/V short convolutions (13 frames of 8x8, 2 heads x 64) vs the reference."""
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+
+    print("case projected_delta short-conv golden", flush=True)
+    t, meta = _load("branch_13f_conv.safetensors")
+    frames, text, heads, dim = int(meta["frames"]), int(meta["text"]), int(meta["heads"]), int(meta["dim"])
+    gh, gw = map(int, meta["grid"].split("x"))
+    tpf = gh * gw
+    w = {k[2:]: v.to(device) for k, v in t.items() if k.startswith("w.")}
+    x, qkv = t["x"].to(device), t["qkv"].to(device)
+    seq = x.shape[0]
+    q, k, v = [y.view(seq, heads, dim) for y in qkv.split(heads * dim, dim=-1)]
+    bounds = wo.window_bounds(frames, 1, 5)
+    br = OptimizedLinearBranch(w, heads, dim, short_conv=("k", "v"), enable_text_state=True)
+    kw = dict(frame_size=(gh, gw), text_x=x[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True)
+    with torch.no_grad():
+        got = br.projected_delta(w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, **kw)
+        readout = br.readout(w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, **kw)
+        with pytest.raises(ValueError, match="short convolution requires frame_size"):
+            br.readout(w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, text_x=x[:text],
+                       text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(got[:tpf]) == 0 and torch.count_nonzero(got[-tpf:]) == 0
+    _parity(got, t["delta"], "short-conv projected_delta vs reference")
+    # the readout is RMS-normalised (values up to ~6, where one bf16 step is 2^-5): compare it in
+    # bf16 steps; the reference's golden used the eager (bf16) temporal sum, this path the fused one
+    _parity(readout, t["readout"], "short-conv readout vs reference", atol=2 ** -4, min_cos=0.9999)
+    _close(readout, t["readout"], 2.0 ** -6, 2e-2, "short-conv readout vs reference")
+
+
+def test_projected_delta_qkv_short_conv(device):
+    """Short convolutions on q, k and v (any subset is a valid checkpoint config) vs the oracle."""
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+
+    print("case projected_delta q/k/v short conv", flush=True)
+    frames, (gh, gw), text, heads, dim, hidden = 12, (6, 10), 24, 2, 128, 256
+    tpf = gh * gw
+    seq = text + frames * tpf
+    gen = {"beta_proj.weight": (heads, hidden), "alpha.down.weight": (dim, hidden),
+           "alpha.up.weight": (heads * dim, dim), "output_gate.down.weight": (dim, hidden),
+           "output_gate.up.weight": (heads * dim, dim), "to_out_linear.weight": (hidden, heads * dim)}
+    w = {name: _rand(shape, 70 + i, 0.02, torch.bfloat16) for i, (name, shape) in enumerate(gen.items())}
+    w["alpha.dt_bias"] = _rand((heads * dim,), 80, 0.5)
+    w["alpha.A_log"] = _rand((heads,), 81, 0.5)
+    w["output_gate.up.bias"] = _rand((heads * dim,), 82, 0.5, torch.bfloat16)
+    w["norm.weight"] = (1 + 0.1 * _rand((dim,), 83)).to(torch.bfloat16)
+    for i, name in enumerate("qkv"):
+        w[f"short_conv.{name}_sp.weight"] = _rand((heads * dim, 1, 5, 5), 84 + i, 0.2, torch.bfloat16)
+        w[f"short_conv.{name}_tm.weight"] = _rand((heads * dim, 1, 5), 87 + i, 0.4, torch.bfloat16)
+    x = _rand((seq, hidden), 90, dtype=torch.bfloat16)
+    qkv = _rand((seq, 3 * heads * dim), 91, dtype=torch.bfloat16)
+    q, k, v = [y.reshape(seq, heads, dim) for y in qkv.split(heads * dim, dim=-1)]
+    bounds = wo.window_bounds(frames, 1, 5)
+    kw = dict(frame_size=(gh, gw), text_x=x[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True)
+    want = bo.projected_delta(w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds,
+                              short_conv=("q", "k", "v"), fused_conv=True, **kw)
+    dw = {name: t.to(device) for name, t in w.items()}
+    dx, dqkv = x.to(device), qkv.to(device)
+    dq, dk, dv = [y.view(seq, heads, dim) for y in dqkv.split(heads * dim, dim=-1)]
+    br = OptimizedLinearBranch(dw, heads, dim, short_conv=("q", "k", "v"), enable_text_state=True)
+    dkw = dict(frame_size=(gh, gw), text_x=dx[:text], text_k_raw=dk[:text], text_v_raw=dv[:text], skip_ends=True)
+    with torch.no_grad():
+        got = br.projected_delta(dw, dx[text:], dq[text:], dk[text:], dv[text:], frames, tpf, bounds, **dkw)
+    torch.cuda.synchronize()
+    _parity(got, want, "q/k/v short-conv projected_delta vs oracle")
 
 
 def test_full_shape_branch(device):

@@ -149,9 +149,56 @@ def test_conv_features_unit_norm_and_conv3d_form():
     torch.testing.assert_close(got, bo.activate(raw, True), atol=1e-5, rtol=1e-4)
 
 
+@pytest.mark.parametrize("ks,kt,l2", [(3, 3, True), (5, 5, True), (5, 5, False), (5, 3, True)])
+def test_conv_features_fused_float64_form(ks, kt, l2):
+    """The CUDA spelling: bf16 spatial output, then temporal sum / SiLU / norm without rounding."""
+    frames, gh, gw, heads, dim = 6, 7, 5, 2, 16
+    ch = heads * dim
+    g = torch.Generator().manual_seed(61)
+    tokens = torch.randn(frames * gh * gw, heads, dim, generator=g).to(torch.bfloat16)
+    sp = (torch.randn(ch, 1, ks, ks, generator=g) * 0.2).to(torch.bfloat16)
+    tm = (torch.randn(ch, 1, kt, generator=g) * 0.4).to(torch.bfloat16)
+    got = bo.conv_features_fused(tokens, sp, tm, frames, (gh, gw), l2)
+    vol = tokens.double().reshape(frames, gh, gw, ch).permute(3, 0, 1, 2).unsqueeze(0)       # [1, C, F, gh, gw]
+    s64 = F.conv3d(vol, sp.double().unsqueeze(2), padding=(0, ks // 2, ks // 2), groups=ch)
+    s64 = s64.to(torch.bfloat16).double()                                                    # the bf16 Conv2d output
+    a = F.conv3d(s64, tm.double().reshape(ch, 1, kt, 1, 1), padding=(kt // 2, 0, 0), groups=ch)
+    y = a[0].permute(1, 2, 3, 0).reshape(-1, heads, dim)
+    y = y * torch.sigmoid(y)
+    if l2:
+        y = y / y.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+    step = 2.0 ** -7 * y.abs() + 2.0 ** -24                                                  # one bf16 step
+    assert ((got.double() - y).abs() <= step).all()
+    # a planted mistake fails it: temporal taps reversed
+    bad = bo.conv_features_fused(tokens, sp, tm.flip(-1), frames, (gh, gw), l2)
+    assert not ((bad.double() - y).abs() <= step).all()
+    # the eager spelling (bf16 products and sums over the taps) differs by its extra roundings only
+    eager = bo.conv_features(tokens, sp, tm, frames, (gh, gw), l2).double()
+    assert F.cosine_similarity(eager.flatten(), y.flatten(), dim=0).item() >= 0.9999
+
+
 def _load(name):
     with safe_open(str(GOLDEN / name), "pt") as f:
         return {k: f.get_tensor(k) for k in f.keys()}, f.metadata()
+
+
+def test_fused_conv_branch_matches_reference_golden():
+    """The CUDA spelling of the short convolutions meets the parity bar on the reference's golden."""
+    t, meta = _load("branch_13f_conv.safetensors")
+    frames, text, heads, dim = int(meta["frames"]), int(meta["text"]), int(meta["heads"]), int(meta["dim"])
+    gh, gw = map(int, meta["grid"].split("x"))
+    w = {k[2:]: v for k, v in t.items() if k.startswith("w.")}
+    x, qkv = t["x"], t["qkv"]
+    seq = x.shape[0]
+    q, k, v = [y.reshape(seq, heads, dim) for y in qkv.split(heads * dim, dim=-1)]
+    delta = bo.projected_delta(w, x[text:], q[text:], k[text:], v[text:], frames, gh * gw,
+                               wo.window_bounds(frames, 1, 5), frame_size=(gh, gw), text_x=x[:text],
+                               text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True, short_conv=("k", "v"),
+                               fused_conv=True)
+    want = t["delta"].float()
+    err = (delta.float() - want).abs().max().item()
+    cos = F.cosine_similarity(delta.double().flatten(), want.double().flatten(), dim=0).item()
+    assert err <= 2e-2 and cos >= 0.9995, (err, cos)
 
 
 @pytest.mark.parametrize("name", ["branch_13f.safetensors", "branch_13f_conv.safetensors"])
