@@ -90,6 +90,19 @@ __device__ __forceinline__ void global_to_lds16_at(const void *src, uint32_t lds
 __device__ __forceinline__ void global_to_lds16(const void *src, void *lds_wave_base) {
   global_to_lds16_at(src, lds_address(lds_wave_base));
 }
+// the same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset
+// (the scalar-base form of the instruction: no 64-bit per-lane address). `sbase` must be the
+// same for the whole wave; it is read from the first active lane.
+__device__ __forceinline__ void global_to_lds16_sbase(const void *sbase, uint32_t lane_bytes,
+                                                      uint32_t lds_wave_addr) {
+  const uint64_t b = reinterpret_cast<uintptr_t>(sbase);
+  // the builtin returns a signed int: go through uint32_t so the low half is zero-extended
+  const uint64_t ub = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b) |
+                      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(lane_bytes), "s"(ub),
+               "s"(__builtin_amdgcn_readfirstlane(lds_wave_addr))
+               : "m0");
+}
 
 }  // namespace vdnh3
 

@@ -151,34 +151,33 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   const int gtid = tid & 255, gw = wave & 3;
   const int kr0 = gtid / KC, vd0 = gtid >> 3;
   const int kslot = k_slot<D>(kr0, gtid % KC) * 8;
-  // per-lane element offsets of this group's chunks inside a tile's source rows (K rows for
-  // group A, V^T rows for group B), the tile's LDS base of this wavefront, and the per-tile
-  // source stride: the issue inside the MFMA stream is one 64-bit add, a scalar M0 and the load
-  int doff[KCG];
+  // per-lane byte offsets of this group's chunks inside a tile's source rows (K rows for group
+  // A, V^T rows for group B) and the tile's LDS base of this wavefront: an issue is a scalar
+  // tile base, a scalar M0 and the load
+  uint32_t doff[KCG];
 #pragma unroll
   for (int i = 0; i < KCG; ++i)
-    doff[i] = group == 0 ? (kr0 + i * (kBN / KCG)) * (int)k_row + kslot
-                         : (vd0 + i * (D / VCG)) * s_pad + v_slot(vd0, gtid & 7) * 8;
+    doff[i] = 2u * (group == 0 ? (uint32_t)((kr0 + i * (kBN / KCG)) * (int)k_row + kslot)
+                               : (uint32_t)((vd0 + i * (D / VCG)) * s_pad + v_slot(vd0, gtid & 7) * 8));
   const uint32_t lds_dma = __builtin_amdgcn_readfirstlane(
       (group == 0 ? lds_address(&Ks[0][0]) : lds_address(&Vs[0][0])) + gw * 64 * 16);
   constexpr uint32_t kTileBytes = KT * 2;
   static_assert(KT == VT, "K and V^T tiles have the same size");
-  // sources of this thread's chunks of the tile whose first key is ks; the last K tile of the
-  // sequence reads rows past seq as row seq - 1 (their scores are masked)
-  auto tile_srcs = [&](int ks, const uint16_t *(&src)[KCG]) __device__ {
+  // this group's loads of the tile whose first key is ks into ring slot `slot`; the last K tile
+  // of the sequence reads rows past seq as row seq - 1 (their scores are masked)
+  auto tile_dma = [&](int ks, int slot) __device__ {
     const uint16_t *base = group == 0 ? kbase + (int64_t)ks * k_row : vbase + ks;
+    uint32_t off[KCG];
 #pragma unroll
-    for (int i = 0; i < KCG; ++i) src[i] = base + doff[i];
-    if (__builtin_amdgcn_readfirstlane(ks + kBN > seq)) {  // uniform: skipped except for the last tile
-      if (group == 0) {
+    for (int i = 0; i < KCG; ++i) off[i] = doff[i];
+    if (group == 0 && ks + kBN > seq) {  // uniform: taken for the last tile of the sequence only
 #pragma unroll
-        for (int i = 0; i < KCG; ++i)
-          src[i] = kbase + (int64_t)min(ks + kr0 + i * (kBN / KCG), seq - 1) * k_row + kslot;
-      }
+      for (int i = 0; i < KCG; ++i)
+        off[i] = 2u * (uint32_t)((min(ks + kr0 + i * (kBN / KCG), seq - 1) - ks) * (int)k_row + kslot);
     }
-  };
-  auto dma_kv = [&](const uint16_t *src, int slot, int i) __device__ {
-    global_to_lds16_at(src, lds_dma + (uint32_t)slot * kTileBytes + (uint32_t)(i * 256 * 16));
+#pragma unroll
+    for (int i = 0; i < KCG; ++i)
+      global_to_lds16_sbase(base, off[i], lds_dma + (uint32_t)slot * kTileBytes + (uint32_t)(i * 256 * 16));
   };
 
   // Fragment offsets inside a tile (elements). The swizzles depend on the row only through
@@ -198,33 +197,29 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   float m_run = -INFINITY, l_run = 0.f;
 
   // Rings: K(tau) and V(tau) live in slot tau % kRing. K(t) and V(t-1) are read in phases 2t
-  // (group A) and 2t+1 (group B). Group A issues K(t+kRing-1) in phase 2t, over K(t-1); group
-  // B issues V(t+kRing-2) in phase 2t+1, over V(t-2); both slots were last read before the
-  // barrier that ended phase 2t-1. Past the end the tile index is clamped to T-1: such loads
-  // rewrite slots that no real tile reads any more, and every issue has the same count, so
-  // each group's vmcnt wait at the end of odd phases is exact.
+  // (group A) and 2t+1 (group B). Tile loads are issued by the group in its VALU phase, so the
+  // MFMA stream carries no memory instruction: in its VALU phase of tile t, group A issues
+  // K(t+kRing-1) (phase 2t+1) over K(t-1), last read in phase 2t-1, and group B issues
+  // V(t+kRing-1) (phase 2t+2) over V(t-1), last read in phase 2t+1. In each phase the slot
+  // being written differs from the K and V slots the MFMA group reads. Past the end the tile index is clamped to T-1: such loads rewrite
+  // slots that no real tile reads any more, and every VALU phase issues the same count, so each
+  // group's vmcnt wait at the end of odd phases is exact.
   // prologue: K(0..kRing-2) by group A, V(0..kRing-3) by group B, all landed; V(-1), the V^T
-  // slot read by the PV of tile 0 (with P(-1) = 0), is zeroed so that product is exactly zero
+  // slot read by the PV of tile 0 (with P(-1) = 0), is zeroed so that product is exactly zero.
+  // Group B's first issue (phase 0) is V(kRing-2).
 #pragma unroll
-  for (int j = 0; j < kRing - 1; ++j) {
-    if (j < kRing - 2 || group == 0) {
-      const uint16_t *src[KCG];
-      tile_srcs(tiles[toff + min(j, T - 1)].x, src);
-#pragma unroll
-      for (int i = 0; i < KCG; ++i) dma_kv(src[i], j, i);
-    }
-  }
+  for (int j = 0; j < kRing - 1; ++j)
+    if (j < kRing - 2 || group == 0) tile_dma(tiles[toff + min(j, T - 1)].x, j);
 #pragma unroll
   for (int i = 0; i < VT / 8 / kThreads; ++i)
     st16(Vs[kRing - 1] + (i * kThreads + tid) * 8, u32x4_t{0, 0, 0, 0});
   wait_vm_lds<0>();
   bare_barrier();
 
-  // Tile descriptors are scalar loads made one or two phases before their use: the DMA key
-  // start of this group's next issue and the mask bounds of its next VALU phase.
-  // (readfirstlane: a provably uniform index keeps the descriptor loads scalar)
-  const int dma_ahead = __builtin_amdgcn_readfirstlane(group == 0 ? kRing - 1 : kRing - 2);
-  int dma_ks = tiles[toff + min(dma_ahead, T - 1)].x;
+  // Descriptors of the next VALU phase of this group (the key start of its tile load and the
+  // mask bounds of its tile), scalar loads made at the end of the group's MFMA phase and
+  // consumed after the barrier. Group B's first VALU phase (phase 0, tile -1) issues V(kRing-2).
+  int dma_ks = group == 0 ? 0 : tiles[toff + min(kRing - 2, T - 1)].x;
   int mask = 0;
 
   const int phases = 2 * T + 2;
@@ -236,18 +231,14 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
     if (group == (p & 1)) {
       // MFMA phase of tile t: O^T += V(t-1)^T P(t-1)^T, S(t)^T = K(t) Q^T (16 + 16 MFMAs at D = 128).
       // t = 0 has no PV and t = T no QK: those phases run on a zero tile / discard the scores,
-      // so the phase is one branch-free block. Fragment reads run eight MFMAs ahead; this
-      // group's tile loads sit between the MFMAs.
+      // so the phase is one branch-free block. Fragment reads run eight MFMAs ahead.
       const int t = t_mfma;
-      const int ld_slot = (t + dma_ahead) & (kRing - 1);
-      const uint16_t *src[KCG];
-      tile_srcs(dma_ks, src);
       const uint16_t *vtile = Vs[(t + kRing - 1) & (kRing - 1)];
       const uint16_t *ktile = Ks[t & (kRing - 1)];
       // MFMA i < NP: PV block m = i % NO, k-step tt = i / NO; i >= NP: QK block kb = (i - NP) % 2,
       // k-step st = (i - NP) / 2. Consecutive MFMAs update different accumulators, so none waits
       // for the result of the one before it.
-      constexpr int NP = NO * 4, NM = NP + 2 * NS, EVERY = NM / KCG;
+      constexpr int NP = NO * 4, NM = NP + 2 * NS;
       auto frag = [&](int i) __device__ {
         return i < NP ? ld16(vtile + (i % NO) * 32 * kBN + vfo[i / NO])
                       : ld16(ktile + ((i - NP) & 1) * 32 * D + kfo[(i - NP) >> 1]);
@@ -269,20 +260,19 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
           sacc[kb] = mfma_bf16_32x32x16(as_bf16x8(a), qf[st], sacc[kb]);
         }
         if (i + 8 < NM) fr[i & 7] = frag(i + 8);
-        if (i % EVERY == EVERY / 2) dma_kv(src[i / EVERY], ld_slot, i / EVERY);
         __builtin_amdgcn_sched_barrier(0);
       }
       __builtin_amdgcn_s_setprio(0);
-      // descriptors for this group's next issue (two phases on) and next VALU phase
-      dma_ks = tiles[toff + min(t + 1 + dma_ahead, T - 1)].x;
+      // descriptors of this group's next VALU phase (tile t): its DMA issue and its mask
+      dma_ks = tiles[toff + min(t + kRing - 1, T - 1)].x;
       mask = t < T ? tiles[toff + t].y : 0;
     } else {
-      // VALU phase of tile t: softmax in base 2, one query per lane. The running max m_run moves
-      // only when this tile's max exceeds it by more than 2^kLazy: probabilities stay below
-      // 2^kLazy (exact softmax either way, a common shift cancels in O / l) and most tiles skip
-      // the rescale.
+      // VALU phase of tile t: first this group's tile loads (three tiles ahead), then the softmax
+      // in base 2, one query per lane. The running max m_run moves only when this tile's max
+      // exceeds it by more than 2^kLazy: probabilities stay below 2^kLazy (exact softmax either
+      // way, a common shift cancels in O / l) and most tiles skip the rescale.
+      tile_dma(dma_ks, (t_valu + kRing - 1) & (kRing - 1));
       const bool work = p >= 1 + group && t_valu < T;
-      float mt = 0.f;
       if (work) {
         const int lo = mask & 0xffff, hi = mask >> 16;
         if (lo > 0 || hi < kBN) {
@@ -294,18 +284,19 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
               if (ko < lo || ko >= hi) sacc[kb][i] = -INFINITY;
             }
         }
-        // tile row max: a balanced tree over the lane's 32 scores (depth 5 instead of a 32-long
-        // chain), then the other half-wave's value through v_permlane32_swap (no LDS round trip)
-        float mx[16];
+        // tile row max over the lane's 32 scores as a tree of three-input maxima (16 v_max3),
+        // then the other half-wave's value through v_permlane32_swap (no LDS round trip)
+        float m1[11];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx[i] = fmaxf(sacc[0][i], sacc[1][i]);
-#pragma unroll
-        for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-          for (int i = 0; i < w; ++i) mx[i] = fmaxf(mx[i], mx[i + w]);
-        mt = fmaxf(mx[0], other_half(mx[0])) * scale_log2;
-      }
-      if (work) {
+        for (int i = 0; i < 10; ++i) {
+          const int a = 3 * i, b = 3 * i + 1, c = 3 * i + 2;
+          m1[i] = fmaxf(fmaxf(sacc[a >> 4][a & 15], sacc[b >> 4][b & 15]), sacc[c >> 4][c & 15]);
+        }
+        m1[10] = fmaxf(sacc[1][14], sacc[1][15]);
+        const float m2a = fmaxf(fmaxf(m1[0], m1[1]), m1[2]), m2b = fmaxf(fmaxf(m1[3], m1[4]), m1[5]);
+        const float m2c = fmaxf(fmaxf(m1[6], m1[7]), m1[8]), m2d = fmaxf(m1[9], m1[10]);
+        const float mx = fmaxf(fmaxf(fmaxf(m2a, m2b), m2c), m2d);
+        const float mt = fmaxf(mx, other_half(mx)) * scale_log2;
         const bool grow = mt > m_run + kLazy;
         if (__any(grow)) {
           const float m_new = grow ? mt : m_run;
@@ -315,14 +306,22 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
 #pragma unroll
           for (int m = 0; m < NO; ++m) oacc[m] *= corr;
         }
-        float rs[4] = {0.f, 0.f, 0.f, 0.f};  // four partial sums: short dependency chains
+        // P in bf16 pairs; the row sum adds the bf16 values the PV product uses, two per
+        // v_dot2c_f32_bf16 against (1, 1), in four independent chains
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+        const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+        float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i], scale_log2, -m_run));
-            rs[i & 3] += pv;
-            pb[2 * kb + (i >> 3)][i & 7] = (__bf16)pv;
+          for (int i = 0; i < 16; i += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i], scale_log2, -m_run));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i + 1], scale_log2, -m_run));
+            const uint32_t pk = pack_bf2(p0, p1);
+            pb[2 * kb + (i >> 3)][i & 7] = __builtin_bit_cast(__bf16, (uint16_t)(pk & 0xffffu));
+            pb[2 * kb + (i >> 3)][(i & 7) + 1] = __builtin_bit_cast(__bf16, (uint16_t)(pk >> 16));
+            rs[(i >> 1) & 3] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones,
+                                                               rs[(i >> 1) & 3], false);
           }
         l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
       }
