@@ -131,6 +131,10 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   const int group = wave >> 2;
   const int qr = q0 + wave * 32 + l32;
   const int qrc = min(qr, q1 - 1);
+  // a wavefront whose 32 rows all lie past the item's end (the short last item of a run) skips
+  // its fragment reads, MFMAs and softmax; it still issues its share of the tile loads and
+  // joins every barrier
+  const bool rows_live = q0 + wave * 32 < q1;
 
   bf16x8_t qf[NS];
   {
@@ -229,6 +233,10 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
     const int t_mfma = p >> 1;            // A: p = 2t; B: p = 2t + 1
     const int t_valu = (p - 1) >> 1;      // A: p = 2t + 1 (odd); B: p = 2t + 2 (even)
     if (group == (p & 1)) {
+      if (!rows_live) {
+        // descriptors of this group's next VALU phase (tile t_mfma)
+        dma_ks = tiles[toff + min(t_mfma + kRing - 1, T - 1)].x;
+      } else {
       // MFMA phase of tile t: O^T += V(t-1)^T P(t-1)^T, S(t)^T = K(t) Q^T (16 + 16 MFMAs at D = 128).
       // t = 0 has no PV and t = T no QK: those phases run on a zero tile / discard the scores,
       // so the phase is one branch-free block. Fragment reads run eight MFMAs ahead.
@@ -266,13 +274,14 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
       // descriptors of this group's next VALU phase (tile t): its DMA issue and its mask
       dma_ks = tiles[toff + min(t + kRing - 1, T - 1)].x;
       mask = t < T ? tiles[toff + t].y : 0;
+      }
     } else {
       // VALU phase of tile t: first this group's tile loads (three tiles ahead), then the softmax
       // in base 2, one query per lane. The running max m_run moves only when this tile's max
       // exceeds it by more than 2^kLazy: probabilities stay below 2^kLazy (exact softmax either
       // way, a common shift cancels in O / l) and most tiles skip the rescale.
       tile_dma(dma_ks, (t_valu + kRing - 1) & (kRing - 1));
-      const bool work = p >= 1 + group && t_valu < T;
+      const bool work = rows_live && p >= 1 + group && t_valu < T;
       if (work) {
         const int lo = mask & 0xffff, hi = mask >> 16;
         if (lo > 0 || hi < kBN) {
