@@ -3,6 +3,10 @@
 //   qk_rmsnorm : the block's q_norm / k_norm over the head dim (vdn_h3/hybrid.py:271-273 with
 //                rope_freqs=None), y = bf16(x * rsqrt(mean(x^2) + eps) * w), fp32 statistics,
 //                written to separate normalised copies (the VDN branch reads the raw q / k);
+//                with rope_freqs (vdn_h3/hybrid.py:274-292, the fused RMSNorm + split-half RoPE
+//                the reference calls), the normalised fp32 vector y is rotated before its one
+//                rounding: for i < rot/2 the pair (y_i, y_{i+rot/2}) becomes F_i (y_i, y_{i+rot/2})
+//                with F_i the row's 2x2 matrix [[f00, f01], [f10, f11]]; channels >= rot pass;
 //   head_gate  : apply_softmax_gate (vdn_h3/softmax_kernels.py:8-9), out = bf16(O * g) per
 //                (row, head), flattened to [S, H*D].
 //
@@ -27,13 +31,16 @@ __device__ __forceinline__ u32x4_t pack8(const float *y) {
 }
 
 // One thread = 8 consecutive channels of one head vector. vec indexes (row, which, head) with
-// which = 0 for q, 1 for k; grid covers seq * 2 * heads vectors.
-template <int D>
+// which = 0 for q, 1 for k; grid covers seq * 2 * heads vectors. ROPE: freqs element
+// (row, i, r, c) at freqs[row * f_row + 4 i + 2 r + c] (f_row = 0: one set for every row); the
+// partner channel i +- rot/2 lives rot/16 lanes away in the same lane group.
+template <int D, bool ROPE>
 __global__ __launch_bounds__(256) void qk_rmsnorm_kernel(const uint16_t *__restrict__ q, int64_t q_row,
                                                          int64_t q_head, const uint16_t *__restrict__ k,
                                                          int64_t k_row, int64_t k_head,
                                                          const uint16_t *__restrict__ wq,
                                                          const uint16_t *__restrict__ wk, float eps,
+                                                         const float *__restrict__ freqs, int64_t f_row, int rot,
                                                          uint16_t *__restrict__ qo, int64_t qo_row, int64_t qo_head,
                                                          uint16_t *__restrict__ ko, int64_t ko_row, int64_t ko_head,
                                                          int64_t n_vec, int heads) {
@@ -59,6 +66,25 @@ __global__ __launch_bounds__(256) void qk_rmsnorm_kernel(const uint16_t *__restr
   const float r = 1.f / sqrtf(ss / (float)D + eps);
 #pragma unroll
   for (int j = 0; j < 8; ++j) y[j] = x[j] * r * wf[j];
+  if constexpr (ROPE) {
+    const int half = rot >> 1, step = half >> 3;  // rot is a multiple of 16 (host check)
+    const bool first = 8 * c < half, rotated = 8 * c < rot;
+    const int lane = __lane_id();
+    const int partner = first ? lane + step : lane - step;
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = __shfl(y[j], rotated ? partner : lane);
+    if (rotated) {
+      const int i0 = first ? 8 * c : 8 * c - half;       // pair index of channel 8c
+      const float *f = freqs + row * f_row + 4 * i0 + (first ? 0 : 2);  // matrix row 0 or 1
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a = f[4 * j], b = f[4 * j + 1];
+        // first half: out_i = f00 y_i + f01 y_{i+h}; second half: out_{i+h} = f10 y_i + f11 y_{i+h}
+        y[j] = first ? fmaf(a, y[j], b * o[j]) : fmaf(a, o[j], b * y[j]);
+      }
+    }
+  }
   st16(dst + 8 * c, pack8(y));
 }
 
@@ -93,11 +119,12 @@ int check_rows(const void *p, int64_t row, int64_t head, const char *name) {
 }  // namespace
 }  // namespace vdnh3
 
-extern "C" int vdnh3_qk_rmsnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
-                                int64_t k_head, const uint16_t *q_weight, const uint16_t *k_weight, float eps,
-                                uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
-                                int64_t ko_head, int seq, int heads, int head_dim, void *stream) {
-  using namespace vdnh3;
+namespace vdnh3 {
+namespace {
+int qk_norm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row, int64_t k_head,
+            const uint16_t *q_weight, const uint16_t *k_weight, float eps, const float *freqs, int64_t f_row,
+            int rot, uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
+            int64_t ko_head, int seq, int heads, int head_dim, void *stream) {
   VDNH3_HOST_CHECK(head_dim == 64 || head_dim == 128, VDNH3_ERR_INVALID,
                    "qk_rmsnorm supports head_dim 64 or 128, got %d", head_dim);
   VDNH3_HOST_CHECK(seq > 0 && heads > 0, VDNH3_ERR_INVALID, "qk_rmsnorm: seq and heads must be positive");
@@ -108,17 +135,51 @@ extern "C" int vdnh3_qk_rmsnorm(const uint16_t *q, int64_t q_row, int64_t q_head
   if (!rc) rc = check_rows(q_weight, 0, 0, "q_weight");
   if (!rc) rc = check_rows(k_weight, 0, 0, "k_weight");
   if (rc) return rc;
+  if (freqs) {
+    VDNH3_HOST_CHECK(rot > 0 && rot % 16 == 0 && rot <= head_dim, VDNH3_ERR_INVALID,
+                     "rope: rot_dim must be a positive multiple of 16 and at most head_dim %d, got %d", head_dim,
+                     rot);
+    VDNH3_HOST_CHECK(f_row >= 0 && reinterpret_cast<uintptr_t>(freqs) % 4 == 0, VDNH3_ERR_INVALID,
+                     "rope: bad frequency row stride or alignment");
+  }
   const int64_t n_vec = (int64_t)seq * 2 * heads;
   const int64_t threads = n_vec * (head_dim / 8);
   const dim3 grid((unsigned)((threads + 255) / 256));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(qk_rmsnorm_kernel<128>, grid, dim3(256), 0, s, q, q_row, q_head, k, k_row, k_head, q_weight,
-                       k_weight, eps, q_out, qo_row, qo_head, k_out, ko_row, ko_head, n_vec, heads);
-  else
-    hipLaunchKernelGGL(qk_rmsnorm_kernel<64>, grid, dim3(256), 0, s, q, q_row, q_head, k, k_row, k_head, q_weight,
-                       k_weight, eps, q_out, qo_row, qo_head, k_out, ko_row, ko_head, n_vec, heads);
+#define VDNH3_QKN(D, R)                                                                                        \
+  hipLaunchKernelGGL((qk_rmsnorm_kernel<D, R>), grid, dim3(256), 0, s, q, q_row, q_head, k, k_row, k_head,     \
+                     q_weight, k_weight, eps, freqs, f_row, rot, q_out, qo_row, qo_head, k_out, ko_row, ko_head, \
+                     n_vec, heads)
+  if (head_dim == 128) {
+    if (freqs) VDNH3_QKN(128, true);
+    else VDNH3_QKN(128, false);
+  } else {
+    if (freqs) VDNH3_QKN(64, true);
+    else VDNH3_QKN(64, false);
+  }
+#undef VDNH3_QKN
   return check_launch("qk_rmsnorm");
+}
+}  // namespace
+}  // namespace vdnh3
+
+extern "C" int vdnh3_qk_rmsnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
+                                int64_t k_head, const uint16_t *q_weight, const uint16_t *k_weight, float eps,
+                                uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
+                                int64_t ko_head, int seq, int heads, int head_dim, void *stream) {
+  return vdnh3::qk_norm(q, q_row, q_head, k, k_row, k_head, q_weight, k_weight, eps, nullptr, 0, 0, q_out, qo_row,
+                        qo_head, k_out, ko_row, ko_head, seq, heads, head_dim, stream);
+}
+
+extern "C" int vdnh3_qk_rmsnorm_rope(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k,
+                                     int64_t k_row, int64_t k_head, const uint16_t *q_weight,
+                                     const uint16_t *k_weight, float eps, const float *freqs, int64_t freqs_row,
+                                     int rot_dim, uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out,
+                                     int64_t ko_row, int64_t ko_head, int seq, int heads, int head_dim,
+                                     void *stream) {
+  VDNH3_HOST_CHECK(freqs != nullptr, VDNH3_ERR_INVALID, "rope: null frequencies");
+  return vdnh3::qk_norm(q, q_row, q_head, k, k_row, k_head, q_weight, k_weight, eps, freqs, freqs_row, rot_dim,
+                        q_out, qo_row, qo_head, k_out, ko_row, ko_head, seq, heads, head_dim, stream);
 }
 
 extern "C" int vdnh3_head_gate(const uint16_t *o, int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row,

@@ -66,6 +66,9 @@ SIGNATURES = {
     "vdnh3_fill_rows_bf16": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_float, _vp]),
     "vdnh3_qk_rmsnorm": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _c_float,
                                   _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp]),
+    "vdnh3_qk_rmsnorm_rope": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _c_float, _vp, _c_i64,
+                                       _c_int, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int,
+                                       _vp]),
     "vdnh3_head_gate": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _vp]),
 }
 

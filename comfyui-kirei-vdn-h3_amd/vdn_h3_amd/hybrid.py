@@ -7,7 +7,7 @@ layout contract (the request-local ``VDNLayout``; without one the original forwa
 and the same exception types. Per call, on the caller's current stream:
 
   qkv = attn.qkv_proj(x)                         raw q / k / v views [S, H, D]
-  q, k = q_norm(q_raw), k_norm(k_raw)            one HIP pass into a separate buffer
+  q, k = q_norm(q_raw), k_norm(k_raw) [+ RoPE]   one HIP pass into a separate buffer
   g = sigmoid(x W_g^T + b_g)                     [S, H], GEMM with a sigmoid epilogue
   flat = bf16(window_attention(q, k, v) * g)     one HIP kernel, the gate in its epilogue
   out = attn.out_proj(flat)
@@ -16,8 +16,9 @@ and the same exception types. Per call, on the caller's current stream:
 The branch runs after ``out_proj`` here (the reference computes it first and adds it last):
 the sum is the same bf16 addition, ``bf16(out + bf16(delta))``. A full-cover layout runs
 dense attention and no branch (``:422``, ``:495-499``). The path is inference-only
-(``torch.no_grad`` / ``inference_mode``); RoPE (``rope_freqs`` not ``None``) is not
-implemented on the HIP path and raises ``RuntimeError``.
+(``torch.no_grad`` / ``inference_mode``). With ``rope_freqs`` the q/k pass also applies the
+split-half rotary embedding (``vdn_h3/hybrid.py:274-292``; ``rope_table`` gives the layout),
+with the q_norm epsilon for both, as the reference does.
 """
 
 from __future__ import annotations
@@ -125,9 +126,33 @@ class VDNState:
     close = release
 
 
+def rope_table(rope_freqs: torch.Tensor, seq: int, head_dim: int, device) -> tuple[torch.Tensor, int, int]:
+    """``(table, row_stride, rot_dim)`` of ``rope_freqs`` for ``vdnh3_qk_rmsnorm_rope``.
+
+    ``rope_freqs`` holds one 2x2 matrix per (row, pair): shape ``[..., rot_dim/2, 2, 2]`` whose
+    leading dims hold one entry per row (``seq`` in total, e.g. ``[1, seq, 1, ...]``) or one entry
+    shared by every row; ``rot_dim = 2 * rope_freqs.shape[-3]`` (``vdn_h3/hybrid.py:283``).
+    """
+    if rope_freqs.ndim < 3 or tuple(rope_freqs.shape[-2:]) != (2, 2):
+        raise ValueError(f"rope_freqs must end in [rot_dim/2, 2, 2], got {tuple(rope_freqs.shape)}")
+    half = int(rope_freqs.shape[-3])
+    rot = 2 * half
+    if rot % 16 or rot > head_dim:
+        raise ValueError(f"rope rot_dim {rot} must be a multiple of 16 and at most head_dim {head_dim}")
+    rows = rope_freqs.numel() // (4 * half)
+    if rows not in (1, seq):
+        raise ValueError(f"rope_freqs holds {rows} row entries; expected 1 or {seq}")
+    table = rope_freqs.reshape(rows, half, 2, 2).to(device=device, dtype=torch.float32).contiguous()
+    return table, (0 if rows == 1 else 4 * half), rot
+
+
 def normalise_qk(q_raw: torch.Tensor, k_raw: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
-                 eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
-    """``attn.q_norm(q), attn.k_norm(k)`` (RMSNorm over the head dim) into one new ``[S, 2, H, D]`` buffer."""
+                 eps: float = 1e-6, rope_freqs: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``attn.q_norm(q), attn.k_norm(k)`` (RMSNorm over the head dim) into one new ``[S, 2, H, D]`` buffer.
+
+    With ``rope_freqs`` the normalised vectors are also rotated (split-half RoPE, the fused op of
+    ``vdn_h3/hybrid.py:274-292``), before their one rounding to bf16.
+    """
     if q_raw.shape != k_raw.shape or q_raw.ndim != 3:
         raise ValueError("q and k must share shape [sequence, heads, dim]")
     device = _lib.require_device(q_raw, k_raw, q_weight, k_weight)
@@ -139,6 +164,14 @@ def normalise_qk(q_raw: torch.Tensor, k_raw: torch.Tensor, q_weight: torch.Tenso
         raise ValueError(f"q/k norm weights must have {dim} entries")
     buf = torch.empty((seq, 2, heads, dim), dtype=torch.bfloat16, device=device)
     qn, kn = buf[:, 0], buf[:, 1]
+    if rope_freqs is not None:
+        table, row_stride, rot = rope_table(rope_freqs, seq, dim, device)
+        rc = _lib.lib().vdnh3_qk_rmsnorm_rope(
+            _lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), _lib.ptr(k_raw), k_raw.stride(0), k_raw.stride(1),
+            _lib.ptr(wq), _lib.ptr(wk), float(eps), _lib.ptr(table), row_stride, rot, _lib.ptr(qn), qn.stride(0),
+            qn.stride(1), _lib.ptr(kn), kn.stride(0), kn.stride(1), seq, heads, dim, _lib.stream_handle(device))
+        _lib.check(rc, "vdnh3_qk_rmsnorm_rope")
+        return qn, kn
     rc = _lib.lib().vdnh3_qk_rmsnorm(_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), _lib.ptr(k_raw),
                                      k_raw.stride(0), k_raw.stride(1), _lib.ptr(wq), _lib.ptr(wk), float(eps),
                                      _lib.ptr(qn), qn.stride(0), qn.stride(1), _lib.ptr(kn), kn.stride(0),
@@ -181,8 +214,6 @@ def make_vdn_forward(attn: Any, state: VDNState, block_index: int):
             raise RuntimeError(f"VDN layout has {layout.seq_len} rows but attention received {x.shape[0]}")
         if torch.is_grad_enabled():
             raise RuntimeError("the MI355X VDN-H3 block is inference-only; run it under torch.no_grad()")
-        if rope_freqs is not None:
-            raise RuntimeError("RoPE execution is not implemented on the MI355X VDN-H3 path (rope_freqs must be None)")
         linear_active = bool(config.get("linear_enabled", True)) and not layout.full_cover
         gate_enabled = bool(config.get("enable_softmax_gate", True))
         device = x.device
@@ -194,7 +225,7 @@ def make_vdn_forward(attn: Any, state: VDNState, block_index: int):
         qw, q_eps = _norm_weight_eps(attn.q_norm, head_dim, device)
         kw, _ = _norm_weight_eps(attn.k_norm, head_dim, device)
         with scope("attention.rope_norm", device):
-            query, key = normalise_qk(q_raw, k_raw, qw, kw, q_eps)
+            query, key = normalise_qk(q_raw, k_raw, qw, kw, q_eps, rope_freqs=rope_freqs)
 
         gate = None
         if gate_enabled:

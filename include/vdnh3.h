@@ -272,6 +272,22 @@ int vdnh3_qk_rmsnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uin
                      int64_t ko_head, int seq, int heads, int head_dim, void *stream);
 
 /*
+ * The same with RoPE (vdn_h3/hybrid.py:274-292: the fused RMSNorm + split-half rotary embedding
+ * the reference runs when rope_freqs is given, comfy-kitchen rms_rope_split_half_ with
+ * rot_dim = 2 * rope_freqs.shape[-3] and the q_norm epsilon for both). After the RMSNorm and
+ * weight (fp32, not rounded), for i < rot_dim / 2 the pair (y_i, y_{i + rot_dim/2}) is replaced
+ * by F (y_i, y_{i + rot_dim/2}) with F the 2x2 matrix of (row, i): element (r, c) at
+ * freqs[row*freqs_row + 4*i + 2*r + c] (fp32; freqs_row = 0 shares one set across rows);
+ * channels >= rot_dim pass unchanged; one bf16 rounding at the end. rot_dim: a multiple of 16,
+ * at most head_dim.
+ */
+int vdnh3_qk_rmsnorm_rope(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
+                          int64_t k_head, const uint16_t *q_weight, const uint16_t *k_weight, float eps,
+                          const float *freqs, int64_t freqs_row, int rot_dim, uint16_t *q_out, int64_t qo_row,
+                          int64_t qo_head, uint16_t *k_out, int64_t ko_row, int64_t ko_head, int seq, int heads,
+                          int head_dim, void *stream);
+
+/*
  * apply_softmax_gate (vdn_h3/softmax_kernels.py:8-9): out[s][h*D + d] = bf16(O[s][h][d] * gate[s][h])
  * with O a [seq, heads, head_dim] bf16 view and gate bf16 (element (s, h) at gate[s*gate_row + h]).
  * The window attention kernel fuses the same gate into its epilogue; this is the standalone op.

@@ -3,12 +3,14 @@
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
 Restates the inference spelling of ``make_vdn_forward.vdn_forward``
-(``vdn_h3/hybrid.py:409-579``) for ``rope_freqs=None``:
+(``vdn_h3/hybrid.py:409-579``):
 
 * ``qkv``             -> ``_qkv`` (``vdn_h3/hybrid.py:260-268``): one projection, split into
   ``[S, H, D]`` views of the raw q / k / v;
 * ``rms_norm_bf16``   -> ``attn.q_norm`` / ``attn.k_norm`` (``vdn_h3/hybrid.py:271-273``): an
   ``F.rms_norm`` over the head dim, fp32 statistics, ``x * rsqrt(mean x^2 + eps) * w`` rounded once;
+* ``rms_rope_split_half`` -> the same with RoPE (``vdn_h3/hybrid.py:274-292``) when ``rope_freqs``
+  is given (parity unpinned: the comfy-kitchen op is absent);
 * the branch          -> ``oracle.branch_oracle.projected_delta`` on the *raw* video rows, with
   ``skip_ends = (anchor_frames == "both")`` and the text rows as text state (``:443-477``);
 * attention           -> ``oracle.window_oracle.window_attention_grouped`` on the normalised
@@ -43,6 +45,26 @@ def rms_norm_bf16(x, weight, eps=1e-6):
     return (xf * r * weight.float()).to(x.dtype)
 
 
+def rms_rope_split_half(x, weight, eps, freqs, rot_dim, rounded=True):
+    """RMSNorm + split-half rotary embedding (``vdn_h3/hybrid.py:274-292``, the fused comfy-kitchen op).
+
+    ``y = x * rsqrt(mean x^2 + eps) * w`` in fp32; for ``i < rot_dim / 2`` the pair
+    ``(y_i, y_{i + rot_dim/2})`` becomes ``F (y_i, y_{i + rot_dim/2})`` with ``F = freqs[row, i]``
+    (``[rows or 1, rot_dim/2, 2, 2]``); channels ``>= rot_dim`` pass; one bf16 rounding unless
+    ``rounded`` is false. PARITY UNPINNED against comfy-kitchen (absent, version unpinned): pinned
+    by closed forms only (identity, quarter turn, inverse rotation, per-pair norm).
+    """
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + eps) * weight.float()
+    half = rot_dim // 2
+    f = freqs.float().reshape(-1, 1, half, 2, 2)                  # [rows or 1, 1 (heads), half, 2, 2]
+    a, b = y[..., :half], y[..., half:rot_dim]
+    out = y.clone()
+    out[..., :half] = f[..., 0, 0] * a + f[..., 0, 1] * b
+    out[..., half:rot_dim] = f[..., 1, 0] * a + f[..., 1, 1] * b
+    return out.to(x.dtype) if rounded else out
+
+
 def qkv(x, weight, heads, head_dim, project=None):
     """``_qkv``: the fused projection split into three ``[S, H, D]`` tensors."""
     projected = project(x) if project is not None else bo.linear_bf16(x, weight)
@@ -54,7 +76,7 @@ def qkv(x, weight, heads, head_dim, project=None):
 
 def vdn_forward(x, layout, attn_weights, branch_weights, heads, head_dim, *, eps=1e-6, gate_enabled=True,
                 linear_enabled=True, text_state=True, project_qkv=None, project_out=None, branch_projector=None,
-                return_parts=False):
+                return_parts=False, rope_freqs=None, short_conv=()):
     """Block output ``[S, hidden]`` bf16 for ``x`` ``[S, hidden]`` bf16 and a ``VDNLayout``-like ``layout``.
 
     ``attn_weights``: ``qkv_proj.weight``, ``out_proj.weight``, ``q_norm.weight``, ``k_norm.weight``.
@@ -71,9 +93,14 @@ def vdn_forward(x, layout, attn_weights, branch_weights, heads, head_dim, *, eps
         delta = bo.projected_delta(branch_weights, x[va:vb], q_raw[va:vb], k_raw[va:vb], v_raw[va:vb],
                                    layout.num_frames, layout.tokens_per_frame, list(layout.bounds),
                                    frame_size=layout.frame_size, skip_ends=layout.anchor_frames == "both",
-                                   projector=branch_projector, **kw)
-    query = rms_norm_bf16(q_raw, attn_weights["q_norm.weight"], eps)
-    key = rms_norm_bf16(k_raw, attn_weights["k_norm.weight"], eps)
+                                   projector=branch_projector, short_conv=short_conv, fused_conv=True, **kw)
+    if rope_freqs is None:
+        query = rms_norm_bf16(q_raw, attn_weights["q_norm.weight"], eps)
+        key = rms_norm_bf16(k_raw, attn_weights["k_norm.weight"], eps)
+    else:
+        rot = 2 * int(rope_freqs.shape[-3])
+        query = rms_rope_split_half(q_raw, attn_weights["q_norm.weight"], eps, rope_freqs, rot)
+        key = rms_rope_split_half(k_raw, attn_weights["k_norm.weight"], eps, rope_freqs, rot)
     scale = head_dim ** -0.5
     if layout.full_cover:
         soft = wo.window_attention_grouped(query, key, v_raw, 0, x.shape[0], 1, x.shape[0], [(0, 0)], scale, "none")

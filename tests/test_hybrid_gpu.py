@@ -191,3 +191,54 @@ def test_qk_rmsnorm_and_softmax_gate_ops(device):
         g = torch.sigmoid(synth.randn((seq, heads), 64)).to(torch.bfloat16)
         got = apply_softmax_gate(o.to(device), g.to(device).unsqueeze(-1))
         assert torch.equal(got.cpu(), (o * g.unsqueeze(-1)).reshape(seq, heads * dim))
+
+
+@pytest.mark.parametrize("dim,rot,shared", [(128, 128, False), (128, 64, True), (64, 64, False), (64, 32, False)])
+def test_qk_rmsnorm_rope_op(device, dim, rot, shared):
+    """Fused RMSNorm + split-half RoPE vs the oracle (one bf16 rounding; fp32 FMA order may move it)."""
+    from vdn_h3_amd import synth
+    from vdn_h3_amd.hybrid import normalise_qk
+
+    print(f"case qk rmsnorm+rope D={dim} rot={rot} shared={shared}", flush=True)
+    seq, heads = 777, 3
+    qkv = (3 * synth.randn((seq, 3 * heads * dim), 65)).to(torch.bfloat16)
+    q, k, _ = synth.split_qkv(qkv, heads, dim)
+    wq = (1 + 0.1 * synth.randn((dim,), 66)).to(torch.bfloat16)
+    wk = (1 + 0.1 * synth.randn((dim,), 67)).to(torch.bfloat16)
+    rows = 1 if shared else seq
+    theta = synth.randn((rows, rot // 2), 68) * 3
+    c, s_ = torch.cos(theta), torch.sin(theta)
+    freqs = torch.stack([torch.stack([c, -s_], -1), torch.stack([s_, c], -1)], -2)
+    freqs = freqs.reshape(1, rows, 1, rot // 2, 2, 2)                       # a ComfyUI-style broadcast shape
+    dq, dk, _ = synth.split_qkv(qkv.to(device), heads, dim)
+    qn, kn = normalise_qk(dq, dk, wq.to(device), wk.to(device), 1e-6, rope_freqs=freqs.to(device))
+    for got, x, w in ((qn, q, wq), (kn, k, wk)):
+        want = ho.rms_rope_split_half(x, w, 1e-6, freqs, rot).float()
+        exact = ho.rms_rope_split_half(x, w, 1e-6, freqs, rot, rounded=False)
+        g32 = got.cpu().float()
+        # one bf16 step at the exact value, plus fp32 rounding of the rotation's two terms (|y| <~ 8)
+        # for results that nearly cancel: the kernel fuses a * y + b * y' into one FMA
+        ulp = torch.ldexp(torch.ones_like(want), torch.frexp(exact)[1] - 8) + 2.0 ** -19
+        excess = ((g32 - exact).abs() / ulp).max().item()
+        assert excess <= 1.0, excess
+        assert (g32 == want).float().mean().item() >= 0.99
+
+
+def test_block_with_rope_vs_oracle(device):
+    """The block forward with rope_freqs (RoPE on the softmax q/k; the branch reads the raw q/k)."""
+    print("case hybrid block with rope", flush=True)
+    heads, dim, hidden = 4, 128, 512
+    layout, x, aw, bw = _synthetic(13, (16, 16), 64, heads, dim, hidden, seed=9)
+    g = torch.Generator().manual_seed(90)
+    theta = torch.randn(layout.seq_len, dim // 2, generator=g) * 3
+    c, s_ = torch.cos(theta), torch.sin(theta)
+    freqs = torch.stack([torch.stack([c, -s_], -1), torch.stack([s_, c], -1)], -2).reshape(
+        1, layout.seq_len, 1, dim // 2, 2, 2)
+    forward, _ = _block(aw, {k: v.to(device) for k, v in bw.items()}, heads, dim, device)
+    from vdn_h3_amd.hybrid import forward_scope
+
+    with torch.no_grad(), forward_scope(layout):
+        out = forward(x.to(device), rope_freqs=freqs.to(device))
+    torch.cuda.synchronize()
+    torch.set_num_threads(16)
+    _parity(out, ho.vdn_forward(x, layout, aw, bw, heads, dim, rope_freqs=freqs), "block with rope vs oracle")

@@ -104,3 +104,45 @@ def test_full_cover_skips_branch_and_runs_dense():
     half = (dense.to(torch.bfloat16).float() * 0.5).to(torch.bfloat16)
     torch.testing.assert_close(parts["flat"].reshape(half.shape).float(), half.float(), atol=2 * 2.0 ** -8, rtol=0)
     torch.testing.assert_close(out.float(), bo.linear_bf16(parts["flat"], aw["out_proj.weight"]).float())
+
+
+def _rope_case(rows, heads, dim, rot, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = (2 * torch.randn(rows, heads, dim, generator=g)).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).to(torch.bfloat16)
+    theta = torch.randn(rows, rot // 2, generator=g) * 3
+    c, s_ = torch.cos(theta), torch.sin(theta)
+    freqs = torch.stack([torch.stack([c, -s_], -1), torch.stack([s_, c], -1)], -2)   # [rows, rot/2, 2, 2]
+    return x, w, theta, freqs
+
+
+@pytest.mark.parametrize("dim,rot", [(128, 128), (128, 64), (64, 32)])
+def test_rms_rope_closed_forms(dim, rot):
+    """The split-half RoPE restatement: identity, quarter turn, inverse rotation, per-pair norms."""
+    rows, heads, half = 37, 3, rot // 2
+    x, w, theta, freqs = _rope_case(rows, heads, dim, rot, 70 + dim + rot)
+    plain = ho.rms_norm_bf16(x, w, 1e-6)
+    eye = torch.eye(2).expand(rows, half, 2, 2)
+    assert torch.equal(ho.rms_rope_split_half(x, w, 1e-6, eye, rot), plain)
+    # a quarter turn maps (y_i, y_{i+h}) to (-y_{i+h}, y_i) exactly: pairing and matrix layout
+    quarter = torch.tensor([[0.0, -1.0], [1.0, 0.0]]).expand(1, half, 2, 2)
+    got = ho.rms_rope_split_half(x, w, 1e-6, quarter, rot)
+    assert torch.equal(got[..., :half], -plain[..., half:rot])
+    assert torch.equal(got[..., half:rot], plain[..., :half])
+    assert torch.equal(got[..., rot:], plain[..., rot:])
+    # rotating by theta then by -theta returns the normalised vector; pair norms are kept
+    y = ho.rms_rope_split_half(x, w, 1e-6, freqs, rot, rounded=False)
+    back_freqs = freqs.transpose(-1, -2)                                  # R(-theta) = R(theta)^T
+    yplain = ho.rms_rope_split_half(x, w, 1e-6, eye, rot, rounded=False)
+    a, b = y[..., :half], y[..., half:rot]
+    fb = back_freqs.reshape(rows, 1, half, 2, 2)
+    a0 = fb[..., 0, 0] * a + fb[..., 0, 1] * b
+    b0 = fb[..., 1, 0] * a + fb[..., 1, 1] * b
+    torch.testing.assert_close(a0, yplain[..., :half], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(b0, yplain[..., half:rot], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(a * a + b * b, yplain[..., :half] ** 2 + yplain[..., half:rot] ** 2,
+                               atol=1e-4, rtol=1e-5)
+    # a planted mistake (interleaved pairs instead of split halves) fails the quarter-turn check
+    yi = plain.float()
+    inter = torch.stack([-yi[..., 1:rot:2], yi[..., 0:rot:2]], -1).reshape(rows, heads, rot).to(torch.bfloat16)
+    assert not torch.equal(inter, got[..., :rot])
