@@ -16,7 +16,8 @@ stage in ``config.work_per_step``); ``roofline`` is the window attention kernel 
 kernel), timed with HIP events on the stream it runs on; ``stages_ms`` are per-stage event
 timings of the same timed steps.
 
-Other workloads: ``window`` (attention alone), ``branch`` (VDN branch alone),
+Other workloads: ``stack`` (50 blocks x ``--steps`` denoising steps, ``x <- x + block(rms_norm(x))``; use
+``--steps 8 --warmup 1`` for the 8-step pass), ``window`` (attention alone), ``branch`` (VDN branch alone),
 ``gemm_{i8,f8}_{qkv,out}`` (W8A8 GEMMs alone), ``hbm_copy`` (counter calibration).
 ``cpu_baseline`` times the CPU oracle on a bounded sample of query rows.
 """
@@ -47,8 +48,9 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="block", choices=["block", "window", "hbm_copy", "branch", "gemm_i8_qkv",
-                                                             "gemm_i8_out", "gemm_f8_qkv", "gemm_f8_out"],
+    ap.add_argument("--workload", default="block", choices=["block", "stack", "window", "hbm_copy", "branch",
+                                                             "gemm_i8_qkv", "gemm_i8_out", "gemm_f8_qkv",
+                                                             "gemm_f8_out"],
                     help="hbm_copy: a plain 1 GiB device copy, the reference point for scaling rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes")
     ap.add_argument("--short-conv", default="k,v",
@@ -275,6 +277,89 @@ def bench_block(args, torch, device):
     }
 
 
+def _block_parts(torch, device, heads, dim, hidden, seed, conv):
+    """Random-init attention module and int8-prepared branch weights of one block."""
+    from types import SimpleNamespace
+
+    from vdn_h3_amd import projection, synth
+    from vdn_h3_amd.linear import HipLinear
+
+    attn = SimpleNamespace(
+        heads=heads, head_dim=dim, forward=None,
+        qkv_proj=HipLinear(synth.randn((3 * heads * dim, hidden), seed + 1, device, torch.bfloat16, 0.02), "int8"),
+        out_proj=HipLinear(synth.randn((hidden, heads * dim), seed + 2, device, torch.bfloat16, 0.02), "int8"),
+        q_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), seed + 3, device)).to(torch.bfloat16),
+                               eps=1e-6),
+        k_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), seed + 4, device)).to(torch.bfloat16),
+                               eps=1e-6))
+    (bw,), _ = projection.prepare_projection_maps(
+        [synth.branch_weights(heads, dim, hidden, device=device, seed=seed + 42, short_conv=conv)], device, "int8")
+    return attn, bw
+
+
+def bench_stack(args, torch, device):
+    """The 50-block hybrid attention stack over one 8-step denoising pass (x <- x + block(rms_norm(x)))."""
+    from vdn_h3_amd import synth
+    from vdn_h3_amd.hybrid import VDNState, forward_scope, make_vdn_forward
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+
+    w = synth.WINDOW_FULL
+    lay = w.layout
+    heads, dim, hidden, blocks = w.heads, w.head_dim, 5120, 50
+    conv = _short_conv(args)
+    parts = [_block_parts(torch, device, heads, dim, hidden, 1000 * (i + 1), conv) for i in range(blocks)]
+    branches = [OptimizedLinearBranch(bw, heads, dim, short_conv=conv) for _, bw in parts]
+    state = VDNState("bench-stack", {"enable_softmax_gate": True, "linear_enabled": True,
+                                     "enable_text_state": True}, branches, heads, dim,
+                     projection_precision="int8")
+    forwards = [make_vdn_forward(attn, state, i) for i, (attn, _) in enumerate(parts)]
+    x0 = synth.randn((lay.seq_len, hidden), 0, device=device, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream(device)
+
+    def denoise_step(x):
+        # pre-norm residual, as H3's blocks normalise their input before attention: random-init
+        # blocks fed the raw stream would double it per block and overflow within the pass
+        for fwd in forwards:
+            x = x + fwd(torch.nn.functional.rms_norm(x, (hidden,), eps=1e-6))
+        return x
+
+    with torch.no_grad(), forward_scope(lay):
+        x = x0.clone()
+        for _ in range(args.warmup):
+            x = denoise_step(x)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        x = x0.clone()
+        ev[0].record(stream)
+        for i in range(args.steps):
+            x = denoise_step(x)
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+    step_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
+    total_ms = ev[0].elapsed_time(ev[-1])
+    plan = state.window_cache.plan(lay.seq_len, lay.video_start, lay.video_end, lay.num_frames,
+                                   lay.tokens_per_frame, lay.bounds, lay.anchor_frames, device)
+    work = block_flops(lay, heads, dim, hidden, plan.pairs_per_head, conv)
+    per_block = sum(work.values())
+    total_work = per_block * blocks * args.steps
+    finite = bool(torch.isfinite(x).all().item())
+    return {
+        "metric": "VDN-H3 50-block hybrid attention stack, 8-step denoising pass: ms per step + TFLOP/s, 1 GPU",
+        "value": round(total_work / (total_ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(total_ms / args.steps, 3),
+        "dtype": "int8+bf16",
+        "config": {"workload": "stack_50blocks_s40688_h40_d128_hidden5120_int8proj", "blocks": blocks,
+                   "denoising_steps": args.steps, "seq_len": lay.seq_len, "heads": heads, "head_dim": dim,
+                   "hidden": hidden, "branch_short_conv": ",".join(conv) or "none",
+                   "residual": "x <- x + block(rms_norm(x)) per block (bf16, torch rms_norm)", "work_per_block": per_block},
+        "total_ms": round(total_ms, 2),
+        "step_ms": [round(v, 3) for v in step_ms],
+        "block_ms_mean": round(total_ms / (args.steps * blocks), 4),
+        "output_finite": finite,
+    }
+
+
 def bench_gemm(args, torch, device):
     """W8A8 projection GEMM at the block's shapes: M=40,688 tokens, K=5,120, N=15,360 (qkv) or 5,120 (out)."""
     from vdn_h3_amd import linear, synth
@@ -408,6 +493,8 @@ def main():
             result["cpu_baseline"] = cpu_baseline_window(torch, qkv, w, w.layout, args.cpu_sample_rows)
             result["cpu_baseline"]["sample"] += (" - the window attention stage, 63% of the block's work; "
                                                  "the value is that stage's CPU throughput")
+    elif args.workload == "stack":
+        result = bench_stack(args, torch, device)
     elif args.workload == "hbm_copy":
         result = bench_hbm_copy(args, torch, device)
     elif args.workload == "branch":
