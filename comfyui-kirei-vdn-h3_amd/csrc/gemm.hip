@@ -261,14 +261,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
   // holds chunk slot ^ swz(row) of that row. Load instruction q (0..3) of a wavefront covers
   // positions 256 q + tid, i.e. rows 64 q + tid / 4. Rows past M (N) read the last row; their
   // results are not stored.
+  // The source of a load is a wave-uniform base (the tile's first row, advanced by the stage)
+  // plus a per-lane 32-bit byte offset that stays the same for every stage (the host checks
+  // that 256 rows of A and B span less than 4 GB).
   const int lrow = tid >> 2;
   const int lchunk = gemm_slot(lrow, tid & 3);
-  const uint8_t *a_src[4], *b_src[4];
+  uint32_t a_off[4], b_off[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    a_src[q] = A + (int64_t)min(m0 + 64 * q + lrow, M - 1) * lda_b + lchunk * 16;
-    b_src[q] = B + (int64_t)min(n0 + 64 * q + lrow, N - 1) * ldb_b + lchunk * 16;
+    a_off[q] = (uint32_t)((min(m0 + 64 * q + lrow, M - 1) - m0) * lda_b + lchunk * 16);
+    b_off[q] = (uint32_t)((min(n0 + 64 * q + lrow, N - 1) - n0) * ldb_b + lchunk * 16);
   }
+  const uint8_t *a_tile = A + (int64_t)m0 * lda_b, *b_tile = B + (int64_t)n0 * ldb_b;
   // load q (0..7) of stage st into ring slot `slot`: A rows 64 q .. +64 (q < 4), else B rows
   // 64 (q - 4) .. +64
   const uint32_t lds_wave = lds_address(&smem[0][0][0]) + wave * 64 * 16;
@@ -276,7 +280,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
     const int64_t off = (int64_t)st * kGemmSK;
     const int i = q & 3;
     const uint32_t dst = lds_wave + (uint32_t)(((q >> 2) * kGemmStages + slot) * STAGE_BYTES + i * kGemmThreads * 16);
-    global_to_lds16_at((q >= 4 ? b_src[i] : a_src[i]) + off, dst);
+    global_to_lds16_sbase((q >= 4 ? b_tile : a_tile) + off, q >= 4 ? b_off[i] : a_off[i], dst);
   };
 
   // fragment byte offsets inside an operand's stage (rows 32 i + l32 share l32's swizzle):
@@ -442,6 +446,8 @@ int launch_gemm(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                    VDNH3_ERR_INVALID, "gemm: leading dimensions must cover K/N and be 16-byte multiples");
   VDNH3_HOST_CHECK(reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0,
                    VDNH3_ERR_INVALID, "gemm: A and B must be 16-byte aligned");
+  VDNH3_HOST_CHECK((int64_t)kGemmBM * lda * eb < (int64_t(1) << 32) && (int64_t)kGemmBN * ldb * eb < (int64_t(1) << 32),
+                   VDNH3_ERR_INVALID, "gemm: a 256-row panel of A or B must span less than 4 GB");
   const int tiles_m = (M + kGemmBM - 1) / kGemmBM, tiles_n = (N + kGemmBN - 1) / kGemmBN;
   const int total = tiles_m * tiles_n, per_xcd = (total + 7) / 8;
   hipLaunchKernelGGL(gemm_nt_kernel<KIND>, dim3(per_xcd * 8), dim3(kGemmThreads), 0, stream,
