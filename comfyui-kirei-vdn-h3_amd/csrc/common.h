@@ -41,6 +41,55 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
+// ---- exact SiLU in bf16 and the W8A8 quantisation codes (device) ---------------------
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+
+// True when fp32 value y lies within 32 ulp of a bf16 rounding midpoint (its low 16 bits
+// near 0x8000): only there can an approximation with a smaller error round differently.
+__device__ __forceinline__ bool near_bf16_midpoint(float y) {
+  return ((__float_as_uint(y) & 0xffffu) - 0x7fe0u) < 0x40u;
+}
+
+// bf16(SiLU(x)) as fp32, bit-identical to round_bf(silu_f(x)): the hardware exp2 / reciprocal
+// form is within ~15 ulp of x / (1 + e^-x) for |x| <= 16 (argument rounding of -x log2(e),
+// v_exp_f32, 1 + e, v_rcp_f32, the product), so it rounds to the same bf16 value unless it
+// lies near a midpoint; those values and |x| > 16 take the exact expression.
+__device__ __forceinline__ float silu_bf(float x) {
+  const float y = x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+  if (__builtin_expect(fabsf(x) > 16.f || near_bf16_midpoint(y), 0)) return round_bf(silu_f(x));
+  return round_bf(y);
+}
+
+constexpr float kF8Max = 448.f;
+constexpr float kI8Max = 127.f;
+
+// fp32 (finite, |x| <= 448) -> OCP e4m3fn code, round to nearest even.
+__device__ __forceinline__ uint32_t e4m3_code(float x) {
+  const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
+  const float a = fabsf(x);
+  uint32_t code;
+  if (a < 0.015625f) {
+    // zero and subnormals: multiples of 2^-9; rounding up to 8 gives the smallest normal (0x08)
+    code = (uint32_t)rintf(a * 512.f);
+  } else {
+    uint32_t ua = __float_as_uint(a);
+    ua += 0x7ffffu + ((ua >> 20) & 1u);  // keep 3 mantissa bits, ties to even (carries into the exponent)
+    code = (((ua >> 23) - 120u) << 3) | ((ua >> 20) & 7u);
+  }
+  return sign | code;
+}
+
+// int8 code of x / scale: round half to even, clamp to +-127
+__device__ __forceinline__ uint32_t i8_code(float x) {
+  return (uint32_t)(int32_t)fminf(fmaxf(rintf(x), -kI8Max), kI8Max) & 0xffu;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
 // ---- MFMA wrappers ------------------------------------------------------------------
 // 32x32x16 bf16 -> fp32. Lane l holds A[m = l%32][k = 8*(l/32) + j], B[k = 8*(l/32) + j][n = l%32]
 // for j = 0..7, and C[m = 8*(i/4) + 4*(l/32) + i%4][n = l%32] for i = 0..15.

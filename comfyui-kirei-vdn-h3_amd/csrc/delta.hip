@@ -18,24 +18,6 @@
 namespace vdnh3 {
 namespace {
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
-
-// True when fp32 value y lies within 32 ulp of a bf16 rounding midpoint (its low 16 bits
-// near 0x8000): only there can an approximation with a smaller error round differently.
-__device__ __forceinline__ bool near_bf16_midpoint(float y) {
-  return ((__float_as_uint(y) & 0xffffu) - 0x7fe0u) < 0x40u;
-}
-
-// bf16(SiLU(x)) as fp32, bit-identical to round_bf(silu_f(x)): the hardware exp2 / reciprocal
-// form is within ~15 ulp of x / (1 + e^-x) for |x| <= 16 (argument rounding of -x log2(e),
-// v_exp_f32, 1 + e, v_rcp_f32, the product), so it rounds to the same bf16 value unless it
-// lies near a midpoint; those values and |x| > 16 take the exact expression.
-__device__ __forceinline__ float silu_bf(float x) {
-  const float y = x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
-  if (__builtin_expect(fabsf(x) > 16.f || near_bf16_midpoint(y), 0)) return round_bf(silu_f(x));
-  return round_bf(y);
-}
-
 // bf16(s / n) as fp32, bit-identical to round_bf(s / n); rn = 1 / n (correctly rounded), so
 // s * rn is within 1.5 ulp of the quotient.
 __device__ __forceinline__ float div_bf(float s, float n, float rn) {

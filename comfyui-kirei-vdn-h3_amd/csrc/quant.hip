@@ -15,35 +15,6 @@
 namespace vdnh3 {
 namespace {
 
-constexpr float kF8Max = 448.f;
-constexpr float kI8Max = 127.f;
-
-// fp32 (finite, |x| <= 448) -> OCP e4m3fn code, round to nearest even.
-__device__ __forceinline__ uint32_t e4m3_code(float x) {
-  const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
-  const float a = fabsf(x);
-  uint32_t code;
-  if (a < 0.015625f) {
-    // zero and subnormals: multiples of 2^-9; rounding up to 8 gives the smallest normal (0x08)
-    code = (uint32_t)rintf(a * 512.f);
-  } else {
-    uint32_t ua = __float_as_uint(a);
-    ua += 0x7ffffu + ((ua >> 20) & 1u);  // keep 3 mantissa bits, ties to even (carries into the exponent)
-    code = (((ua >> 23) - 120u) << 3) | ((ua >> 20) & 7u);
-  }
-  return sign | code;
-}
-
-__device__ __forceinline__ uint32_t i8_code(float x) {
-  return (uint32_t)(int32_t)fminf(fmaxf(rintf(x), -kI8Max), kI8Max) & 0xffu;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-
 // One wavefront per row (4 rows per 256-thread workgroup). Two sweeps over the row: amax,
 // then quantise (the second sweep is served from L2).
 template <int KIND>

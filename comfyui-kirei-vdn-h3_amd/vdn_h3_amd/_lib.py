@@ -69,6 +69,12 @@ SIGNATURES = {
     "vdnh3_qk_rmsnorm_rope": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _c_float, _vp, _c_i64,
                                        _c_int, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int,
                                        _vp]),
+    "vdnh3_rmsnorm_modulate": (_c_int, [_vp, _c_i64, _vp, _c_float, _vp, _vp, _c_i64, _c_int, _vp, _vp, _c_i64,
+                                        _c_int, _c_int, _vp]),
+    "vdnh3_gated_residual": (_c_int, [_vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp, _c_i64, _vp, _c_i64, _c_int,
+                                      _c_int, _vp]),
+    "vdnh3_swiglu": (_c_int, [_vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp]),
+    "vdnh3_swiglu_quant_rows": (_c_int, [_c_int, _vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _vp]),
     "vdnh3_head_gate": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _vp]),
 }
 

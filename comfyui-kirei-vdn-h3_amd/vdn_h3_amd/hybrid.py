@@ -48,7 +48,7 @@ class VDNState:
     def __init__(self, name: str, config: Mapping[str, Any], branches: Sequence[Any], num_heads: int,
                  head_dim: int, *, attention_backend: str = "hip", weight_maps=None, inference: bool = True,
                  projection_precision: str = "bf16", projection_info: Any = None, diagnostics: bool = False,
-                 **_runtime):
+                 block_fusion: bool = False, **_runtime):
         if attention_backend not in _window.ATTENTION_BACKENDS:
             raise ValueError(f"unsupported attention backend {attention_backend!r}")
         if projection_precision not in _projection.PROJECTION_PRECISIONS:
@@ -69,6 +69,7 @@ class VDNState:
         self.last_layout = None
         self.branch_execution = "serial"
         self.diagnostics = DiagnosticsRecorder(diagnostics)
+        self.block_fusion = bool(block_fusion)
         if weight_maps is None:
             maps = []
             for index, branch in enumerate(self.branches):
@@ -109,6 +110,10 @@ class VDNState:
             return cached
         return {k: cached[k] for k in keys if k in cached}
 
+    @property
+    def weight_mode(self):
+        return "resident"
+
     def mark_weights_consumed(self, index, device, dtype):
         del index, device, dtype
 
@@ -121,6 +126,10 @@ class VDNState:
     def release(self):
         self._resident.clear()
         self.window_cache.release()
+        if self.block_fusion:
+            from .block_kernels import release_block_fusions
+
+            release_block_fusions(self)
         return self
 
     close = release
@@ -299,6 +308,9 @@ def apply_vdn(model_patcher: Any, state: VDNState):
     for index, block in enumerate(blocks):
         model_patcher.add_object_patch(f"diffusion_model.blocks.{index}.attn.forward",
                                        make_vdn_forward(block.attn, state, index))
+    from .block_kernels import install_block_fusions
+
+    install_block_fusions(model_patcher, state, blocks)
     return model_patcher
 
 

@@ -295,6 +295,35 @@ int vdnh3_qk_rmsnorm_rope(const uint16_t *q, int64_t q_row, int64_t q_head, cons
 int vdnh3_head_gate(const uint16_t *o, int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row,
                     uint16_t *out, int64_t out_row, int seq, int heads, int head_dim, void *stream);
 
+/* ------------------------------------------------------------------------------
+ * DiT block pointwise passes around attention and the MLP (reference vdn_h3/block_kernels.py)
+ * Every op rounds to bf16 where the reference's torch op returns a bf16 tensor. `idx[row]`
+ * (int32) selects the modulation row of each token (BlockPointwiseCache.indices,
+ * vdn_h3/block_kernels.py:25-82); modulation tables are [n, hidden], fp32 (rounded to bf16 on
+ * load, the reference's .to(bf16)) or bf16 (mod_bf16 / gate_bf16 = 1), row stride mod_row.
+ * hidden is a multiple of 8; bf16 rows and tables are 16-byte aligned.
+ * ------------------------------------------------------------------------------ */
+
+/* _pre_body (vdn_h3/block_kernels.py:85-89): out = bf16(bf16(n * bf16(1 + scale[idx])) +
+ * shift[idx]) with n = F.rms_norm(x, weight, eps) (fp32 statistics, one rounding); hidden <= 8192. */
+int vdnh3_rmsnorm_modulate(const uint16_t *x, int64_t x_row, const uint16_t *weight, float eps, const void *scale,
+                           const void *shift, int64_t mod_row, int mod_bf16, const int32_t *idx, uint16_t *out,
+                           int64_t out_row, int rows, int hidden, void *stream);
+
+/* _post_body (vdn_h3/block_kernels.py:92-93): out = bf16(x + bf16(gate[idx] * branch)); out may be x. */
+int vdnh3_gated_residual(const uint16_t *x, int64_t x_row, const void *gate, int64_t gate_row, int gate_bf16,
+                         const int32_t *idx, const uint16_t *branch, int64_t branch_row, uint16_t *out,
+                         int64_t out_row, int rows, int hidden, void *stream);
+
+/* _swiglu_body (vdn_h3/block_kernels.py:113-116): with h = [gate | up] ([rows, 2 ffn]),
+ * out = bf16(bf16(silu(gate)) * up). */
+int vdnh3_swiglu(const uint16_t *h, int64_t h_row, int rows, int ffn, uint16_t *out, int64_t out_row, void *stream);
+
+/* The SwiGLU output quantised row-wise for a W8A8 fc2 (kind 1 int8, 2 fp8 e4m3fn), equal to
+ * vdnh3_quant_rows(kind, swiglu(h)) without materialising the bf16 activation. */
+int vdnh3_swiglu_quant_rows(int kind, const uint16_t *h, int64_t h_row, int rows, int ffn, uint8_t *q, int64_t q_row,
+                            float *scale, void *stream);
+
 /* Fill rows x cols of a bf16 matrix with a constant (anchor-frame rows of the branch output). */
 int vdnh3_fill_rows_bf16(uint16_t *p, int64_t ld, int rows, int cols, float value, void *stream);
 

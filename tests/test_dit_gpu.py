@@ -1,0 +1,150 @@
+"""Parity of the DiT block pointwise kernels and the fused block forward with the oracle (GPU).
+
+The pointwise passes follow the reference's bf16 ops, so they are compared element by element
+(bit-exact where every input of an op is exact, otherwise within one bf16 step where the fp32
+statistics of the RMSNorm or the exponential of SiLU may round a midpoint differently); the
+whole block against the north-star bar (max-abs 2e-2, cosine >= 0.9995).
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import branch_oracle as bo
+from oracle import dit_oracle as do
+from oracle import quant_oracle as qo
+
+pytestmark = pytest.mark.gpu
+
+
+def _steps(got, want):
+    g, w = got.float().cpu(), want.float()
+    ulp = torch.ldexp(torch.ones_like(w), torch.frexp(w)[1] - 8).clamp_min(2.0 ** -133)
+    return (g - w).abs() / ulp
+
+
+def _case(rows, hidden, n_mod, seed, mod_dtype):
+    g = torch.Generator().manual_seed(seed)
+    x = (2 * torch.randn(rows, hidden, generator=g)).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16)
+    scale = (0.3 * torch.randn(n_mod, hidden, generator=g)).to(mod_dtype)
+    shift = (0.3 * torch.randn(n_mod, hidden, generator=g)).to(mod_dtype)
+    idx = torch.randint(0, n_mod, (rows,), generator=g)
+    return x, w, scale, shift, idx
+
+
+@pytest.mark.parametrize("hidden,mod_dtype", [(5120, torch.float32), (192, torch.bfloat16), (8192, torch.float32)])
+def test_rmsnorm_modulate(device, hidden, mod_dtype):
+    from vdn_h3_amd import block_kernels as bk
+
+    print(f"case rmsnorm_modulate hidden={hidden} {mod_dtype}", flush=True)
+    x, w, scale, shift, idx = _case(300, hidden, 3, 1, mod_dtype)
+    got = bk.rmsnorm_modulate(x.to(device), w.to(device), 1e-6, scale.to(device), shift.to(device),
+                              idx.to(torch.int32).to(device))
+    want = do.pre(x, w, 1e-6, scale, shift, idx)
+    steps = _steps(got, want)
+    assert steps.max().item() <= 2, steps.max().item()
+    assert (steps == 0).float().mean().item() >= 0.99
+
+
+@pytest.mark.parametrize("gate_dtype", [torch.float32, torch.bfloat16])
+def test_gated_residual(device, gate_dtype):
+    from vdn_h3_amd import block_kernels as bk
+
+    print(f"case gated_residual {gate_dtype}", flush=True)
+    x, _, gate, _, idx = _case(257, 5120, 4, 2, gate_dtype)
+    b = torch.randn(x.shape, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    want = do.post(x, gate, idx, b)
+    dx = x.to(device)
+    got = bk.gated_residual(dx, gate.to(device), idx.to(torch.int32).to(device), b.to(device))
+    assert torch.equal(got.cpu(), want)
+    bk.gated_residual(dx, gate.to(device), idx.to(torch.int32).to(device), b.to(device), out=dx)  # in place
+    assert torch.equal(dx.cpu(), want)
+
+
+def test_swiglu_and_fused_quantisation(device):
+    from vdn_h3_amd import block_kernels as bk
+    from vdn_h3_amd import linear
+
+    print("case swiglu + quantisation", flush=True)
+    h = (3 * torch.randn(333, 2 * 1040, generator=torch.Generator().manual_seed(4))).to(torch.bfloat16)
+    dh = h.to(device)
+    got = bk.swiglu(dh)
+    steps = _steps(got, do.swiglu(h))
+    assert steps.max().item() <= 1 and (steps == 0).float().mean().item() >= 0.999
+    for kind in (linear.KIND_I8, linear.KIND_F8):
+        q, s = bk.swiglu_quantize_rows(dh, kind)
+        q2, s2 = linear.quantize_rows(got, kind)
+        assert torch.equal(q.view(torch.uint8).cpu(), q2.view(torch.uint8).cpu()) and torch.equal(s.cpu(), s2.cpu())
+    wq, ws = qo.int8_quantize_rows(got.cpu())
+    q, s = bk.swiglu_quantize_rows(dh, linear.KIND_I8)
+    assert torch.equal(q.cpu(), wq) and torch.equal(s.cpu().reshape(-1), ws.reshape(-1))
+
+
+def _block(hidden, ffn, heads, device, precision, seed=5):
+    from vdn_h3_amd.diagnostics import DiagnosticsRecorder
+    from vdn_h3_amd.linear import HipLinear
+
+    g = torch.Generator().manual_seed(seed)
+    w = {"attn": (0.05 * torch.randn(hidden, hidden, generator=g)).to(torch.bfloat16),
+         "fc1": (0.05 * torch.randn(2 * ffn, hidden, generator=g)).to(torch.bfloat16),
+         "fc2": (0.05 * torch.randn(hidden, ffn, generator=g)).to(torch.bfloat16),
+         "norm1": (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16),
+         "norm2": (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16)}
+    mod = tuple(0.3 * torch.randn(2, hidden, generator=g) for _ in range(6))
+    attn_lin = HipLinear(w["attn"].to(device), "bf16")
+    calls = []
+
+    def attn(h, rope_freqs=None, transformer_options=None):
+        calls.append(rope_freqs)
+        return attn_lin(h)
+
+    block = SimpleNamespace(
+        norm1=SimpleNamespace(weight=w["norm1"].to(device), eps=1e-6),
+        norm2=SimpleNamespace(weight=w["norm2"].to(device), eps=1e-6),
+        adaln_proj=lambda t_emb: tuple(m.to(device) for m in mod),
+        attn=attn,
+        mlp=SimpleNamespace(fc1=HipLinear(w["fc1"].to(device), "bf16"), fc2=HipLinear(w["fc2"].to(device), precision)),
+        forward=lambda *a, **k: "original")
+    state = SimpleNamespace(block_fusion=True, inference=True, weight_mode="resident",
+                            diagnostics=DiagnosticsRecorder(False))
+    return block, state, w, mod, calls
+
+
+@pytest.mark.parametrize("precision", ["bf16", "int8"])
+def test_fast_block_forward_vs_oracle(device, precision):
+    from vdn_h3_amd.block_kernels import make_fast_block_forward
+
+    print(f"case fast block forward fc2={precision}", flush=True)
+    hidden, ffn, rows = 512, 1024, 300
+    block, state, w, mod, calls = _block(hidden, ffn, 4, device, precision)
+    x = torch.randn(rows, hidden, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    segments = [(0, 40, 0), (40, rows, 1)]
+    forward = make_fast_block_forward(block, state, 0)
+    with torch.no_grad():
+        got = forward(x.to(device), torch.zeros(1), segments, "freqs")
+    torch.cuda.synchronize()
+    assert calls == ["freqs"]
+
+    def fc2(a):
+        if precision == "bf16":
+            return bo.linear_bf16(a, w["fc2"])
+        wq, ws = qo.int8_quantize_rows(w["fc2"])
+        return qo.int8_linear(*qo.int8_quantize_rows(a), wq, ws.reshape(1, -1))
+
+    want = do.block_forward(x, mod, segments, w["norm1"], w["norm2"], lambda h: bo.linear_bf16(h, w["attn"]),
+                            lambda h: bo.linear_bf16(h, w["fc1"]), fc2)
+    g32, w32 = got.float().cpu(), want.float()
+    err = (g32 - w32).abs().max().item()
+    cos = F.cosine_similarity(g32.flatten().double(), w32.flatten().double(), dim=0).item()
+    print(f"fast block {precision}: max abs {err:.3e}, cosine {cos:.7f}", flush=True)
+    # max-abs 2e-2, or one bf16 step of the largest output where that step is coarser
+    assert err <= max(2e-2, w32.abs().max().item() * 2.0 ** -7) and cos >= 0.9995
+    # the reference's fallbacks: an explicit attention callable, or fusion switched off
+    assert forward(x.to(device), torch.zeros(1), segments, None, attention=object()) == "original"
+    state.block_fusion = False
+    assert forward(x.to(device), torch.zeros(1), segments, None) == "original"
