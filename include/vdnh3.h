@@ -296,6 +296,23 @@ int vdnh3_head_gate(const uint16_t *o, int64_t o_row, int64_t o_head, const uint
                     uint16_t *out, int64_t out_row, int seq, int heads, int head_dim, void *stream);
 
 /* ------------------------------------------------------------------------------
+ * Token-level chunked Gated DeltaNet (chunk 64). No counterpart in the reference, whose Video
+ * Delta Attention solves its delta rule per frame (vdn_h3/branch.py:148-160): this is the
+ * published Gated DeltaNet recurrence in chunk (WY) form, per head with an fp32 state S (dv x dk):
+ *   S_t = a_t S_{t-1} (I - b_t k_t k_t^T) + b_t v_t k_t^T,  o_t = S_t q_t,  a_t = exp(log_decay_t)
+ * q, k, v: [tokens, heads, 128] bf16 views (element (t, h, d) at p[t*row + h*head + d]);
+ * beta, log_decay: fp32 (element (t, h) at p[t*row + h]); out: bf16 like q; initial_state /
+ * final_state: fp32 [heads][128][128] (dv rows, dk columns) or NULL (zero start / not written).
+ * workspace: vdnh3_gdn_workspace_bytes(tokens, heads, 128) bytes, 16-byte aligned.
+ * ------------------------------------------------------------------------------ */
+size_t vdnh3_gdn_workspace_bytes(int tokens, int heads, int head_dim);
+int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
+                        int64_t k_head, const uint16_t *v, int64_t v_row, int64_t v_head, const float *beta,
+                        int64_t beta_row, const float *log_decay, int64_t decay_row, const float *initial_state,
+                        float *final_state, uint16_t *out, int64_t o_row, int64_t o_head, int tokens, int heads,
+                        int head_dim, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------------------------
  * DiT block pointwise passes around attention and the MLP (reference vdn_h3/block_kernels.py)
  * Every op rounds to bf16 where the reference's torch op returns a bf16 tensor. `idx[row]`
  * (int32) selects the modulation row of each token (BlockPointwiseCache.indices,

@@ -1,0 +1,74 @@
+"""Parity of the chunked Gated DeltaNet kernels with the float64 oracle (GPU).
+
+Not reference parity: the reference has no token-level delta rule (its branch is per frame).
+Bars: cosine >= 0.9995 and max-abs within max(2e-2, 2^-6 * max|o|) (a few bf16 steps of the
+largest output: q, k K^T, W, U~, P and U enter the MFMAs in bf16) for the outputs; the final
+fp32 state within 1e-2 relative to its largest entry.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import gdn_oracle as go
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(tokens, heads, seed, decay_scale):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(tokens, heads, 128, generator=g).to(torch.bfloat16)
+    k = F.normalize(torch.randn(tokens, heads, 128, generator=g), dim=-1).to(torch.bfloat16)
+    v = torch.randn(tokens, heads, 128, generator=g).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(tokens, heads, generator=g))
+    lg = -F.softplus(torch.randn(tokens, heads, generator=g)) * decay_scale
+    return q, k, v, beta, lg
+
+
+def _check(got, want, what):
+    g32, w = got.float().cpu().double(), want.double()
+    err = (g32 - w).abs().max().item()
+    cos = F.cosine_similarity(g32.flatten(), w.flatten(), dim=0).item()
+    bar = max(2e-2, 2.0 ** -6 * w.abs().max().item())
+    print(f"{what}: max abs {err:.3e} (bar {bar:.3e}), cosine {cos:.7f}", flush=True)
+    assert torch.isfinite(g32).all() and err <= bar and cos >= 0.9995, what
+
+
+@pytest.mark.parametrize("tokens,heads,decay,init", [(300, 3, 0.05, True), (64, 2, 0.05, False),
+                                                     (1000, 2, 1.0, False), (129, 1, 0.0, True)])
+def test_gdn_matches_recurrence(device, tokens, heads, decay, init):
+    from vdn_h3_amd.gdn import chunk_gated_delta_rule
+
+    print(f"case gdn T={tokens} H={heads} decay x{decay} init={init}", flush=True)
+    q, k, v, beta, lg = _inputs(tokens, heads, tokens + heads, decay)
+    s0 = torch.randn(heads, 128, 128, generator=torch.Generator().manual_seed(7)) * 0.1 if init else None
+    want, s_want = go.recurrence(q, k, v, beta, lg, s0)
+    fused = torch.cat([q, k, v], dim=-1).to(device)                  # strided q / k / v views
+    dq, dk, dv = fused[..., :128], fused[..., 128:256], fused[..., 256:]
+    out, s_got = chunk_gated_delta_rule(dq, dk, dv, beta.to(device), lg.to(device),
+                                        initial_state=None if s0 is None else s0.to(device), output_final_state=True)
+    torch.cuda.synchronize()
+    _check(out, want, "gdn output")
+    s_err = (s_got.cpu().double() - s_want).abs().max().item()
+    assert s_err <= 1e-2 * s_want.abs().max().item(), s_err
+
+
+def test_gdn_full_shape_sampled_heads(device):
+    """40,688 tokens x 40 heads (the chunk-64 benchmark shape); heads 0 and 39 against the oracle."""
+    from vdn_h3_amd.gdn import chunk_gated_delta_rule
+
+    print("case gdn full shape", flush=True)
+    tokens, heads = 40688, 40
+    g = torch.Generator(device=device).manual_seed(11)
+    q = torch.randn(tokens, heads, 128, generator=g, device=device).to(torch.bfloat16)
+    k = F.normalize(torch.randn(tokens, heads, 128, generator=g, device=device), dim=-1).to(torch.bfloat16)
+    v = torch.randn(tokens, heads, 128, generator=g, device=device).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(tokens, heads, generator=g, device=device))
+    lg = -F.softplus(torch.randn(tokens, heads, generator=g, device=device))
+    out, _ = chunk_gated_delta_rule(q, k, v, beta, lg)
+    torch.cuda.synchronize()
+    sel = [0, 39]
+    want, _ = go.chunked(q[:, sel].cpu(), k[:, sel].cpu(), v[:, sel].cpu(), beta[:, sel].cpu(), lg[:, sel].cpu())
+    _check(out[:, sel], want, "gdn full shape heads 0, 39")
