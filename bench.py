@@ -18,7 +18,8 @@ timings of the same timed steps.
 
 Other workloads: ``stack`` (50 blocks x ``--steps`` denoising steps, ``x <- x + block(rms_norm(x))``; use
 ``--steps 8 --warmup 1`` for the 8-step pass), ``window`` (attention alone), ``branch`` (VDN branch alone),
-``gemm_{i8,f8}_{qkv,out}`` (W8A8 GEMMs alone), ``hbm_copy`` (counter calibration).
+``gemm_{i8,f8}_{qkv,out}`` (W8A8 GEMMs alone), ``gdn`` (token-level chunk-64 Gated DeltaNet),
+``hbm_copy`` (counter calibration).
 ``cpu_baseline`` times the CPU oracle on a bounded sample of query rows.
 """
 
@@ -50,7 +51,7 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="block", choices=["block", "stack", "window", "hbm_copy", "branch",
                                                              "gemm_i8_qkv", "gemm_i8_out", "gemm_f8_qkv",
-                                                             "gemm_f8_out"],
+                                                             "gemm_f8_out", "gdn"],
                     help="hbm_copy: a plain 1 GiB device copy, the reference point for scaling rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes")
     ap.add_argument("--short-conv", default="k,v",
@@ -444,6 +445,64 @@ def bench_branch(args, torch, device):
     }
 
 
+def bench_gdn(args, torch, device):
+    """Token-level chunk-64 Gated DeltaNet (the delta rule over all tokens, not per frame) at 40,688 x 40 x 128."""
+    import torch.nn.functional as F
+
+    from vdn_h3_amd import _lib
+    from vdn_h3_amd.gdn import gdn_flops
+
+    tokens, heads, dim = 40688, 40, 128
+    g = torch.Generator(device=device).manual_seed(50)
+    qkv = torch.randn(tokens, heads, 3 * dim, generator=g, device=device).to(torch.bfloat16)
+    q, v = qkv[..., :dim], qkv[..., 2 * dim:]
+    k = qkv[..., dim:2 * dim]
+    k.copy_(F.normalize(k.float(), dim=-1).to(torch.bfloat16))
+    beta = torch.sigmoid(torch.randn(tokens, heads, generator=g, device=device))
+    lg = -F.softplus(torch.randn(tokens, heads, generator=g, device=device))
+    out = torch.empty((tokens, heads, dim), dtype=torch.bfloat16, device=device)
+    lib = _lib.lib()
+    ws_bytes = lib.vdnh3_gdn_workspace_bytes(tokens, heads, dim)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device)
+    sh = _lib.stream_handle(device)
+
+    def step():
+        _lib.check(lib.vdnh3_gdn_chunk_fwd(
+            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(v), v.stride(0),
+            v.stride(1), _lib.ptr(beta), beta.stride(0), _lib.ptr(lg), lg.stride(0), None, None, _lib.ptr(out),
+            out.stride(0), out.stride(1), tokens, heads, dim, _lib.ptr(ws), ws_bytes, sh), "gdn")
+
+    ms = _time_steps(torch, stream, args.steps, args.warmup, step)
+    flops = gdn_flops(tokens, heads, dim)
+    io_bytes = 4.0 * tokens * heads * dim * 2 + 2.0 * tokens * heads * 4     # q, k, v in; o out; beta, g in
+    gbs = io_bytes / (ms * 1e-3) / 1e9
+    result = {
+        "metric": "chunk-64 Gated DeltaNet forward ms + TFLOP/s at 40,688 tok x 40 heads x 128, 1 GPU",
+        "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+        "dtype": "bf16",
+        "config": {"workload": "gdn_chunk64_t40688_h40_d128", "tokens": tokens, "heads": heads, "head_dim": dim,
+                   "chunk": 64, "flop_per_step": flops, "io_bytes_per_step": io_bytes,
+                   "workspace_bytes": ws_bytes},
+        "roofline": {"bound": "hbm", "kernel": "gdn_prep_kernel + gdn_scan_kernel", "achieved": round(gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": _traffic(args.traffic_json, "gdn")},
+    }
+    if args.cpu_sample_rows > 0:
+        from oracle import gdn_oracle as go
+
+        sel = list(range(heads))
+        hq, hk, hv, hb, hg = (t[:, sel].cpu() for t in (q, k, v, beta, lg))
+        t0 = time.perf_counter()
+        go.chunked(hq, hk, hv, hb, hg)
+        dt = time.perf_counter() - t0
+        result["cpu_baseline"] = {
+            "value": round(gdn_flops(tokens, len(sel), dim) / dt / 1e12, 5), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port", "seconds": round(dt, 2),
+            "sample": f"the whole workload: all {tokens} tokens x {heads} heads, float64 chunk-form oracle (oracle/gdn_oracle.py)"}
+    return result
+
+
 def cpu_baseline_window(torch, qkv, w, lay, n_rows):
     """Time the CPU oracle (``oracle.window_oracle``) on ``n_rows`` query rows of the same problem."""
     from oracle import window_oracle as wo
@@ -501,6 +560,8 @@ def main():
         result = bench_branch(args, torch, device)
     elif args.workload.startswith("gemm_"):
         result = bench_gemm(args, torch, device)
+    elif args.workload == "gdn":
+        result = bench_gdn(args, torch, device)
     else:
         result = bench_window(args, torch, device)
     line = {
