@@ -7,23 +7,85 @@
 // output as a bf16 tensor; the temporal sum, SiLU and norm stay in fp32 up to the one final
 // rounding, as in the reference's fused temporal kernel.
 //
-// One workgroup owns the D channels of one head on a TX x TY tile of the frame grid and walks
-// the frames in order. Per frame it stages the raw tile with its halo in LDS (the next frame's
-// loads are in flight during the arithmetic), forms the spatial sums, keeps the last KT of them
-// per position in registers (bf16 pairs) and emits the temporal output of frame f - KT/2.
-// D/4 lanes share one position, 4 channels (8 bytes) each, so the norm over the head is a
-// lane reduction; the filter taps of a lane's 4 channels live in registers.
+// One workgroup (1024 threads) owns the D channels of one head on a TX x TY tile of the frame
+// grid and walks the frames in order. Per frame it stages the raw tile with its halo in LDS (the
+// next frame's loads are in flight during the arithmetic), forms the spatial sums, keeps the last
+// KT of them per position in registers (bf16 pairs) and emits the temporal output of frame
+// f - KT/2. D/4 lanes share one position, 4 channels (8 bytes) each, so the norm over the head
+// is a DPP / swizzle reduction. Taps are bf16 pairs (t, t + 1) and v_dot2_f32_bf16 takes two
+// taps of one channel per instruction; one v_perm_b32 re-pairs two staged words by channel. The
+// spatial pairs sit in LDS (read once per row and frame), the temporal pairs in registers.
+// Workgroups are numbered XCD-aware: the tiles of one head run on one XCD, so the halo rows a
+// tile shares with its neighbours come from that XCD's L2 (HBM reads equal the input once).
+#include <type_traits>
+
 #include "common.h"
 
 namespace vdnh3 {
 namespace {
 
-constexpr int SC_THREADS = 512;
+constexpr int SC_THREADS = 1024;
 constexpr int SC_MAX_POS = 64;     // positions of one tile (TX * TY)
 constexpr int SC_MAX_STAGE = 160;  // staged positions, tile plus halo ((TX + 2P) * (TY + 2P))
 
-__device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+typedef __bf16 sc_bf16x2_t __attribute__((ext_vector_type(2)));
+// a.lo * b.lo + a.hi * b.hi + c over bf16 pairs, fp32 accumulate (v_dot2_f32_bf16)
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(sc_bf16x2_t, a), __builtin_bit_cast(sc_bf16x2_t, b), c,
+                                         false);
+}
+// (a.lo, b.lo) and (a.hi, b.hi) of two bf16-pair words, one v_perm_b32 each (selector bytes
+// 0-3 pick from the second operand, 4-7 from the first)
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+// sum over aligned groups of L lanes (16 or 32), every lane of a group gets the group's sum:
+// DPP quad xor 1, quad xor 2, half-row mirror, row mirror, then a swizzle xor 16
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+  auto dpp = [](float x, auto ctrl) __device__ {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  v += dpp(v, std::integral_constant<int, 0xb1>{});
+  v += dpp(v, std::integral_constant<int, 0x4e>{});
+  v += dpp(v, std::integral_constant<int, 0x141>{});
+  v += dpp(v, std::integral_constant<int, 0x140>{});
+  if constexpr (L == 32) v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+  return v;
+}
+
+// acc[4] (channels 4 cl .. 4 cl + 3) += sum over the NT taps of staged words src[0 .. NT) (each
+// u32x2: channels (0, 1) and (2, 3)) with tap pairs w[pr][channel] (odd last tap zero-padded)
+template <int NT>
+__device__ __forceinline__ void taps_dot2(const u32x2_t *src, const uint32_t (*w)[4], float *acc) {
+#pragma unroll
+  for (int pr = 0; pr < (NT + 1) / 2; ++pr) {
+#pragma unroll
+    for (int wi = 0; wi < 2; ++wi) {
+      const uint32_t a = src[2 * pr][wi];
+      uint32_t lo = a, hi = a;  // the odd last tap: the raw word against a zero-padded pair
+      if (2 * pr + 1 < NT) {
+        lo = pair_lo(a, src[2 * pr + 1][wi]);
+        hi = pair_hi(a, src[2 * pr + 1][wi]);
+      }
+      acc[2 * wi] = dot2_bf16(lo, w[pr][2 * wi], acc[2 * wi]);
+      acc[2 * wi + 1] = dot2_bf16(hi, w[pr][2 * wi + 1], acc[2 * wi + 1]);
+    }
+  }
+}
+
+// tap pairs of channel j (0..3 within a lane's 4) from NT bf16 taps: (t, t + 1) per pair, the
+// odd last tap on the half of its channel's position in the staged word
+template <int NT>
+__device__ __forceinline__ void load_tap_pairs(const uint16_t *taps, int j, uint32_t (*w)[4]) {
+#pragma unroll
+  for (int pr = 0; pr < NT / 2; ++pr)
+    w[pr][j] = (uint32_t)taps[2 * pr] | ((uint32_t)taps[2 * pr + 1] << 16);
+  if constexpr (NT & 1) {
+    const uint32_t last = taps[NT - 1];
+    w[NT / 2][j] = (j & 1) ? last << 16 : last;
+  }
+}
 
 template <int D, int KS, int KT>
 __global__ __launch_bounds__(SC_THREADS) void short_conv_kernel(
@@ -38,22 +100,38 @@ __global__ __launch_bounds__(SC_THREADS) void short_conv_kernel(
   constexpr int MAXL = (SC_MAX_STAGE * CPP + SC_THREADS - 1) / SC_THREADS;
   __shared__ __attribute__((aligned(16))) uint16_t tile[SC_MAX_STAGE * D];
 
-  const int h = blockIdx.x / n_tiles, ti = blockIdx.x - h * n_tiles;
+  // XCD-aware numbering: dispatch deals workgroups to the 8 XCDs round-robin; XCD x takes the
+  // x-th contiguous run of the logical order (head-major), so a head's tiles share one L2
+  const int nb = gridDim.x, per = nb >> 3, rem = nb & 7, xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int logical = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  const int h = logical / n_tiles, ti = logical - h * n_tiles;
   const int y0 = (ti / nx) * TY, x0 = (ti % nx) * TX;
   const int tid = threadIdx.x, cl = tid % LPP, ps = tid / LPP;
   const int SX = TX + 2 * P, SY = TY + 2 * P, n_stage = SX * SY * CPP;
   const int T = gh * gw;
 
-  // filter taps of this lane's 4 channels, fp32
-  float wsp[KS * KS][4], wtm[KT][4];
+  // filter taps of this lane's 4 channels: spatial as bf16 pairs (dx, dx + 1) per row, the odd
+  // last tap of a row paired with zero on the side of the other channel of its staged word
+  // (dot2 of the raw word then picks this channel); temporal in fp32
+  // The spatial pairs live in LDS as [dy][pair][lane group cl][4 channels] (one 16-byte read per
+  // pair and row, consecutive across cl), the temporal pairs in registers.
+  constexpr int NPR = (KS + 1) / 2;
+  __shared__ __attribute__((aligned(16))) uint32_t wlds[KS * NPR * LPP * 4];
+  if (tid < LPP) {
+    uint32_t row[NPR][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t c = (int64_t)h * D + 4 * cl + j;
+    for (int dy = 0; dy < KS; ++dy) {
 #pragma unroll
-    for (int t = 0; t < KS * KS; ++t) wsp[t][j] = bf2f(w_sp[c * KS * KS + t]);
+      for (int j = 0; j < 4; ++j) load_tap_pairs<KS>(w_sp + (((int64_t)h * D + 4 * tid + j) * KS + dy) * KS, j, row);
 #pragma unroll
-    for (int t = 0; t < KT; ++t) wtm[t][j] = bf2f(w_tm[c * KT + t]);
+      for (int pr = 0; pr < NPR; ++pr)
+        *reinterpret_cast<u32x4_t *>(wlds + ((dy * NPR + pr) * LPP + tid) * 4) =
+            u32x4_t{row[pr][0], row[pr][1], row[pr][2], row[pr][3]};
+    }
   }
+  uint32_t wtm[(KT + 1) / 2][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) load_tap_pairs<KT>(w_tm + ((int64_t)h * D + 4 * cl + j) * KT, j, wtm);
 
   // this thread's tile positions (one per pass); slots past the tile read position 0
   int lbase[NPASS];
@@ -69,20 +147,24 @@ __global__ __launch_bounds__(SC_THREADS) void short_conv_kernel(
     obase[i] = valid[i] ? (int64_t)((y0 + py) * gw + x0 + px) * o_row + (int64_t)h * o_head + 4 * cl : 0;
   }
 
-  // staging of frame f: chunk e = position (ly, lx) of the tile plus halo, 16-byte piece e % CPP
+  // staging of frame f: chunk e = position (ly, lx) of the tile plus halo, 16-byte piece e % CPP;
+  // its element offset inside a frame is the same for every frame (-1: outside the grid, zero)
+  int soff[MAXL];
+#pragma unroll
+  for (int u = 0; u < MAXL; ++u) {
+    const int e = tid + u * SC_THREADS;
+    soff[u] = -1;
+    if (e < n_stage) {
+      const int sp = e / CPP, ch = e - sp * CPP, ly = sp / SX, lx = sp - ly * SX;
+      const int gy = y0 + ly - P, gx = x0 + lx - P;
+      if (gy >= 0 && gy < gh && gx >= 0 && gx < gw) soff[u] = (gy * gw + gx) * (int)x_row + 8 * ch;
+    }
+  }
   u32x4_t pre[MAXL];
   auto stage_load = [&](int f) __device__ {
+    const uint16_t *xf = x + (int64_t)f * T * x_row + (int64_t)h * x_head;
 #pragma unroll
-    for (int u = 0; u < MAXL; ++u) {
-      const int e = tid + u * SC_THREADS;
-      pre[u] = u32x4_t{0, 0, 0, 0};
-      if (e < n_stage) {
-        const int sp = e / CPP, ch = e - sp * CPP, ly = sp / SX, lx = sp - ly * SX;
-        const int gy = y0 + ly - P, gx = x0 + lx - P;
-        if (gy >= 0 && gy < gh && gx >= 0 && gx < gw)
-          pre[u] = ld16(x + ((int64_t)f * T + gy * gw + gx) * x_row + (int64_t)h * x_head + 8 * ch);
-      }
-    }
+    for (int u = 0; u < MAXL; ++u) pre[u] = soff[u] >= 0 ? ld16(xf + soff[u]) : u32x4_t{0, 0, 0, 0};
   };
   auto stage_store = [&]() __device__ {
 #pragma unroll
@@ -106,22 +188,30 @@ __global__ __launch_bounds__(SC_THREADS) void short_conv_kernel(
       stage_store();
       __syncthreads();
       if (f + 1 < F) stage_load(f + 1);
+      float acc[NPASS][4];
+#pragma unroll
+      for (int i = 0; i < NPASS; ++i) acc[i][0] = acc[i][1] = acc[i][2] = acc[i][3] = 0.f;
+#pragma unroll
+      for (int dy = 0; dy < KS; ++dy) {
+        uint32_t wr[NPR][4];
+#pragma unroll
+        for (int pr = 0; pr < NPR; ++pr) {
+          const u32x4_t w4 = *reinterpret_cast<const u32x4_t *>(wlds + ((dy * NPR + pr) * LPP + cl) * 4);
+          wr[pr][0] = w4[0], wr[pr][1] = w4[1], wr[pr][2] = w4[2], wr[pr][3] = w4[3];
+        }
+#pragma unroll
+        for (int i = 0; i < NPASS; ++i) {
+          u32x2_t v[KS];
+#pragma unroll
+          for (int dx = 0; dx < KS; ++dx)
+            v[dx] = *reinterpret_cast<const u32x2_t *>(tile + lbase[i] + (dy * SX + dx) * D);
+          taps_dot2<KS>(v, wr, acc[i]);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < NPASS; ++i) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int dy = 0; dy < KS; ++dy)
-#pragma unroll
-          for (int dx = 0; dx < KS; ++dx) {
-            const u32x2_t v = *reinterpret_cast<const u32x2_t *>(tile + lbase[i] + (dy * SX + dx) * D);
-            const int t = dy * KS + dx;
-            acc[0] = fmaf(lo_f(v[0]), wsp[t][0], acc[0]);
-            acc[1] = fmaf(hi_f(v[0]), wsp[t][1], acc[1]);
-            acc[2] = fmaf(lo_f(v[1]), wsp[t][2], acc[2]);
-            acc[3] = fmaf(hi_f(v[1]), wsp[t][3], acc[3]);
-          }
-        fresh[i][0] = pack_bf2(acc[0], acc[1]);
-        fresh[i][1] = pack_bf2(acc[2], acc[3]);
+        fresh[i][0] = pack_bf2(acc[i][0], acc[i][1]);
+        fresh[i][1] = pack_bf2(acc[i][2], acc[i][3]);
       }
     } else {
 #pragma unroll
@@ -143,25 +233,23 @@ __global__ __launch_bounds__(SC_THREADS) void short_conv_kernel(
 #pragma unroll
     for (int i = 0; i < NPASS; ++i) {
       float a[4] = {0.f, 0.f, 0.f, 0.f};
+      u32x2_t r[KT];
 #pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        a[0] = fmaf(lo_f(ring[i][t][0]), wtm[t][0], a[0]);
-        a[1] = fmaf(hi_f(ring[i][t][0]), wtm[t][1], a[1]);
-        a[2] = fmaf(lo_f(ring[i][t][1]), wtm[t][2], a[2]);
-        a[3] = fmaf(hi_f(ring[i][t][1]), wtm[t][3], a[3]);
-      }
+      for (int t = 0; t < KT; ++t) r[t] = u32x2_t{ring[i][t][0], ring[i][t][1]};
+      taps_dot2<KT>(r, wtm, a);
+      // SiLU and the norm with the hardware exp2 / reciprocal (a few fp32 ulps, far below the
+      // one bf16 rounding of the output)
       float y[4], ss = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        y[j] = a[j] / (1.f + expf(-a[j]));
+        y[j] = a[j] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(a[j] * -1.44269504088896341f));
         ss = fmaf(y[j], y[j], ss);
       }
       if (l2norm) {
+        // 1 / max(||y||, 1e-6) = rsqrt(max(||y||^2, 1e-12))
+        const float inv = __builtin_amdgcn_rsqf(fmaxf(group_sum<LPP>(ss), 1e-12f));
 #pragma unroll
-        for (int o = 1; o < LPP; o <<= 1) ss += __shfl_xor(ss, o);
-        const float nrm = fmaxf(sqrtf(ss), 1e-6f);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) y[j] = y[j] / nrm;
+        for (int j = 0; j < 4; ++j) y[j] *= inv;
       }
       if (valid[i])
         *reinterpret_cast<u32x2_t *>(out + obase[i] + (int64_t)fo * T * o_row) =
@@ -219,6 +307,8 @@ extern "C" int vdnh3_short_conv(const uint16_t *x, int64_t x_row, int64_t x_head
                    VDNH3_ERR_INVALID, "short_conv: empty or null operand");
   VDNH3_HOST_CHECK(x_row % 8 == 0 && x_head % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0,
                    VDNH3_ERR_INVALID, "short_conv: x must be 16-byte aligned with strides multiple of 8");
+  VDNH3_HOST_CHECK((int64_t)grid_h * grid_w * x_row < ((int64_t)1 << 31), VDNH3_ERR_INVALID,
+                   "short_conv: one frame of x must span fewer than 2^31 elements");
   VDNH3_HOST_CHECK(out_row % 4 == 0 && out_head % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0,
                    VDNH3_ERR_INVALID, "short_conv: out must be 8-byte aligned with strides multiple of 4");
   hipStream_t s = static_cast<hipStream_t>(stream);
