@@ -11,10 +11,11 @@
 // gdn_prep_kernel (grid chunks x heads, fully parallel): K K^T and Q K^T on bf16 MFMA; the
 // unit-triangular systems by fp32 forward substitution, one right-hand-side column per thread
 // (W's 128 columns and U~'s 128 columns: no barrier inside the solve); writes W, U~, Q^ = e^G Q,
-// K^T^ = (e^{G_C - G} K)^T, P = Q K^T o D (bf16) and G (fp32) for each chunk.
+// K^T^ = (e^{G_C - G} K)^T, P = Q K^T o D (bf16) and G (fp32) for each chunk, every output
+// through LDS as 16-byte stores.
 // gdn_scan_kernel (grid heads x dv/32, sequential over chunks): one workgroup carries a 32-row
 // slice of the state in MFMA accumulators (fp32); per chunk U = U~ - W S^T, O = Q^ S^T + P U and
-// S = e^{G_C} S + U^T K^, with the next chunk's operands loaded into registers during the step.
+// S = e^{G_C} S + U^T K^, with the next chunk's operands loaded straight into LDS during the step.
 #include "common.h"
 
 namespace vdnh3 {
@@ -34,10 +35,10 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
     int64_t b_row, const float *__restrict__ lg, int64_t g_row, int T, int heads, uint16_t *__restrict__ Wo,
     uint16_t *__restrict__ Uo, uint16_t *__restrict__ Qo, uint16_t *__restrict__ Ko, uint16_t *__restrict__ Po,
     float *__restrict__ Go) {
-  constexpr int C = kGdnC, KP = D + 8, CH = D / 8, AP = C + 1;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[C * KP], Qs[C * KP], Vs[C * KP];
-  __shared__ float As[C * AP];
-  __shared__ float Gs[C], Bs[C];
+  constexpr int C = kGdnC, KP = D + 8, CH = D / 8, AP = C + 4, PP = C + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[C * KP], Qs[C * KP], Vs[C * KP], Ps[C * PP];
+  __shared__ __attribute__((aligned(16))) float As[C * AP];  // rows 16-byte aligned: vector reads in the solve
+  __shared__ float Gs[C], Bs[C], Eg[C], Ec[C];                // G, b, e^G, e^{G_C - G}
   const int c = blockIdx.x, h = blockIdx.y, t0 = c * C, n = min(C, T - t0);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, gl = lane >> 5;
   const int64_t ch = (int64_t)c * heads + h;
@@ -56,7 +57,7 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
     st16(Qs + r * KP + 8 * cc, qv);
     st16(Vs + r * KP + 8 * cc, vv);
   }
-  if (wave == 0) {  // inclusive prefix sum of the log-decay over the chunk
+  if (wave == 0) {  // inclusive prefix sum of the log-decay over the chunk, and its exponentials
     float x = lane < n ? lg[(int64_t)(t0 + lane) * g_row + h] : 0.f;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -65,10 +66,12 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
     }
     Gs[lane] = x;
     Bs[lane] = lane < n ? beta[(int64_t)(t0 + lane) * b_row + h] : 0.f;
+    Eg[lane] = expf(x);
+    Ec[lane] = expf(__shfl(x, 63) - x);
   }
   __syncthreads();
 
-  // K K^T and Q K^T: wave w owns the 32 x 32 block (w / 2, w % 2)
+  // K K^T and Q K^T: wave w owns the 32 x 32 block (w / 2, w % 2); A (fp32) and P (bf16) to LDS
   {
     const int mb = wave >> 1, nb = wave & 1;
     f32x16_t akk = {}, aqk = {};
@@ -81,52 +84,93 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
       aqk = mfma_bf16_32x32x16(aq, bk, aqk);
     }
     const int nn = 32 * nb + l32;
-    uint16_t *pc = Po + ch * GdnWs<D>::P;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int m = 32 * mb + 8 * (i >> 2) + 4 * gl + (i & 3);
       const float dec = nn <= m ? expf(Gs[m] - Gs[nn]) : 0.f;
       As[m * AP + nn] = nn < m ? Bs[m] * dec * akk[i] : 0.f;
-      pc[m * C + nn] = f2bf(aqk[i] * dec);
+      Ps[m * PP + nn] = f2bf(aqk[i] * dec);
     }
   }
   __syncthreads();
 
+  // Q^ = e^G Q (rows), K^T^ = (e^{G_C - G} K)^T ([D][C]) and P: 16-byte stores, before the
+  // solve overwrites Ks
+  {
+    uint16_t *qc = Qo + ch * GdnWs<D>::Q, *kc = Ko + ch * GdnWs<D>::K, *pc = Po + ch * GdnWs<D>::P;
+#pragma unroll
+    for (int u = 0; u < C * CH / 256; ++u) {
+      const int e = tid + 256 * u, r = e / CH, cc = e - r * CH;
+      const u32x4_t x = ld16(Qs + r * KP + 8 * cc);
+      const float sc = Eg[r];
+      st16(qc + r * D + 8 * cc,
+           u32x4_t{pack_bf2(bf2f((uint16_t)x[0]) * sc, bf2f((uint16_t)(x[0] >> 16)) * sc),
+                   pack_bf2(bf2f((uint16_t)x[1]) * sc, bf2f((uint16_t)(x[1] >> 16)) * sc),
+                   pack_bf2(bf2f((uint16_t)x[2]) * sc, bf2f((uint16_t)(x[2] >> 16)) * sc),
+                   pack_bf2(bf2f((uint16_t)x[3]) * sc, bf2f((uint16_t)(x[3] >> 16)) * sc)});
+    }
+#pragma unroll
+    for (int u = 0; u < D * (C / 8) / 256; ++u) {
+      const int e = tid + 256 * u, tc = e / D, d = e - tc * D;  // lanes walk d: conflict-free LDS reads
+      float y[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = bf2f(Ks[(8 * tc + j) * KP + d]) * Ec[8 * tc + j];
+      st16(kc + d * C + 8 * tc,
+           u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])});
+    }
+#pragma unroll
+    for (int u = 0; u < C * (C / 8) / 256; ++u) {
+      const int e = tid + 256 * u, r = e >> 3, cc = e & 7;
+      st16(pc + r * C + 8 * cc, ld16(Ps + r * PP + 8 * cc));
+    }
+    if (tid < C) Go[ch * GdnWs<D>::G + tid] = Gs[tid];
+  }
+  __syncthreads();
+
   // (I + A) X = R by forward substitution, column `col` per thread: W (col < D) with
-  // R = diag(b e^G) K, U~ (col >= D) with R = diag(b) V
+  // R = diag(b e^G) K, U~ (col >= D) with R = diag(b) V. Row i of X replaces row i of R in
+  // LDS (bf16) as soon as it is known.
   if (tid < 2 * D) {
     const int col = tid < D ? tid : tid - D;
     const bool is_w = tid < D;
-    const uint16_t *src = is_w ? Ks : Vs;
-    uint16_t *dst = (is_w ? Wo : Uo) + ch * GdnWs<D>::W + col;
+    uint16_t *src = is_w ? Ks : Vs;
     float x[C];
 #pragma unroll
     for (int i = 0; i < C; ++i) {
       float r = Bs[i] * bf2f(src[i * KP + col]);
-      if (is_w) r *= expf(Gs[i]);
+      if (is_w) r *= Eg[i];
 #pragma unroll
       for (int j = 0; j < i; ++j) r = fmaf(-As[i * AP + j], x[j], r);
       x[i] = r;
-      dst[(int64_t)i * D] = f2bf(r);
+      src[i * KP + col] = f2bf(r);
     }
   }
-  // Q^ = e^G Q (rows) and K^T^ = (e^{G_C - G} K)^T ([D][C]), and G
+  __syncthreads();
   {
-    const float gc = Gs[C - 1];
-    uint16_t *qc = Qo + ch * GdnWs<D>::Q;
-    uint16_t *kc = Ko + ch * GdnWs<D>::K;
-    for (int e = tid; e < C * D; e += 256) {
-      const int r = e / D, d = e - r * D;  // Q^ row-major: lanes walk d
-      qc[e] = f2bf(bf2f(Qs[r * KP + d]) * expf(Gs[r]));
-      const int dd = e / C, rr = e - dd * C;  // K^T^: lanes walk tokens
-      kc[e] = f2bf(bf2f(Ks[rr * KP + dd]) * expf(gc - Gs[rr]));
+    uint16_t *wc = Wo + ch * GdnWs<D>::W, *uc = Uo + ch * GdnWs<D>::U;
+#pragma unroll
+    for (int u = 0; u < 2 * C * CH / 256; ++u) {
+      const int e = tid + 256 * u, which = e / (C * CH), x = e - which * (C * CH), r = x / CH, cc = x - r * CH;
+      st16((which ? uc : wc) + r * D + 8 * cc, ld16((which ? Vs : Ks) + r * KP + 8 * cc));
     }
-    if (tid < C) Go[ch * GdnWs<D>::G + tid] = Gs[tid];
   }
 }
 
-// One workgroup = head h, state rows (dv) 32 s .. 32 s + 31; wave w holds the state block of dk
-// columns 32 w .. 32 w + 31 as one 32x32 MFMA accumulator (fp32).
+// One workgroup = head h, state rows (dv) 32 sl .. 32 sl + 31; wave w holds the state block of
+// dk columns 32 w .. 32 w + 31 as one 32x32 MFMA accumulator (fp32).
+//
+// A chunk's operands reach LDS by direct-to-LDS loads (global_load_lds_dwordx4) into one of
+// two slots, issued one chunk ahead; no register staging, and the only wait is an explicit
+// vmcnt(0) at the end of each step. A slot is [W | Q^ | K^T^ | P | U~ slice | G], unpadded;
+// 16-byte chunk c of row r sits at chunk position c ^ swizzle(r) (16 chunks per row: r & 15;
+// 8 per row: (r >> 1) & 7), so the 16 lanes of an MFMA fragment read 16 different bank groups.
+// Wave instruction i (0..59, i = 4 u + wave) fills slot bytes 1024 i .. 1024 i + 1023; lane L
+// loads the source chunk that lands at piece 64 i + L. The outputs of chunk c go to LDS (Os)
+// in step c and to global memory at the start of step c + 1 (one 16-byte store per thread).
+constexpr int kScanSlotBytes = 3 * 64 * 128 * 2 + 64 * 64 * 2 + 64 * 32 * 2 + 64 * 4;  // 61,696
+__device__ __forceinline__ int swz16(int r, int c) { return c ^ (r & 15); }
+__device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }
+
 template <int D>
 __global__ __launch_bounds__(256) void gdn_scan_kernel(
     const uint16_t *__restrict__ Wi, const uint16_t *__restrict__ Ui, const uint16_t *__restrict__ Qi,
@@ -134,12 +178,48 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
     int T, int heads, const float *__restrict__ s_init, float *__restrict__ s_final, uint16_t *__restrict__ out,
     int64_t o_row, int64_t o_head) {
   static_assert(D == 128, "the scan keeps one 32-column state block per wave: head_dim 128");
-  constexpr int C = kGdnC, KP = D + 8, CP = C + 8, UP = 32 + 8;
-  __shared__ __attribute__((aligned(16))) uint16_t Wl[C * KP], Ql[C * KP], Kt[D * CP], Pl[C * CP], Ul[C * UP];
-  __shared__ __attribute__((aligned(16))) uint16_t Sb[32 * KP], Ut[32 * CP];
-  __shared__ float Gl[C];
+  constexpr int C = kGdnC, KP = D + 8, CP = C + 8, OP = 32 + 8;
+  constexpr int OFF_Q = 64 * 128 * 2, OFF_K = 2 * OFF_Q, OFF_P = 3 * OFF_Q, OFF_U = OFF_P + 64 * 64 * 2,
+                OFF_G = OFF_U + 64 * 32 * 2;
+  static_assert(OFF_G + 256 == kScanSlotBytes, "slot layout");
+  __shared__ __attribute__((aligned(1024))) uint8_t slots[2 * kScanSlotBytes];
+  __shared__ __attribute__((aligned(16))) uint16_t Sb[32 * KP], Ut[32 * CP], Os[C * OP];
   const int h = blockIdx.x, sl = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, gl = lane >> 5;
+
+  // per-lane source byte offsets of the 15 wave instructions inside a chunk's blocks (the same
+  // for every chunk), and the region each instruction reads
+  uint32_t src_off[15];
+#pragma unroll
+  for (int u = 0; u < 15; ++u) {
+    const int i = 4 * u + wave;
+    if (u < 8) {  // W (u 0-3) or Q^ (u 4-7): 64 x 128, 16 chunks per row
+      const int q = 64 * (i & 15) + lane, r = q >> 4;
+      src_off[u] = (uint32_t)(r * 128 + 8 * swz16(r, q & 15)) * 2;
+    } else if (u < 12) {  // K^T^: 128 x 64, 8 chunks per row
+      const int q = 64 * (i - 32) + lane, r = q >> 3;
+      src_off[u] = (uint32_t)(r * 64 + 8 * swz8(r, q & 7)) * 2;
+    } else if (u < 14) {  // P: 64 x 64
+      const int q = 64 * (i - 48) + lane, r = q >> 3;
+      src_off[u] = (uint32_t)(r * 64 + 8 * swz8(r, q & 7)) * 2;
+    } else {  // U~ columns 32 sl .. 32 sl + 31 of 64 rows: 4 chunks per row, no swizzle
+      const int q = 64 * (i - 56) + lane, r = q >> 2;
+      src_off[u] = (uint32_t)(r * 128 + 32 * sl + 8 * (q & 3)) * 2;
+    }
+  }
+  const uint32_t slots_lds = lds_address(slots);
+  auto dma = [&](int c, int slot) __device__ {
+    const int64_t ch = (int64_t)c * heads + h;
+    const uint32_t base = slots_lds + (uint32_t)(slot * kScanSlotBytes);
+#pragma unroll
+    for (int u = 0; u < 15; ++u) {
+      const uint16_t *src = u < 4 ? Wi + ch * GdnWs<D>::W : u < 8 ? Qi + ch * GdnWs<D>::Q
+                          : u < 12 ? Ki + ch * GdnWs<D>::K : u < 14 ? Pi + ch * GdnWs<D>::P : Ui + ch * GdnWs<D>::U;
+      global_to_lds16_sbase(src, src_off[u], base + (uint32_t)((4 * u + wave) * 1024));
+    }
+    if (wave == 0 && lane < 16)  // G: 64 fp32
+      global_to_lds16_sbase(Gi + ch * GdnWs<D>::G, (uint32_t)lane * 16u, base + OFF_G);
+  };
 
   // state block of this wave: S[v = 32 sl + row][k = 32 wave + l32]
   f32x16_t st = {};
@@ -157,99 +237,77 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
       Sb[vr * KP + 32 * wave + l32] = f2bf(st[i]);
     }
   };
+  // outputs of chunk c (in Os) to global memory: thread = (token tid / 4, 8 dv columns)
+  auto store_o = [&](int c) __device__ {
+    const int tk = tid >> 2, pc = tid & 3, tok = c * C + tk;
+    const u32x4_t val = ld16(Os + tk * OP + 8 * pc);
+    if (tok < T) st16(out + (int64_t)tok * o_row + (int64_t)h * o_head + 32 * sl + 8 * pc, val);
+  };
 
-  // operands of chunk c, 16-byte pieces: W, Q^ (C x D), K^T^ (D x C), P (C x C), U~ slice (C x 32), G
-  constexpr int NW = C * D / 8, NP = C * C / 8, NU = C * 32 / 8;
-  constexpr int NTOT = 3 * NW + NP + NU;               // 3072 + 512 + 256 = 3840
-  constexpr int PER = (NTOT + 255) / 256;             // 15 per thread
-  u32x4_t reg[PER];
-  float greg = 0.f;
-  auto fetch = [&](int c) __device__ {
-    const int64_t ch = (int64_t)c * heads + h;
+  // fragment element offsets inside a slot (bf16 units)
+  int wfo[D / 16], pfo[C / 16], kfo[C / 16];
+  const int tb = wave & 1;
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int e = tid + 256 * u;
-      u32x4_t val = {0, 0, 0, 0};
-      if (e < NW) val = ld16(Wi + ch * GdnWs<D>::W + 8 * e);
-      else if (e < 2 * NW) val = ld16(Qi + ch * GdnWs<D>::Q + 8 * (e - NW));
-      else if (e < 3 * NW) val = ld16(Ki + ch * GdnWs<D>::K + 8 * (e - 2 * NW));
-      else if (e < 3 * NW + NP) val = ld16(Pi + ch * GdnWs<D>::P + 8 * (e - 3 * NW));
-      else if (e < NTOT) {
-        const int x = e - 3 * NW - NP, r = x >> 2, cc = x & 3;
-        val = ld16(Ui + ch * GdnWs<D>::U + (int64_t)r * D + 32 * sl + 8 * cc);
-      }
-      reg[u] = val;
-    }
-    if (tid < C) greg = Gi[ch * GdnWs<D>::G + tid];
-  };
-  auto stash = [&]() __device__ {
+  for (int s = 0; s < D / 16; ++s) {
+    const int r = 32 * tb + l32;
+    wfo[s] = (wave < 2 ? 0 : OFF_Q / 2) + r * 128 + 8 * swz16(r, 2 * s + gl);
+  }
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {
-      const int e = tid + 256 * u;
-      if (e < NW) st16(Wl + (e >> 4) * KP + 8 * (e & 15), reg[u]);
-      else if (e < 2 * NW) { const int x = e - NW; st16(Ql + (x >> 4) * KP + 8 * (x & 15), reg[u]); }
-      else if (e < 3 * NW) { const int x = e - 2 * NW; st16(Kt + (x >> 3) * CP + 8 * (x & 7), reg[u]); }
-      else if (e < 3 * NW + NP) { const int x = e - 3 * NW; st16(Pl + (x >> 3) * CP + 8 * (x & 7), reg[u]); }
-      else if (e < NTOT) { const int x = e - 3 * NW - NP; st16(Ul + (x >> 2) * UP + 8 * (x & 3), reg[u]); }
-    }
-    if (tid < C) Gl[tid] = greg;
-  };
+  for (int s = 0; s < C / 16; ++s) {
+    const int r = 32 * tb + l32, d = 32 * wave + l32;
+    pfo[s] = OFF_P / 2 + r * 64 + 8 * swz8(r, 2 * s + gl);
+    kfo[s] = OFF_K / 2 + d * 64 + 8 * swz8(d, 2 * s + gl);
+  }
 
   write_sb();
-  fetch(0);
-  stash();
-  __syncthreads();
+  dma(0, 0);
+  wait_vm_lds<0>();
+  bare_barrier();
   for (int c = 0; c < n_chunks; ++c) {
-    if (c + 1 < n_chunks) fetch(c + 1);  // in flight during the step
+    const uint16_t *sb = reinterpret_cast<const uint16_t *>(slots + (c & 1) * kScanSlotBytes);
+    const float *gsl = reinterpret_cast<const float *>(slots + (c & 1) * kScanSlotBytes + OFF_G);
+    if (c > 0) store_o(c - 1);
+    if (c + 1 < n_chunks) dma(c + 1, (c + 1) & 1);
     // (a) waves 0, 1: U = U~ - W S^T for tokens 32 w ..; waves 2, 3: O = Q^ S^T for tokens 32 (w - 2) ..
-    const int tb = wave & 1;
     f32x16_t acc = {};
-    {
-      const uint16_t *arow = (wave < 2 ? Wl : Ql) + (32 * tb + l32) * KP + 8 * gl;
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s)
-        acc = mfma_bf16_32x32x16(as_bf16x8(ld16(arow + 16 * s)), as_bf16x8(ld16(Sb + l32 * KP + 16 * s + 8 * gl)),
-                                 acc);
-    }
+    for (int s = 0; s < D / 16; ++s)
+      acc = mfma_bf16_32x32x16(as_bf16x8(ld16(sb + wfo[s])), as_bf16x8(ld16(Sb + l32 * KP + 16 * s + 8 * gl)), acc);
     if (wave < 2) {
       // U[tok][dv] = U~ - acc; stored transposed (Ut[dv][tok]), four consecutive tokens per write
+      const uint16_t *ul = sb + OFF_U / 2;
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const int tok = 32 * tb + 8 * i4 + 4 * gl;
         float u[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) u[e] = bf2f(Ul[(tok + e) * UP + l32]) - acc[4 * i4 + e];
+        for (int e = 0; e < 4; ++e) u[e] = bf2f(ul[(tok + e) * 32 + l32]) - acc[4 * i4 + e];
         *reinterpret_cast<u32x2_t *>(Ut + l32 * CP + tok) = u32x2_t{pack_bf2(u[0], u[1]), pack_bf2(u[2], u[3])};
       }
     }
-    __syncthreads();
-    // (b) waves 2, 3: O += P U and store; every wave: S = e^{G_C} S + U^T K^
+    bare_barrier();  // Ut complete; every read of Sb and of the Os of chunk c - 1 is done
+    // (b) waves 2, 3: O += P U into Os; every wave: S = e^{G_C} S + U^T K^, then its bf16 copy
     if (wave >= 2) {
 #pragma unroll
       for (int s = 0; s < C / 16; ++s)
-        acc = mfma_bf16_32x32x16(as_bf16x8(ld16(Pl + (32 * tb + l32) * CP + 16 * s + 8 * gl)),
-                                 as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)), acc);
-      const int t0 = c * C;
+        acc = mfma_bf16_32x32x16(as_bf16x8(ld16(sb + pfo[s])), as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)),
+                                 acc);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int tok = t0 + 32 * tb + 8 * (i >> 2) + 4 * gl + (i & 3);
-        if (tok < T) out[(int64_t)tok * o_row + (int64_t)h * o_head + 32 * sl + l32] = f2bf(acc[i]);
-      }
+      for (int i = 0; i < 16; ++i) Os[(32 * tb + 8 * (i >> 2) + 4 * gl + (i & 3)) * OP + l32] = f2bf(acc[i]);
     }
     {
-      const float decay = expf(Gl[C - 1]);
+      const float decay = expf(gsl[C - 1]);
 #pragma unroll
       for (int i = 0; i < 16; ++i) st[i] *= decay;
 #pragma unroll
       for (int s = 0; s < C / 16; ++s)
-        st = mfma_bf16_32x32x16(as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)),
-                                as_bf16x8(ld16(Kt + (32 * wave + l32) * CP + 16 * s + 8 * gl)), st);
+        st = mfma_bf16_32x32x16(as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)), as_bf16x8(ld16(sb + kfo[s])), st);
     }
-    __syncthreads();  // every read of this chunk's operands and of Sb / Ut is done
     write_sb();
-    if (c + 1 < n_chunks) stash();
-    __syncthreads();
+    wait_vm_lds<0>();  // the next chunk's operands have landed; this wave's LDS writes are done
+    bare_barrier();
   }
+  store_o(n_chunks - 1);
   if (s_final) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -288,6 +346,8 @@ extern "C" int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_h
                        reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
                    VDNH3_ERR_INVALID, "gdn: q/k/v and workspace must be 16-byte aligned with strides multiple of 8");
+  VDNH3_HOST_CHECK(o_row % 8 == 0 && o_head % 8 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+                   VDNH3_ERR_INVALID, "gdn: out must be 16-byte aligned with strides multiple of 8");
   constexpr int D = 128;
   const int chunks = (tokens + kGdnC - 1) / kGdnC;
   const int64_t n = (int64_t)chunks * heads;
