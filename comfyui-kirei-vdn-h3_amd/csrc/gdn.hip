@@ -8,9 +8,9 @@
 //   U = U~ - W S0^T,   O = diag(e^G) Q S0^T + (Q K^T o D) U,   D[t][j] = exp(G_t - G_j) (j <= t)
 //   S_C = e^{G_C} S0 + U^T diag(e^{G_C - G}) K
 //
-// gdn_prep_kernel (grid chunks x heads, fully parallel): K K^T and Q K^T on bf16 MFMA; the
-// unit-triangular systems by fp32 forward substitution, one right-hand-side column per thread
-// (W's 128 columns and U~'s 128 columns: no barrier inside the solve); writes W, U~, Q^ = e^G Q,
+// gdn_prep_kernel (grid heads x chunks, fully parallel): K K^T and Q K^T on bf16 MFMA; the
+// inverse T = (I + A)^-1 in fp32 by 16 x 16 blocks, then W = T diag(b e^G) K and U~ = T diag(b) V
+// on bf16 MFMA (T's scaled columns rounded to bf16); writes W, U~, Q^ = e^G Q,
 // K^T^ = (e^{G_C - G} K)^T, P = Q K^T o D (bf16) and G (fp32) for each chunk, every output
 // through LDS as 16-byte stores.
 // gdn_scan_kernel (grid heads x dv/32, sequential over chunks): one workgroup carries a 32-row
@@ -39,7 +39,7 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t Ks[C * KP], Qs[C * KP], Vs[C * KP], Ps[C * PP];
   __shared__ __attribute__((aligned(16))) float As[C * AP];  // rows 16-byte aligned: vector reads in the solve
   __shared__ float Gs[C], Bs[C], Eg[C], Ec[C];                // G, b, e^G, e^{G_C - G}
-  const int c = blockIdx.x, h = blockIdx.y, t0 = c * C, n = min(C, T - t0);
+  const int h = blockIdx.x, c = blockIdx.y, t0 = c * C, n = min(C, T - t0);  // heads fastest: rows read whole
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, gl = lane >> 5;
   const int64_t ch = (int64_t)c * heads + h;
 
@@ -127,23 +127,110 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
   }
   __syncthreads();
 
-  // (I + A) X = R by forward substitution, column `col` per thread: W (col < D) with
-  // R = diag(b e^G) K, U~ (col >= D) with R = diag(b) V. Row i of X replaces row i of R in
-  // LDS (bf16) as soon as it is known.
-  if (tid < 2 * D) {
-    const int col = tid < D ? tid : tid - D;
-    const bool is_w = tid < D;
-    uint16_t *src = is_w ? Ks : Vs;
-    float x[C];
+  // T = (I + A)^-1 (unit lower triangular) by 16 x 16 blocks, in fp32. T[i][j] (i > j) is kept
+  // transposed in the upper triangle of As (at As[j][i]), A stays in the lower one. The diagonal
+  // blocks come from forward substitution (wave I, lane c: column c of block I); the blocks
+  // below follow by distance d = I - J from the diagonal:
+  //   X = sum_{K=J}^{I-1} A_IK T_KJ,   T_IJ = -T_II X
+  // with X in the (now free) P staging area.
+  auto t_at = [&](int i, int j) __device__ { return As[j * AP + i]; };  // T[i][j], i > j
+  if (lane < 16) {
+    const int I = wave, cc = lane;
+    float t[16];
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-      float r = Bs[i] * bf2f(src[i * KP + col]);
-      if (is_w) r *= Eg[i];
+    for (int r = 0; r < 16; ++r) {
+      float acc = 0.f;
 #pragma unroll
-      for (int j = 0; j < i; ++j) r = fmaf(-As[i * AP + j], x[j], r);
-      x[i] = r;
-      src[i * KP + col] = f2bf(r);
+      for (int m = 0; m < r; ++m) acc = fmaf(As[(16 * I + r) * AP + 16 * I + m], t[m], acc);
+      t[r] = r == cc ? 1.f : (r < cc ? 0.f : -acc);
+      if (r > cc) As[(16 * I + cc) * AP + 16 * I + r] = t[r];
     }
+  }
+  float *Xs = reinterpret_cast<float *>(Ps);  // [block][16][16]
+  const int br = tid >> 4, bc = tid & 15;     // this thread's element of every 16 x 16 block
+#pragma unroll
+  for (int d = 1; d < 4; ++d) {
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 4 - d; ++b) {
+      const int I = d + b, J = b;
+      float x = 0.f;
+#pragma unroll
+      for (int K = J; K < I; ++K) {
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+          float tv;  // T[16 K + m][16 J + bc]
+          if (K > J) tv = t_at(16 * K + m, 16 * J + bc);
+          else tv = m == bc ? 1.f : (m > bc ? t_at(16 * J + m, 16 * J + bc) : 0.f);
+          x = fmaf(As[(16 * I + br) * AP + 16 * K + m], tv, x);
+        }
+      }
+      Xs[(b * 16 + br) * 16 + bc] = x;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 4 - d; ++b) {
+      const int I = d + b, J = b;
+      float y = Xs[(b * 16 + br) * 16 + bc];
+#pragma unroll
+      for (int m = 0; m < 15; ++m)
+        if (m < br) y = fmaf(t_at(16 * I + br, 16 * I + m), Xs[(b * 16 + m) * 16 + bc], y);
+      As[(16 * J + bc) * AP + 16 * I + br] = -y;
+    }
+  }
+  __syncthreads();
+
+  // Tw = T diag(b e^G), Tu = T diag(b) in bf16, row-major 64 x 64 with 16-byte chunk c of row i at
+  // c ^ ((i >> 1) & 7), in the Q staging area (free now)
+  uint16_t *Tw = Qs, *Tu = Qs + C * C;
+#pragma unroll
+  for (int u = 0; u < C * (C / 8) / 256; ++u) {
+    const int e = tid + 256 * u, i = e & 63, jc = e >> 6;  // lanes walk rows: conflict-free reads
+    float w[8], v8[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const int j = 8 * jc + jj;
+      const float tv = j == i ? 1.f : (j < i ? t_at(i, j) : 0.f);
+      v8[jj] = tv * Bs[j];
+      w[jj] = v8[jj] * Eg[j];
+    }
+    const int off = i * C + 8 * (jc ^ ((i >> 1) & 7));
+    st16(Tw + off, u32x4_t{pack_bf2(w[0], w[1]), pack_bf2(w[2], w[3]), pack_bf2(w[4], w[5]), pack_bf2(w[6], w[7])});
+    st16(Tu + off,
+         u32x4_t{pack_bf2(v8[0], v8[1]), pack_bf2(v8[2], v8[3]), pack_bf2(v8[4], v8[5]), pack_bf2(v8[6], v8[7])});
+  }
+  __syncthreads();
+
+  // W = Tw K and U~ = Tu V on MFMA: wave w owns columns 32 w .. 32 w + 31 of both, all 64 rows.
+  // B fragments are 8 tokens of one column (8 LDS reads); row block 0 skips tokens 32..63 (zero in Tw, Tu).
+  {
+    f32x16_t aw[2] = {}, au[2] = {};
+#pragma unroll
+    for (int s = 0; s < C / 16; ++s) {
+      bf16x8_t bk, bv;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int j = 16 * s + 8 * gl + jj;
+        bk[jj] = __builtin_bit_cast(__bf16, Ks[j * KP + 32 * wave + l32]);
+        bv[jj] = __builtin_bit_cast(__bf16, Vs[j * KP + 32 * wave + l32]);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        if (mb == 0 && s >= 2) continue;
+        const int i = 32 * mb + l32, off = i * C + 8 * ((2 * s + gl) ^ ((i >> 1) & 7));
+        aw[mb] = mfma_bf16_32x32x16(as_bf16x8(ld16(Tw + off)), bk, aw[mb]);
+        au[mb] = mfma_bf16_32x32x16(as_bf16x8(ld16(Tu + off)), bv, au[mb]);
+      }
+    }
+    __syncthreads();  // every read of Ks / Vs is done: W and U~ replace them
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = 32 * mb + 8 * (i >> 2) + 4 * gl + (i & 3);
+        Ks[r * KP + 32 * wave + l32] = f2bf(aw[mb][i]);
+        Vs[r * KP + 32 * wave + l32] = f2bf(au[mb][i]);
+      }
   }
   __syncthreads();
   {
@@ -358,7 +445,7 @@ extern "C" int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_h
   uint16_t *P = Kt + n * GdnWs<D>::K;
   float *G = reinterpret_cast<float *>(P + n * GdnWs<D>::P);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(chunks, heads), dim3(256), 0, s, q, q_row, q_head, k, k_row, k_head,
+  hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(heads, chunks), dim3(256), 0, s, q, q_row, q_head, k, k_row, k_head,
                      v, v_row, v_head, beta, beta_row, log_decay, decay_row, tokens, heads, W, U, Qh, Kt, P, G);
   int rc = check_launch("gdn_prep");
   if (rc) return rc;
