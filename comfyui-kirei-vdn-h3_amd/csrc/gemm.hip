@@ -53,6 +53,7 @@ struct GemmEpi {
   const void *bias;  // [N] or null
   int bias_bf16;
   int act;            // 0 none, 1 sigmoid
+  int act_cols;       // with the sigmoid: it applies to columns n < act_cols only (0: every column)
   int out_type;       // OutType
   int accumulate;     // C += epi(acc)
   int round_linear;   // bf16 output: round the linear result to bf16 before the activation
@@ -119,6 +120,7 @@ __device__ __forceinline__ void store_block(const Acc (&acc)[4][4], uint32_t *st
   const bool vec = epi.vec && n < N;  // the host sets vec only when N % 4 == 0 and C allows 4-wide stores
   using old_t = typename std::conditional<OUT == kOutF32, f32x4_t, u32x2_t>::type;
   const bool round_linear = epi.round_linear;
+  const int act_cols = epi.act_cols > 0 ? epi.act_cols : N;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     // stage rows 32 i .. +32 of the block
@@ -185,7 +187,7 @@ __device__ __forceinline__ void store_block(const Acc (&acc)[4][4], uint32_t *st
             // bf16 output: rounding the linear value first only matters before the sigmoid (a
             // second rounding of a bf16 value, or the accumulation's own rounding, is exact)
             if constexpr (OUT == kOutBF16 && ACT) x = round_linear ? round_bf(x) : x;
-            if constexpr (ACT) x = sigmoidf_(x);
+            if constexpr (ACT) x = n + k < act_cols ? sigmoidf_(x) : x;
             v[k] = x;
           }
           if constexpr (OUT == kOutF32) {
@@ -467,7 +469,7 @@ extern "C" int vdnh3_gemm(int kind, const void *A, int64_t lda, const void *B, i
   VDNH3_HOST_CHECK(A && B && C, VDNH3_ERR_INVALID, "gemm: null operand");
   VDNH3_HOST_CHECK(out_type >= kOutBF16 && out_type <= kOutI32, VDNH3_ERR_INVALID, "gemm: bad out_type %d", out_type);
   VDNH3_HOST_CHECK(out_type != kOutI32 || kind == kI8, VDNH3_ERR_INVALID, "gemm: int32 output needs int8 operands");
-  VDNH3_HOST_CHECK(act == 0 || act == 1, VDNH3_ERR_INVALID, "gemm: bad activation %d", act);
+  VDNH3_HOST_CHECK(act == 0 || (act & 1 && (act >> 1) <= N), VDNH3_ERR_INVALID, "gemm: bad activation %d", act);
   VDNH3_HOST_CHECK(!(act && accumulate), VDNH3_ERR_INVALID, "gemm: a sigmoid epilogue cannot accumulate");
   VDNH3_HOST_CHECK(!a_scale || a_scale_n == 1 || a_scale_n == M, VDNH3_ERR_INVALID,
                    "gemm: a_scale must have 1 or M entries");
@@ -475,8 +477,8 @@ extern "C" int vdnh3_gemm(int kind, const void *A, int64_t lda, const void *B, i
                    "gemm: b_scale must have 1 or N entries");
   const int esize = out_type == kOutBF16 ? 2 : 4;
   const int vec = N % 4 == 0 && ldc % 4 == 0 && reinterpret_cast<uintptr_t>(C) % (4 * esize) == 0;
-  GemmEpi epi{a_scale, b_scale, b_scale_n, a_scale_n, alpha, bias, bias_bf16, act, out_type, accumulate, round_linear,
-              vec};
+  GemmEpi epi{a_scale, b_scale, b_scale_n, a_scale_n, alpha, bias, bias_bf16, act & 1, act >> 1, out_type, accumulate,
+              round_linear, vec};
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (kind) {
     case kBF16:

@@ -26,8 +26,12 @@ def _operand(t: torch.Tensor) -> torch.Tensor:
 
 def gemm(kind: int, a: torch.Tensor, b: torch.Tensor, *, a_scale=None, b_scale=None, alpha: float = 1.0,
          bias=None, act: str | None = None, out_dtype=torch.bfloat16, out: torch.Tensor | None = None,
-         accumulate: bool = False, round_linear: bool = True) -> torch.Tensor:
-    """``C = act(A B^T * scales + bias)``; ``a``: ``[M, K]``, ``b``: ``[N, K]`` (nn.Linear weight layout)."""
+         accumulate: bool = False, round_linear: bool = True, act_cols: int = 0) -> torch.Tensor:
+    """``C = act(A B^T * scales + bias)``; ``a``: ``[M, K]``, ``b``: ``[N, K]`` (nn.Linear weight layout).
+
+    ``act_cols`` > 0 limits the activation to the first ``act_cols`` output columns (the rest are the
+    plain linear result), so two projections of the same rows run as one GEMM.
+    """
     if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[1]:
         raise ValueError(f"gemm operands must be [M, K] and [N, K]; got {tuple(a.shape)} and {tuple(b.shape)}")
     device = _lib.require_device(a, b, a_scale, b_scale, bias, out)
@@ -54,6 +58,10 @@ def gemm(kind: int, a: torch.Tensor, b: torch.Tensor, *, a_scale=None, b_scale=N
         elif bias.dtype != torch.float32:
             bias = bias.float()
     act_code = {None: 0, "sigmoid": 1}[act]
+    if act_cols:
+        if act_code == 0 or not 0 < act_cols <= n:
+            raise ValueError(f"act_cols must lie in (0, {n}] and needs an activation")
+        act_code |= int(act_cols) << 1
     rc = _lib.lib().vdnh3_gemm(
         kind, _lib.ptr(a), a.stride(0), _lib.ptr(b), b.stride(0), _lib.ptr(out), out.stride(0), m, n, k,
         _lib.ptr(a_scale), 0 if a_scale is None else a_scale.numel(), _lib.ptr(b_scale),
@@ -68,6 +76,14 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias=None, *, out=None, accumu
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         raise TypeError("linear computes in bf16")
     return gemm(KIND_BF16, x, weight, bias=bias, out=out, accumulate=accumulate)
+
+
+def sigmoid_linear_split(x: torch.Tensor, weight: torch.Tensor, act_cols: int) -> torch.Tensor:
+    """``F.linear(x, weight)`` in bf16 with ``sigmoid`` on the first ``act_cols`` columns (the linear
+    value rounded to bf16 first there, as ``sigmoid_linear``); the remaining columns equal ``linear``."""
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("sigmoid_linear_split computes in bf16")
+    return gemm(KIND_BF16, x, weight, act="sigmoid", round_linear=True, act_cols=act_cols)
 
 
 def sigmoid_linear(x: torch.Tensor, weight: torch.Tensor, bias=None, *, out=None) -> torch.Tensor:

@@ -65,6 +65,16 @@ class OptimizedLinearBranch:
         _, jay = self._backend(length).factor_apply(None, a, b, jay_scale=_b.TEXT_STATE_SCALE, need_phi=False)
         return jay[0]
 
+    def _beta_down_weight(self, weights):
+        """``[W_beta; W_down]`` (``[heads + rank, hidden]`` bf16), rebuilt when either weight changes."""
+        wb, wd = weights["beta_proj.weight"], weights["output_gate.down.weight"]
+        key = (wb.data_ptr(), wb._version, tuple(wb.shape), wd.data_ptr(), wd._version, tuple(wd.shape))
+        cached = getattr(self, "_beta_down", None)
+        if cached is None or cached[0] != key:
+            cached = (key, torch.cat([wb, wd], dim=0).contiguous())
+            self._beta_down = cached
+        return cached[1]
+
     def _features(self, weights, name, raw, num_frames, frame_size):
         """Short-convolution features of ``q``/``k``/``v`` (``vdn_h3/runtime.py:311-341``), or the raw
         rows when ``name`` has no short convolution (its feature map is fused into the consumer)."""
@@ -79,7 +89,10 @@ class OptimizedLinearBranch:
     def _readout_flat(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, text_x,
                       text_k_raw, text_v_raw, frame_size=None, out=None):
         heads, dim = self.num_heads, self.head_dim
-        beta = _linear.sigmoid_linear(xv, weights["beta_proj.weight"])
+        # beta = sigmoid(x W_beta^T) and the output-gate down-projection x W_down^T read the same rows:
+        # one GEMM over [W_beta; W_down] with the sigmoid on the first `heads` columns
+        both = _linear.sigmoid_linear_split(xv, self._beta_down_weight(weights), heads)
+        beta, gate_hidden = both[:, :heads], both[:, heads:]
         k_in, k_feat = self._features(weights, "k", k_raw, num_frames, frame_size)
         v_in, v_feat = self._features(weights, "v", v_raw, num_frames, frame_size)
         a, b = _b.frame_statistics_raw(k_in, v_in, beta, num_frames, tokens_per_frame, k_features=k_feat,
@@ -91,8 +104,9 @@ class OptimizedLinearBranch:
         text_state = self._text_state(weights, text_x, text_k_raw, text_v_raw)
         prefix, suffix = _b.run_scans_inference(self._backend(tokens_per_frame), alpha, a, b, text_state)
         del a, b
-        hidden = _linear.linear(xv, weights["output_gate.down.weight"])
-        gate = _linear.sigmoid_linear(hidden, weights["output_gate.up.weight"], weights.get("output_gate.up.bias"))
+        gate = _linear.sigmoid_linear(gate_hidden, weights["output_gate.up.weight"],
+                                      weights.get("output_gate.up.bias"))
+        del both, gate_hidden
         q_in, q_feat = self._features(weights, "q", q_raw, num_frames, frame_size)
         return _b.readout_epilogue(q_in, prefix, suffix, alpha, bounds, weights["norm.weight"], gate,
                                    text_state=text_state, bridge=self.bridge, num_frames=num_frames,

@@ -129,8 +129,9 @@ int vdnh3_window_attn_prepared(const uint16_t *q, int64_t q_row, int64_t q_head,
  * C[m][n] = act( acc[m][n] * a_scale[m] * alpha * b_scale[n] + bias[n] ),  acc = sum_k A[m][k] B[n][k]
  * A: [M, K] row-major (lda), B: [N, K] row-major (ldb) - the nn.Linear weight layout - so C = A B^T.
  * a_scale / b_scale: fp32, NULL, or with 1 or M (N) entries; bias: fp32 or bf16 [N] or NULL;
- * act: 0 none, 1 sigmoid; accumulate: C = bf16(C + bf16(result)) (bf16 out) or C += result
- * (not together with the sigmoid).
+ * act: 0 none, 1 sigmoid, 2 c + 1 (0 < c <= N) sigmoid on columns n < c only, the others plain
+ * (two projections of the same rows in one pass, e.g. beta and the output-gate down-projection);
+ * accumulate: C = bf16(C + bf16(result)) (bf16 out) or C += result (not together with the sigmoid).
  * round_linear (bf16 out): round the linear result to bf16 before the activation, as
  * torch.sigmoid(F.linear(x, W, b)) does in bf16. K * element size must be a multiple of 128 bytes.
  * Replaces F.linear (vdn_h3/projection.py:259-261, vdn_h3/branch.py:736, :754-758,

@@ -60,6 +60,22 @@ def test_sigmoid_bias_and_accumulate_epilogues(device):
     assert_bf16_close(out, want, steps=2)
 
 
+def test_split_sigmoid_epilogue_equals_two_gemms(device):
+    """beta and the output-gate down-projection as one GEMM (sigmoid on the first 40 columns only)
+    equal sigmoid_linear and linear run separately, bit for bit."""
+    from vdn_h3_amd import linear as L
+
+    m, k, heads, rank = 1000, 5120, 40, 128
+    x = _rand((m, k), 21).to(device)
+    wb, wd = _rand((heads, k), 22, 0.02).to(device), _rand((rank, k), 23, 0.02).to(device)
+    both = L.sigmoid_linear_split(x, torch.cat([wb, wd]).contiguous(), heads)
+    torch.cuda.synchronize()
+    assert torch.equal(both[:, :heads], L.sigmoid_linear(x, wb))
+    assert torch.equal(both[:, heads:], L.linear(x, wd))
+    with pytest.raises(ValueError):
+        L.gemm(L.KIND_BF16, x, wb, act="sigmoid", act_cols=heads + 1)
+
+
 @pytest.mark.parametrize("m,k", [(257, 512), (64, 5120)])
 def test_quant_codes_bit_exact(device, m, k):
     from vdn_h3_amd import linear
