@@ -25,6 +25,27 @@ from . import linear as _linear
 from . import projection as _projection
 
 
+def _row_span(first: torch.Tensor | None, second: torch.Tensor):
+    """``(view, gap)``: the rows from ``first[0]`` through ``second[-1]`` as one view, with ``second``
+    starting ``gap`` rows in, when both are row slices of one row-major matrix and the rows between
+    them add at most a quarter to the total; otherwise ``None``."""
+    if first is None or first.ndim != 2 or second.ndim != 2 or first.shape[1] != second.shape[1]:
+        return None
+    if first.stride() != second.stride() or first.stride(1) != 1 or first.dtype != second.dtype:
+        return None
+    if first.untyped_storage().data_ptr() != second.untyped_storage().data_ptr():
+        return None
+    row = first.stride(0)
+    off = second.storage_offset() - first.storage_offset()
+    if row <= 0 or off % row or off // row < first.shape[0]:
+        return None
+    gap = off // row
+    total = gap + second.shape[0]
+    if total * 4 > 5 * (first.shape[0] + second.shape[0]):
+        return None
+    return first.as_strided((total, first.shape[1]), first.stride()), gap
+
+
 class OptimizedLinearBranch:
     """One block's VDN branch (weights are passed per call, as in the reference)."""
 
@@ -52,7 +73,7 @@ class OptimizedLinearBranch:
     def _backend(self, tokens):
         return _b.DELTA_BACKENDS[self.delta_rule](tokens)
 
-    def _text_state(self, weights, text_x, text_k_raw, text_v_raw):
+    def _text_state(self, weights, text_x, text_k_raw, text_v_raw, beta=None):
         if not self.enable_text_state or text_x is None:
             return None
         if text_k_raw is None or text_v_raw is None:
@@ -60,7 +81,8 @@ class OptimizedLinearBranch:
         length = text_x.shape[0]
         if length <= 0 or text_k_raw.shape[0] != length or text_v_raw.shape[0] != length:
             raise ValueError("text tensors must share a positive sequence length")
-        beta = _linear.sigmoid_linear(text_x, weights["beta_proj.weight"])
+        if beta is None:
+            beta = _linear.sigmoid_linear(text_x, weights["beta_proj.weight"])
         a, b = _b.frame_statistics_raw(text_k_raw, text_v_raw, beta, 1, length)
         _, jay = self._backend(length).factor_apply(None, a, b, jay_scale=_b.TEXT_STATE_SCALE, need_phi=False)
         return jay[0]
@@ -91,7 +113,15 @@ class OptimizedLinearBranch:
         heads, dim = self.num_heads, self.head_dim
         # beta = sigmoid(x W_beta^T) and the output-gate down-projection x W_down^T read the same rows:
         # one GEMM over [W_beta; W_down] with the sigmoid on the first `heads` columns
-        both = _linear.sigmoid_linear_split(xv, self._beta_down_weight(weights), heads)
+        span = _row_span(text_x, xv) if self.enable_text_state else None
+        if span is None:
+            both = _linear.sigmoid_linear_split(xv, self._beta_down_weight(weights), heads)
+            text_beta = None
+        else:  # text rows and video rows are row slices of one matrix: one launch covers both
+            rows_view, gap = span
+            both = _linear.sigmoid_linear_split(rows_view, self._beta_down_weight(weights), heads)
+            text_beta = both[:text_x.shape[0], :heads]
+            both = both[gap:]
         beta, gate_hidden = both[:, :heads], both[:, heads:]
         k_in, k_feat = self._features(weights, "k", k_raw, num_frames, frame_size)
         v_in, v_feat = self._features(weights, "v", v_raw, num_frames, frame_size)
@@ -101,7 +131,7 @@ class OptimizedLinearBranch:
         mean = _b.frame_mean(xv, num_frames, tokens_per_frame)
         alpha = _b.alpha_gate(mean, weights["alpha.down.weight"], weights["alpha.up.weight"],
                               weights["alpha.dt_bias"], weights["alpha.A_log"], heads, dim)
-        text_state = self._text_state(weights, text_x, text_k_raw, text_v_raw)
+        text_state = self._text_state(weights, text_x, text_k_raw, text_v_raw, text_beta)
         prefix, suffix = _b.run_scans_inference(self._backend(tokens_per_frame), alpha, a, b, text_state)
         del a, b
         gate = _linear.sigmoid_linear(gate_hidden, weights["output_gate.up.weight"],
