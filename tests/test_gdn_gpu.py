@@ -37,7 +37,8 @@ def _check(got, want, what):
 
 
 @pytest.mark.parametrize("tokens,heads,decay,init", [(300, 3, 0.05, True), (64, 2, 0.05, False),
-                                                     (1000, 2, 1.0, False), (129, 1, 0.0, True)])
+                                                     (1000, 2, 1.0, False), (129, 1, 0.0, True),
+                                                     (10, 2, 0.05, True), (65, 1, 0.05, False)])
 def test_gdn_matches_recurrence(device, tokens, heads, decay, init):
     from vdn_h3_amd.gdn import chunk_gated_delta_rule
 
