@@ -388,17 +388,32 @@ __global__ void alpha_logsum_kernel(const float *__restrict__ alpha, float *__re
 // gate is read and the output written as row-contiguous 16-byte pieces; the tile's gate rows
 // are loaded before its MFMAs, the next tile's q after its features.
 // QF: q already holds the features q~ (the output of a short convolution).
-template <int D, bool QF>
+// FG: the output gate is computed here, gate = bf16(sigmoid(bf16(gate_hidden W_up^T + b_up))) for
+// this head's D columns (vdn_h3/branch.py:754-758), as MFMAs beside r: W_up's head slice and the
+// bias sit in LDS in place of the y stage, and the output leaves from the accumulator layout.
+struct ReadoutGate {
+  const uint16_t *gate;    // !FG: [rows][heads * D] bf16
+  int64_t gate_row;
+  const uint16_t *hidden;  // FG: [rows][D] bf16 (x W_down^T)
+  int64_t hidden_row;
+  const uint16_t *w_up;    // FG: [heads * D][D] bf16
+  const uint16_t *b_up;    // FG: [heads * D] bf16 or null
+};
+
+__device__ __forceinline__ float gate_sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+
+template <int D, bool QF, bool FG>
 __global__ __launch_bounds__(256, 2) void readout_kernel(
     const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const float *__restrict__ prefix,
     const float *__restrict__ suffix, const float *__restrict__ logsum, const float *__restrict__ text,
-    const int *__restrict__ bounds, int use_alpha, const uint16_t *__restrict__ norm_w,
-    const uint16_t *__restrict__ gate, int64_t gate_row, uint16_t *__restrict__ out, int64_t out_row, int F, int T,
-    int heads) {
+    const int *__restrict__ bounds, int use_alpha, const uint16_t *__restrict__ norm_w, ReadoutGate gin,
+    uint16_t *__restrict__ out, int64_t out_row, int F, int T, int heads) {
   constexpr int LP = D + 8, NS = D / 16, NO = D / 32, YP = D + 8, CPR = D / 8;  // CPR: 16-byte chunks per row
   constexpr int RPI = 64 / CPR;                                                  // rows per wave instruction
   __shared__ __attribute__((aligned(16))) uint16_t Ls[D * LP];
-  __shared__ __attribute__((aligned(16))) uint16_t Ys[4][32 * YP];
+  __shared__ __attribute__((aligned(16))) uint16_t Ys[FG ? 1 : 4][FG ? 8 : 32 * YP];
+  __shared__ __attribute__((aligned(16))) uint16_t Wg[FG ? D * LP : 8];
+  __shared__ float Bg[FG ? D : 1];
   __shared__ float dec[2][D];
   __shared__ __attribute__((aligned(16))) uint16_t Wn[D];
   const int fh = blockIdx.x, f = fh / heads, h = fh - f * heads;
@@ -440,7 +455,21 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
     }
   }
   if (tid < D / 4) *reinterpret_cast<u32x2_t *>(Wn + 4 * tid) = *reinterpret_cast<const u32x2_t *>(norm_w + 4 * tid);
+  if constexpr (FG) {
+#pragma unroll
+    for (int u = 0; u < D * CPR / 256; ++u) {
+      const int e = tid + 256 * u, r = e / CPR, c = e - r * CPR;
+      st16(Wg + r * LP + 8 * c, ld16(gin.w_up + ((int64_t)h * D + r) * D + 8 * c));
+    }
+    if (tid < D) Bg[tid] = gin.b_up ? bf2f(gin.b_up[h * D + tid]) : 0.f;
+  }
   __syncthreads();
+
+  // gate hidden rows of a tile (FG): lane = token, like q
+  auto h_ptr = [&](int tile) __device__ {
+    const int64_t row = (int64_t)f * T + min(tile * 32 + l32, T - 1);
+    return gin.hidden + row * gin.hidden_row + 8 * g;
+  };
 
   // q tiles: lane = token; the next tile's raw q is loaded after this tile's features
   const int ntiles = (T + 31) / 32;
@@ -454,16 +483,19 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
 #pragma unroll
     for (int st = 0; st < NS; ++st) raw[st] = ld16(qp + 16 * st);
   }
-  uint16_t *Yw = Ys[wave];
+  uint16_t *Yw = Ys[FG ? 0 : wave];
   const int orow = lane / CPR, ochunk = lane % CPR;  // row-major pass: row it * RPI + orow, chunk ochunk
   for (int tile = wave; tile < ntiles; tile += 4) {
     // this tile's gate rows, row-major (used at the end of the tile)
-    u32x4_t gv[32 / RPI];
+    u32x4_t gv[FG ? 1 : 32 / RPI];
+    if constexpr (!FG) {
 #pragma unroll
-    for (int it = 0; it < 32 / RPI; ++it) {
-      const int t = min(tile * 32 + it * RPI + orow, T - 1);
-      gv[it] = ld16(gate + ((int64_t)f * T + t) * gate_row + (int64_t)h * D + 8 * ochunk);
+      for (int it = 0; it < 32 / RPI; ++it) {
+        const int t = min(tile * 32 + it * RPI + orow, T - 1);
+        gv[it] = ld16(gin.gate + ((int64_t)f * T + t) * gin.gate_row + (int64_t)h * D + 8 * ochunk);
+      }
     }
+
     bf16x8_t qf[NS];
     if (QF) {
 #pragma unroll
@@ -509,6 +541,13 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
       for (int st = 0; st < NS; ++st)
         acc[mb] = mfma_bf16_32x32x16(as_bf16x8(ld16(Ls + (32 * mb + l32) * LP + 16 * st + 8 * g)), qf[st], acc[mb]);
     }
+    // FG: this tile's gate hidden rows, loaded once q's fragments are dead (used after the norm)
+    u32x4_t hraw[FG ? NS : 1];
+    if constexpr (FG) {
+      const uint16_t *hp = h_ptr(tile);
+#pragma unroll
+      for (int st = 0; st < NS; ++st) hraw[st] = ld16(hp + 16 * st);
+    }
     float ss = 0.f;
 #pragma unroll
     for (int mb = 0; mb < NO; ++mb)
@@ -522,6 +561,38 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
     ss += __shfl_xor(ss, 32);
     const float nv = sqrtf(ss);
     const float inv = round_bf(1.f / sqrtf(nv * nv / (float)D + 1e-6f));
+    if constexpr (FG) {
+      // per 32-row block of v: the gate's pre-activation, transposed like r (rows = v, lane =
+      // token), then out = bf16(y * gate), y = bf16(bf16(r * inv) * w), four consecutive v per
+      // 8-byte store
+      const int t = tile * 32 + l32;
+#pragma unroll
+      for (int mb = 0; mb < NO; ++mb) {
+        __builtin_amdgcn_sched_barrier(0);  // one block's W_up fragments live at a time
+        f32x16_t gacc = {};
+#pragma unroll
+        for (int st = 0; st < NS; ++st)
+          gacc = mfma_bf16_32x32x16(as_bf16x8(ld16(Wg + (32 * mb + l32) * LP + 16 * st + 8 * g)),
+                                    as_bf16x8(hraw[st]), gacc);
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int v0 = 32 * mb + 8 * i4 + 4 * g;
+          const u32x2_t nw = *reinterpret_cast<const u32x2_t *>(Wn + v0);
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t ww = nw[e >> 1];
+            const float y = round_bf(round_bf(acc[mb][4 * i4 + e] * inv) * ((e & 1) ? bf_hi(ww) : bf_lo(ww)));
+            const float gt = round_bf(gate_sigmoid(round_bf(gacc[4 * i4 + e] + Bg[v0 + e])));
+            o[e] = y * gt;
+          }
+          if (t < T)
+            *reinterpret_cast<u32x2_t *>(out + ((int64_t)f * T + t) * out_row + (int64_t)h * D + v0) =
+                u32x2_t{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+        }
+      }
+      continue;
+    }
     // y = bf16(bf16(r * inv) * w) into the stage, row = token l32
 #pragma unroll
     for (int mb = 0; mb < NO; ++mb)
@@ -553,6 +624,25 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
     }
     asm volatile("" ::: "memory");
   }
+}
+
+template <bool FG>
+int launch_readout(const uint16_t *q, int64_t q_row, int64_t q_head, int q_features, const float *prefix,
+                   const float *suffix, const float *alpha_logsum, const float *text_state, const int32_t *bounds,
+                   int use_alpha, const uint16_t *norm_w, const ReadoutGate &gin, uint16_t *out, int64_t out_row,
+                   int frames, int tokens, int heads, int head_dim, hipStream_t s) {
+  VDNH3_HOST_CHECK(q_features == 0 || q_features == 1, VDNH3_ERR_INVALID, "readout: q_features must be 0 or 1");
+  const dim3 grid(frames * heads);
+#define VDNH3_RO(D, QF)                                                                                          \
+  if (head_dim == D && q_features == QF)                                                                         \
+    hipLaunchKernelGGL((readout_kernel<D, QF, FG>), grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix,      \
+                       alpha_logsum, text_state, bounds, use_alpha, norm_w, gin, out, out_row, frames, tokens, heads);
+  VDNH3_RO(128, 0)
+  VDNH3_RO(128, 1)
+  VDNH3_RO(64, 0)
+  VDNH3_RO(64, 1)
+#undef VDNH3_RO
+  return check_launch("readout");
 }
 
 // ---------------------------------------------------------------------------------------
@@ -768,20 +858,35 @@ extern "C" int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, i
                        reinterpret_cast<uintptr_t>(prefix) % 16 == 0 && reinterpret_cast<uintptr_t>(suffix) % 16 == 0 &&
                        reinterpret_cast<uintptr_t>(text_state) % 16 == 0,
                    VDNH3_ERR_INVALID, "readout: misaligned q / gate / out / norm weight / states");
-  VDNH3_HOST_CHECK(q_features == 0 || q_features == 1, VDNH3_ERR_INVALID, "readout: q_features must be 0 or 1");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(frames * heads);
-#define VDNH3_RO(D, QF)                                                                                        \
-  if (head_dim == D && q_features == QF)                                                                       \
-    hipLaunchKernelGGL((vdnh3::readout_kernel<D, QF>), grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix, \
-                       alpha_logsum, text_state, bounds, use_alpha, norm_w, gate, gate_row, out, out_row, frames,  \
-                       tokens, heads);
-  VDNH3_RO(128, 0)
-  VDNH3_RO(128, 1)
-  VDNH3_RO(64, 0)
-  VDNH3_RO(64, 1)
-#undef VDNH3_RO
-  return check_launch("readout");
+  const vdnh3::ReadoutGate gin{gate, gate_row, nullptr, 0, nullptr, nullptr};
+  return vdnh3::launch_readout<false>(q, q_row, q_head, q_features, prefix, suffix, alpha_logsum, text_state, bounds,
+                                      use_alpha, norm_w, gin, out, out_row, frames, tokens, heads, head_dim,
+                                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int vdnh3_readout_fused_gate(const uint16_t *q, int64_t q_row, int64_t q_head, int q_features,
+                                        const float *prefix, const float *suffix, const float *alpha_logsum,
+                                        const float *text_state, const int32_t *bounds, int use_alpha,
+                                        const uint16_t *norm_w, const uint16_t *gate_hidden, int64_t hidden_row,
+                                        const uint16_t *gate_up_w, const uint16_t *gate_up_b, uint16_t *out,
+                                        int64_t out_row, int frames, int tokens, int heads, int head_dim,
+                                        void *stream) {
+  int rc = check_dim(head_dim);
+  if (rc) return rc;
+  VDNH3_HOST_CHECK(q && prefix && suffix && (alpha_logsum || !use_alpha) && bounds && norm_w && gate_hidden &&
+                       gate_up_w && out && frames > 0 && tokens > 0,
+                   VDNH3_ERR_INVALID, "readout: empty or null operand");
+  VDNH3_HOST_CHECK(q_row % 8 == 0 && q_head % 8 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                       hidden_row % 8 == 0 && reinterpret_cast<uintptr_t>(gate_hidden) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(gate_up_w) % 16 == 0 && out_row % 4 == 0 &&
+                       reinterpret_cast<uintptr_t>(out) % 8 == 0 && reinterpret_cast<uintptr_t>(norm_w) % 8 == 0 &&
+                       reinterpret_cast<uintptr_t>(prefix) % 16 == 0 && reinterpret_cast<uintptr_t>(suffix) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(text_state) % 16 == 0,
+                   VDNH3_ERR_INVALID, "readout: misaligned q / gate hidden / gate weight / out / norm weight / states");
+  const vdnh3::ReadoutGate gin{nullptr, 0, gate_hidden, hidden_row, gate_up_w, gate_up_b};
+  return vdnh3::launch_readout<true>(q, q_row, q_head, q_features, prefix, suffix, alpha_logsum, text_state, bounds,
+                                     use_alpha, norm_w, gin, out, out_row, frames, tokens, heads, head_dim,
+                                     static_cast<hipStream_t>(stream));
 }
 
 extern "C" int vdnh3_frame_mean(const uint16_t *x, int64_t x_row, int frames, int tokens, int hidden, float *out,

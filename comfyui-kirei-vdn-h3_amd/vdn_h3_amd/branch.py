@@ -306,11 +306,14 @@ def _device_bounds(bounds, device) -> torch.Tensor:
 
 
 def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *, text_state=None,
-                     bridge="alpha", num_frames, tokens_per_frame, out=None, q_features=False):
+                     bridge="alpha", num_frames, tokens_per_frame, out=None, q_features=False, gate_hidden=None,
+                     gate_up_weight=None, gate_up_bias=None):
     """Gather, readout and RMSNorm/gate epilogue: ``[F*T, H*D]`` bf16.
 
     ``q_raw`` is the raw query (``L2(SiLU(q))`` is applied on load) unless ``q_features`` says it
-    already holds the query features (short-convolution output).
+    already holds the query features (short-convolution output). With ``gate=None`` the output
+    gate ``sigmoid(gate_hidden @ gate_up_weight.T + gate_up_bias)`` (``vdn_h3/branch.py:754-758``,
+    ``gate_hidden`` = the down-projection ``[F*T, D]``) is computed inside the readout kernel.
     """
     if bridge not in ("alpha", "none"):
         raise ValueError("bridge must be 'alpha' or 'none'")
@@ -321,19 +324,37 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
     for frame, (lo, hi) in enumerate(bounds):
         if lo > frame or hi < frame or lo > hi:
             raise ValueError(f"bounds[{frame}] does not contain its query frame")
-    device = _lib.require_device(q_raw, prefix, suffix, alpha, gate, text_state, out)
+    fused = gate is None
+    if fused:
+        if gate_hidden is None or gate_up_weight is None:
+            raise ValueError("readout needs the gate or gate_hidden and gate_up_weight")
+        if gate_hidden.shape != (rows, dim) or gate_up_weight.shape != (heads * dim, dim):
+            raise ValueError(f"gate_hidden must be [{rows}, {dim}] and gate_up_weight [{heads * dim}, {dim}]")
+        if gate_up_bias is not None and gate_up_bias.shape != (heads * dim,):
+            raise ValueError(f"gate_up_bias must be [{heads * dim}]")
+    device = _lib.require_device(q_raw, prefix, suffix, alpha, gate, text_state, out, gate_hidden, gate_up_weight,
+                                 gate_up_bias)
     q_raw = _rows(q_raw)
     bounds_t = _device_bounds(bounds, device)
     norm_w = norm_weight.to(torch.bfloat16).contiguous()
-    gate = gate.to(torch.bfloat16)
-    if gate.stride(1) != 1:
-        gate = gate.contiguous()
+    if fused:
+        gate_hidden = gate_hidden.to(torch.bfloat16)
+        if gate_hidden.stride(1) != 1 or gate_hidden.stride(0) % 8 or gate_hidden.data_ptr() % 16:
+            gate_hidden = gate_hidden.contiguous()
+        gate_up_weight = gate_up_weight.to(torch.bfloat16).contiguous()
+        if gate_up_bias is not None:
+            gate_up_bias = gate_up_bias.to(torch.bfloat16).contiguous()
+        gate = gate_hidden  # alignment checks below are for the gate path only
+    else:
+        gate = gate.to(torch.bfloat16)
+        if gate.stride(1) != 1:
+            gate = gate.contiguous()
     text = None if text_state is None else text_state.float().contiguous()
     if out is None:
         out = torch.empty((rows, heads * dim), dtype=torch.bfloat16, device=device)
     if out.stride(-1) != 1 or out.stride(0) % 8 or out.data_ptr() % 16:
         raise ValueError("out must have contiguous, 16-byte aligned rows")
-    if gate.stride(0) % 8 or gate.data_ptr() % 16:
+    if not fused and (gate.stride(0) % 8 or gate.data_ptr() % 16):
         gate = gate.contiguous()
     logsum = None
     if bridge == "alpha":
@@ -342,13 +363,17 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
         rc = _lib.lib().vdnh3_alpha_logsum(_lib.ptr(alpha), num_frames, heads, dim, _lib.ptr(logsum),
                                            _lib.stream_handle(device))
         _lib.check(rc, "vdnh3_alpha_logsum")
-    rc = _lib.lib().vdnh3_readout(_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), int(bool(q_features)),
-                                  _lib.ptr(prefix.contiguous()),
-                                  _lib.ptr(suffix.contiguous()), _lib.ptr(logsum), _lib.ptr(text), _lib.ptr(bounds_t),
-                                  int(bridge == "alpha"), _lib.ptr(norm_w), _lib.ptr(gate), gate.stride(0),
-                                  _lib.ptr(out), out.stride(0), num_frames, tokens_per_frame, heads, dim,
-                                  _lib.stream_handle(device))
-    _lib.check(rc, "vdnh3_readout")
+    common = (_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), int(bool(q_features)), _lib.ptr(prefix.contiguous()),
+              _lib.ptr(suffix.contiguous()), _lib.ptr(logsum), _lib.ptr(text), _lib.ptr(bounds_t),
+              int(bridge == "alpha"), _lib.ptr(norm_w))
+    tail = (_lib.ptr(out), out.stride(0), num_frames, tokens_per_frame, heads, dim, _lib.stream_handle(device))
+    if fused:
+        rc = _lib.lib().vdnh3_readout_fused_gate(*common, _lib.ptr(gate_hidden), gate_hidden.stride(0),
+                                                 _lib.ptr(gate_up_weight), _lib.ptr(gate_up_bias), *tail)
+        _lib.check(rc, "vdnh3_readout_fused_gate")
+    else:
+        rc = _lib.lib().vdnh3_readout(*common, _lib.ptr(gate), gate.stride(0), *tail)
+        _lib.check(rc, "vdnh3_readout")
     return out
 
 

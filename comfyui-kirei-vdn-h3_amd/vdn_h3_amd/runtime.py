@@ -134,13 +134,13 @@ class OptimizedLinearBranch:
         text_state = self._text_state(weights, text_x, text_k_raw, text_v_raw, text_beta)
         prefix, suffix = _b.run_scans_inference(self._backend(tokens_per_frame), alpha, a, b, text_state)
         del a, b
-        gate = _linear.sigmoid_linear(gate_hidden, weights["output_gate.up.weight"],
-                                      weights.get("output_gate.up.bias"))
-        del both, gate_hidden
         q_in, q_feat = self._features(weights, "q", q_raw, num_frames, frame_size)
-        return _b.readout_epilogue(q_in, prefix, suffix, alpha, bounds, weights["norm.weight"], gate,
+        # the output gate's up-projection and sigmoid run inside the readout kernel
+        return _b.readout_epilogue(q_in, prefix, suffix, alpha, bounds, weights["norm.weight"], None,
                                    text_state=text_state, bridge=self.bridge, num_frames=num_frames,
-                                   tokens_per_frame=tokens_per_frame, out=out, q_features=q_feat)
+                                   tokens_per_frame=tokens_per_frame, out=out, q_features=q_feat,
+                                   gate_hidden=gate_hidden, gate_up_weight=weights["output_gate.up.weight"],
+                                   gate_up_bias=weights.get("output_gate.up.bias"))
 
     def _check(self, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds):
         if torch.is_grad_enabled():

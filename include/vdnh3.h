@@ -242,6 +242,21 @@ int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, int q_featur
                   uint16_t *out, int64_t out_row, int frames, int tokens, int heads, int head_dim,
                   void *stream);
 
+/*
+ * vdnh3_readout with the output gate computed inside (vdn_h3/branch.py:754-758): for head h,
+ *   gate[row][h*D + v] = bf16(sigmoid(bf16(sum_j gate_hidden[row][j] * gate_up_w[h*D + v][j] + gate_up_b[h*D + v])))
+ * with gate_hidden = x W_down^T ([frames*tokens, D] bf16, row stride hidden_row, 16-byte aligned),
+ * gate_up_w [heads*D, D] bf16 and gate_up_b [heads*D] bf16 or NULL. The same values as
+ * vdnh3_gemm's sigmoid epilogue followed by vdnh3_readout, without the [rows, heads*D] gate in
+ * memory. out: 8-byte aligned rows.
+ */
+int vdnh3_readout_fused_gate(const uint16_t *q, int64_t q_row, int64_t q_head, int q_features, const float *prefix,
+                             const float *suffix, const float *alpha_logsum, const float *text_state,
+                             const int32_t *bounds, int use_alpha, const uint16_t *norm_w,
+                             const uint16_t *gate_hidden, int64_t hidden_row, const uint16_t *gate_up_w,
+                             const uint16_t *gate_up_b, uint16_t *out, int64_t out_row, int frames, int tokens,
+                             int heads, int head_dim, void *stream);
+
 /* Per-frame mean over tokens in fp32: out[f][c] = mean_t x[(f*tokens + t)*x_row + c]
  * (vdn_h3/branch.py:743-745). */
 int vdnh3_frame_mean(const uint16_t *x, int64_t x_row, int frames, int tokens, int hidden, float *out,

@@ -123,6 +123,35 @@ def test_readout_epilogue(device, text, bridge):
     _close(got, want, 4 * 2.0 ** -8, 4 * 2.0 ** -8, "readout")
 
 
+@pytest.mark.parametrize("dim,qf,bias", [(128, False, True), (128, True, False), (64, False, True)])
+def test_readout_fused_gate_equals_gemm_then_readout(device, dim, qf, bias):
+    """The output gate computed inside the readout kernel (vdnh3_readout_fused_gate) gives the same
+    bits as the bf16 sigmoid GEMM (vdnh3_gemm) followed by vdnh3_readout."""
+    from vdn_h3_amd import branch
+    from vdn_h3_amd import linear as L
+
+    print(f"case readout fused gate D={dim} q_features={qf} bias={bias}", flush=True)
+    frames, tokens, heads = 5, 77, 3
+    rows = frames * tokens
+    bounds = [(lo - 1, hi - 1) for lo, hi in wo.window_bounds(frames + 2, 1, 5)[1:-1]]
+    q = _rand((rows, heads, dim), 31, dtype=torch.bfloat16).to(device)
+    prefix = _rand((frames, heads, dim, dim), 32, 0.1).to(device)
+    suffix = _rand((frames, heads, dim, dim), 33, 0.1).to(device)
+    alpha = (torch.rand(frames, heads, dim, generator=torch.Generator().manual_seed(34)) * 0.5 + 0.5).to(device)
+    norm_w = (1 + 0.1 * _rand((dim,), 35)).to(torch.bfloat16).to(device)
+    x = _rand((rows, 3 * dim), 36, dtype=torch.bfloat16).to(device)
+    hidden = x[:, dim:2 * dim]                                   # a strided view, as in the branch
+    w_up = _rand((heads * dim, dim), 37, 0.1, torch.bfloat16).to(device)
+    b_up = _rand((heads * dim,), 38, 0.5, torch.bfloat16).to(device) if bias else None
+    kw = dict(text_state=None, bridge="alpha", num_frames=frames, tokens_per_frame=tokens, q_features=qf)
+    gate = L.sigmoid_linear(hidden, w_up, b_up)
+    want = branch.readout_epilogue(q, prefix, suffix, alpha, bounds, norm_w, gate, **kw)
+    got = branch.readout_epilogue(q, prefix, suffix, alpha, bounds, norm_w, None, gate_hidden=hidden,
+                                  gate_up_weight=w_up, gate_up_bias=b_up, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), (got.float() - want.float()).abs().max().item()
+
+
 @pytest.mark.parametrize("dim,ks,kt,l2,grid,frames", [
     (128, 5, 5, True, (48, 27), 4), (128, 5, 5, False, (48, 27), 3), (128, 5, 5, True, (8, 8), 1),
     (64, 3, 3, True, (7, 5), 6), (64, 5, 3, False, (2, 2), 5), (128, 3, 5, True, (17, 40), 3)])
