@@ -469,7 +469,8 @@ extern "C" int vdnh3_gemm(int kind, const void *A, int64_t lda, const void *B, i
   VDNH3_HOST_CHECK(A && B && C, VDNH3_ERR_INVALID, "gemm: null operand");
   VDNH3_HOST_CHECK(out_type >= kOutBF16 && out_type <= kOutI32, VDNH3_ERR_INVALID, "gemm: bad out_type %d", out_type);
   VDNH3_HOST_CHECK(out_type != kOutI32 || kind == kI8, VDNH3_ERR_INVALID, "gemm: int32 output needs int8 operands");
-  VDNH3_HOST_CHECK(act == 0 || (act & 1 && (act >> 1) <= N), VDNH3_ERR_INVALID, "gemm: bad activation %d", act);
+  VDNH3_HOST_CHECK(act == 0 || (act > 0 && (act & 1) && (act >> 1) <= N), VDNH3_ERR_INVALID,
+                   "gemm: bad activation %d", act);
   VDNH3_HOST_CHECK(!(act && accumulate), VDNH3_ERR_INVALID, "gemm: a sigmoid epilogue cannot accumulate");
   VDNH3_HOST_CHECK(!a_scale || a_scale_n == 1 || a_scale_n == M, VDNH3_ERR_INVALID,
                    "gemm: a_scale must have 1 or M entries");

@@ -57,3 +57,19 @@ def test_layout_mirror_matches_reference_semantics():
         assert current_layout() is lay
     with pytest.raises(RuntimeError):
         current_layout()
+
+
+def test_c_abi_rejects_bad_arguments_before_any_launch(built_lib):
+    """The C ABI validates on the host and returns VDNH3_ERR_INVALID (1) without touching a device:
+    a negative or out-of-range activation code, and a Gated DeltaNet head size other than 128."""
+    import ctypes
+
+    buf = (ctypes.c_uint8 * 4096)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    gemm = lambda act: built_lib.vdnh3_gemm(0, p, 64, p, 64, p, 64, 4, 4, 64, None, 0, None, 0, 1.0, None, 0, act,  # noqa: E731
+                                            0, 0, 1, None)
+    assert gemm(-1) == 1 and b"activation" in built_lib.vdnh3_last_error()
+    assert gemm(2 * 5 + 1) == 1                          # sigmoid on 5 leading columns of a 4-column output
+    rc = built_lib.vdnh3_gdn_chunk_fwd(p, 64, 64, p, 64, 64, p, 64, 64, p, 1, p, 1, None, None, p, 64, 64, 8, 1, 64, p,
+                                       4096, None)
+    assert rc == 1 and b"head_dim" in built_lib.vdnh3_last_error()
