@@ -236,12 +236,21 @@ def make_vdn_forward(attn: Any, state: VDNState, block_index: int):
         with scope("attention.rope_norm", device):
             query, key = normalise_qk(q_raw, k_raw, qw, kw, q_eps, rope_freqs=rope_freqs)
 
-        gate = None
+        gate, proj_rows = None, None
         if gate_enabled:
             try:
                 with scope("attention.gate", device):
-                    gate = _linear.sigmoid_linear(x, weights["softmax_gate.up.weight"],
-                                                  weights.get("softmax_gate.up.bias"))
+                    fused = _gate_branch_weights(state, block_index, weights, branch) if linear_active else None
+                    if fused is None:
+                        gate = _linear.sigmoid_linear(x, weights["softmax_gate.up.weight"],
+                                                      weights.get("softmax_gate.up.bias"))
+                    else:
+                        # one GEMM over x: [softmax gate | branch beta] (sigmoid) and the branch's
+                        # output-gate down-projection, x read once for both
+                        w_all, b_all = fused
+                        rows = _linear.gemm(_linear.KIND_BF16, x, w_all, bias=b_all, act="sigmoid",
+                                            round_linear=True, act_cols=2 * heads)
+                        gate, proj_rows = rows[:, :heads], rows[:, heads:]
             except KeyError as exc:
                 raise RuntimeError(f"VDN branch block {block_index} is missing softmax gate tensor "
                                    f"{exc.args[0]!r}") from exc
@@ -275,7 +284,9 @@ def make_vdn_forward(attn: Any, state: VDNState, block_index: int):
                     text_x=x[ta:tb] if text_enabled else None,
                     text_k_raw=k_raw[ta:tb] if text_enabled else None,
                     text_v_raw=value[ta:tb] if text_enabled else None, skip_ends=(layout.anchor_frames == "both"),
-                    inference=True, projector=projector, out=out[va:vb], accumulate=True)
+                    inference=True, projector=projector, out=out[va:vb], accumulate=True,
+                    **({} if proj_rows is None else
+                       {"proj_rows": proj_rows[va:vb], "text_proj_rows": proj_rows[ta:tb] if text_enabled else None}))
         state.forwards += 1
         state.last_layout = layout
         return out
@@ -283,6 +294,36 @@ def make_vdn_forward(attn: Any, state: VDNState, block_index: int):
     vdn_forward._vdn_h3_forward = True
     vdn_forward._vdn_h3_original = original_forward
     return vdn_forward
+
+
+def _gate_branch_weights(state, block_index, weights, branch):
+    """``([W_softmax_gate; W_beta; W_down], bias)`` for one GEMM over the block input, or ``None`` when the
+    branch is not this library's ``OptimizedLinearBranch`` or a weight is missing. Cached per block and
+    rebuilt when a weight changes."""
+    from .runtime import OptimizedLinearBranch
+
+    if not isinstance(branch, OptimizedLinearBranch):
+        return None
+    try:
+        ws, wb, wd = (weights["softmax_gate.up.weight"], weights["beta_proj.weight"],
+                      weights["output_gate.down.weight"])
+    except KeyError:
+        return None
+    bs = weights.get("softmax_gate.up.bias")
+    parts = [t for t in (ws, wb, wd, bs) if t is not None]
+    if ws.dtype != torch.bfloat16 or wb.dtype != torch.bfloat16 or wd.dtype != torch.bfloat16:
+        return None
+    key = tuple((t.data_ptr(), t._version, tuple(t.shape)) for t in parts)
+    cache = state.__dict__.setdefault("_gate_branch_cache", {})
+    hit = cache.get(block_index)
+    if hit is None or hit[0] != key:
+        w_all = torch.cat([ws, wb, wd], dim=0).contiguous()
+        b_all = torch.zeros(w_all.shape[0], dtype=torch.float32, device=ws.device)
+        if bs is not None:
+            b_all[:ws.shape[0]] = bs.float()
+        hit = (key, (w_all, b_all))
+        cache[block_index] = hit
+    return hit[1]
 
 
 @contextmanager

@@ -109,12 +109,16 @@ class OptimizedLinearBranch:
         return feats, True
 
     def _readout_flat(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, text_x,
-                      text_k_raw, text_v_raw, frame_size=None, out=None):
+                      text_k_raw, text_v_raw, frame_size=None, out=None, proj_rows=None, text_proj_rows=None):
         heads, dim = self.num_heads, self.head_dim
         # beta = sigmoid(x W_beta^T) and the output-gate down-projection x W_down^T read the same rows:
-        # one GEMM over [W_beta; W_down] with the sigmoid on the first `heads` columns
-        span = _row_span(text_x, xv) if self.enable_text_state else None
-        if span is None:
+        # one GEMM over [W_beta; W_down] with the sigmoid on the first `heads` columns (or rows the
+        # caller computed with a wider GEMM over the same x)
+        span = _row_span(text_x, xv) if self.enable_text_state and proj_rows is None else None
+        if proj_rows is not None:
+            both = proj_rows
+            text_beta = None if text_proj_rows is None else text_proj_rows[:, :heads]
+        elif span is None:
             both = _linear.sigmoid_linear_split(xv, self._beta_down_weight(weights), heads)
             text_beta = None
         else:  # text rows and video rows are row slices of one matrix: one launch covers both
@@ -177,13 +181,17 @@ class OptimizedLinearBranch:
 
     def projected_delta(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, *,
                         frame_size=None, text_x=None, text_k_raw=None, text_v_raw=None, skip_ends=False,
-                        inference=True, projector=None, tile_frames=None, out=None, accumulate=False):
+                        inference=True, projector=None, tile_frames=None, out=None, accumulate=False,
+                        proj_rows=None, text_proj_rows=None):
         """Branch output after ``to_out_linear``, ``[F*T, hidden]`` bf16, anchor rows zero.
 
         ``out``/``accumulate``: write (or add, ``out += delta``) straight into an existing
         ``[F*T, hidden]`` bf16 view, e.g. the video rows of the block output; with
         ``accumulate`` the anchor rows of ``out`` are left untouched (their delta is zero).
         ``projector(rows, out=..., accumulate=...)`` defaults to ``projection.project``.
+        ``proj_rows`` / ``text_proj_rows`` (optional, ``[rows, heads + rank]`` bf16): ``[beta | x W_down^T]``
+        of the rows of ``xv`` / ``text_x``, already computed by the caller (the block computes them in the
+        softmax gate's GEMM); without them the branch computes them itself.
         """
         del inference, tile_frames
         self._check(xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds)
@@ -206,11 +214,13 @@ class OptimizedLinearBranch:
                 _b.fill_rows(out[(num_frames - 1) * t:])
             flat = self._readout_flat(weights, xv[inner], q_raw[inner], k_raw[inner], v_raw[inner],
                                       num_frames - 2, t, [(lo - 1, hi - 1) for lo, hi in bounds[1:-1]], text_x,
-                                      text_k_raw, text_v_raw, frame_size)
+                                      text_k_raw, text_v_raw, frame_size,
+                                      proj_rows=None if proj_rows is None else proj_rows[inner],
+                                      text_proj_rows=text_proj_rows)
             proj(flat, out=out[inner], accumulate=accumulate)
             return out
         flat = self._readout_flat(weights, xv, q_raw, k_raw, v_raw, num_frames, t, bounds, text_x, text_k_raw,
-                                  text_v_raw, frame_size)
+                                  text_v_raw, frame_size, proj_rows=proj_rows, text_proj_rows=text_proj_rows)
         proj(flat, out=out, accumulate=accumulate)
         return out
 
