@@ -686,10 +686,56 @@ __global__ __launch_bounds__(256) void frame_mean_kernel(const uint16_t *__restr
 }
 
 // out[m][n] = sum_k x[m][k] W[n][k] (+ bias[n]) in fp32 (the small alpha projections: few rows,
-// K up to the hidden size). One wavefront per output column n: lanes stride K so that the rows
-// of x and W are read coalesced, eight rows of x at a time, then a butterfly sum over lanes.
+// K up to the hidden size), grid (N / 4, M / 8).
 template <bool WBF16>
 __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict__ x, int64_t x_row,
+                                                         const void *__restrict__ w, int64_t w_row,
+                                                         const float *__restrict__ bias, float *__restrict__ out,
+                                                         int64_t out_row, int M, int N, int K) {
+  // one workgroup per block of 8 rows x 4 columns; its 256 threads split K (thread t takes
+  // k = t, t + 256, ...), each holding the 32 partial sums, then a tree over the threads in LDS
+  constexpr int BM = 8, BN = 4;
+  __shared__ float red[BM * BN][257];
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, tid = threadIdx.x;
+  const float *xr[BM];
+#pragma unroll
+  for (int i = 0; i < BM; ++i) xr[i] = x + (int64_t)min(m0 + i, M - 1) * x_row;
+  int64_t wo[BN];
+#pragma unroll
+  for (int j = 0; j < BN; ++j) wo[j] = (int64_t)min(n0 + j, N - 1) * w_row;
+  float acc[BM][BN] = {};
+  for (int k = tid; k < K; k += 256) {
+    float wk[BN], xk[BM];
+#pragma unroll
+    for (int j = 0; j < BN; ++j)
+      wk[j] = WBF16 ? bf2f(static_cast<const uint16_t *>(w)[wo[j] + k]) : static_cast<const float *>(w)[wo[j] + k];
+#pragma unroll
+    for (int i = 0; i < BM; ++i) xk[i] = xr[i][k];
+#pragma unroll
+    for (int i = 0; i < BM; ++i)
+#pragma unroll
+      for (int j = 0; j < BN; ++j) acc[i][j] = fmaf(xk[i], wk[j], acc[i][j]);
+  }
+#pragma unroll
+  for (int i = 0; i < BM; ++i)
+#pragma unroll
+    for (int j = 0; j < BN; ++j) red[i * BN + j][tid] = acc[i][j];
+  __syncthreads();
+  // 32 outputs x 256 partials: thread group of 8 per output sums 32 partials each, then 3 shuffles
+  const int o = tid >> 3, part = tid & 7;
+  float sum = 0.f;
+#pragma unroll
+  for (int u = 0; u < 32; ++u) sum += red[o][part * 32 + u];
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  sum += __shfl_xor(sum, 4);
+  const int m = m0 + o / BN, n = n0 + o % BN;
+  if (part == 0 && m < M && n < N) out[(int64_t)m * out_row + n] = sum + (bias ? bias[n] : 0.f);
+}
+
+// short K: one wavefront per output column n, lanes striding K, eight rows of x at a time
+template <bool WBF16>
+__global__ __launch_bounds__(256) void linear_f32_cols_kernel(const float *__restrict__ x, int64_t x_row,
                                                          const void *__restrict__ w, int64_t w_row,
                                                          const float *__restrict__ bias, float *__restrict__ out,
                                                          int64_t out_row, int M, int N, int K) {
@@ -903,13 +949,24 @@ extern "C" int vdnh3_frame_mean(const uint16_t *x, int64_t x_row, int frames, in
 extern "C" int vdnh3_linear_f32(const float *x, int64_t x_row, const void *w, int w_bf16, int64_t w_row,
                                 const float *bias, float *out, int64_t out_row, int M, int N, int K, void *stream) {
   VDNH3_HOST_CHECK(x && w && out && M > 0 && N > 0 && K > 0, VDNH3_ERR_INVALID, "linear_f32: empty or null operand");
-  const dim3 grid((unsigned)((N + 3) / 4));
-  if (w_bf16)
-    hipLaunchKernelGGL(vdnh3::linear_f32_kernel<true>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x, x_row,
-                       w, w_row, bias, out, out_row, M, N, K);
-  else
-    hipLaunchKernelGGL(vdnh3::linear_f32_kernel<false>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x,
-                       x_row, w, w_row, bias, out, out_row, M, N, K);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (K >= 1024) {  // long K: split over the workgroup's threads
+    const dim3 grid((unsigned)((N + 3) / 4), (unsigned)((M + 7) / 8));
+    if (w_bf16)
+      hipLaunchKernelGGL(vdnh3::linear_f32_kernel<true>, grid, dim3(256), 0, s, x, x_row, w, w_row, bias, out,
+                         out_row, M, N, K);
+    else
+      hipLaunchKernelGGL(vdnh3::linear_f32_kernel<false>, grid, dim3(256), 0, s, x, x_row, w, w_row, bias, out,
+                         out_row, M, N, K);
+  } else {
+    const dim3 grid((unsigned)((N + 3) / 4));
+    if (w_bf16)
+      hipLaunchKernelGGL(vdnh3::linear_f32_cols_kernel<true>, grid, dim3(256), 0, s, x, x_row, w, w_row, bias, out,
+                         out_row, M, N, K);
+    else
+      hipLaunchKernelGGL(vdnh3::linear_f32_cols_kernel<false>, grid, dim3(256), 0, s, x, x_row, w, w_row, bias, out,
+                         out_row, M, N, K);
+  }
   return check_launch("linear_f32");
 }
 

@@ -123,6 +123,24 @@ def test_readout_epilogue(device, text, bridge):
     _close(got, want, 4 * 2.0 ** -8, 4 * 2.0 ** -8, "readout")
 
 
+
+@pytest.mark.parametrize("m,n,k,w_bf16,bias", [(29, 128, 5120, True, False), (29, 5120, 128, True, True),
+                                               (5, 7, 1100, False, True), (1, 3, 64, False, False)])
+def test_linear_f32(device, m, n, k, w_bf16, bias):
+    """The fp32 alpha projections (vdnh3_linear_f32): both the long-K (split over a workgroup) and the
+    short-K (one wavefront per column) kernels against a float64 product."""
+    from vdn_h3_amd import branch
+
+    print(f"case linear_f32 m={m} n={n} k={k}", flush=True)
+    x = _rand((m, k), 41)
+    w = _rand((n, k), 42, 0.05, torch.bfloat16 if w_bf16 else torch.float32)
+    b = _rand((n,), 43) if bias else None
+    got = branch.linear_f32(x.to(device), w.to(device), None if b is None else b.to(device))
+    torch.cuda.synchronize()
+    want = x.double() @ w.double().t() + (0 if b is None else b.double())
+    err = (got.double().cpu() - want).abs().max().item()
+    assert err <= 1e-5 * (1 + want.abs().max().item()), err
+
 @pytest.mark.parametrize("dim,qf,bias", [(128, False, True), (128, True, False), (64, False, True)])
 def test_readout_fused_gate_equals_gemm_then_readout(device, dim, qf, bias):
     """The output gate computed inside the readout kernel (vdnh3_readout_fused_gate) gives the same
