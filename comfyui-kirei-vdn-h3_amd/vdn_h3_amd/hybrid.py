@@ -125,6 +125,7 @@ class VDNState:
 
     def release(self):
         self._resident.clear()
+        self.__dict__.pop("_gate_branch_cache", None)
         self.window_cache.release()
         if self.block_fusion:
             from .block_kernels import release_block_fusions
