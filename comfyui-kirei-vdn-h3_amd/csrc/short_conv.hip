@@ -87,11 +87,24 @@ __device__ __forceinline__ void load_tap_pairs(const uint16_t *taps, int j, uint
   }
 }
 
+// up to four tensors of one frame grid convolved by one launch (e.g. k and v): their workgroups
+// fill the same rounds instead of each launch ending on a partly empty one
+constexpr int SC_MAX_JOBS = 4;
+struct ConvJob {
+  const uint16_t *x;
+  int64_t x_row, x_head;
+  const uint16_t *w_sp, *w_tm;
+  int l2norm;
+  uint16_t *out;
+  int64_t o_row, o_head;
+};
+struct ConvJobs {
+  ConvJob j[SC_MAX_JOBS];
+};
+
 template <int D, int KS, int KT>
-__global__ __launch_bounds__(SC_THREADS) void short_conv_kernel(
-    const uint16_t *__restrict__ x, int64_t x_row, int64_t x_head, const uint16_t *__restrict__ w_sp,
-    const uint16_t *__restrict__ w_tm, int F, int gh, int gw, int TX, int TY, int nx, int n_tiles, int l2norm,
-    uint16_t *__restrict__ out, int64_t o_row, int64_t o_head) {
+__global__ __launch_bounds__(SC_THREADS) void short_conv_kernel(ConvJobs jobs, int F, int gh, int gw, int TX, int TY,
+                                                                 int nx, int n_tiles, int heads) {
   constexpr int P = KS / 2, PT = KT / 2;
   constexpr int LPP = D / 4;                      // lanes per position
   constexpr int PPP = SC_THREADS / LPP;           // positions per pass
@@ -104,7 +117,15 @@ __global__ __launch_bounds__(SC_THREADS) void short_conv_kernel(
   // x-th contiguous run of the logical order (head-major), so a head's tiles share one L2
   const int nb = gridDim.x, per = nb >> 3, rem = nb & 7, xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int logical = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
-  const int h = logical / n_tiles, ti = logical - h * n_tiles;
+  const int job = logical / (heads * n_tiles), hti = logical - job * heads * n_tiles;
+  const int h = hti / n_tiles, ti = hti - h * n_tiles;
+  const ConvJob &J = jobs.j[job];
+  const uint16_t *__restrict__ x = J.x;
+  const uint16_t *__restrict__ w_sp = J.w_sp;
+  const uint16_t *__restrict__ w_tm = J.w_tm;
+  uint16_t *__restrict__ out = J.out;
+  const int64_t x_row = J.x_row, x_head = J.x_head, o_row = J.o_row, o_head = J.o_head;
+  const int l2norm = J.l2norm;
   const int y0 = (ti / nx) * TY, x0 = (ti % nx) * TX;
   const int tid = threadIdx.x, cl = tid % LPP, ps = tid / LPP;
   const int SX = TX + 2 * P, SY = TY + 2 * P, n_stage = SX * SY * CPP;
@@ -281,41 +302,40 @@ void pick_tile(int gh, int gw, int P, int *TX, int *TY, int *nx, int *ny) {
 }
 
 template <int D, int KS, int KT>
-void launch(const uint16_t *x, int64_t x_row, int64_t x_head, const uint16_t *w_sp, const uint16_t *w_tm, int F,
-            int gh, int gw, int heads, int l2norm, uint16_t *out, int64_t o_row, int64_t o_head, hipStream_t s) {
+void launch(const ConvJobs &jobs, int n_jobs, int F, int gh, int gw, int heads, hipStream_t s) {
   int TX = 1, TY = 1, nx = gw, ny = gh;
   pick_tile(gh, gw, KS / 2, &TX, &TY, &nx, &ny);
   const int n_tiles = nx * ny;
-  hipLaunchKernelGGL((short_conv_kernel<D, KS, KT>), dim3(heads * n_tiles), dim3(SC_THREADS), 0, s, x, x_row,
-                     x_head, w_sp, w_tm, F, gh, gw, TX, TY, nx, n_tiles, l2norm, out, o_row, o_head);
+  hipLaunchKernelGGL((short_conv_kernel<D, KS, KT>), dim3(n_jobs * heads * n_tiles), dim3(SC_THREADS), 0, s, jobs, F,
+                     gh, gw, TX, TY, nx, n_tiles, heads);
 }
 
-}  // namespace
-}  // namespace vdnh3
-
-extern "C" int vdnh3_short_conv(const uint16_t *x, int64_t x_row, int64_t x_head, const uint16_t *w_spatial,
-                                int kernel_h, int kernel_w, const uint16_t *w_temporal, int kernel_t, int frames,
-                                int grid_h, int grid_w, int heads, int head_dim, int l2norm, uint16_t *out,
-                                int64_t out_row, int64_t out_head, void *stream) {
+int run_jobs(const vdnh3_short_conv_job *jobs, int n_jobs, int kernel_h, int kernel_w, int kernel_t, int frames,
+             int grid_h, int grid_w, int heads, int head_dim, hipStream_t s) {
+  VDNH3_HOST_CHECK(jobs && n_jobs >= 1 && n_jobs <= SC_MAX_JOBS, VDNH3_ERR_INVALID,
+                   "short_conv: 1 to %d tensors per launch, got %d", SC_MAX_JOBS, n_jobs);
   VDNH3_HOST_CHECK(head_dim == 64 || head_dim == 128, VDNH3_ERR_INVALID,
                    "short_conv: head_dim must be 64 or 128, got %d", head_dim);
   VDNH3_HOST_CHECK(kernel_h == kernel_w && (kernel_h == 3 || kernel_h == 5) && (kernel_t == 3 || kernel_t == 5),
                    VDNH3_ERR_INVALID,
                    "short_conv: supported kernels are 3x3 or 5x5 spatial and 3 or 5 temporal taps, got %dx%d and %d",
                    kernel_h, kernel_w, kernel_t);
-  VDNH3_HOST_CHECK(x && w_spatial && w_temporal && out && frames > 0 && grid_h > 0 && grid_w > 0 && heads > 0,
-                   VDNH3_ERR_INVALID, "short_conv: empty or null operand");
-  VDNH3_HOST_CHECK(x_row % 8 == 0 && x_head % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0,
-                   VDNH3_ERR_INVALID, "short_conv: x must be 16-byte aligned with strides multiple of 8");
-  VDNH3_HOST_CHECK((int64_t)grid_h * grid_w * x_row < ((int64_t)1 << 31), VDNH3_ERR_INVALID,
-                   "short_conv: one frame of x must span fewer than 2^31 elements");
-  VDNH3_HOST_CHECK(out_row % 4 == 0 && out_head % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0,
-                   VDNH3_ERR_INVALID, "short_conv: out must be 8-byte aligned with strides multiple of 4");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-#define VDNH3_SC(D, KS, KT)                                                                                  \
-  if (head_dim == D && kernel_h == KS && kernel_t == KT)                                                     \
-    vdnh3::launch<D, KS, KT>(x, x_row, x_head, w_spatial, w_temporal, frames, grid_h, grid_w, heads, l2norm, \
-                             out, out_row, out_head, s);
+  VDNH3_HOST_CHECK(frames > 0 && grid_h > 0 && grid_w > 0 && heads > 0, VDNH3_ERR_INVALID,
+                   "short_conv: empty frame grid or no heads");
+  ConvJobs cj{};
+  for (int i = 0; i < n_jobs; ++i) {
+    const vdnh3_short_conv_job &j = jobs[i];
+    VDNH3_HOST_CHECK(j.x && j.w_spatial && j.w_temporal && j.out, VDNH3_ERR_INVALID, "short_conv: null operand");
+    VDNH3_HOST_CHECK(j.x_row % 8 == 0 && j.x_head % 8 == 0 && reinterpret_cast<uintptr_t>(j.x) % 16 == 0,
+                     VDNH3_ERR_INVALID, "short_conv: x must be 16-byte aligned with strides multiple of 8");
+    VDNH3_HOST_CHECK((int64_t)grid_h * grid_w * j.x_row < ((int64_t)1 << 31), VDNH3_ERR_INVALID,
+                     "short_conv: one frame of x must span fewer than 2^31 elements");
+    VDNH3_HOST_CHECK(j.out_row % 4 == 0 && j.out_head % 4 == 0 && reinterpret_cast<uintptr_t>(j.out) % 8 == 0,
+                     VDNH3_ERR_INVALID, "short_conv: out must be 8-byte aligned with strides multiple of 4");
+    cj.j[i] = ConvJob{j.x, j.x_row, j.x_head, j.w_spatial, j.w_temporal, j.l2norm, j.out, j.out_row, j.out_head};
+  }
+#define VDNH3_SC(D, KS, KT) \
+  if (head_dim == D && kernel_h == KS && kernel_t == KT) launch<D, KS, KT>(cj, n_jobs, frames, grid_h, grid_w, heads, s);
   VDNH3_SC(128, 5, 5)
   VDNH3_SC(128, 5, 3)
   VDNH3_SC(128, 3, 5)
@@ -325,5 +345,24 @@ extern "C" int vdnh3_short_conv(const uint16_t *x, int64_t x_row, int64_t x_head
   VDNH3_SC(64, 3, 5)
   VDNH3_SC(64, 3, 3)
 #undef VDNH3_SC
-  return vdnh3::check_launch("short_conv");
+  return check_launch("short_conv");
+}
+
+}  // namespace
+}  // namespace vdnh3
+
+extern "C" int vdnh3_short_conv(const uint16_t *x, int64_t x_row, int64_t x_head, const uint16_t *w_spatial,
+                                int kernel_h, int kernel_w, const uint16_t *w_temporal, int kernel_t, int frames,
+                                int grid_h, int grid_w, int heads, int head_dim, int l2norm, uint16_t *out,
+                                int64_t out_row, int64_t out_head, void *stream) {
+  const vdnh3_short_conv_job job{x, x_row, x_head, w_spatial, w_temporal, l2norm, out, out_row, out_head};
+  return vdnh3::run_jobs(&job, 1, kernel_h, kernel_w, kernel_t, frames, grid_h, grid_w, heads, head_dim,
+                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int vdnh3_short_conv_batch(const vdnh3_short_conv_job *jobs, int n_jobs, int kernel_h, int kernel_w,
+                                      int kernel_t, int frames, int grid_h, int grid_w, int heads, int head_dim,
+                                      void *stream) {
+  return vdnh3::run_jobs(jobs, n_jobs, kernel_h, kernel_w, kernel_t, frames, grid_h, grid_w, heads, head_dim,
+                         static_cast<hipStream_t>(stream));
 }

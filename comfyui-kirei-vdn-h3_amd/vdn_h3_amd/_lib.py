@@ -53,6 +53,8 @@ SIGNATURES = {
                                    _c_int, _c_int, _c_int, _vp, _vp, _vp]),
     "vdnh3_short_conv": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,
                                   _c_int, _c_int, _c_int, _vp, _c_i64, _c_i64, _vp]),
+    "vdnh3_short_conv_batch": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                        _vp]),
     "vdnh3_delta_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_float, _vp, _c_int, _c_int, _vp]),
     "vdnh3_sana_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_delta_scan": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),

@@ -24,6 +24,8 @@ from contextlib import contextmanager
 from contextvars import ContextVar
 from typing import Any
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -123,14 +125,14 @@ def frame_statistics_raw(k_raw: torch.Tensor, v_raw: torch.Tensor, beta: torch.T
     return a, b
 
 
-def conv_features(tokens: torch.Tensor, spatial_weight: torch.Tensor, temporal_weight: torch.Tensor,
-                  num_frames: int, frame_size, l2norm: bool, *, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Short-convolution features ``[F*T, H, D]`` bf16 (``vdn_h3/branch.py:443-480``, ``vdn_h3/runtime.py:319-341``).
+class _ConvJob(ctypes.Structure):
+    """``vdnh3_short_conv_job`` (include/vdnh3.h)."""
+    _fields_ = [("x", ctypes.c_void_p), ("x_row", ctypes.c_int64), ("x_head", ctypes.c_int64),
+                ("w_spatial", ctypes.c_void_p), ("w_temporal", ctypes.c_void_p), ("l2norm", ctypes.c_int),
+                ("out", ctypes.c_void_p), ("out_row", ctypes.c_int64), ("out_head", ctypes.c_int64)]
 
-    Depthwise ``kh x kw`` spatial convolution per frame (rounded to bf16), depthwise temporal
-    convolution over the ``num_frames`` frames (zero padded), SiLU, and with ``l2norm`` a unit
-    L2 norm over each head's ``D`` channels, as one kernel.
-    """
+
+def _conv_job(tokens, spatial_weight, temporal_weight, num_frames, frame_size, l2norm, out):
     if tokens.ndim != 3 or frame_size is None:
         raise ValueError("conv features need [rows, heads, dim] and frame_size")
     heads, head_dim = tokens.shape[-2:]
@@ -157,11 +159,53 @@ def conv_features(tokens: torch.Tensor, spatial_weight: torch.Tensor, temporal_w
         out = torch.empty((tokens.shape[0], heads, head_dim), dtype=torch.bfloat16, device=device)
     elif out.shape != tokens.shape or out.dtype != torch.bfloat16 or out.stride(-1) != 1:
         raise ValueError("out must be a bf16 [rows, heads, dim] view with contiguous dim")
-    rc = _lib.lib().vdnh3_short_conv(_lib.ptr(tokens), tokens.stride(0), tokens.stride(1), _lib.ptr(sp), kh, kw,
-                                     _lib.ptr(tm), kt, num_frames, gh, gw, heads, head_dim, int(bool(l2norm)),
-                                     _lib.ptr(out), out.stride(0), out.stride(1), _lib.stream_handle(device))
+    job = _ConvJob(_lib.ptr(tokens), tokens.stride(0), tokens.stride(1), _lib.ptr(sp), _lib.ptr(tm), int(bool(l2norm)),
+                   _lib.ptr(out), out.stride(0), out.stride(1))
+    return job, (kh, kw, kt, gh, gw, heads, head_dim), device, out, (tokens, sp, tm)
+
+
+def conv_features(tokens: torch.Tensor, spatial_weight: torch.Tensor, temporal_weight: torch.Tensor,
+                  num_frames: int, frame_size, l2norm: bool, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Short-convolution features ``[F*T, H, D]`` bf16 (``vdn_h3/branch.py:443-480``, ``vdn_h3/runtime.py:319-341``).
+
+    Depthwise ``kh x kw`` spatial convolution per frame (rounded to bf16), depthwise temporal
+    convolution over the ``num_frames`` frames (zero padded), SiLU, and with ``l2norm`` a unit
+    L2 norm over each head's ``D`` channels, as one kernel.
+    """
+    job, (kh, kw, kt, gh, gw, heads, head_dim), device, out, held = _conv_job(
+        tokens, spatial_weight, temporal_weight, num_frames, frame_size, l2norm, out)
+    rc = _lib.lib().vdnh3_short_conv(job.x, job.x_row, job.x_head, job.w_spatial, kh, kw, job.w_temporal, kt,
+                                     num_frames, gh, gw, heads, head_dim, job.l2norm, job.out, job.out_row,
+                                     job.out_head, _lib.stream_handle(device))
     _lib.check(rc, "vdnh3_short_conv")
+    del held
     return out
+
+
+def conv_features_batch(items, num_frames: int, frame_size) -> list:
+    """``conv_features`` of up to four ``(tokens, spatial_weight, temporal_weight, l2norm, out)`` over the
+    same frame grid and kernel sizes in one launch (``vdnh3_short_conv_batch``); returns the outputs."""
+    if not 1 <= len(items) <= 4:
+        raise ValueError("conv_features_batch takes 1 to 4 tensors")
+    jobs, shapes, outs, keep, device = [], set(), [], [], None
+    for tokens, sw, tw, l2, out in items:
+        job, shape, dev, out, held = _conv_job(tokens, sw, tw, num_frames, frame_size, l2, out)
+        if device is not None and dev != device:
+            raise ValueError("all tensors of a batch must be on one device")
+        device = dev
+        jobs.append(job)
+        shapes.add(shape)
+        outs.append(out)
+        keep.append(held)
+    if len(shapes) != 1:
+        raise ValueError("a batch needs one frame grid, kernel size and head geometry")
+    kh, kw, kt, gh, gw, heads, head_dim = shapes.pop()
+    arr = (_ConvJob * len(jobs))(*jobs)
+    rc = _lib.lib().vdnh3_short_conv_batch(ctypes.addressof(arr), len(jobs), kh, kw, kt, num_frames, gh, gw, heads,
+                                           head_dim, _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_short_conv_batch")
+    del keep
+    return outs
 
 
 class VdnDelta:

@@ -127,8 +127,16 @@ class OptimizedLinearBranch:
             text_beta = both[:text_x.shape[0], :heads]
             both = both[gap:]
         beta, gate_hidden = both[:, :heads], both[:, heads:]
-        k_in, k_feat = self._features(weights, "k", k_raw, num_frames, frame_size)
-        v_in, v_feat = self._features(weights, "v", v_raw, num_frames, frame_size)
+        if "k" in self.short_conv and "v" in self.short_conv and frame_size is not None:
+            # both convolutions in one launch (their workgroups share the launch's rounds)
+            k_in, v_in = _b.conv_features_batch(
+                [(k_raw, weights["short_conv.k_sp.weight"], weights["short_conv.k_tm.weight"], True, None),
+                 (v_raw, weights["short_conv.v_sp.weight"], weights["short_conv.v_tm.weight"], False, None)],
+                num_frames, frame_size)
+            k_feat = v_feat = True
+        else:
+            k_in, k_feat = self._features(weights, "k", k_raw, num_frames, frame_size)
+            v_in, v_feat = self._features(weights, "v", v_raw, num_frames, frame_size)
         a, b = _b.frame_statistics_raw(k_in, v_in, beta, num_frames, tokens_per_frame, k_features=k_feat,
                                        v_features=v_feat)
         del k_in, v_in

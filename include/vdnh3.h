@@ -196,6 +196,22 @@ int vdnh3_short_conv(const uint16_t *x, int64_t x_row, int64_t x_head, const uin
                      void *stream);
 
 /*
+ * Several short convolutions over the same frame grid and kernel sizes in one launch (the
+ * reference convolves k and v one after the other, vdn_h3/runtime.py:319-341): 1 to 4 jobs, each
+ * with the operands and meaning of vdnh3_short_conv.
+ */
+typedef struct vdnh3_short_conv_job {
+  const uint16_t *x;
+  int64_t x_row, x_head;
+  const uint16_t *w_spatial, *w_temporal;
+  int l2norm;
+  uint16_t *out;
+  int64_t out_row, out_head;
+} vdnh3_short_conv_job;
+int vdnh3_short_conv_batch(const vdnh3_short_conv_job *jobs, int n_jobs, int kernel_h, int kernel_w, int kernel_t,
+                           int frames, int grid_h, int grid_w, int heads, int head_dim, void *stream);
+
+/*
  * VdnDelta.factor_apply (vdn_h3/branch.py:148-160) over n matrices with the status of
  * torch.linalg.cholesky_ex (vdn_h3/branch.py:62-71): L = chol(I + A), M = L^-T L^-1,
  * phi = alpha[i] * M[i][j] (phi may be NULL; alpha NULL means ones), jay = jay_scale * (B M),

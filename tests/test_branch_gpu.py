@@ -227,6 +227,26 @@ def test_projected_delta_matches_reference_golden(device):
     _parity(readout, t["readout"], "readout vs reference")
 
 
+
+def test_short_conv_batch_equals_single_calls(device):
+    """k (with the L2 norm) and v (without) convolved in one vdnh3_short_conv_batch launch give the
+    same bits as two vdnh3_short_conv calls."""
+    from vdn_h3_amd import branch
+
+    print("case short conv batch", flush=True)
+    frames, (gh, gw), heads, dim = 5, (12, 9), 3, 128
+    rows, ch = frames * gh * gw, heads * dim
+    fused = _rand((rows, 3 * ch), 70, dtype=torch.bfloat16).to(device)
+    k = fused[:, ch:2 * ch].view(rows, heads, dim)
+    v = fused[:, 2 * ch:].view(rows, heads, dim)
+    w = [_rand((ch, 1, 5, 5), 71 + i, 0.2, torch.bfloat16).to(device) for i in range(2)]
+    t = [_rand((ch, 1, 5), 73 + i, 0.4, torch.bfloat16).to(device) for i in range(2)]
+    kb, vb = branch.conv_features_batch([(k, w[0], t[0], True, None), (v, w[1], t[1], False, None)], frames, (gh, gw))
+    ks = branch.conv_features(k, w[0], t[0], frames, (gh, gw), True)
+    vs = branch.conv_features(v, w[1], t[1], frames, (gh, gw), False)
+    torch.cuda.synchronize()
+    assert torch.equal(kb, ks) and torch.equal(vb, vs)
+
 def test_projected_delta_short_conv_matches_reference_golden(device):
     """The branch with K/V short convolutions (13 frames of 8x8, 2 heads x 64) vs the reference."""
     from vdn_h3_amd.runtime import OptimizedLinearBranch
