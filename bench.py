@@ -57,7 +57,7 @@ def _parse():
     ap.add_argument("--short-conv", default="k,v",
                     help="branch short-convolution targets of the block / branch workloads (the released "
                          "checkpoints convolve k and v); '' for none")
-    ap.add_argument("--cpu-sample-rows", type=int, default=6144,
+    ap.add_argument("--cpu-sample-rows", type=int, default=9216,
                     help="query rows of the CPU-oracle baseline sample (0 disables it)")
     ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "traffic.json"),
                     help="HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE/WRITE_SIZE)")
