@@ -73,3 +73,20 @@ def test_c_abi_rejects_bad_arguments_before_any_launch(built_lib):
     rc = built_lib.vdnh3_gdn_chunk_fwd(p, 64, 64, p, 64, 64, p, 64, 64, p, 1, p, 1, None, None, p, 64, 64, 8, 1, 64, p,
                                        4096, None)
     assert rc == 1 and b"head_dim" in built_lib.vdnh3_last_error()
+
+
+def test_row_span_joins_row_slices_of_one_matrix():
+    """The branch computes the text rows' beta in the video rows' GEMM only when both are row slices of
+    one row-major matrix, text first, with at most a quarter of extra rows between them."""
+    from vdn_h3_amd.runtime import _row_span
+
+    x = torch.arange(100 * 8, dtype=torch.float32).view(100, 8)
+    view, gap = _row_span(x[:10], x[20:90])
+    assert gap == 20 and torch.equal(view, x[:90])
+    assert _row_span(x[20:30], x[:10]) is None        # text after the video rows
+    assert _row_span(x[:5], x[50:60]) is None         # too many rows in between
+    assert _row_span(x[:10], x[5:20]) is None         # overlapping
+    view, gap = _row_span(x[:10, :4], x[20:90, :4])   # column slices keep the row stride
+    assert gap == 20 and torch.equal(view, x[:90, :4])
+    assert _row_span(x[:10].clone(), x[20:90]) is None  # different storage
+    assert _row_span(None, x[20:90]) is None

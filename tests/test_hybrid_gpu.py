@@ -242,3 +242,21 @@ def test_block_with_rope_vs_oracle(device):
     torch.cuda.synchronize()
     torch.set_num_threads(16)
     _parity(out, ho.vdn_forward(x, layout, aw, bw, heads, dim, rope_freqs=freqs), "block with rope vs oracle")
+
+
+def test_shared_gate_branch_gemm_is_bit_identical(device, monkeypatch):
+    """The softmax gate, the branch's beta and its gate down-projection from one GEMM over x give the
+    same block output, bit for bit, as the separate GEMMs."""
+    from vdn_h3_amd import hybrid
+
+    print("case hybrid block shared gate GEMM", flush=True)
+    heads, dim, hidden = 4, 128, 512
+    layout, x, aw, bw = _synthetic(13, (16, 16), 64, heads, dim, hidden)
+    bwd = {k: v.to(device) for k, v in bw.items()}
+    forward, state = _block(aw, bwd, heads, dim, device)
+    shared = _run(forward, x.to(device), layout)
+    assert state.__dict__.get("_gate_branch_cache"), "the shared GEMM did not run"
+    monkeypatch.setattr(hybrid, "_gate_branch_weights", lambda *args: None)
+    forward, _ = _block(aw, bwd, heads, dim, device)
+    separate = _run(forward, x.to(device), layout)
+    assert torch.equal(shared, separate)
