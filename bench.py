@@ -18,7 +18,8 @@ timings of the same timed steps.
 
 Other workloads: ``stack`` (50 blocks x ``--steps`` denoising steps, ``x <- x + block(rms_norm(x))``; use
 ``--steps 8 --warmup 1`` for the 8-step pass), ``window`` (attention alone), ``branch`` (VDN branch alone),
-``gemm_{i8,f8}_{qkv,out}`` (W8A8 GEMMs alone), ``gdn`` (token-level chunk-64 Gated DeltaNet),
+``gemm_{i8,f8}_{qkv,out}`` (W8A8 GEMMs alone), ``gdn`` (token-level chunk-64 Gated DeltaNet), ``dit``
+(the DiT block pointwise passes), ``rope`` (q/k RMSNorm + RoPE),
 ``hbm_copy`` (counter calibration).
 ``cpu_baseline`` times the CPU oracle on a bounded sample of query rows.
 """
@@ -51,7 +52,7 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="block", choices=["block", "stack", "window", "hbm_copy", "branch",
                                                              "gemm_i8_qkv", "gemm_i8_out", "gemm_f8_qkv",
-                                                             "gemm_f8_out", "gdn"],
+                                                             "gemm_f8_out", "gdn", "dit", "rope"],
                     help="hbm_copy: a plain 1 GiB device copy, the reference point for scaling rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes")
     ap.add_argument("--short-conv", default="k,v",
@@ -503,6 +504,82 @@ def bench_gdn(args, torch, device):
     return result
 
 
+def bench_dit(args, torch, device):
+    """The DiT block pointwise passes around the attention at 40,688 rows x hidden 5120: RMSNorm + AdaLN
+    modulation, the gated residual, and the SwiGLU fused into fc2's per-token int8 quantisation (MLP
+    width 13,824 = 2 x 6,912 per half is an assumption: the reference does not pin it)."""
+    from vdn_h3_amd import block_kernels as bk
+    from vdn_h3_amd import linear as L
+    from vdn_h3_amd import synth
+
+    rows, hidden, ffn = 40688, 5120, 13824
+    x = synth.randn((rows, hidden), 60, device=device, dtype=torch.bfloat16)
+    b = synth.randn((rows, hidden), 61, device=device, dtype=torch.bfloat16)
+    w = (1 + 0.1 * synth.randn((hidden,), 62, device=device)).to(torch.bfloat16)
+    scale = 0.3 * synth.randn((1, hidden), 63, device=device)
+    shift = 0.3 * synth.randn((1, hidden), 64, device=device)
+    gate = 0.3 * synth.randn((1, hidden), 65, device=device)
+    idx = torch.zeros(rows, dtype=torch.int32, device=device)
+    h = synth.randn((rows, 2 * ffn), 66, device=device, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream(device)
+    with torch.no_grad():
+        t_mod = _time_steps(torch, stream, args.steps, args.warmup, lambda: bk.rmsnorm_modulate(x, w, 1e-6, scale, shift, idx))
+        t_res = _time_steps(torch, stream, args.steps, args.warmup, lambda: bk.gated_residual(x, gate, idx, b))
+        t_swq = _time_steps(torch, stream, args.steps, args.warmup, lambda: bk.swiglu_quantize_rows(h, L.KIND_I8))
+    mb = {"rmsnorm_modulate": 2 * rows * hidden * 2, "gated_residual": 3 * rows * hidden * 2,
+          "swiglu_quant_rows_i8": rows * 2 * ffn * 2 + rows * ffn + rows * 4}
+    ms = {"rmsnorm_modulate": t_mod, "gated_residual": t_res, "swiglu_quant_rows_i8": t_swq}
+    total_ms = sum(ms.values())
+    gbs = {k: mb[k] / (ms[k] * 1e-3) / 1e9 for k in ms}
+    return {
+        "metric": "DiT block pointwise passes (RMSNorm+AdaLN, gated residual, SwiGLU->int8) ms + GB/s at 40,688 x 5120, 1 GPU",
+        "value": round(sum(mb.values()) / (total_ms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(total_ms, 4),
+        "dtype": "bf16",
+        "config": {"workload": "dit_pointwise_r40688_h5120_ffn13824", "rows": rows, "hidden": hidden, "ffn": ffn,
+                   "bytes_per_kernel": mb},
+        "roofline": {"bound": "hbm", "kernel": "swiglu_quant_kernel<int8>", "achieved": round(gbs["swiglu_quant_rows_i8"], 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs["swiglu_quant_rows_i8"] / PEAK_HBM_GBS, 4),
+                     "traffic": None},
+        "breakdown": {k: {"ms": round(ms[k], 4), "GBs": round(gbs[k], 1)} for k in ms},
+    }
+
+
+def bench_rope(args, torch, device):
+    """q/k RMSNorm with split-half RoPE (one 2x2 rotation per row and pair, rot_dim 128) on the raw q / k
+    views of the fused qkv rows at 40,688 x 40 x 128, beside the plain q/k RMSNorm."""
+    import math
+
+    from vdn_h3_amd import synth
+    from vdn_h3_amd.hybrid import normalise_qk
+
+    seq, heads, dim = 40688, 40, 128
+    qkv = synth.fused_qkv(seq, heads, dim, device=device, seed=70)
+    q, k, _ = synth.split_qkv(qkv, heads, dim)
+    wq = (1 + 0.1 * synth.randn((dim,), 71, device=device)).to(torch.bfloat16)
+    wk = (1 + 0.1 * synth.randn((dim,), 72, device=device)).to(torch.bfloat16)
+    pos = torch.arange(seq, device=device, dtype=torch.float32)[:, None]
+    inv = torch.pow(10000.0, -torch.arange(dim // 2, device=device, dtype=torch.float32) / (dim // 2))[None, :]
+    ang = pos * inv
+    c, s_ = torch.cos(ang), torch.sin(ang)
+    freqs = torch.stack([torch.stack([c, -s_], -1), torch.stack([s_, c], -1)], -2).view(1, seq, 1, dim // 2, 2, 2)
+    stream = torch.cuda.current_stream(device)
+    with torch.no_grad():
+        t_rope = _time_steps(torch, stream, args.steps, args.warmup, lambda: normalise_qk(q, k, wq, wk, 1e-6, rope_freqs=freqs))
+        t_norm = _time_steps(torch, stream, args.steps, args.warmup, lambda: normalise_qk(q, k, wq, wk, 1e-6))
+    io = 4 * seq * heads * dim * 2                        # q, k read; normalised q, k written
+    table = seq * (dim // 2) * 4 * 4                      # the fp32 rotation table
+    gbs = (io + table) / (t_rope * 1e-3) / 1e9
+    return {
+        "metric": "q/k RMSNorm + split-half RoPE ms + GB/s at 40,688 tok x 40 heads x 128, 1 GPU",
+        "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(t_rope, 4), "dtype": "bf16",
+        "config": {"workload": "qk_rmsnorm_rope_s40688_h40_d128", "seq_len": seq, "heads": heads, "head_dim": dim,
+                   "rot_dim": dim, "bytes_per_step": io + table, "note": "rope table built in the timed call"},
+        "roofline": {"bound": "hbm", "kernel": "qk_rmsnorm_kernel<128, rope>", "achieved": round(gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        "plain_qk_rmsnorm_ms": round(t_norm, 4),
+    }
+
+
 def cpu_baseline_window(torch, qkv, w, lay, n_rows):
     """Time the CPU oracle (``oracle.window_oracle``) on ``n_rows`` query rows of the same problem."""
     from oracle import window_oracle as wo
@@ -562,6 +639,10 @@ def main():
         result = bench_gemm(args, torch, device)
     elif args.workload == "gdn":
         result = bench_gdn(args, torch, device)
+    elif args.workload == "dit":
+        result = bench_dit(args, torch, device)
+    elif args.workload == "rope":
+        result = bench_rope(args, torch, device)
     else:
         result = bench_window(args, torch, device)
     line = {

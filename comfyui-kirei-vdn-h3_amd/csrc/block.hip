@@ -44,10 +44,23 @@ __global__ __launch_bounds__(256) void qk_rmsnorm_kernel(const uint16_t *__restr
                                                          uint16_t *__restrict__ qo, int64_t qo_row, int64_t qo_head,
                                                          uint16_t *__restrict__ ko, int64_t ko_row, int64_t ko_head,
                                                          int64_t n_vec, int heads) {
-  constexpr int LANES = D / 8;
+  constexpr int LANES = D / 8, VPW = 256 / LANES;  // vectors per workgroup
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t vec = t / LANES;
   const int c = (int)(t % LANES);
+  // RoPE: when every vector of this workgroup belongs to one row (2 * heads a multiple of VPW) or
+  // all rows share one table, the row's rot/2 rotation matrices are read once into LDS
+  [[maybe_unused]] __shared__ f32x4_t tab[ROPE ? D / 2 : 1];
+  bool tab_lds = false;
+  if constexpr (ROPE) {
+    tab_lds = f_row == 0 || (2 * heads) % VPW == 0;
+    if (tab_lds) {
+      const int64_t wrow = f_row == 0 ? 0 : ((int64_t)blockIdx.x * VPW) / (2 * heads);
+      if ((int)threadIdx.x < rot / 2 && wrow * 2 * heads < n_vec)
+        tab[threadIdx.x] = reinterpret_cast<const f32x4_t *>(freqs + wrow * f_row)[threadIdx.x];
+      __syncthreads();
+    }
+  }
   if (vec >= n_vec) return;  // lane groups are aligned: a group is wholly in range or wholly out
   const int head = (int)(vec % heads);
   const int which = (int)((vec / heads) & 1);
@@ -72,14 +85,23 @@ __global__ __launch_bounds__(256) void qk_rmsnorm_kernel(const uint16_t *__restr
     const int lane = __lane_id();
     const int partner = first ? lane + step : lane - step;
     float o[8];
+    if (D == 128 && rot == 128) {
+      // full rotation: the partner is 8 lanes away inside the vector's 16-lane DPP row (row_ror:8)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = __shfl(y[j], rotated ? partner : lane);
+      for (int j = 0; j < 8; ++j)
+        o[j] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y[j]), 0x128, 0xf, 0xf, false));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = __shfl(y[j], rotated ? partner : lane);
+    }
     if (rotated) {
       const int i0 = first ? 8 * c : 8 * c - half;       // pair index of channel 8c
-      const float *f = freqs + row * f_row + 4 * i0 + (first ? 0 : 2);  // matrix row 0 or 1
+      // the eight 2x2 matrices of pairs i0 .. i0 + 7, 16 bytes each (f00 f01 f10 f11)
+      const f32x4_t *f = tab_lds ? tab + i0 : reinterpret_cast<const f32x4_t *>(freqs + row * f_row + 4 * i0);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float a = f[4 * j], b = f[4 * j + 1];
+        const f32x4_t m = f[j];
+        const float a = first ? m[0] : m[2], b = first ? m[1] : m[3];  // matrix row 0 or 1
         // first half: out_i = f00 y_i + f01 y_{i+h}; second half: out_{i+h} = f10 y_i + f11 y_{i+h}
         y[j] = first ? fmaf(a, y[j], b * o[j]) : fmaf(a, o[j], b * y[j]);
       }
@@ -139,8 +161,8 @@ int qk_norm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k,
     VDNH3_HOST_CHECK(rot > 0 && rot % 16 == 0 && rot <= head_dim, VDNH3_ERR_INVALID,
                      "rope: rot_dim must be a positive multiple of 16 and at most head_dim %d, got %d", head_dim,
                      rot);
-    VDNH3_HOST_CHECK(f_row >= 0 && reinterpret_cast<uintptr_t>(freqs) % 4 == 0, VDNH3_ERR_INVALID,
-                     "rope: bad frequency row stride or alignment");
+    VDNH3_HOST_CHECK(f_row >= 0 && f_row % 4 == 0 && reinterpret_cast<uintptr_t>(freqs) % 16 == 0,
+                     VDNH3_ERR_INVALID, "rope: frequencies must be 16-byte aligned with a row stride multiple of 4");
   }
   const int64_t n_vec = (int64_t)seq * 2 * heads;
   const int64_t threads = n_vec * (head_dim / 8);

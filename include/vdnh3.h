@@ -309,7 +309,8 @@ int vdnh3_qk_rmsnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uin
  * rot_dim = 2 * rope_freqs.shape[-3] and the q_norm epsilon for both). After the RMSNorm and
  * weight (fp32, not rounded), for i < rot_dim / 2 the pair (y_i, y_{i + rot_dim/2}) is replaced
  * by F (y_i, y_{i + rot_dim/2}) with F the 2x2 matrix of (row, i): element (r, c) at
- * freqs[row*freqs_row + 4*i + 2*r + c] (fp32; freqs_row = 0 shares one set across rows);
+ * freqs[row*freqs_row + 4*i + 2*r + c] (fp32, 16-byte aligned, freqs_row a multiple of 4; freqs_row = 0
+ * shares one set across rows);
  * channels >= rot_dim pass unchanged; one bf16 rounding at the end. rot_dim: a multiple of 16,
  * at most head_dim.
  */
