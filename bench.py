@@ -537,7 +537,7 @@ def bench_dit(args, torch, device):
         "dtype": "bf16",
         "config": {"workload": "dit_pointwise_r40688_h5120_ffn13824", "rows": rows, "hidden": hidden, "ffn": ffn,
                    "bytes_per_kernel": mb},
-        "roofline": {"bound": "hbm", "kernel": "swiglu_quant_kernel<int8>", "achieved": round(gbs["swiglu_quant_rows_i8"], 1),
+        "roofline": {"bound": "hbm", "kernel": "swiglu_quant_row_kernel<int8>", "achieved": round(gbs["swiglu_quant_rows_i8"], 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs["swiglu_quant_rows_i8"] / PEAK_HBM_GBS, 4),
                      "traffic": None},
         "breakdown": {k: {"ms": round(ms[k], 4), "GBs": round(gbs[k], 1)} for k in ms},

@@ -44,6 +44,14 @@ __device__ __forceinline__ void load_mod8(const void *p, int64_t off, int bf16, 
   }
 }
 
+__device__ __forceinline__ float block_max(float v, float *red) {
+  v = wave_max(v);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
 __device__ __forceinline__ float block_sum(float v, float *red) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -138,8 +146,9 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict_
   st16(out + row * out_row + 8 * c, pack8f(a));
 }
 
-// One wavefront per row, like quant_rows: amax of a over the row, then the codes (the second
-// sweep recomputes a from the fc1 output, served from L2). scale[row] = max(amax / qmax, 1e-12).
+// For ffn > 8 * 256 * kQuantChunks: one wavefront per row, like quant_rows: amax of a over the row,
+// then the codes (the second sweep recomputes a from the fc1 output, served from L2).
+// scale[row] = max(amax / qmax, 1e-12).
 template <int KIND>
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t *__restrict__ h, int64_t h_row, int rows,
                                                            int ffn, uint8_t *__restrict__ q, int64_t q_row,
@@ -166,6 +175,68 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t *__res
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float e = a[j] / s;
+      const uint32_t code = KIND == 1 ? i8_code(e) : e4m3_code(fminf(fmaxf(e, -kF8Max), kF8Max));
+      if (j < 4)
+        lo |= code << (8 * j);
+      else
+        hi |= code << (8 * (j - 4));
+    }
+    *reinterpret_cast<u32x2_t *>(qr + 8 * c) = u32x2_t{lo, hi};
+  }
+}
+
+// One 256-thread workgroup per row for ffn <= 8 * 256 * kQuantChunks: each thread loads all its
+// chunks of g and u up front, keeps a = bf16(silu(g) * u) as packed bf16 between the row's amax
+// and the codes, so the fc1 output is read once. Same arithmetic as swiglu_quant_kernel.
+constexpr int kQuantChunks = 8;
+
+template <int KIND>
+__global__ __launch_bounds__(256) void swiglu_quant_row_kernel(const uint16_t *__restrict__ h, int64_t h_row,
+                                                               int ffn, uint8_t *__restrict__ q, int64_t q_row,
+                                                               float *__restrict__ scale) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t *hr = h + row * h_row;
+  const int chunks = ffn / 8;
+  u32x4_t gr[kQuantChunks], ur[kQuantChunks];
+#pragma unroll
+  for (int u = 0; u < kQuantChunks; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    if (c < chunks) {
+      gr[u] = ld16(hr + 8 * c);
+      ur[u] = ld16(hr + ffn + 8 * c);
+    }
+  }
+  u32x4_t a[kQuantChunks];
+  float amax = 0.f;
+#pragma unroll
+  for (int u = 0; u < kQuantChunks; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    if (c >= chunks) continue;
+    float g[8], uv[8], av[8];
+    unpack8f(gr[u], g);
+    unpack8f(ur[u], uv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      av[j] = round_bf(silu_bf(g[j]) * uv[j]);
+      amax = fmaxf(amax, fabsf(av[j]));
+    }
+    a[u] = pack8f(av);  // exact: av holds bf16 values
+  }
+  amax = block_max(amax, red);
+  const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f);
+  if (threadIdx.x == 0) scale[row] = s;
+  uint8_t *qr = q + row * q_row;
+#pragma unroll
+  for (int u = 0; u < kQuantChunks; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    if (c >= chunks) continue;
+    float av[8];
+    unpack8f(a[u], av);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = av[j] / s;
       const uint32_t code = KIND == 1 ? i8_code(e) : e4m3_code(fminf(fmaxf(e, -kF8Max), kF8Max));
       if (j < 4)
         lo |= code << (8 * j);
@@ -248,8 +319,17 @@ extern "C" int vdnh3_swiglu_quant_rows(int kind, const uint16_t *h, int64_t h_ro
   if (rc) return rc;
   VDNH3_HOST_CHECK(q && scale && q_row % 8 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0, VDNH3_ERR_INVALID,
                    "swiglu_quant_rows: codes must be 8-byte aligned with a row stride of a multiple of 8");
-  const dim3 grid((unsigned)((rows + 3) / 4));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ffn <= 8 * 256 * vdnh3::kQuantChunks) {
+    if (kind == 1)
+      hipLaunchKernelGGL(vdnh3::swiglu_quant_row_kernel<1>, dim3(rows), dim3(256), 0, s, h, h_row, ffn, q, q_row,
+                         scale);
+    else
+      hipLaunchKernelGGL(vdnh3::swiglu_quant_row_kernel<2>, dim3(rows), dim3(256), 0, s, h, h_row, ffn, q, q_row,
+                         scale);
+    return vdnh3::check_launch("swiglu_quant_rows");
+  }
+  const dim3 grid((unsigned)((rows + 3) / 4));
   if (kind == 1)
     hipLaunchKernelGGL(vdnh3::swiglu_quant_kernel<1>, grid, dim3(256), 0, s, h, h_row, rows, ffn, q, q_row, scale);
   else

@@ -27,6 +27,13 @@ def _steps(got, want):
     return (g - w).abs() / ulp
 
 
+def _steps_mag(got, want, mag):
+    """|got - want| in ulps (bf16, 8 significant bits) of ``mag``."""
+    g, w = got.float().cpu(), want.float()
+    ulp = torch.ldexp(torch.ones_like(mag), torch.frexp(mag)[1] - 8).clamp_min(2.0 ** -133)
+    return (g - w).abs() / ulp
+
+
 def _case(rows, hidden, n_mod, seed, mod_dtype):
     g = torch.Generator().manual_seed(seed)
     x = (2 * torch.randn(rows, hidden, generator=g)).to(torch.bfloat16)
@@ -46,7 +53,13 @@ def test_rmsnorm_modulate(device, hidden, mod_dtype):
     got = bk.rmsnorm_modulate(x.to(device), w.to(device), 1e-6, scale.to(device), shift.to(device),
                               idx.to(torch.int32).to(device))
     want = do.pre(x, w, 1e-6, scale, shift, idx)
-    steps = _steps(got, want)
+    # The result is p + shift with p = bf16(rms_norm(x) * (1 + scale)). The fp32 sum of squares depends
+    # on the summation order (torch's CPU kernel and the GPU's wavefront tree differ), which can move p
+    # by one of its own ulps; where p + shift cancels, that is many ulps of the result. So the steps are
+    # counted in ulps of max(|result|, |p|).
+    prod = do.pre(x, w, 1e-6, scale, torch.zeros_like(shift), idx)
+    steps = _steps_mag(got, want, torch.maximum(want.float().abs(), prod.float().abs()))
+    print(f"  steps > 0: {(steps > 0).sum().item()} of {steps.numel()}, max {steps.max().item()}", flush=True)
     assert steps.max().item() <= 2, steps.max().item()
     assert (steps == 0).float().mean().item() >= 0.99
 
@@ -81,6 +94,26 @@ def test_swiglu_and_fused_quantisation(device):
         q2, s2 = linear.quantize_rows(got, kind)
         assert torch.equal(q.view(torch.uint8).cpu(), q2.view(torch.uint8).cpu()) and torch.equal(s.cpu(), s2.cpu())
     wq, ws = qo.int8_quantize_rows(got.cpu())
+    q, s = bk.swiglu_quantize_rows(dh, linear.KIND_I8)
+    assert torch.equal(q.cpu(), wq) and torch.equal(s.cpu().reshape(-1), ws.reshape(-1))
+
+
+@pytest.mark.parametrize("ffn", [13824, 16384, 16392])
+def test_fused_quantisation_wide_rows(device, ffn):
+    """One workgroup per row up to ffn 16,384 (the row kept in registers), one wavefront per row with a
+    second sweep beyond it: both give the codes and scales of quantising the SwiGLU output."""
+    from vdn_h3_amd import block_kernels as bk
+    from vdn_h3_amd import linear
+
+    print(f"case swiglu quantisation ffn={ffn}", flush=True)
+    h = (3 * torch.randn(37, 2 * ffn, generator=torch.Generator().manual_seed(ffn))).to(torch.bfloat16)
+    dh = h.to(device)
+    a = bk.swiglu(dh)
+    for kind in (linear.KIND_I8, linear.KIND_F8):
+        q, s = bk.swiglu_quantize_rows(dh, kind)
+        q2, s2 = linear.quantize_rows(a, kind)
+        assert torch.equal(q.view(torch.uint8).cpu(), q2.view(torch.uint8).cpu()) and torch.equal(s.cpu(), s2.cpu())
+    wq, ws = qo.int8_quantize_rows(a.cpu())
     q, s = bk.swiglu_quantize_rows(dh, linear.KIND_I8)
     assert torch.equal(q.cpu(), wq) and torch.equal(s.cpu().reshape(-1), ws.reshape(-1))
 
