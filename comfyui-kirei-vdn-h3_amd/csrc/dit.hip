@@ -44,12 +44,16 @@ __device__ __forceinline__ void load_mod8(const void *p, int64_t off, int bf16, 
   }
 }
 
+template <int NW>
 __device__ __forceinline__ float block_max(float v, float *red) {
   v = wave_max(v);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (lane == 0) red[wave] = v;
   __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float m = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) m = fmaxf(m, red[i]);
+  return m;
 }
 
 __device__ __forceinline__ float block_sum(float v, float *red) {
@@ -146,8 +150,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict_
   st16(out + row * out_row + 8 * c, pack8f(a));
 }
 
-// For ffn > 8 * 256 * kQuantChunks: one wavefront per row, like quant_rows: amax of a over the row,
-// then the codes (the second sweep recomputes a from the fc1 output, served from L2).
+// For ffn > 8 * kQuantThreads * kQuantChunks: one wavefront per row, like quant_rows: amax of a over
+// the row, then the codes (the second sweep recomputes a from the fc1 output, served from L2).
 // scale[row] = max(amax / qmax, 1e-12).
 template <int KIND>
 __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t *__restrict__ h, int64_t h_row, int rows,
@@ -185,23 +189,25 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t *__res
   }
 }
 
-// One 256-thread workgroup per row for ffn <= 8 * 256 * kQuantChunks: each thread loads all its
-// chunks of g and u up front, keeps a = bf16(silu(g) * u) as packed bf16 between the row's amax
-// and the codes, so the fc1 output is read once. Same arithmetic as swiglu_quant_kernel.
-constexpr int kQuantChunks = 8;
+// One workgroup of kQuantThreads threads per row for ffn <= 8 * kQuantThreads * kQuantChunks (16,384):
+// each thread loads all its chunks of g and u up front, keeps a = bf16(silu(g) * u) as packed bf16
+// between the row's amax and the codes, so the fc1 output is read once. Same arithmetic as
+// swiglu_quant_kernel. 512 threads per row measured faster than 256 or 1024.
+constexpr int kQuantThreads = 512, kQuantChunks = 4;
 
 template <int KIND>
-__global__ __launch_bounds__(256) void swiglu_quant_row_kernel(const uint16_t *__restrict__ h, int64_t h_row,
+__global__ __launch_bounds__(kQuantThreads) void swiglu_quant_row_kernel(const uint16_t *__restrict__ h,
+                                                                         int64_t h_row,
                                                                int ffn, uint8_t *__restrict__ q, int64_t q_row,
                                                                float *__restrict__ scale) {
-  __shared__ float red[4];
+  __shared__ float red[kQuantThreads / 64];
   const int64_t row = blockIdx.x;
   const uint16_t *hr = h + row * h_row;
   const int chunks = ffn / 8;
   u32x4_t gr[kQuantChunks], ur[kQuantChunks];
 #pragma unroll
   for (int u = 0; u < kQuantChunks; ++u) {
-    const int c = threadIdx.x + 256 * u;
+    const int c = threadIdx.x + kQuantThreads * u;
     if (c < chunks) {
       gr[u] = ld16(hr + 8 * c);
       ur[u] = ld16(hr + ffn + 8 * c);
@@ -211,7 +217,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_row_kernel(const uint16_t *_
   float amax = 0.f;
 #pragma unroll
   for (int u = 0; u < kQuantChunks; ++u) {
-    const int c = threadIdx.x + 256 * u;
+    const int c = threadIdx.x + kQuantThreads * u;
     if (c >= chunks) continue;
     float g[8], uv[8], av[8];
     unpack8f(gr[u], g);
@@ -223,13 +229,13 @@ __global__ __launch_bounds__(256) void swiglu_quant_row_kernel(const uint16_t *_
     }
     a[u] = pack8f(av);  // exact: av holds bf16 values
   }
-  amax = block_max(amax, red);
+  amax = block_max<kQuantThreads / 64>(amax, red);
   const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f);
   if (threadIdx.x == 0) scale[row] = s;
   uint8_t *qr = q + row * q_row;
 #pragma unroll
   for (int u = 0; u < kQuantChunks; ++u) {
-    const int c = threadIdx.x + 256 * u;
+    const int c = threadIdx.x + kQuantThreads * u;
     if (c >= chunks) continue;
     float av[8];
     unpack8f(a[u], av);
@@ -320,12 +326,14 @@ extern "C" int vdnh3_swiglu_quant_rows(int kind, const uint16_t *h, int64_t h_ro
   VDNH3_HOST_CHECK(q && scale && q_row % 8 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0, VDNH3_ERR_INVALID,
                    "swiglu_quant_rows: codes must be 8-byte aligned with a row stride of a multiple of 8");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (ffn <= 8 * 256 * vdnh3::kQuantChunks) {
+  if (ffn <= 8 * vdnh3::kQuantThreads * vdnh3::kQuantChunks) {
     if (kind == 1)
-      hipLaunchKernelGGL(vdnh3::swiglu_quant_row_kernel<1>, dim3(rows), dim3(256), 0, s, h, h_row, ffn, q, q_row,
+      hipLaunchKernelGGL(vdnh3::swiglu_quant_row_kernel<1>, dim3(rows), dim3(vdnh3::kQuantThreads), 0, s, h, h_row,
+                         ffn, q, q_row,
                          scale);
     else
-      hipLaunchKernelGGL(vdnh3::swiglu_quant_row_kernel<2>, dim3(rows), dim3(256), 0, s, h, h_row, ffn, q, q_row,
+      hipLaunchKernelGGL(vdnh3::swiglu_quant_row_kernel<2>, dim3(rows), dim3(vdnh3::kQuantThreads), 0, s, h, h_row,
+                         ffn, q, q_row,
                          scale);
     return vdnh3::check_launch("swiglu_quant_rows");
   }
