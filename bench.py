@@ -21,7 +21,9 @@ Other workloads: ``stack`` (50 blocks x ``--steps`` denoising steps, ``x <- x + 
 ``gemm_{i8,f8}_{qkv,out}`` (W8A8 GEMMs alone), ``gdn`` (token-level chunk-64 Gated DeltaNet), ``dit``
 (the DiT block pointwise passes), ``rope`` (q/k RMSNorm + RoPE),
 ``hbm_copy`` (counter calibration).
-``cpu_baseline`` times the CPU oracle on a bounded sample of query rows.
+``cpu_baseline`` times the fp32 CPU oracle on the host cores (16 threads, the box's CPU share) on bounded
+samples (1 warm-up, median of 3): for ``block``, the window attention on sampled query rows, the projections
+on sampled rows and the VDN branch on 7 of its 29 inner frames, combined at the block's per-part work.
 """
 
 from __future__ import annotations
@@ -58,7 +60,7 @@ def _parse():
     ap.add_argument("--short-conv", default="k,v",
                     help="branch short-convolution targets of the block / branch workloads (the released "
                          "checkpoints convolve k and v); '' for none")
-    ap.add_argument("--cpu-sample-rows", type=int, default=9216,
+    ap.add_argument("--cpu-sample-rows", type=int, default=2304,
                     help="query rows of the CPU-oracle baseline sample (0 disables it)")
     ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "traffic.json"),
                     help="HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE/WRITE_SIZE)")
@@ -77,9 +79,7 @@ def bench_window(args, torch, device):
     from vdn_h3_amd import _lib, synth, window
 
     w = synth.WINDOW_FULL
-    lay = w.layout
-    qkv = synth.fused_qkv(lay.seq_len, w.heads, w.head_dim, device=device, seed=0)
-    q, k, v = synth.split_qkv(qkv, w.heads, w.head_dim)
+    qkv, q, k, v, lay, _ = synth.window_inputs(w, device=device)   # q, k, v ~ N(0, 1) / sqrt(128)
     plan = window.make_plan(lay.seq_len, lay.video_start, lay.video_end, lay.num_frames, lay.tokens_per_frame,
                             lay.bounds, lay.anchor_frames, device)
     lib = _lib.lib()
@@ -203,30 +203,16 @@ def block_flops(lay, heads, dim, hidden, pairs_per_head, short_conv=()):
 
 def bench_block(args, torch, device):
     """One VDN-H3 hybrid attention block at the full shape (the patched attn.forward)."""
-    from types import SimpleNamespace
-
-    from vdn_h3_amd import projection, synth
-    from vdn_h3_amd.hybrid import VDNState, forward_scope, make_vdn_forward
-    from vdn_h3_amd.linear import HipLinear
-    from vdn_h3_amd.runtime import OptimizedLinearBranch
+    from vdn_h3_amd import synth
+    from vdn_h3_amd.hybrid import forward_scope
 
     w = synth.WINDOW_FULL
     lay = w.layout
     heads, dim, hidden = w.heads, w.head_dim, 5120
     x = synth.randn((lay.seq_len, hidden), 0, device=device, dtype=torch.bfloat16)
-    attn = SimpleNamespace(
-        heads=heads, head_dim=dim, forward=None,
-        qkv_proj=HipLinear(synth.randn((3 * heads * dim, hidden), 1, device, torch.bfloat16, 0.02), "int8"),
-        out_proj=HipLinear(synth.randn((hidden, heads * dim), 2, device, torch.bfloat16, 0.02), "int8"),
-        q_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), 3, device)).to(torch.bfloat16), eps=1e-6),
-        k_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), 4, device)).to(torch.bfloat16), eps=1e-6))
     conv = _short_conv(args)
-    (bw,), _ = projection.prepare_projection_maps(
-        [synth.branch_weights(heads, dim, hidden, device=device, short_conv=conv)], device, "int8")
-    branch = OptimizedLinearBranch(bw, heads, dim, short_conv=conv)
-    state = VDNState("bench", {"enable_softmax_gate": True, "linear_enabled": True, "enable_text_state": True},
-                     [branch], heads, dim, projection_precision="int8", diagnostics=True)
-    forward = make_vdn_forward(attn, state, 0)
+    state, (forward,) = synth.hybrid_stack(1, heads, dim, hidden, device, short_conv=conv, precision="int8")
+    state.diagnostics.enabled = True
     stream = torch.cuda.current_stream(device)
     with torch.no_grad(), forward_scope(lay):
         for _ in range(args.warmup):
@@ -279,62 +265,26 @@ def bench_block(args, torch, device):
     }
 
 
-def _block_parts(torch, device, heads, dim, hidden, seed, conv):
-    """Random-init attention module and int8-prepared branch weights of one block."""
-    from types import SimpleNamespace
-
-    from vdn_h3_amd import projection, synth
-    from vdn_h3_amd.linear import HipLinear
-
-    attn = SimpleNamespace(
-        heads=heads, head_dim=dim, forward=None,
-        qkv_proj=HipLinear(synth.randn((3 * heads * dim, hidden), seed + 1, device, torch.bfloat16, 0.02), "int8"),
-        out_proj=HipLinear(synth.randn((hidden, heads * dim), seed + 2, device, torch.bfloat16, 0.02), "int8"),
-        q_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), seed + 3, device)).to(torch.bfloat16),
-                               eps=1e-6),
-        k_norm=SimpleNamespace(weight=(1 + 0.1 * synth.randn((dim,), seed + 4, device)).to(torch.bfloat16),
-                               eps=1e-6))
-    (bw,), _ = projection.prepare_projection_maps(
-        [synth.branch_weights(heads, dim, hidden, device=device, seed=seed + 42, short_conv=conv)], device, "int8")
-    return attn, bw
-
-
 def bench_stack(args, torch, device):
     """The 50-block hybrid attention stack over one 8-step denoising pass (x <- x + block(rms_norm(x)))."""
     from vdn_h3_amd import synth
-    from vdn_h3_amd.hybrid import VDNState, forward_scope, make_vdn_forward
-    from vdn_h3_amd.runtime import OptimizedLinearBranch
+    from vdn_h3_amd.hybrid import forward_scope
 
     w = synth.WINDOW_FULL
     lay = w.layout
     heads, dim, hidden, blocks = w.heads, w.head_dim, 5120, 50
     conv = _short_conv(args)
-    parts = [_block_parts(torch, device, heads, dim, hidden, 1000 * (i + 1), conv) for i in range(blocks)]
-    branches = [OptimizedLinearBranch(bw, heads, dim, short_conv=conv) for _, bw in parts]
-    state = VDNState("bench-stack", {"enable_softmax_gate": True, "linear_enabled": True,
-                                     "enable_text_state": True}, branches, heads, dim,
-                     projection_precision="int8")
-    forwards = [make_vdn_forward(attn, state, i) for i, (attn, _) in enumerate(parts)]
+    state, forwards = synth.hybrid_stack(blocks, heads, dim, hidden, device, short_conv=conv, precision="int8")
     x0 = synth.randn((lay.seq_len, hidden), 0, device=device, dtype=torch.bfloat16)
     stream = torch.cuda.current_stream(device)
-
-    def denoise_step(x):
-        # pre-norm residual, as H3's blocks normalise their input before attention: random-init
-        # blocks fed the raw stream would double it per block and overflow within the pass
-        for fwd in forwards:
-            x = x + fwd(torch.nn.functional.rms_norm(x, (hidden,), eps=1e-6))
-        return x
-
     with torch.no_grad(), forward_scope(lay):
-        x = x0.clone()
-        for _ in range(args.warmup):
-            x = denoise_step(x)
+        synth.denoise_pass(forwards, x0.clone(), args.warmup)
         torch.cuda.synchronize()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
         x = x0.clone()
         ev[0].record(stream)
         for i in range(args.steps):
-            x = denoise_step(x)
+            x = synth.denoise_pass(forwards, x, 1)
             ev[i + 1].record(stream)
         torch.cuda.synchronize()
     step_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
@@ -493,14 +443,16 @@ def bench_gdn(args, torch, device):
         from oracle import gdn_oracle as go
 
         sel = list(range(heads))
+        sel = list(range(8))
         hq, hk, hv, hb, hg = (t[:, sel].cpu() for t in (q, k, v, beta, lg))
-        t0 = time.perf_counter()
-        go.chunked(hq, hk, hv, hb, hg)
-        dt = time.perf_counter() - t0
+        dt, runs = _median_seconds(lambda: go.chunked(hq, hk, hv, hb, hg))
+        model, physical = _cpu_description()
         result["cpu_baseline"] = {
             "value": round(gdn_flops(tokens, len(sel), dim) / dt / 1e12, 5), "unit": "TFLOP/s",
-            "cores": torch.get_num_threads(), "kind": "port", "seconds": round(dt, 2),
-            "sample": f"the whole workload: all {tokens} tokens x {heads} heads, float64 chunk-form oracle (oracle/gdn_oracle.py)"}
+            "cores": torch.get_num_threads(), "kind": "port", "seconds_median": round(dt, 3),
+            "seconds_runs": [round(t, 3) for t in runs], "cpu": model, "physical_cores": physical,
+            "sample": f"all {tokens} tokens x {len(sel)} of the {heads} heads, float64 chunk-form oracle "
+                      "(oracle/gdn_oracle.py); 1 warm-up, median of 3"}
     return result
 
 
@@ -580,28 +532,124 @@ def bench_rope(args, torch, device):
     }
 
 
-def cpu_baseline_window(torch, qkv, w, lay, n_rows):
-    """Time the CPU oracle (``oracle.window_oracle``) on ``n_rows`` query rows of the same problem."""
+CPU_THREADS = 16   # the GPU box's CPU share for one GPU
+
+
+def _cpu_description():
+    """``(model name, physical cores)`` from /proc/cpuinfo (``platform.machine()`` / None if unreadable)."""
+    model, cores, phys = None, set(), None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            key, _, value = line.partition(":")
+            key, value = key.strip(), value.strip()
+            if key == "model name" and model is None:
+                model = value
+            elif key == "physical id":
+                phys = value
+            elif key == "core id":
+                cores.add((phys, value))
+    except OSError:
+        pass
+    return model or platform.machine(), len(cores) or None
+
+
+def _median_seconds(fn, reps=3):
+    """Median wall time of ``reps`` runs of ``fn`` after one untimed warm-up run, and all the times."""
+    fn()
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return sorted(times)[len(times) // 2], times
+
+
+def _cpu_window_sample(torch, w, lay, qkv_host, n_rows):
+    """``(FLOP, median s, times)`` of the window-attention oracle on ``n_rows`` evenly spaced query rows."""
     from oracle import window_oracle as wo
     from vdn_h3_amd import synth
 
-    host = qkv.cpu()
-    hq, hk, hv = synth.split_qkv(host, w.heads, w.head_dim)
-    seq = lay.seq_len
-    rows = torch.linspace(0, seq - 1, n_rows).long().tolist()
-    keys = 0
-    for r in rows:
-        keys += sum(b - a for a, b in wo.row_key_intervals(r, seq, lay.video_start, lay.video_end, lay.num_frames,
-                                                          lay.tokens_per_frame, lay.bounds, lay.anchor_frames))
-    t = time.perf_counter()
-    wo.window_attention_rows(hq, hk, hv, rows, lay.video_start, lay.video_end, lay.num_frames,
-                             lay.tokens_per_frame, lay.bounds, w.scale, lay.anchor_frames)
-    dt = time.perf_counter() - t
-    flops = 4.0 * w.head_dim * w.heads * keys
-    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port", "seconds": round(dt, 2), "cpu": platform.processor() or platform.machine(),
-            "sample": f"{n_rows} evenly spaced query rows x {w.heads} heads of the 40,688-row layout, "
-                      f"fp32 oracle (oracle/window_oracle.py), {keys} keys in total"}
+    hq, hk, hv = synth.split_qkv(qkv_host, w.heads, w.head_dim)
+    rows = torch.linspace(0, lay.seq_len - 1, n_rows).long().tolist()
+    keys = sum(b - a for r in rows for a, b in wo.row_key_intervals(
+        r, lay.seq_len, lay.video_start, lay.video_end, lay.num_frames, lay.tokens_per_frame, lay.bounds,
+        lay.anchor_frames))
+    med, times = _median_seconds(lambda: wo.window_attention_rows(
+        hq, hk, hv, rows, lay.video_start, lay.video_end, lay.num_frames, lay.tokens_per_frame, lay.bounds, w.scale,
+        lay.anchor_frames))
+    return 4.0 * w.head_dim * w.heads * keys, med, times
+
+
+def cpu_baseline_window(torch, qkv, w, lay, n_rows):
+    """The window-attention oracle (``oracle/window_oracle.py``) on the host cores, on ``n_rows`` query rows."""
+    model, physical = _cpu_description()
+    flops, med, times = _cpu_window_sample(torch, w, lay, qkv.cpu(), n_rows)
+    return {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "seconds_median": round(med, 3), "seconds_runs": [round(t, 3) for t in times],
+            "cpu": model, "physical_cores": physical,
+            "sample": f"{n_rows} evenly spaced query rows x {w.heads} heads of the 40,688-row layout, fp32 oracle "
+                      "(oracle/window_oracle.py); 1 warm-up, median of 3"}
+
+
+def cpu_baseline_block(torch, device, lay, work, conv, n_rows):
+    """CPU throughput of one hybrid block from bounded samples of its three parts, each the median of 3
+    runs after a warm-up of the fp32 oracle on the host cores:
+
+    * window attention: ``n_rows`` evenly spaced query rows x 40 heads of the 40,688-row layout;
+    * projections: ``oracle.branch_oracle.linear_bf16`` (fp32 GEMM, bf16 out) on 512 rows x K 5120 x N 15,360;
+    * VDN branch: ``oracle.branch_oracle.projected_delta`` on 9 frames (7 inner) of 1296 tokens, 40 x 128,
+      hidden 5120, text state and k/v short convolutions, scaled to the block's 29 inner frames.
+
+    The block's CPU time is the sum of each part's work at its sampled rate; ``value`` is the block's
+    work over that time. ``stack_extrapolated_s`` is 400 block calls (50 blocks x 8 steps) at that time.
+    """
+    from oracle import branch_oracle as bo
+    from oracle import window_oracle as wo
+    from vdn_h3_amd import synth
+
+    model, physical = _cpu_description()
+    w = synth.WINDOW_FULL
+    qkv_host = synth.fused_qkv(lay.seq_len, w.heads, w.head_dim, device=device, seed=0, scale=w.scale).cpu()
+    win_flop, win_s, win_times = _cpu_window_sample(torch, w, lay, qkv_host, n_rows)
+    del qkv_host
+    x = synth.randn((512, 5120), 60, dtype=torch.bfloat16)
+    wt = synth.randn((15360, 5120), 61, dtype=torch.bfloat16, scale=0.02)
+    proj_s, proj_times = _median_seconds(lambda: bo.linear_bf16(x, wt))
+    proj_flop = 2.0 * 512 * 5120 * 15360
+    del x, wt
+    frames, inner, text, heads, dim, hidden, tpf = 9, 7, 512, w.heads, w.head_dim, 5120, lay.tokens_per_frame
+    seq = text + frames * tpf
+    bqkv = synth.fused_qkv(seq, heads, dim, seed=40)
+    bx = synth.randn((seq, hidden), 41, dtype=torch.bfloat16)
+    bw = synth.branch_weights(heads, dim, hidden, short_conv=conv)
+    q, k, v = synth.split_qkv(bqkv, heads, dim)
+    bounds = wo.window_bounds(frames, 1, 5)
+    branch_s, branch_times = _median_seconds(lambda: bo.projected_delta(
+        bw, bx[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, frame_size=lay.frame_size,
+        text_x=bx[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True, short_conv=conv,
+        fused_conv=True))
+    inner_block = lay.num_frames - 2
+    gemm_work = work["qkv_proj"] + work["out_proj"] + work["softmax_gate"]
+    block_s = (work["window_attention"] / (win_flop / win_s) + gemm_work / (proj_flop / proj_s)
+               + branch_s * inner_block / inner)
+    total = sum(work.values())
+    return {"value": round(total / block_s / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "cpu": model, "physical_cores": physical,
+            "block_seconds_estimated": round(block_s, 2), "stack_extrapolated_s": round(400 * block_s, 1),
+            "stack_note": "extrapolation: 50 blocks x 8 steps at the estimated CPU block time, not measured",
+            "parts": {
+                "window_attention": {"TFLOP/s": round(win_flop / win_s / 1e12, 5), "seconds_median": round(win_s, 3),
+                                     "seconds_runs": [round(t, 3) for t in win_times],
+                                     "sample": f"{n_rows} query rows x {heads} heads"},
+                "projections": {"TFLOP/s": round(proj_flop / proj_s / 1e12, 5), "seconds_median": round(proj_s, 3),
+                                "seconds_runs": [round(t, 3) for t in proj_times],
+                                "sample": "512 x 5120 x 15360 fp32 GEMM, bf16 out"},
+                "branch": {"seconds_median": round(branch_s, 3), "seconds_runs": [round(t, 3) for t in branch_times],
+                           "sample": f"projected_delta, {frames} frames ({inner} inner) x {tpf} tokens, scaled by "
+                                     f"{inner_block}/{inner}"}},
+            "sample": "fp32 oracle on the host cores: window attention on sampled query rows, the projections on "
+                      "sampled rows, the VDN branch on 7 of the 29 inner frames; each part the median of 3 runs after "
+                      "a warm-up, combined at the block's per-part work"}
 
 
 def main():
@@ -617,18 +665,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
-    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    torch.set_num_threads(min(CPU_THREADS, os.cpu_count() or 1))
     device = torch.device("cuda:0")
     if args.workload == "block":
         result = bench_block(args, torch, device)
         if args.cpu_sample_rows > 0:
             from vdn_h3_amd import synth
 
-            w = synth.WINDOW_FULL
-            qkv = synth.fused_qkv(w.layout.seq_len, w.heads, w.head_dim, device=device, seed=0)
-            result["cpu_baseline"] = cpu_baseline_window(torch, qkv, w, w.layout, args.cpu_sample_rows)
-            result["cpu_baseline"]["sample"] += (" - the window attention stage, 63% of the block's work; "
-                                                 "the value is that stage's CPU throughput")
+            result["cpu_baseline"] = cpu_baseline_block(torch, device, synth.WINDOW_FULL.layout,
+                                                        result["config"]["work_per_step"], _short_conv(args),
+                                                        args.cpu_sample_rows)
     elif args.workload == "stack":
         result = bench_stack(args, torch, device)
     elif args.workload == "hbm_copy":

@@ -39,8 +39,8 @@ __global__ __launch_bounds__(256) void qk_rmsnorm_kernel(const uint16_t *__restr
                                                          int64_t q_head, const uint16_t *__restrict__ k,
                                                          int64_t k_row, int64_t k_head,
                                                          const uint16_t *__restrict__ wq,
-                                                         const uint16_t *__restrict__ wk, float eps,
-                                                         const float *__restrict__ freqs, int64_t f_row, int rot,
+                                                         const uint16_t *__restrict__ wk, float q_eps,
+                                                         float k_eps, const float *__restrict__ freqs, int64_t f_row, int rot,
                                                          uint16_t *__restrict__ qo, int64_t qo_row, int64_t qo_head,
                                                          uint16_t *__restrict__ ko, int64_t ko_row, int64_t ko_head,
                                                          int64_t n_vec, int heads) {
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void qk_rmsnorm_kernel(const uint16_t *__restr
   for (int j = 0; j < 8; ++j) ss = fmaf(x[j], x[j], ss);
 #pragma unroll
   for (int o = 1; o < LANES; o <<= 1) ss += __shfl_xor(ss, o);
-  const float r = 1.f / sqrtf(ss / (float)D + eps);
+  const float r = 1.f / sqrtf(ss / (float)D + (which ? k_eps : q_eps));
 #pragma unroll
   for (int j = 0; j < 8; ++j) y[j] = x[j] * r * wf[j];
   if constexpr (ROPE) {
@@ -144,7 +144,8 @@ int check_rows(const void *p, int64_t row, int64_t head, const char *name) {
 namespace vdnh3 {
 namespace {
 int qk_norm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row, int64_t k_head,
-            const uint16_t *q_weight, const uint16_t *k_weight, float eps, const float *freqs, int64_t f_row,
+            const uint16_t *q_weight, const uint16_t *k_weight, float q_eps, float k_eps, const float *freqs,
+            int64_t f_row,
             int rot, uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
             int64_t ko_head, int seq, int heads, int head_dim, void *stream) {
   VDNH3_HOST_CHECK(head_dim == 64 || head_dim == 128, VDNH3_ERR_INVALID,
@@ -170,7 +171,8 @@ int qk_norm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k,
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define VDNH3_QKN(D, R)                                                                                        \
   hipLaunchKernelGGL((qk_rmsnorm_kernel<D, R>), grid, dim3(256), 0, s, q, q_row, q_head, k, k_row, k_head,     \
-                     q_weight, k_weight, eps, freqs, f_row, rot, q_out, qo_row, qo_head, k_out, ko_row, ko_head, \
+                     q_weight, k_weight, q_eps, k_eps, freqs, f_row, rot, q_out, qo_row, qo_head, k_out, ko_row,  \
+                     ko_head,                                                                                  \
                      n_vec, heads)
   if (head_dim == 128) {
     if (freqs) VDNH3_QKN(128, true);
@@ -186,10 +188,11 @@ int qk_norm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k,
 }  // namespace vdnh3
 
 extern "C" int vdnh3_qk_rmsnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
-                                int64_t k_head, const uint16_t *q_weight, const uint16_t *k_weight, float eps,
-                                uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
+                                int64_t k_head, const uint16_t *q_weight, const uint16_t *k_weight, float q_eps,
+                                float k_eps, uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
                                 int64_t ko_head, int seq, int heads, int head_dim, void *stream) {
-  return vdnh3::qk_norm(q, q_row, q_head, k, k_row, k_head, q_weight, k_weight, eps, nullptr, 0, 0, q_out, qo_row,
+  return vdnh3::qk_norm(q, q_row, q_head, k, k_row, k_head, q_weight, k_weight, q_eps, k_eps, nullptr, 0, 0, q_out,
+                        qo_row,
                         qo_head, k_out, ko_row, ko_head, seq, heads, head_dim, stream);
 }
 
@@ -200,7 +203,7 @@ extern "C" int vdnh3_qk_rmsnorm_rope(const uint16_t *q, int64_t q_row, int64_t q
                                      int64_t ko_row, int64_t ko_head, int seq, int heads, int head_dim,
                                      void *stream) {
   VDNH3_HOST_CHECK(freqs != nullptr, VDNH3_ERR_INVALID, "rope: null frequencies");
-  return vdnh3::qk_norm(q, q_row, q_head, k, k_row, k_head, q_weight, k_weight, eps, freqs, freqs_row, rot_dim,
+  return vdnh3::qk_norm(q, q_row, q_head, k, k_row, k_head, q_weight, k_weight, eps, eps, freqs, freqs_row, rot_dim,
                         q_out, qo_row, qo_head, k_out, ko_row, ko_head, seq, heads, head_dim, stream);
 }
 

@@ -776,17 +776,26 @@ __global__ void alpha_decay_kernel(const float *__restrict__ delta, const float 
   alpha[e] = expf(-expf(a_log[h]) * sp);
 }
 
-// Sana rule: Phi = alpha[i] * (I - A / T)[i][j], J = B / sqrt(T)  (vdn_h3/branch.py:163-177)
+// Sana rule (vdn_h3/branch.py:163-177): Phi = alpha[i] * (I - A / T)[i][j], J = B / sqrt(T), each
+// product and difference rounded to fp32 on its own like the reference's tensor ops (contraction
+// into fused multiply-adds is off for this kernel), then J * j_scale (the text state's exact 1/2).
+// Phi may be null (not needed).
 __global__ void sana_factor_kernel(const float *__restrict__ A, const float *__restrict__ B,
                                    const float *__restrict__ alpha, float *__restrict__ Phi, float *__restrict__ J,
-                                   float inv_t, float inv_sqrt_t, int64_t n, int D) {
+                                   float inv_t, float inv_sqrt_t, float j_scale, int64_t n, int D) {
+#pragma clang fp contract(off)
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= n) return;
-  const int64_t mat = e / ((int64_t)D * D);
-  const int i = (int)((e / D) % D), j = (int)(e % D);
-  const float a = alpha ? alpha[mat * D + i] : 1.f;
-  Phi[e] = a * ((i == j ? 1.f : 0.f) - inv_t * A[e]);
-  J[e] = inv_sqrt_t * B[e];
+  if (Phi) {
+    const int64_t mat = e / ((int64_t)D * D);
+    const int i = (int)((e / D) % D), j = (int)(e % D);
+    const float a = alpha ? alpha[mat * D + i] : 1.f;
+    const float scaled = inv_t * A[e];
+    const float diff = (i == j ? 1.f : 0.f) - scaled;
+    Phi[e] = a * diff;
+  }
+  const float jb = inv_sqrt_t * B[e];
+  J[e] = jb * j_scale;
 }
 
 __global__ void fill_rows_bf16_kernel(uint16_t *__restrict__ p, int64_t ld, int rows, int cols, uint16_t value) {
@@ -854,13 +863,15 @@ extern "C" int vdnh3_delta_factor(const float *A, const float *B, const float *a
 }
 
 extern "C" int vdnh3_sana_factor(const float *A, const float *B, const float *alpha, float *phi, float *jay,
-                                 int tokens_per_frame, int n, int head_dim, void *stream) {
-  VDNH3_HOST_CHECK(A && B && phi && jay && n > 0 && head_dim > 0 && tokens_per_frame > 0, VDNH3_ERR_INVALID,
+                                 float jay_scale, int tokens_per_frame, int n, int head_dim, void *stream) {
+  VDNH3_HOST_CHECK(A && B && jay && n > 0 && head_dim > 0 && tokens_per_frame > 0, VDNH3_ERR_INVALID,
                    "sana_factor: empty or null operand");
   const int64_t total = (int64_t)n * head_dim * head_dim;
-  const float inv_t = 1.f / (float)tokens_per_frame;
+  // the reference's Python floats 1 / T and (1 / T) ** 0.5, rounded once to fp32
+  const double inv_t = 1.0 / (double)tokens_per_frame;
   hipLaunchKernelGGL(vdnh3::sana_factor_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), A, B, alpha, phi, jay, inv_t, sqrtf(inv_t), total, head_dim);
+                     static_cast<hipStream_t>(stream), A, B, alpha, phi, jay, (float)inv_t, (float)sqrt(inv_t),
+                     jay_scale, total, head_dim);
   return check_launch("sana_factor");
 }
 

@@ -75,7 +75,7 @@ constexpr int kRowChunks = 4;
 __global__ __launch_bounds__(256) void rmsnorm_modulate_kernel(
     const uint16_t *__restrict__ x, int64_t x_row, const uint16_t *__restrict__ w, float eps,
     const void *__restrict__ scale, const void *__restrict__ shift, int64_t mod_row, int mod_bf16,
-    const int32_t *__restrict__ idx, uint16_t *__restrict__ out, int64_t out_row, int hidden) {
+    const int32_t *__restrict__ idx, int table_rows, uint16_t *__restrict__ out, int64_t out_row, int hidden) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const uint16_t *xr = x + row * x_row;
@@ -92,7 +92,11 @@ __global__ __launch_bounds__(256) void rmsnorm_modulate_kernel(
     }
   }
   const float r = 1.f / sqrtf(block_sum(ss, red) / (float)hidden + eps);
-  const int64_t mrow = (int64_t)idx[row] * mod_row;
+  // a segment index outside the modulation table reads row 0 and writes a NaN row instead of
+  // reading past the table
+  const int seg = idx[row];
+  const bool seg_ok = (unsigned)seg < (unsigned)table_rows;
+  const int64_t mrow = (int64_t)(seg_ok ? seg : 0) * mod_row;
 #pragma unroll
   for (int u = 0; u < kRowChunks; ++u) {
     const int c = threadIdx.x + 256 * u;
@@ -105,7 +109,7 @@ __global__ __launch_bounds__(256) void rmsnorm_modulate_kernel(
     for (int j = 0; j < 8; ++j) {
       const float n = round_bf(v[u][j] * r * wf[j]);  // F.rms_norm, one rounding
       const float p = round_bf(n * round_bf(1.f + sc[j]));
-      y[j] = p + sh[j];
+      y[j] = seg_ok ? p + sh[j] : __builtin_nanf("");
     }
     st16(out + row * out_row + 8 * c, pack8f(y));
   }
@@ -114,8 +118,8 @@ __global__ __launch_bounds__(256) void rmsnorm_modulate_kernel(
 // x' = bf16(x + bf16(bf16(gate[seg]) * branch)); 8 channels per thread, any number of rows
 __global__ __launch_bounds__(256) void gated_residual_kernel(
     const uint16_t *__restrict__ x, int64_t x_row, const void *__restrict__ gate, int64_t gate_row, int gate_bf16,
-    const int32_t *__restrict__ idx, const uint16_t *__restrict__ b, int64_t b_row, uint16_t *__restrict__ out,
-    int64_t out_row, int64_t rows, int chunks) {
+    const int32_t *__restrict__ idx, int table_rows, const uint16_t *__restrict__ b, int64_t b_row,
+    uint16_t *__restrict__ out, int64_t out_row, int64_t rows, int chunks) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= rows * chunks) return;
   const int64_t row = t / chunks;
@@ -123,9 +127,11 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(
   float xv[8], bv[8], gv[8], y[8];
   unpack8f(ld16(x + row * x_row + 8 * c), xv);
   unpack8f(ld16(b + row * b_row + 8 * c), bv);
-  load_mod8(gate, (int64_t)idx[row] * gate_row + 8 * c, gate_bf16, gv);
+  const int seg = idx[row];
+  const bool seg_ok = (unsigned)seg < (unsigned)table_rows;  // else row 0 is read and NaN written
+  load_mod8(gate, (int64_t)(seg_ok ? seg : 0) * gate_row + 8 * c, gate_bf16, gv);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) y[j] = xv[j] + round_bf(gv[j] * bv[j]);
+  for (int j = 0; j < 8; ++j) y[j] = seg_ok ? xv[j] + round_bf(gv[j] * bv[j]) : __builtin_nanf("");
   st16(out + row * out_row + 8 * c, pack8f(y));
 }
 
@@ -267,8 +273,8 @@ using vdnh3::check_vec8;
 
 extern "C" int vdnh3_rmsnorm_modulate(const uint16_t *x, int64_t x_row, const uint16_t *weight, float eps,
                                       const void *scale, const void *shift, int64_t mod_row, int mod_bf16,
-                                      const int32_t *idx, uint16_t *out, int64_t out_row, int rows, int hidden,
-                                      void *stream) {
+                                      const int32_t *idx, int table_rows, uint16_t *out, int64_t out_row, int rows,
+                                      int hidden, void *stream) {
   VDNH3_HOST_CHECK(rows > 0 && hidden > 0 && hidden % 8 == 0 && hidden <= 8 * 256 * vdnh3::kRowChunks,
                    VDNH3_ERR_INVALID, "rmsnorm_modulate: hidden must be a positive multiple of 8 up to %d, got %d",
                    8 * 256 * vdnh3::kRowChunks, hidden);
@@ -278,14 +284,16 @@ extern "C" int vdnh3_rmsnorm_modulate(const uint16_t *x, int64_t x_row, const ui
   if (!rc) rc = check_vec8(scale, mod_row, "scale", mod_bf16 ? 2 : 4);
   if (!rc) rc = check_vec8(shift, mod_row, "shift", mod_bf16 ? 2 : 4);
   if (rc) return rc;
-  VDNH3_HOST_CHECK(idx != nullptr, VDNH3_ERR_INVALID, "rmsnorm_modulate: null segment index");
+  VDNH3_HOST_CHECK(idx != nullptr && table_rows > 0, VDNH3_ERR_INVALID,
+                   "rmsnorm_modulate: null segment index or empty modulation table");
   hipLaunchKernelGGL(vdnh3::rmsnorm_modulate_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream), x,
-                     x_row, weight, eps, scale, shift, mod_row, mod_bf16, idx, out, out_row, hidden);
+                     x_row, weight, eps, scale, shift, mod_row, mod_bf16, idx, table_rows, out, out_row, hidden);
   return vdnh3::check_launch("rmsnorm_modulate");
 }
 
 extern "C" int vdnh3_gated_residual(const uint16_t *x, int64_t x_row, const void *gate, int64_t gate_row,
-                                    int gate_bf16, const int32_t *idx, const uint16_t *branch, int64_t branch_row,
+                                    int gate_bf16, const int32_t *idx, int table_rows, const uint16_t *branch,
+                                    int64_t branch_row,
                                     uint16_t *out, int64_t out_row, int rows, int hidden, void *stream) {
   VDNH3_HOST_CHECK(rows > 0 && hidden > 0 && hidden % 8 == 0, VDNH3_ERR_INVALID,
                    "gated_residual: hidden must be a positive multiple of 8, got %d", hidden);
@@ -294,11 +302,13 @@ extern "C" int vdnh3_gated_residual(const uint16_t *x, int64_t x_row, const void
   if (!rc) rc = check_vec8(out, out_row, "out");
   if (!rc) rc = check_vec8(gate, gate_row, "gate", gate_bf16 ? 2 : 4);
   if (rc) return rc;
-  VDNH3_HOST_CHECK(idx != nullptr, VDNH3_ERR_INVALID, "gated_residual: null segment index");
+  VDNH3_HOST_CHECK(idx != nullptr && table_rows > 0, VDNH3_ERR_INVALID,
+                   "gated_residual: null segment index or empty modulation table");
   const int chunks = hidden / 8;
   const int64_t threads = (int64_t)rows * chunks;
   hipLaunchKernelGGL(vdnh3::gated_residual_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, x_row, gate, gate_row, gate_bf16, idx, branch, branch_row,
+                     static_cast<hipStream_t>(stream), x, x_row, gate, gate_row, gate_bf16, idx, table_rows, branch,
+                     branch_row,
                      out, out_row, (int64_t)rows, chunks);
   return vdnh3::check_launch("gated_residual");
 }

@@ -56,7 +56,7 @@ SIGNATURES = {
     "vdnh3_short_conv_batch": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                         _vp]),
     "vdnh3_delta_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_float, _vp, _c_int, _c_int, _vp]),
-    "vdnh3_sana_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "vdnh3_sana_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_float, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_delta_scan": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_readout": (_c_int, [_vp, _c_i64, _c_i64, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_i64,
                                _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp]),
@@ -68,7 +68,7 @@ SIGNATURES = {
     "vdnh3_alpha_decay": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_alpha_logsum": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "vdnh3_fill_rows_bf16": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_float, _vp]),
-    "vdnh3_qk_rmsnorm": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _c_float,
+    "vdnh3_qk_rmsnorm": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _c_float, _c_float,
                                   _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_qk_rmsnorm_rope": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _c_float, _vp, _c_i64,
                                        _c_int, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int,
@@ -77,10 +77,10 @@ SIGNATURES = {
     "vdnh3_gdn_chunk_fwd": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64,
                                      _vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp,
                                      _c_size, _vp]),
-    "vdnh3_rmsnorm_modulate": (_c_int, [_vp, _c_i64, _vp, _c_float, _vp, _vp, _c_i64, _c_int, _vp, _vp, _c_i64,
-                                        _c_int, _c_int, _vp]),
-    "vdnh3_gated_residual": (_c_int, [_vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp, _c_i64, _vp, _c_i64, _c_int,
-                                      _c_int, _vp]),
+    "vdnh3_rmsnorm_modulate": (_c_int, [_vp, _c_i64, _vp, _c_float, _vp, _vp, _c_i64, _c_int, _vp, _c_int, _vp,
+                                        _c_i64, _c_int, _c_int, _vp]),
+    "vdnh3_gated_residual": (_c_int, [_vp, _c_i64, _vp, _c_i64, _c_int, _vp, _c_int, _vp, _c_i64, _vp, _c_i64,
+                                      _c_int, _c_int, _vp]),
     "vdnh3_swiglu": (_c_int, [_vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp]),
     "vdnh3_swiglu_quant_rows": (_c_int, [_c_int, _vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _vp]),
     "vdnh3_head_gate": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _vp]),

@@ -244,18 +244,22 @@ class SanaDelta:
         self.tokens = int(tokens_per_frame)
 
     def factor_apply(self, alpha, a_raw, b_raw, *, jay_scale: float = 1.0, need_phi: bool = True):
+        """``(Phi, J)``; ``alpha=None`` means ones. ``jay_scale`` multiplies ``J`` after its own rounding (the
+        text state's exact 1/2); with ``need_phi=False`` no ``Phi`` is written and ``None`` is returned for it."""
         if a_raw.shape != b_raw.shape or a_raw.shape[-1] != a_raw.shape[-2]:
             raise ValueError("A and B must share a square [..., D, D] shape")
+        if alpha is not None and alpha.shape != a_raw.shape[:-1]:
+            raise ValueError("alpha must have shape A.shape[:-1]")
         dim = a_raw.shape[-1]
         device = _lib.require_device(a_raw, b_raw, alpha)
         a32, b32 = a_raw.float().contiguous(), b_raw.float().contiguous()
-        phi, jay = torch.empty_like(a32), torch.empty_like(a32)
+        phi = torch.empty_like(a32) if need_phi else None
+        jay = torch.empty_like(a32)
         al = None if alpha is None else alpha.float().contiguous()
         rc = _lib.lib().vdnh3_sana_factor(_lib.ptr(a32), _lib.ptr(b32), _lib.ptr(al), _lib.ptr(phi), _lib.ptr(jay),
-                                          self.tokens, a32.numel() // (dim * dim), dim, _lib.stream_handle(device))
+                                          float(jay_scale), self.tokens, a32.numel() // (dim * dim), dim,
+                                          _lib.stream_handle(device))
         _lib.check(rc, "vdnh3_sana_factor")
-        if jay_scale != 1.0:
-            jay.mul_(jay_scale)
         return phi, jay
 
 
@@ -368,6 +372,16 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
     for frame, (lo, hi) in enumerate(bounds):
         if lo > frame or hi < frame or lo > hi:
             raise ValueError(f"bounds[{frame}] does not contain its query frame")
+    frames_state = (num_frames, heads, dim, dim)
+    for name, t in (("prefix", prefix), ("suffix", suffix)):
+        if t.dtype != torch.float32 or tuple(t.shape) != frames_state:
+            raise ValueError(f"{name} must be fp32 {list(frames_state)}, got {t.dtype} {list(t.shape)}")
+    if bridge == "alpha" and (alpha is None or tuple(alpha.shape) != frames_state[:3]):
+        raise ValueError(f"alpha must be [{num_frames}, {heads}, {dim}]")
+    if text_state is not None and tuple(text_state.shape) != (heads, dim, dim):
+        raise ValueError(f"text_state must be [{heads}, {dim}, {dim}]")
+    if rows != num_frames * tokens_per_frame:
+        raise ValueError(f"q holds {rows} rows, not num_frames * tokens_per_frame = {num_frames * tokens_per_frame}")
     fused = gate is None
     if fused:
         if gate_hidden is None or gate_up_weight is None:
@@ -407,8 +421,11 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
         rc = _lib.lib().vdnh3_alpha_logsum(_lib.ptr(alpha), num_frames, heads, dim, _lib.ptr(logsum),
                                            _lib.stream_handle(device))
         _lib.check(rc, "vdnh3_alpha_logsum")
-    common = (_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), int(bool(q_features)), _lib.ptr(prefix.contiguous()),
-              _lib.ptr(suffix.contiguous()), _lib.ptr(logsum), _lib.ptr(text), _lib.ptr(bounds_t),
+    # the operands stay bound to locals until the launch has been enqueued (a temporary copy freed
+    # earlier could hand its memory to the next copy)
+    prefix, suffix = prefix.contiguous(), suffix.contiguous()
+    common = (_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), int(bool(q_features)), _lib.ptr(prefix),
+              _lib.ptr(suffix), _lib.ptr(logsum), _lib.ptr(text), _lib.ptr(bounds_t),
               int(bridge == "alpha"), _lib.ptr(norm_w))
     tail = (_lib.ptr(out), out.stride(0), num_frames, tokens_per_frame, heads, dim, _lib.stream_handle(device))
     if fused:

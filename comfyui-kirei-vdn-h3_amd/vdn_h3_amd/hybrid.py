@@ -42,6 +42,26 @@ _LOG = logging.getLogger("vdn_h3_amd")
 _STATE_PATCH = "diffusion_model._vdn_h3_state"
 
 
+def _branch_weights(index: int, branch: Any) -> Mapping:
+    """The weight mapping a branch carries: the branch itself when it is a mapping, else its ``.w``."""
+    if branch is None:
+        raise ValueError(f"block {index} has no branch (None)")
+    source = branch if isinstance(branch, Mapping) else getattr(branch, "w", None)
+    if isinstance(source, Mapping):
+        return source
+    raise TypeError(f"the branch of block {index} ({type(branch).__name__}) carries no weight mapping in .w")
+
+
+def _block_weight_maps(branches: Sequence[Any], weight_maps) -> list:
+    """One weight mapping per block: the given ``weight_maps`` (one per branch), or each branch's own."""
+    if weight_maps is None:
+        return [_branch_weights(i, b) for i, b in enumerate(branches)]
+    maps = list(weight_maps)
+    if len(maps) == len(branches):
+        return maps
+    raise ValueError(f"{len(maps)} weight maps were given for {len(branches)} branches")
+
+
 class VDNState:
     """Runtime state of one patched model: config, per-block branches and weights, plan cache."""
 
@@ -70,20 +90,7 @@ class VDNState:
         self.branch_execution = "serial"
         self.diagnostics = DiagnosticsRecorder(diagnostics)
         self.block_fusion = bool(block_fusion)
-        if weight_maps is None:
-            maps = []
-            for index, branch in enumerate(self.branches):
-                if branch is None:
-                    raise ValueError(f"branch {index} is None")
-                mapping = branch if isinstance(branch, Mapping) else getattr(branch, "w", None)
-                if not isinstance(mapping, Mapping):
-                    raise TypeError(f"branch {index} does not expose a weight mapping as .w")
-                maps.append(mapping)
-        else:
-            maps = list(weight_maps)
-            if len(maps) != len(self.branches):
-                raise ValueError("weight_maps must match branch count")
-        self._maps = maps
+        self._maps = _block_weight_maps(self.branches, weight_maps)
         self._resident: dict[tuple[int, Any], dict[str, torch.Tensor]] = {}
 
     # Weights are resident in HBM (a block's branch weights are ~55 MB at hidden 5120; all
@@ -157,11 +164,14 @@ def rope_table(rope_freqs: torch.Tensor, seq: int, head_dim: int, device) -> tup
 
 
 def normalise_qk(q_raw: torch.Tensor, k_raw: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
-                 eps: float = 1e-6, rope_freqs: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                 eps: float = 1e-6, rope_freqs: torch.Tensor | None = None,
+                 k_eps: float | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """``attn.q_norm(q), attn.k_norm(k)`` (RMSNorm over the head dim) into one new ``[S, 2, H, D]`` buffer.
 
-    With ``rope_freqs`` the normalised vectors are also rotated (split-half RoPE, the fused op of
-    ``vdn_h3/hybrid.py:274-292``), before their one rounding to bf16.
+    ``eps`` is q_norm's epsilon and ``k_eps`` k_norm's (``eps`` when ``None``). With ``rope_freqs``
+    the normalised vectors are also rotated (split-half RoPE, the fused op of
+    ``vdn_h3/hybrid.py:274-292``, which takes q_norm's epsilon for both), before their one rounding
+    to bf16.
     """
     if q_raw.shape != k_raw.shape or q_raw.ndim != 3:
         raise ValueError("q and k must share shape [sequence, heads, dim]")
@@ -184,7 +194,7 @@ def normalise_qk(q_raw: torch.Tensor, k_raw: torch.Tensor, q_weight: torch.Tenso
         return qn, kn
     rc = _lib.lib().vdnh3_qk_rmsnorm(_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), _lib.ptr(k_raw),
                                      k_raw.stride(0), k_raw.stride(1), _lib.ptr(wq), _lib.ptr(wk), float(eps),
-                                     _lib.ptr(qn), qn.stride(0), qn.stride(1), _lib.ptr(kn), kn.stride(0),
+                                     float(eps if k_eps is None else k_eps), _lib.ptr(qn), qn.stride(0), qn.stride(1), _lib.ptr(kn), kn.stride(0),
                                      kn.stride(1), seq, heads, dim, _lib.stream_handle(device))
     _lib.check(rc, "vdnh3_qk_rmsnorm")
     return qn, kn
@@ -198,103 +208,125 @@ def _norm_weight_eps(module, dim, device):
     return weight.to(device), 1e-6 if eps is None else float(eps)
 
 
-def _qkv(attn: Any, x: torch.Tensor):
-    heads, head_dim = int(attn.heads), int(attn.head_dim)
-    inner = heads * head_dim
-    projected = attn.qkv_proj(x)
-    if projected.shape[-1] != inner * 3:
-        raise RuntimeError(f"H3 qkv_proj returned {projected.shape[-1]} features; expected {inner * 3}")
-    q, k, v = projected.split(inner, dim=-1)
-    seq = x.shape[0]
-    return q.view(seq, heads, head_dim), k.view(seq, heads, head_dim), v.view(seq, heads, head_dim)
+def _split_qkv(projected: torch.Tensor, heads: int, head_dim: int):
+    """The raw q / k / v of a fused ``[S, 3*H*D]`` projection as ``[S, H, D]`` views (row stride
+    ``3*H*D``, no copy); ``RuntimeError`` when the width is not ``3*H*D`` (``vdn_h3/hybrid.py:260-268``)."""
+    width = int(projected.shape[-1])
+    if width != 3 * heads * head_dim:
+        raise RuntimeError(f"qkv_proj produced {width} features per token; this block needs "
+                           f"3 x {heads} heads x {head_dim} = {3 * heads * head_dim}")
+    return projected.unflatten(-1, (3, heads, head_dim)).unbind(-3)
 
 
-def make_vdn_forward(attn: Any, state: VDNState, block_index: int):
-    """The patched ``attn.forward`` of block ``block_index``."""
-    original_forward = attn.forward
-    heads, head_dim = int(attn.heads), int(attn.head_dim)
-    config = state.config
-    branch = state.branches[block_index]
+class _VDNBlockForward:
+    """The patched ``attn.forward`` of one block (``vdn_h3/hybrid.py:409-579``).
 
-    def vdn_forward(x, rope_freqs=None, transformer_options=None):
+    Same call signature and contract as the reference's ``vdn_forward``: without a published
+    layout the original forward runs; a layout whose length differs from ``x`` is a
+    ``RuntimeError``; the path is inference-only.
+    """
+
+    def __init__(self, attn: Any, state: VDNState, block_index: int):
+        self.attn, self.state, self.index = attn, state, int(block_index)
+        self.heads, self.head_dim = int(attn.heads), int(attn.head_dim)
+        self.branch = state.branches[block_index]
+        self._vdn_h3_forward = True
+        self._vdn_h3_original = attn.forward
+
+    def __call__(self, x, rope_freqs=None, transformer_options=None):
         layout = current_layout(required=False)
         if layout is None:
-            return original_forward(x, rope_freqs=rope_freqs, transformer_options=transformer_options or {})
-        if int(x.shape[0]) != layout.seq_len:
-            raise RuntimeError(f"VDN layout has {layout.seq_len} rows but attention received {x.shape[0]}")
+            return self._vdn_h3_original(x, rope_freqs=rope_freqs, transformer_options=transformer_options or {})
+        rows = int(x.shape[0])
+        if rows != layout.seq_len:
+            raise RuntimeError(f"attention got {rows} rows but the published VDN layout has {layout.seq_len}")
         if torch.is_grad_enabled():
             raise RuntimeError("the MI355X VDN-H3 block is inference-only; run it under torch.no_grad()")
-        linear_active = bool(config.get("linear_enabled", True)) and not layout.full_cover
-        gate_enabled = bool(config.get("enable_softmax_gate", True))
-        device = x.device
-        weights = state.weights_on(block_index, device, x.dtype)
+        out = self._forward(x, layout, rope_freqs)
+        self.state.forwards += 1
+        self.state.last_layout = layout
+        return out
 
-        scope = state.diagnostics.scope
-        with scope("attention.qkv", device):
-            q_raw, k_raw, value = _qkv(attn, x)
-        qw, q_eps = _norm_weight_eps(attn.q_norm, head_dim, device)
-        kw, _ = _norm_weight_eps(attn.k_norm, head_dim, device)
-        with scope("attention.rope_norm", device):
-            query, key = normalise_qk(q_raw, k_raw, qw, kw, q_eps, rope_freqs=rope_freqs)
+    def _gate(self, x, weights, with_branch: bool):
+        """``(g, proj_rows)``: the softmax gate ``sigmoid(x W_g^T + b_g)`` ``[S, H]`` and, when the branch
+        runs, ``[beta | x W_down^T]`` from the same GEMM over ``x``; ``(None, None)`` with the gate off."""
+        if not bool(self.state.config.get("enable_softmax_gate", True)):
+            return None, None
+        try:
+            fused = _gate_branch_weights(self.state, self.index, weights, self.branch) if with_branch else None
+            if fused is None:
+                gate = _linear.sigmoid_linear(x, weights["softmax_gate.up.weight"],
+                                              weights.get("softmax_gate.up.bias"))
+                return gate, None
+        except KeyError as exc:
+            raise RuntimeError(f"VDN branch block {self.index} is missing softmax gate tensor "
+                               f"{exc.args[0]!r}") from exc
+        # [softmax gate | branch beta] (sigmoid) and the output-gate down-projection: x is read once
+        w_all, b_all = fused
+        rows = _linear.gemm(_linear.KIND_BF16, x, w_all, bias=b_all, act="sigmoid", round_linear=True,
+                            act_cols=2 * self.heads)
+        return rows[:, :self.heads], rows[:, self.heads:]
 
-        gate, proj_rows = None, None
-        if gate_enabled:
-            try:
-                with scope("attention.gate", device):
-                    fused = _gate_branch_weights(state, block_index, weights, branch) if linear_active else None
-                    if fused is None:
-                        gate = _linear.sigmoid_linear(x, weights["softmax_gate.up.weight"],
-                                                      weights.get("softmax_gate.up.bias"))
-                    else:
-                        # one GEMM over x: [softmax gate | branch beta] (sigmoid) and the branch's
-                        # output-gate down-projection, x read once for both
-                        w_all, b_all = fused
-                        rows = _linear.gemm(_linear.KIND_BF16, x, w_all, bias=b_all, act="sigmoid",
-                                            round_linear=True, act_cols=2 * heads)
-                        gate, proj_rows = rows[:, :heads], rows[:, heads:]
-            except KeyError as exc:
-                raise RuntimeError(f"VDN branch block {block_index} is missing softmax gate tensor "
-                                   f"{exc.args[0]!r}") from exc
-        cache = state.window_cache
+    def _plan(self, layout, device):
+        cache = self.state.window_cache
         if layout.full_cover:
-            plan = cache.plan(layout.seq_len, 0, layout.seq_len, 1, layout.seq_len, [(0, 0)], "none", device)
-            state.last_attention_backend = "dense_exact"
-        else:
-            plan = cache.plan(layout.seq_len, layout.video_start, layout.video_end, layout.num_frames,
-                              layout.tokens_per_frame, layout.bounds, layout.anchor_frames, device)
-            state.last_attention_backend = _window.resolve_attention_backend(state.attention_backend, cache=cache)
+            self.state.last_attention_backend = "dense_exact"
+            return cache.plan(layout.seq_len, 0, layout.seq_len, 1, layout.seq_len, [(0, 0)], "none", device)
+        self.state.last_attention_backend = _window.resolve_attention_backend(self.state.attention_backend,
+                                                                              cache=cache)
+        return cache.plan(layout.seq_len, layout.video_start, layout.video_end, layout.num_frames,
+                          layout.tokens_per_frame, layout.bounds, layout.anchor_frames, device)
+
+    def _forward(self, x, layout, rope_freqs):
+        state, attn, heads, head_dim = self.state, self.attn, self.heads, self.head_dim
+        device, scope = x.device, state.diagnostics.scope
+        with_branch = bool(state.config.get("linear_enabled", True)) and not layout.full_cover
+        weights = state.weights_on(self.index, device, x.dtype)
+        with scope("attention.qkv", device):
+            q_raw, k_raw, value = _split_qkv(attn.qkv_proj(x), heads, head_dim)
+        (qw, q_eps), (kw, k_eps) = (_norm_weight_eps(m, head_dim, device) for m in (attn.q_norm, attn.k_norm))
+        with scope("attention.rope_norm", device):
+            # split-half RoPE takes q_norm's epsilon for both (vdn_h3/hybrid.py:284-291)
+            query, key = normalise_qk(q_raw, k_raw, qw, kw, q_eps, rope_freqs=rope_freqs,
+                                      k_eps=q_eps if rope_freqs is not None else k_eps)
+        with scope("attention.gate", device):
+            gate, proj_rows = self._gate(x, weights, with_branch)
+        plan = self._plan(layout, device)
         with scope("attention.softmax", device):
             attended = _window.window_softmax_hip(
                 query, key, value, layout.video_start, layout.video_end, layout.num_frames,
                 layout.tokens_per_frame, layout.bounds, head_dim ** -0.5, layout.anchor_frames, gate=gate, plan=plan,
                 diagnostics=state.diagnostics if state.diagnostics.enabled else None)
         del query, key
-        flat = attended.view(layout.seq_len, heads * head_dim)
         with scope("attention.out_proj", device):
-            out = attn.out_proj(flat)
-        del flat, attended
-        if linear_active:
-            va, vb = layout.video_start, layout.video_end
-            ta, tb = layout.text_start, layout.text_start + layout.text_len
-            text_enabled = bool(getattr(branch, "enable_text_state", config.get("enable_text_state", False)))
-            branch_weights, projector = state.projection_view(weights)
-            with scope("attention.linear_branch", device):
-                branch.projected_delta(
-                    branch_weights, x[va:vb], q_raw[va:vb], k_raw[va:vb], value[va:vb], layout.num_frames,
-                    layout.tokens_per_frame, layout.bounds, frame_size=layout.frame_size,
-                    text_x=x[ta:tb] if text_enabled else None,
-                    text_k_raw=k_raw[ta:tb] if text_enabled else None,
-                    text_v_raw=value[ta:tb] if text_enabled else None, skip_ends=(layout.anchor_frames == "both"),
-                    inference=True, projector=projector, out=out[va:vb], accumulate=True,
-                    **({} if proj_rows is None else
-                       {"proj_rows": proj_rows[va:vb], "text_proj_rows": proj_rows[ta:tb] if text_enabled else None}))
-        state.forwards += 1
-        state.last_layout = layout
+            out = attn.out_proj(attended.view(layout.seq_len, heads * head_dim))
+        del attended
+        if with_branch:
+            self._add_branch(out, x, q_raw, k_raw, value, layout, weights, proj_rows)
         return out
 
-    vdn_forward._vdn_h3_forward = True
-    vdn_forward._vdn_h3_original = original_forward
-    return vdn_forward
+    def _add_branch(self, out, x, q_raw, k_raw, value, layout, weights, proj_rows):
+        """``out[video] += to_out_linear(branch)``, accumulated by the projection GEMM's epilogue."""
+        video = slice(layout.video_start, layout.video_end)
+        text = slice(layout.text_start, layout.text_start + layout.text_len)
+        use_text = bool(getattr(self.branch, "enable_text_state",
+                                self.state.config.get("enable_text_state", False)))
+        branch_weights, projector = self.state.projection_view(weights)
+        extra = {}
+        if proj_rows is not None:
+            extra = {"proj_rows": proj_rows[video], "text_proj_rows": proj_rows[text] if use_text else None}
+        with self.state.diagnostics.scope("attention.linear_branch", x.device):
+            self.branch.projected_delta(
+                branch_weights, x[video], q_raw[video], k_raw[video], value[video], layout.num_frames,
+                layout.tokens_per_frame, layout.bounds, frame_size=layout.frame_size,
+                text_x=x[text] if use_text else None, text_k_raw=k_raw[text] if use_text else None,
+                text_v_raw=value[text] if use_text else None, skip_ends=(layout.anchor_frames == "both"),
+                inference=True, projector=projector, out=out[video], accumulate=True, **extra)
+
+
+def make_vdn_forward(attn: Any, state: VDNState, block_index: int):
+    """The patched ``attn.forward`` of block ``block_index``."""
+    return _VDNBlockForward(attn, state, block_index)
 
 
 def _gate_branch_weights(state, block_index, weights, branch):

@@ -61,9 +61,9 @@ WINDOW_SMALL = WindowWorkload("window_s464_h2_d64", 2, 64, 16, 7, (8, 8))
 WINDOW_SMALL_13F = WindowWorkload("window_s848_h2_d64_13f", 2, 64, 16, 13, (8, 8))
 
 
-def fused_qkv(seq: int, heads: int, head_dim: int, device="cpu", seed: int = 0) -> torch.Tensor:
-    """``[S, 3*H*D]`` bf16 ~ N(0, 1): the layout of the block's fused q/k/v projection."""
-    return randn((seq, 3 * heads * head_dim), seed, device=device, dtype=torch.bfloat16)
+def fused_qkv(seq: int, heads: int, head_dim: int, device="cpu", seed: int = 0, scale: float = 1.0) -> torch.Tensor:
+    """``[S, 3*H*D]`` bf16 ~ N(0, scale^2): the layout of the block's fused q/k/v projection."""
+    return randn((seq, 3 * heads * head_dim), seed, device=device, dtype=torch.bfloat16, scale=scale)
 
 
 def split_qkv(qkv: torch.Tensor, heads: int, head_dim: int):
@@ -74,10 +74,12 @@ def split_qkv(qkv: torch.Tensor, heads: int, head_dim: int):
     return q.view(seq, heads, head_dim), k.view(seq, heads, head_dim), v.view(seq, heads, head_dim)
 
 
-def window_inputs(w: WindowWorkload, device="cpu"):
-    """(qkv buffer, q, k, v views, layout, scale) for a window workload."""
+def window_inputs(w: WindowWorkload, device="cpu", input_scale: float | None = None):
+    """(qkv buffer, q, k, v views, layout, scale) for a window workload: q, k, v ~ N(0, 1) scaled by
+    ``input_scale`` (default ``1/sqrt(head_dim)``, the window-attention benchmark's inputs)."""
     lay = w.layout
-    qkv = fused_qkv(lay.seq_len, w.heads, w.head_dim, device=device, seed=0)
+    scale = w.scale if input_scale is None else input_scale
+    qkv = fused_qkv(lay.seq_len, w.heads, w.head_dim, device=device, seed=0, scale=scale)
     q, k, v = split_qkv(qkv, w.heads, w.head_dim)
     return qkv, q, k, v, lay, w.scale
 
@@ -120,3 +122,58 @@ def branch_weights(heads: int, head_dim: int, hidden: int, device="cpu", seed: i
         "softmax_gate.up.weight": randn((heads, hidden), seed + 10, device, bf, 0.02),
         "softmax_gate.up.bias": randn((heads,), seed + 11, device, bf, 0.5),
     }
+
+
+def attention_module(heads: int, head_dim: int, hidden: int, device, seed: int, precision: str = "int8"):
+    """A random-init MiniMax-H3 attention stand-in with the attributes the patched forward reads
+    (``heads``, ``head_dim``, ``qkv_proj``, ``out_proj``, ``q_norm``, ``k_norm``): W ~ N(0, 0.02) as
+    ``HipLinear`` layers of ``precision``, RMSNorm weights 1 + 0.1 N(0, 1), eps 1e-6."""
+    from types import SimpleNamespace
+
+    from .linear import HipLinear
+
+    bf = torch.bfloat16
+    return SimpleNamespace(
+        heads=heads, head_dim=head_dim, forward=None,
+        qkv_proj=HipLinear(randn((3 * heads * head_dim, hidden), seed + 1, device, bf, 0.02), precision),
+        out_proj=HipLinear(randn((hidden, heads * head_dim), seed + 2, device, bf, 0.02), precision),
+        q_norm=SimpleNamespace(weight=(1 + 0.1 * randn((head_dim,), seed + 3, device)).to(bf), eps=1e-6),
+        k_norm=SimpleNamespace(weight=(1 + 0.1 * randn((head_dim,), seed + 4, device)).to(bf), eps=1e-6))
+
+
+def hybrid_stack(blocks: int, heads: int, head_dim: int, hidden: int, device, *, short_conv=("k", "v"),
+                 precision: str = "int8", config=None, first_seed: int = 1000):
+    """``(state, forwards)``: ``blocks`` random-init VDN-H3 hybrid attention blocks (block i seeded from
+    ``first_seed * (i + 1)``), branch and projections prepared for ``precision``, one ``VDNState``."""
+    from . import projection
+    from .hybrid import VDNState, make_vdn_forward
+    from .runtime import OptimizedLinearBranch
+
+    attns, maps = [], []
+    for i in range(blocks):
+        seed = first_seed * (i + 1)
+        attns.append(attention_module(heads, head_dim, hidden, device, seed, precision))
+        (bw,), _ = projection.prepare_projection_maps(
+            [branch_weights(heads, head_dim, hidden, device=device, seed=seed + 42, short_conv=short_conv)], device,
+            precision)
+        maps.append(bw)
+    branches = [OptimizedLinearBranch(bw, heads, head_dim, short_conv=short_conv) for bw in maps]
+    cfg = {"enable_softmax_gate": True, "linear_enabled": True, "enable_text_state": True}
+    cfg.update(config or {})
+    state = VDNState("hybrid-stack", cfg, branches, heads, head_dim, projection_precision=precision)
+    return state, [make_vdn_forward(attn, state, i) for i, attn in enumerate(attns)]
+
+
+def denoise_pass(forwards, x: torch.Tensor, steps: int, on_block=None) -> torch.Tensor:
+    """``steps`` passes of ``x <- x + block(rms_norm(x))`` over every block (a pre-norm residual, as H3's
+    blocks normalise their input: random-init blocks fed the raw stream would grow it per block).
+    ``on_block(step, index, block_input, block_output)`` sees every block call."""
+    hidden = x.shape[-1]
+    for step in range(steps):
+        for index, forward in enumerate(forwards):
+            h = torch.nn.functional.rms_norm(x, (hidden,), eps=1e-6)
+            y = forward(h)
+            if on_block is not None:
+                on_block(step, index, h, y)
+            x = x + y
+    return x

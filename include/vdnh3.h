@@ -220,9 +220,11 @@ int vdnh3_short_conv_batch(const vdnh3_short_conv_job *jobs, int n_jobs, int ker
 int vdnh3_delta_factor(const float *A, const float *B, const float *alpha, float *phi, float *jay,
                        float jay_scale, int32_t *info, int n, int head_dim, void *stream);
 
-/* SanaDelta.factor_apply (vdn_h3/branch.py:163-177): phi = alpha (I - A/T), jay = B / sqrt(T). */
+/* SanaDelta.factor_apply (vdn_h3/branch.py:163-177): phi = alpha (I - A/T), jay = jay_scale * (B / sqrt(T)),
+ * each fp32 product / difference rounded on its own as the reference's tensor ops do; alpha NULL
+ * means ones, phi may be NULL (not written). */
 int vdnh3_sana_factor(const float *A, const float *B, const float *alpha, float *phi, float *jay,
-                      int tokens_per_frame, int n, int head_dim, void *stream);
+                      float jay_scale, int tokens_per_frame, int n, int head_dim, void *stream);
 
 /*
  * Bidirectional scans (vdn_h3/runtime.py:118-131, vdn_h3/branch.py:315-333) over
@@ -293,14 +295,15 @@ int vdnh3_alpha_decay(const float *delta, const float *a_log, float *alpha, int 
 
 /*
  * q_norm / k_norm of the block (vdn_h3/hybrid.py:271-273, rope_freqs=None: the attention's
- * RMSNorm modules over the head dim): y = bf16(x * rsqrt(mean(x^2) + eps) * w), fp32 statistics.
+ * RMSNorm modules over the head dim): y = bf16(x * rsqrt(mean(x^2) + eps) * w), fp32 statistics,
+ * with q_eps for q (attn.q_norm.eps) and k_eps for k (attn.k_norm.eps).
  * q / k are [seq, heads, head_dim] views (element (s, h, d) at p[s*row + h*head + d]); the
  * results go to separate views q_out / k_out (the raw q / k stay intact for the VDN branch).
  * Weights are bf16 [head_dim]. All pointers 16-byte aligned, strides multiples of 8.
  */
 int vdnh3_qk_rmsnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
-                     int64_t k_head, const uint16_t *q_weight, const uint16_t *k_weight, float eps,
-                     uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
+                     int64_t k_head, const uint16_t *q_weight, const uint16_t *k_weight, float q_eps,
+                     float k_eps, uint16_t *q_out, int64_t qo_row, int64_t qo_head, uint16_t *k_out, int64_t ko_row,
                      int64_t ko_head, int seq, int heads, int head_dim, void *stream);
 
 /*
@@ -351,19 +354,22 @@ int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const 
  * (int32) selects the modulation row of each token (BlockPointwiseCache.indices,
  * vdn_h3/block_kernels.py:25-82); modulation tables are [n, hidden], fp32 (rounded to bf16 on
  * load, the reference's .to(bf16)) or bf16 (mod_bf16 / gate_bf16 = 1), row stride mod_row.
- * hidden is a multiple of 8; bf16 rows and tables are 16-byte aligned.
+ * hidden is a multiple of 8; bf16 rows and tables are 16-byte aligned. `table_rows` is the
+ * number of rows of the modulation table: a token whose idx lies outside [0, table_rows)
+ * reads no table memory and its output row is NaN (the host layer raises ValueError for
+ * indices it can check without a device round trip).
  * ------------------------------------------------------------------------------ */
 
 /* _pre_body (vdn_h3/block_kernels.py:85-89): out = bf16(bf16(n * bf16(1 + scale[idx])) +
  * shift[idx]) with n = F.rms_norm(x, weight, eps) (fp32 statistics, one rounding); hidden <= 8192. */
 int vdnh3_rmsnorm_modulate(const uint16_t *x, int64_t x_row, const uint16_t *weight, float eps, const void *scale,
-                           const void *shift, int64_t mod_row, int mod_bf16, const int32_t *idx, uint16_t *out,
-                           int64_t out_row, int rows, int hidden, void *stream);
+                           const void *shift, int64_t mod_row, int mod_bf16, const int32_t *idx, int table_rows,
+                           uint16_t *out, int64_t out_row, int rows, int hidden, void *stream);
 
 /* _post_body (vdn_h3/block_kernels.py:92-93): out = bf16(x + bf16(gate[idx] * branch)); out may be x. */
 int vdnh3_gated_residual(const uint16_t *x, int64_t x_row, const void *gate, int64_t gate_row, int gate_bf16,
-                         const int32_t *idx, const uint16_t *branch, int64_t branch_row, uint16_t *out,
-                         int64_t out_row, int rows, int hidden, void *stream);
+                         const int32_t *idx, int table_rows, const uint16_t *branch, int64_t branch_row,
+                         uint16_t *out, int64_t out_row, int rows, int hidden, void *stream);
 
 /* _swiglu_body (vdn_h3/block_kernels.py:113-116): with h = [gate | up] ([rows, 2 ffn]),
  * out = bf16(bf16(silu(gate)) * up). */

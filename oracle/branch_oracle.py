@@ -274,14 +274,20 @@ def linear_bf16(x, weight, bias=None):
 
 
 def text_state(weights, text_x, text_k_raw, text_v_raw, num_heads, head_dim, delta_rule="vdn_solve",
-               a_fp32=True):
-    """``0.5 * B_text (I + A_text)^-1`` over all text rows as one frame (``vdn_h3/branch.py:649-670``)."""
+               a_fp32=True, stats=None):
+    """``0.5 * B_text (I + A_text)^-1`` over all text rows as one frame (``vdn_h3/branch.py:649-670``).
+
+    ``stats``: ``(A_text, B_text)`` ``[1, H, D, D]`` to use instead of computing them (a test hook that
+    isolates everything after the statistics)."""
     length = text_x.shape[0]
-    key = activate(text_k_raw, True).reshape(1, length, num_heads, head_dim).permute(0, 2, 1, 3)
-    value = activate(text_v_raw, False).reshape(1, length, num_heads, head_dim).permute(0, 2, 1, 3)
-    beta = torch.sigmoid(linear_bf16(text_x, weights["beta_proj.weight"]))
-    beta = beta.reshape(1, length, num_heads).permute(0, 2, 1)
-    matrix_a, matrix_b = frame_statistics(key, value, beta, a_fp32)
+    if stats is None:
+        key = activate(text_k_raw, True).reshape(1, length, num_heads, head_dim).permute(0, 2, 1, 3)
+        value = activate(text_v_raw, False).reshape(1, length, num_heads, head_dim).permute(0, 2, 1, 3)
+        beta = torch.sigmoid(linear_bf16(text_x, weights["beta_proj.weight"]))
+        beta = beta.reshape(1, length, num_heads).permute(0, 2, 1)
+        matrix_a, matrix_b = frame_statistics(key, value, beta, a_fp32)
+    else:
+        matrix_a, matrix_b = (t.float() for t in stats)
     ones = torch.ones(1, num_heads, head_dim, dtype=matrix_a.dtype)
     if delta_rule == "vdn_solve":
         _, injection, info = vdn_factor(ones, matrix_a, matrix_b)
@@ -312,24 +318,31 @@ def features(weights, q_raw, k_raw, v_raw, num_frames, frame_size, short_conv=()
 
 def readout(weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, *, frame_size=None,
             text_x=None, text_k_raw=None, text_v_raw=None, short_conv=(), delta_rule="vdn_solve",
-            bridge="alpha", a_fp32=True, return_parts=False, fused_conv=False):
+            bridge="alpha", a_fp32=True, return_parts=False, fused_conv=False, stats=None, text_stats=None,
+            gate_hidden=None):
     """Inference readout before ``to_out_linear`` (``vdn_h3/runtime.py:361-419``).
 
     Returns ``[F*T, H*D]`` in the activation dtype (and the intermediate tensors with
-    ``return_parts=True``).
+    ``return_parts=True``). Test hooks: ``stats`` / ``text_stats`` = ``(A, B)`` of the frames / the text
+    rows and ``gate_hidden`` = the output gate's down-projection ``[F*T, D]`` replace the values this
+    function would compute, so a comparison can start after the bf16 roundings they contain.
     """
     heads, head_dim = q_raw.shape[-2:]
     rows = num_frames * tokens_per_frame
     qf, kf, vf = features(weights, q_raw, k_raw, v_raw, num_frames, frame_size, short_conv, fused_conv)
     beta = torch.sigmoid(linear_bf16(xv, weights["beta_proj.weight"]))
     beta = beta.reshape(num_frames, tokens_per_frame, heads).permute(0, 2, 1)
-    matrix_a, matrix_b = frame_statistics(kf, vf, beta, a_fp32)
+    if stats is None:
+        matrix_a, matrix_b = frame_statistics(kf, vf, beta, a_fp32)
+    else:
+        matrix_a, matrix_b = (t.float() for t in stats)
     frame_mean = xv.reshape(num_frames, tokens_per_frame, -1).mean(dim=1, dtype=torch.float32)
     alpha = alpha_gate(frame_mean, weights["alpha.down.weight"], weights["alpha.up.weight"],
                        weights["alpha.dt_bias"], weights["alpha.A_log"], heads, head_dim)
     tstate, tinfo = (None, None)
     if text_x is not None:
-        tstate, tinfo = text_state(weights, text_x, text_k_raw, text_v_raw, heads, head_dim, delta_rule, a_fp32)
+        tstate, tinfo = text_state(weights, text_x, text_k_raw, text_v_raw, heads, head_dim, delta_rule, a_fp32,
+                                   stats=text_stats)
     if delta_rule == "vdn_solve":
         phi, jay, info = vdn_factor(alpha, matrix_a, matrix_b)
     else:
@@ -337,8 +350,8 @@ def readout(weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, boun
         info = torch.zeros(num_frames, heads, dtype=torch.int32)
     initial = torch.zeros_like(jay[0]) if tstate is None else tstate
     prefix, suffix = run_scans(phi, jay, initial)
-    gate = torch.sigmoid(linear_bf16(linear_bf16(xv, weights["output_gate.down.weight"]),
-                                     weights["output_gate.up.weight"], weights.get("output_gate.up.bias")))
+    hidden = linear_bf16(xv, weights["output_gate.down.weight"]) if gate_hidden is None else gate_hidden
+    gate = torch.sigmoid(linear_bf16(hidden, weights["output_gate.up.weight"], weights.get("output_gate.up.bias")))
     state = gather_linear_state(prefix, suffix, alpha, bounds, bridge=bridge, text_state=tstate,
                                 out_dtype=gate.dtype)
     read = bf16_matmul(qf, state.transpose(-1, -2)) if qf.dtype == torch.bfloat16 else qf @ state.transpose(-1, -2)

@@ -14,7 +14,14 @@ inputs / outputs as safetensors next to this script:
   (``vdn_h3/runtime.py:319-341``);
 * ``hybrid_13f.safetensors``      - ``make_vdn_forward`` on a windowed 13-frame layout
   (``vdn_h3/hybrid.py:409-579``): qkv, q/k RMSNorm, window attention, softmax gate,
-  out-projection and the branch delta.
+  out-projection and the branch delta;
+* ``branch_13f_sana.safetensors`` - ``projected_delta`` and ``readout`` with
+  ``delta_rule="sana_scaled"`` (``SanaDelta``, ``vdn_h3/branch.py:163-177``) and the text state;
+* ``dit_block.safetensors``       - ``make_fast_block_forward`` (``vdn_h3/block_kernels.py:149-240``)
+  on a stand-in DiT block (RMSNorm weights, six AdaLN tables, a linear attention, a SwiGLU
+  MLP) with a two-segment modulation map. The fused path only runs for device tensors; its
+  torch ops are device-independent, so the input is a CPU tensor whose ``is_cuda`` reads
+  True, and the state's compiler cache calls each pointwise body eagerly.
 
 Only these composites need the reference: every other oracle function is pinned by
 closed forms in the tests.
@@ -67,7 +74,7 @@ def branch_weights(short_conv):
     return out
 
 
-def make_branch(short_conv):
+def make_branch(short_conv, delta_rule="vdn_solve"):
     from vdn_h3.runtime import OptimizedLinearBranch
     from vdn_h3.window import window_bounds
 
@@ -78,8 +85,9 @@ def make_branch(short_conv):
     q, k, v = [t.reshape(seq, HEADS, DIM) for t in qkv.split(HEADS * DIM, dim=-1)]
     bounds = window_bounds(FRAMES, 1, 5)
     conv = ("k", "v") if short_conv else ()
-    branch = OptimizedLinearBranch(weights, HEADS, DIM, short_conv=conv, enable_text_state=True,
-                                   kernel_backend="eager", compile_policy="off", tile_frames=0)
+    branch = OptimizedLinearBranch(weights, HEADS, DIM, delta_rule=delta_rule, short_conv=conv,
+                                   enable_text_state=True, kernel_backend="eager", compile_policy="off",
+                                   tile_frames=0)
     va, vb = TEXT, seq
     with torch.inference_mode():
         delta = branch.projected_delta(
@@ -92,8 +100,11 @@ def make_branch(short_conv):
     tensors.update({"x": x, "qkv": qkv, "delta": delta.contiguous(), "readout": readout.contiguous()})
     meta = {"frames": str(FRAMES), "grid": f"{GRID[0]}x{GRID[1]}", "text": str(TEXT), "heads": str(HEADS),
             "dim": str(DIM), "hidden": str(HIDDEN), "short_conv": ",".join(conv), "radius": "1", "chunk": "5",
+            "delta_rule": delta_rule,
             "source": "vdn_h3.runtime.OptimizedLinearBranch.projected_delta / readout (inference, skip_ends)"}
     name = "branch_13f_conv.safetensors" if short_conv else "branch_13f.safetensors"
+    if delta_rule != "vdn_solve":
+        name = "branch_13f_sana.safetensors"
     save_file(tensors, str(HERE / name), metadata=meta)
     return name
 
@@ -161,12 +172,87 @@ def make_hybrid():
     return "hybrid_13f.safetensors"
 
 
+DIT_ROWS, DIT_HIDDEN, DIT_FFN = 96, 128, 192
+
+
+class _ReportsDevice(torch.Tensor):
+    """A CPU tensor whose ``is_cuda`` reads True, so ``make_fast_block_forward`` takes its fused path."""
+
+    @property
+    def is_cuda(self):
+        return True
+
+
+class _EagerCompiler:
+    """The compiler cache ``_compiled`` calls (``vdn_h3/block_kernels.py:96-105``), running each body eagerly."""
+
+    def call(self, name, fn, args, key, *, policy=None):
+        del name, key, policy
+        return fn(*args)
+
+
+def make_dit_block():
+    from types import SimpleNamespace
+
+    from vdn_h3.block_kernels import make_fast_block_forward
+    from vdn_h3.diagnostics import DiagnosticsRecorder
+
+    hidden, ffn = DIT_HIDDEN, DIT_FFN
+    w = {
+        "norm1.weight": 1.0 + 0.1 * torch.randn(hidden, generator=gen(301)),
+        "norm2.weight": 1.0 + 0.1 * torch.randn(hidden, generator=gen(302)),
+        "attn.weight": 0.08 * torch.randn(hidden, hidden, generator=gen(303)),
+        "fc1.weight": 0.08 * torch.randn(2 * ffn, hidden, generator=gen(304)),
+        "fc2.weight": 0.08 * torch.randn(hidden, ffn, generator=gen(305)),
+    }
+    w = {k: v.to(torch.bfloat16) for k, v in w.items()}
+    # six distinct [2, hidden] fp32 tables: a mix-up of any two changes the output
+    names = ("shift_msa", "scale_msa", "gate_msa", "shift_mlp", "scale_mlp", "gate_mlp")
+    mod = {n: (0.4 * torch.randn(2, hidden, generator=gen(310 + i)) + 0.1 * (i + 1)) for i, n in enumerate(names)}
+
+    def norm(weight):
+        return SimpleNamespace(weight=weight, eps=1e-6)
+
+    attn_lin = nn.Linear(hidden, hidden, bias=False).to(torch.bfloat16)
+    fc1 = nn.Linear(hidden, 2 * ffn, bias=False).to(torch.bfloat16)
+    fc2 = nn.Linear(ffn, hidden, bias=False).to(torch.bfloat16)
+    with torch.no_grad():
+        attn_lin.weight.copy_(w["attn.weight"])
+        fc1.weight.copy_(w["fc1.weight"])
+        fc2.weight.copy_(w["fc2.weight"])
+
+    def attn(h, rope_freqs=None, transformer_options=None):
+        return attn_lin(h)
+
+    block = SimpleNamespace(norm1=norm(w["norm1.weight"]), norm2=norm(w["norm2.weight"]), attn=attn,
+                            mlp=SimpleNamespace(fc1=fc1, fc2=fc2),
+                            adaln_proj=lambda t_emb: tuple(mod[n] for n in names),
+                            forward=lambda *a, **k: (_ for _ in ()).throw(AssertionError("fallback taken")))
+    state = SimpleNamespace(block_fusion=True, inference=True, weight_mode="resident", compile_policy="shared",
+                            branch_runtime=SimpleNamespace(compiler=_EagerCompiler()),
+                            diagnostics=DiagnosticsRecorder(False))
+    x = (2.0 * torch.randn(DIT_ROWS, hidden, generator=gen(320))).to(torch.bfloat16)
+    segments = [(0, 40, 0), (40, DIT_ROWS, 1)]
+    forward = make_fast_block_forward(block, state, 0)
+    with torch.inference_mode():
+        out = forward(x.as_subclass(_ReportsDevice), torch.zeros(1), segments, None)
+    out = torch.Tensor(out).as_subclass(torch.Tensor)
+    tensors = {f"w.{k}": v.contiguous() for k, v in w.items()}
+    tensors.update({f"mod.{n}": mod[n].contiguous() for n in names})
+    tensors.update({"x": x, "out": out.contiguous()})
+    meta = {"rows": str(DIT_ROWS), "hidden": str(hidden), "ffn": str(ffn), "segments": "0:40:0,40:96:1",
+            "eps": "1e-6", "source": "vdn_h3.block_kernels.make_fast_block_forward (fused path, bf16 MLP)"}
+    save_file(tensors, str(HERE / "dit_block.safetensors"), metadata=meta)
+    return "dit_block.safetensors"
+
+
 def main():
     if not (REF / "vdn_h3").is_dir():
         raise SystemExit(f"reference checkout not found at {REF}")
     sys.path.insert(0, str(REF))
     torch.set_num_threads(4)
-    for name in (make_branch(False), make_branch(True), make_hybrid()):
+    for name in (make_branch(False), make_branch(True), make_hybrid(), make_branch(False, "sana_scaled"),
+                 make_dit_block()):
         print("wrote", HERE / name)
 
 

@@ -363,19 +363,111 @@ def test_full_shape_branch(device):
                       text_x=hx[:text], text_k_raw=hk[:text], text_v_raw=hv[:text])
     got = readout[tpf:-tpf]
     g32, w32 = got.float(), want.float()
-    steps = (g32 - w32).abs() / (2.0 ** -8 * w32.abs() + 2.0 ** -10)   # error in bf16 steps of the oracle value
+    ulp = torch.ldexp(torch.ones_like(w32), torch.frexp(w32)[1] - 8).clamp_min(2.0 ** -133)
+    steps = (g32 - w32).abs() / ulp                                   # error in bf16 ulps of the oracle value
+    small = w32.abs() < 2
+    err_small = (g32 - w32).abs()[small].max().item()
     cos = torch.nn.functional.cosine_similarity(g32.double().flatten(), w32.double().flatten(), dim=0).item()
-    rows = torch.tensor([0, 1, 1295, 1296, 10000, 20000, 30000, 37583])
+    rows = torch.arange(0, 37584, 64)
     want_delta = bo.linear_bf16(want[rows], hw["to_out_linear.weight"])
-    print(f"readout: cosine {cos:.7f}, frac > 2 steps {(steps > 2).float().mean().item():.2e}, "
-          f"frac > 8 steps {(steps > 8).float().mean().item():.2e}, max |want| {w32.abs().max().item():.2f}",
-          flush=True)
+    print(f"readout: cosine {cos:.7f}, ulps: max {steps.max().item():.1f}, frac > 2 {(steps > 2).float().mean():.2e}, "
+          f"frac > 4 {(steps > 4).float().mean():.2e}, frac > 8 {(steps > 8).float().mean():.2e}; "
+          f"max abs where |want| < 2: {err_small:.3e}; max |want| {w32.abs().max().item():.2f}", flush=True)
     # B is rounded to bf16 (the reference's bf16 matmul output): where the fp32 sums of the two
     # paths straddle a rounding boundary, B moves by one bf16 step and J = B M carries it into
     # the state, so a small fraction of readout values differ by more than the local rounding.
     assert cos >= 0.9999, cos
-    assert (steps > 2).float().mean().item() <= 2e-3
-    assert (steps > 8).float().mean().item() <= 1e-4
+    assert (steps > 2).float().mean().item() <= 5e-3
+    assert (steps > 8).float().mean().item() <= 1.5e-3
     assert torch.count_nonzero(readout[:tpf]) == 0 and torch.count_nonzero(readout[-tpf:]) == 0
     _parity(delta[tpf:-tpf][rows], want_delta, "full-shape projected delta")
     assert torch.count_nonzero(delta[:tpf]) == 0 and torch.count_nonzero(delta[-tpf:]) == 0
+
+    # The tail above comes from the bf16 roundings before the factor: B (the reference's bf16 matmul
+    # output), beta and the gate's down-projection, whose fp32 sums differ in summation order between the
+    # two paths and so round differently where they straddle a bf16 midpoint. With the GPU's own A, B (video
+    # and text rows) and gate down-projection handed to the oracle, everything after them - alpha, factor,
+    # scans, gather, readout, RMSNorm and the gate - is held to <= 2 ulps for 99.9% of values, <= 8 ulps where
+    # |value| >= 2 and max-abs 2^-5 (4 ulps at 1) where |value| < 2: the bf16 cast of the gathered state and
+    # of the readout r still round in both paths, and a one-ulp flip of r in a row whose RMS is small moves the
+    # normalised value by a few of its ulps.
+    from vdn_h3_amd import branch
+    from vdn_h3_amd import linear as lin
+
+    inner_rows = slice(va + tpf, va + (frames - 1) * tpf)
+    with torch.no_grad():
+        both = lin.sigmoid_linear_split(x[inner_rows], torch.cat([w["beta_proj.weight"],
+                                                                   w["output_gate.down.weight"]]).contiguous(), heads)
+        a, b = branch.frame_statistics_raw(k[inner_rows], v[inner_rows], both[:, :heads], frames - 2, tpf)
+        at, bt = branch.frame_statistics_raw(k[:text], v[:text], lin.sigmoid_linear(x[:text], w["beta_proj.weight"]),
+                                             1, text)
+    torch.cuda.synchronize()
+    iso = bo.readout(hw, hx[inner], hq[inner], hk[inner], hv[inner], frames - 2, tpf, ibounds, text_x=hx[:text],
+                     text_k_raw=hk[:text], text_v_raw=hv[:text], stats=(a.cpu(), b.cpu()),
+                     text_stats=(at.cpu(), bt.cpu()), gate_hidden=both[:, heads:].cpu()).float()
+    isteps = (g32 - iso).abs() / torch.ldexp(torch.ones_like(iso), torch.frexp(iso)[1] - 8).clamp_min(2.0 ** -133)
+    ismall = (g32 - iso).abs()[iso.abs() < 2].max().item()
+    print(f"readout after the GPU's statistics: ulps max {isteps.max().item():.1f}, frac > 2 "
+          f"{(isteps > 2).float().mean():.2e}, frac > 4 {(isteps > 4).float().mean():.2e}; max abs where "
+          f"|value| < 2: {ismall:.3e}", flush=True)
+    big = iso.abs() >= 2
+    assert (isteps <= 2).float().mean().item() >= 0.999
+    assert not bool(big.any()) or isteps[big].max().item() <= 8
+    assert ismall <= 2.0 ** -5
+
+
+@pytest.mark.parametrize("dim,alpha_ones", [(128, False), (64, False), (128, True)])
+def test_sana_factor(device, dim, alpha_ones):
+    """SanaDelta.factor_apply (vdnh3_sana_factor) against the oracle's torch formula: the same fp32
+    products and differences, so bit-identical; the text state's 1/2 and alpha = None (ones) included."""
+    from vdn_h3_amd import branch
+
+    print(f"case sana factor D={dim} alpha_ones={alpha_ones}", flush=True)
+    frames, heads, tokens = 3, 2, 1296
+    kf = torch.nn.functional.normalize(_rand((frames, heads, 200, dim), 60), dim=-1)
+    a = kf.transpose(-1, -2) @ kf
+    b = _rand((frames, heads, dim, dim), 61)
+    alpha = torch.ones(frames, heads, dim) if alpha_ones else torch.rand(frames, heads, dim,
+                                                                         generator=torch.Generator().manual_seed(62))
+    backend = branch.SanaDelta(tokens)
+    phi, jay = backend.factor_apply(None if alpha_ones else alpha.to(device), a.to(device), b.to(device))
+    wphi, wjay = bo.sana_factor(alpha, a, b, tokens)
+    assert torch.equal(phi.cpu(), wphi) and torch.equal(jay.cpu(), wjay)
+    none_phi, half = backend.factor_apply(None, a.to(device), b.to(device), jay_scale=0.5, need_phi=False)
+    assert none_phi is None and torch.equal(half.cpu(), 0.5 * wjay)
+    with pytest.raises(ValueError, match="alpha"):
+        backend.factor_apply(alpha[:, :, :-1].to(device), a.to(device), b.to(device))
+
+
+def test_projected_delta_sana_matches_reference_golden(device):
+    """The branch with delta_rule='sana_scaled' (13 frames of 8x8, 2 heads x 64, text state) vs the
+    reference's own output and vs the oracle."""
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+
+    print("case projected_delta sana golden", flush=True)
+    t, meta = _load("branch_13f_sana.safetensors")
+    assert meta["delta_rule"] == "sana_scaled"
+    frames, text, heads, dim = int(meta["frames"]), int(meta["text"]), int(meta["heads"]), int(meta["dim"])
+    gh, gw = map(int, meta["grid"].split("x"))
+    tpf = gh * gw
+    w = {k[2:]: v.to(device) for k, v in t.items() if k.startswith("w.")}
+    x, qkv = t["x"].to(device), t["qkv"].to(device)
+    seq = x.shape[0]
+    q, k, v = [y.view(seq, heads, dim) for y in qkv.split(heads * dim, dim=-1)]
+    bounds = wo.window_bounds(frames, 1, 5)
+    br = OptimizedLinearBranch(w, heads, dim, delta_rule="sana_scaled", short_conv=(), enable_text_state=True)
+    kw = dict(frame_size=(gh, gw), text_x=x[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True)
+    with torch.no_grad():
+        got = br.projected_delta(w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, **kw)
+        readout = br.readout(w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, **kw)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(got[:tpf]) == 0 and torch.count_nonzero(got[-tpf:]) == 0
+    _parity(got, t["delta"], "sana projected_delta vs reference")
+    _parity(readout, t["readout"], "sana readout vs reference", atol=2 ** -5, min_cos=0.9999)
+    hw = {k2[2:]: v2 for k2, v2 in t.items() if k2.startswith("w.")}
+    hq, hk, hv = [y.reshape(seq, heads, dim) for y in t["qkv"].split(heads * dim, dim=-1)]
+    hx = t["x"]
+    want = bo.projected_delta(hw, hx[text:], hq[text:], hk[text:], hv[text:], frames, tpf, bounds, frame_size=(gh, gw),
+                              text_x=hx[:text], text_k_raw=hk[:text], text_v_raw=hv[:text], skip_ends=True,
+                              delta_rule="sana_scaled")
+    _parity(got, want, "sana projected_delta vs oracle")

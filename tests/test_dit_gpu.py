@@ -181,3 +181,44 @@ def test_fast_block_forward_vs_oracle(device, precision):
     assert forward(x.to(device), torch.zeros(1), segments, None, attention=object()) == "original"
     state.block_fusion = False
     assert forward(x.to(device), torch.zeros(1), segments, None) == "original"
+
+
+def test_fast_block_forward_matches_reference_golden(device):
+    """make_fast_block_forward on the GPU against the reference's own make_fast_block_forward output
+    (tests/golden/dit_block.safetensors: two modulation segments, bf16 attention stand-in and SwiGLU MLP).
+    Error in bf16 ulps of the reference value: <= 2 ulps for >= 99.9% of values, <= 4 at most, and
+    max-abs 2e-2 where |value| < 2."""
+    from safetensors import safe_open
+
+    from vdn_h3_amd.block_kernels import make_fast_block_forward
+    from vdn_h3_amd.diagnostics import DiagnosticsRecorder
+    from vdn_h3_amd.linear import HipLinear
+
+    print("case fast block forward vs reference golden", flush=True)
+    from pathlib import Path
+
+    with safe_open(str(Path(__file__).resolve().parent / "golden" / "dit_block.safetensors"), "pt") as f:
+        t = {k: f.get_tensor(k) for k in f.keys()}
+    names = ("shift_msa", "scale_msa", "gate_msa", "shift_mlp", "scale_mlp", "gate_mlp")
+    attn_lin = HipLinear(t["w.attn.weight"].to(device), "bf16")
+    block = SimpleNamespace(
+        norm1=SimpleNamespace(weight=t["w.norm1.weight"].to(device), eps=1e-6),
+        norm2=SimpleNamespace(weight=t["w.norm2.weight"].to(device), eps=1e-6),
+        adaln_proj=lambda t_emb: tuple(t[f"mod.{n}"].to(device) for n in names),
+        attn=lambda h, rope_freqs=None, transformer_options=None: attn_lin(h),
+        mlp=SimpleNamespace(fc1=HipLinear(t["w.fc1.weight"].to(device), "bf16"),
+                            fc2=HipLinear(t["w.fc2.weight"].to(device), "bf16")),
+        forward=lambda *a, **k: "original")
+    state = SimpleNamespace(block_fusion=True, inference=True, weight_mode="resident",
+                            diagnostics=DiagnosticsRecorder(False))
+    forward = make_fast_block_forward(block, state, 0)
+    segments = [(0, 40, 0), (40, t["x"].shape[0], torch.tensor(1))]
+    with torch.no_grad():
+        got = forward(t["x"].to(device), torch.zeros(1), segments, None)
+    torch.cuda.synchronize()
+    want = t["out"].float()
+    steps = _steps(got, want)
+    err = (got.float().cpu() - want).abs()
+    print(f"  ulps: max {steps.max().item():.1f}, > 2: {(steps > 2).float().mean().item():.2e}", flush=True)
+    assert (steps <= 2).float().mean().item() >= 0.999 and steps.max().item() <= 4
+    assert err[want.abs() < 2].max().item() <= 2e-2

@@ -174,3 +174,62 @@ def test_full_shape_int8_qkv_accumulators_sampled(device):
     want = torch.from_numpy((a @ b.T).astype(np.int32))
     assert torch.equal(acc[rows.to(device)].cpu(), want)
     assert torch.equal(xq.cpu()[rows], qo.int8_quantize_rows(x.cpu()[rows])[0])
+
+
+def _tile_rows(m, tile=256):
+    """One row per 256-row M tile, at a position that walks through the tile, plus the last row."""
+    rows = [t + (37 * i) % min(tile, m - t) for i, t in enumerate(range(0, m, tile))]
+    return torch.tensor(sorted(set(rows + [m - 1])))
+
+
+@pytest.mark.parametrize("n", [15360, 5120])
+def test_full_shape_fp8_per_tensor_sampled(device, n):
+    """M=40,688, K=5,120 fp8 e4m3 with per-tensor scales (BASELINE's second W8A8 variant), N=15,360
+    (qkv) and 5,120 (out): one row of every M tile against the dequantised float64 product."""
+    from vdn_h3_amd import fp8, synth
+
+    print(f"case full-shape fp8 per-tensor N={n}", flush=True)
+    m, k = 40688, 5120
+    x = synth.randn((m, k), 32, device=device, dtype=torch.bfloat16)
+    w = synth.randn((n, k), 33, device=device, dtype=torch.bfloat16, scale=0.02)
+    xq, xs = fp8.quantize_activation(x, per_tensor=True)
+    wq, ws = fp8.quantize_weight(w, per_tensor=True)
+    got = fp8.project(x, {fp8.FP8_WEIGHT_KEY: wq, fp8.FP8_SCALE_KEY: ws})
+    torch.cuda.synchronize()
+    rows = _tile_rows(m)
+    want = qo.fp8_linear(xq[rows.to(device)].cpu(), xs.cpu(), wq.cpu(), ws.cpu()).float()
+    g = got[rows.to(device)].float().cpu()
+    err = (g - want).abs().max().item()
+    cos = torch.nn.functional.cosine_similarity(g.double().flatten(), want.double().flatten(), dim=0).item()
+    print(f"  {len(rows)} rows: max abs {err:.3e}, cosine {cos:.7f}", flush=True)
+    # outputs reach |7| (K = 5120 products of N(0,1) x N(0, 0.02^2)), where one bf16 step is 2^-5: the bar
+    # is one rounding step of the float64 product (fp32 accumulation order), and max-abs 2e-2 where |want| < 2
+    assert cos >= 0.9995, cos
+    ulp = torch.ldexp(torch.ones_like(want), torch.frexp(want)[1] - 8).clamp_min(2.0 ** -133)
+    steps = (g - want).abs() / ulp
+    print(f"  ulps of the float64 value: max {steps.max().item():.2f}", flush=True)
+    assert steps.max().item() <= 1.0
+    assert (g - want).abs()[want.abs() < 2].max().item() <= 2e-2
+
+
+def test_full_shape_int8_out_projection_sampled(device):
+    """The out-projection shape M=40,688, K=5,120, N=5,120 W8A8 int8: the int32 accumulators of one row
+    per M tile bit-exact, and the scaled bf16 output within one rounding step."""
+    from vdn_h3_amd import linear, synth
+
+    print("case full-shape int8 out", flush=True)
+    m, k, n = 40688, 5120, 5120
+    x = synth.randn((m, k), 34, device=device, dtype=torch.bfloat16)
+    w = synth.randn((n, k), 35, device=device, dtype=torch.bfloat16, scale=0.02)
+    xq, xs = linear.quantize_rows(x, linear.KIND_I8)
+    wq, ws = linear.quantize_rows(w, linear.KIND_I8)
+    acc = linear.int8_accumulators(xq, wq)
+    out = linear.gemm_w8a8(xq, xs, wq, ws.reshape(1, -1))
+    torch.cuda.synchronize()
+    rows = _tile_rows(m)
+    a = xq[rows.to(device)].cpu().numpy().astype(np.int64)
+    b = wq.cpu().numpy().astype(np.int64)
+    want_acc = torch.from_numpy((a @ b.T).astype(np.int32))
+    assert torch.equal(acc[rows.to(device)].cpu(), want_acc)
+    want = qo.int8_linear(xq[rows.to(device)].cpu(), xs[rows.to(device)].cpu(), wq.cpu(), ws.cpu().reshape(1, -1))
+    assert_bf16_close(out[rows.to(device)], want, steps=1)

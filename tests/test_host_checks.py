@@ -90,3 +90,34 @@ def test_row_span_joins_row_slices_of_one_matrix():
     assert gap == 20 and torch.equal(view, x[:90, :4])
     assert _row_span(x[:10].clone(), x[20:90]) is None  # different storage
     assert _row_span(None, x[20:90]) is None
+
+
+def test_segment_index_is_built_without_device_reads_and_range_checked():
+    """BlockPointwiseCache turns a segment map into the per-token index (same values as the oracle's
+    brute-force map), knows its range on the host for integer and CPU-tensor rows, and the pointwise
+    ops reject an index outside the modulation table before any launch (ValueError, as index_select)."""
+    from oracle import dit_oracle as do
+    from vdn_h3_amd import block_kernels as bk
+
+    segs = [(0, 5, 2), (5, 9, torch.tensor([0, 1, 1, 0])), (9, 12, torch.tensor(1)), (12, 12, 7)]
+    idx = bk.build_segment_index(segs, 12, torch.device("cpu"))
+    assert idx.ids.dtype == torch.int32 and idx.ids.tolist() == do.segment_indices(segs[:3], 12).tolist()
+    assert (idx.low, idx.high) == (0, 2)
+    cache = bk.BlockPointwiseCache(limit=2)
+    ints = [(0, 7, 1), (7, 12, 0)]
+    first = cache.index(ints, 12, "cpu")
+    assert first is cache.index(ints, 12, "cpu") and (first.low, first.high) == (0, 1)
+    assert cache.indices(ints, 12, "cpu").tolist() == [1] * 7 + [0] * 5
+    with pytest.raises(ValueError):
+        bk.build_segment_index([(0, 5, 0), (6, 12, 1)], 12, "cpu")        # a gap
+    with pytest.raises(ValueError):
+        bk.build_segment_index([(0, 5, 0)], 12, "cpu")                    # short of the sequence
+    with pytest.raises(ValueError):
+        bk.build_segment_index([(0, 12, torch.tensor([0, 1]))], 12, "cpu")  # wrong row count
+    x = torch.zeros(12, 16, dtype=torch.bfloat16)
+    table = torch.zeros(2, 16)
+    bad = bk.build_segment_index([(0, 6, 0), (6, 12, 2)], 12, "cpu")     # row 2 of a 2-row table
+    with pytest.raises(ValueError, match="out of range"):
+        bk.rmsnorm_modulate(x, torch.ones(16), 1e-6, table, table, bad)
+    with pytest.raises(ValueError, match="out of range"):
+        bk.gated_residual(x, table, torch.tensor([0] * 11 + [-1]), x)

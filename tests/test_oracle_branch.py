@@ -225,3 +225,50 @@ def test_branch_oracle_matches_reference_golden(name):
     cos = F.cosine_similarity(delta.double().flatten(), want.double().flatten(), dim=0).item()
     assert cos >= 0.99999, cos
     assert torch.count_nonzero(delta[:tpf]) == 0 and torch.count_nonzero(delta[-tpf:]) == 0
+
+
+def test_sana_factor_closed_forms():
+    """SanaDelta (vdn_h3/branch.py:163-177): A = 0 gives Phi = diag(alpha); A = T I gives Phi = 0; B = I gives
+    J = I / sqrt(T); alpha scales rows (a transposed product fails it); Phi is linear in A."""
+    g = torch.Generator().manual_seed(7)
+    tokens, d = 49, 8
+    alpha = torch.rand(3, 2, d, generator=g) + 0.5
+    eye = torch.eye(d).expand(3, 2, d, d)
+    phi, jay = bo.sana_factor(alpha, torch.zeros(3, 2, d, d), eye.clone(), tokens)
+    assert torch.equal(phi, torch.diag_embed(alpha))
+    assert torch.allclose(jay, eye / 7.0, rtol=0, atol=1e-7)
+    phi, _ = bo.sana_factor(alpha, tokens * eye.clone(), eye.clone(), tokens)
+    assert torch.count_nonzero(phi) == 0
+    a = torch.randn(3, 2, d, d, generator=g)
+    phi, _ = bo.sana_factor(alpha, a, a, tokens)
+    want = alpha[..., :, None] * (torch.eye(d) - a / tokens)           # row i scaled by alpha[i]
+    assert torch.allclose(phi, want, rtol=1e-6, atol=1e-7)
+    assert not torch.allclose(phi, alpha[..., None, :] * (torch.eye(d) - a / tokens), rtol=1e-3, atol=1e-4)
+    p1, _ = bo.sana_factor(alpha, a, a, tokens)
+    p2, _ = bo.sana_factor(alpha, 2 * a, a, tokens)
+    p0, _ = bo.sana_factor(alpha, torch.zeros_like(a), a, tokens)
+    assert torch.allclose(p2 - p0, 2 * (p1 - p0), rtol=1e-5, atol=1e-6)
+
+
+def test_sana_branch_oracle_matches_reference_golden():
+    """The oracle's sana_scaled branch (frames and text state) reproduces the reference's own output."""
+    t, meta = _load("branch_13f_sana.safetensors")
+    assert meta["delta_rule"] == "sana_scaled"
+    frames, text, heads, dim = int(meta["frames"]), int(meta["text"]), int(meta["heads"]), int(meta["dim"])
+    gh, gw = map(int, meta["grid"].split("x"))
+    tpf = gh * gw
+    w = {k[2:]: v for k, v in t.items() if k.startswith("w.")}
+    x, qkv = t["x"], t["qkv"]
+    seq = x.shape[0]
+    q, k, v = [y.reshape(seq, heads, dim) for y in qkv.split(heads * dim, dim=-1)]
+    bounds = wo.window_bounds(frames, 1, 5)
+    args = (w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds)
+    kw = dict(frame_size=(gh, gw), text_x=x[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True)
+    delta = bo.projected_delta(*args, **kw, delta_rule="sana_scaled")
+    want = t["delta"].float()
+    err = (delta.float() - want).abs().max().item()
+    assert err <= 4e-3 * max(1.0, want.abs().max().item()), err
+    assert (delta.float() == want).float().mean().item() >= 0.999
+    # the vdn_solve rule on the same inputs is far from it: the golden pins the rule
+    other = bo.projected_delta(*args, **kw)
+    assert (other.float() - want).abs().max().item() > 50 * max(err, 1e-3)

@@ -55,3 +55,51 @@ def test_segment_indices_brute_force_and_errors():
         do.segment_indices([(0, 5, 0), (6, 12, 1)], 12)
     with pytest.raises(ValueError, match="cover"):
         do.segment_indices([(0, 5, 0)], 12)
+
+
+def _dit_golden():
+    from pathlib import Path
+
+    from safetensors import safe_open
+
+    path = Path(__file__).resolve().parent / "golden" / "dit_block.safetensors"
+    with safe_open(str(path), "pt") as f:
+        return {k: f.get_tensor(k) for k in f.keys()}, f.metadata()
+
+
+def _dit_oracle(t, mod_order=None, norms=("w.norm1.weight", "w.norm2.weight")):
+    from oracle import branch_oracle as bo
+
+    names = ("shift_msa", "scale_msa", "gate_msa", "shift_mlp", "scale_mlp", "gate_mlp")
+    mod = tuple(t[f"mod.{n}"] for n in (mod_order or names))
+    segments = [(0, 40, 0), (40, t["x"].shape[0], 1)]
+    return do.block_forward(t["x"], mod, segments, t[norms[0]], t[norms[1]],
+                            lambda h: bo.linear_bf16(h, t["w.attn.weight"]),
+                            lambda h: bo.linear_bf16(h, t["w.fc1.weight"]),
+                            lambda a: bo.linear_bf16(a, t["w.fc2.weight"]))
+
+
+def test_block_forward_matches_reference_golden():
+    """dit_oracle.block_forward against the reference's make_fast_block_forward output: the modulation
+    order, which norm feeds which half and the SwiGLU MLP. Swapping two modulation tables, the two norms,
+    or the SwiGLU halves each fails it."""
+    t, meta = _dit_golden()
+    assert meta["segments"] == "0:40:0,40:96:1"
+    want = t["out"].float()
+    got = _dit_oracle(t).float()
+    steps = (got - want).abs() / torch.ldexp(torch.ones_like(want), torch.frexp(want)[1] - 8)
+    assert steps.max().item() <= 1 and (steps == 0).float().mean().item() >= 0.99, steps.max().item()
+    bar = 8 * (got - want).abs().max().item() + 1e-2
+    for order in (("scale_msa", "shift_msa", "gate_msa", "shift_mlp", "scale_mlp", "gate_mlp"),
+                  ("shift_mlp", "scale_mlp", "gate_mlp", "shift_msa", "scale_msa", "gate_msa"),
+                  ("shift_msa", "scale_msa", "gate_mlp", "shift_mlp", "scale_mlp", "gate_msa")):
+        assert (_dit_oracle(t, order).float() - want).abs().max().item() > bar, order
+    swapped = _dit_oracle(t, norms=("w.norm2.weight", "w.norm1.weight")).float()
+    assert (swapped - want).abs().max().item() > bar
+    flipped = do.block_forward(t["x"], tuple(t[f"mod.{n}"] for n in ("shift_msa", "scale_msa", "gate_msa",
+                                                                      "shift_mlp", "scale_mlp", "gate_mlp")),
+                               [(0, 40, 0), (40, 96, 1)], t["w.norm1.weight"], t["w.norm2.weight"],
+                               lambda h: h @ t["w.attn.weight"].t(),
+                               lambda h: torch.cat((h @ t["w.fc1.weight"].t()).chunk(2, -1)[::-1], -1),
+                               lambda a: a @ t["w.fc2.weight"].t()).float()
+    assert (flipped - want).abs().max().item() > bar

@@ -96,23 +96,30 @@ def test_fused_gate(device):
     assert_parity(out, want)
 
 
-def test_full_shape_sampled_rows(device):
-    """40 688 tokens x 40 heads x 128: the whole problem on the GPU, exact oracle on sampled rows."""
+@pytest.mark.parametrize("input_scale", [1.0, 128 ** -0.5])
+def test_full_shape_sampled_rows(device, input_scale):
+    """40 688 tokens x 40 heads x 128: the whole problem on the GPU, exact oracle on one row of every work
+    item of the plan (at a position that walks through the item) plus the layout's boundary rows, all 40
+    heads. Inputs ~ N(0, 1) (a sharp softmax) and ~ N(0, 1) / sqrt(128) (the benchmark's inputs)."""
     from vdn_h3_amd import synth, window
 
     w = synth.WINDOW_FULL
-    lay = w.layout
-    print(f"case full shape S={lay.seq_len}", flush=True)
-    qkv = synth.fused_qkv(lay.seq_len, w.heads, w.head_dim, device=device, seed=0)
-    q, k, v = synth.split_qkv(qkv, w.heads, w.head_dim)
+    print(f"case full shape S={w.layout.seq_len} input scale {input_scale:.4f}", flush=True)
+    qkv, q, k, v, lay, _ = synth.window_inputs(w, device=device, input_scale=input_scale)
     out = window.window_softmax_hip(q, k, v, lay.video_start, lay.video_end, lay.num_frames, lay.tokens_per_frame,
                                     lay.bounds, w.scale, lay.anchor_frames)
     torch.cuda.synchronize()
+    items, _, _ = window.build_plan_host(lay.seq_len, lay.video_start, lay.video_end, lay.num_frames,
+                                         lay.tokens_per_frame, lay.bounds, lay.anchor_frames)
     host = qkv.cpu()
     hq, hk, hv = synth.split_qkv(host, w.heads, w.head_dim)
     T, vs = lay.tokens_per_frame, lay.video_start
-    rows = [0, 511, vs, vs + T - 1, vs + T, vs + 2 * T + 127, vs + 2 * T + 128, vs + 5 * T - 1, vs + 5 * T,
-            vs + 12 * T + 700, vs + 25 * T, vs + 29 * T + 1295, vs + 30 * T, lay.seq_len - 1]
+    rows = {0, 511, vs, vs + T - 1, vs + T, vs + 2 * T + 127, vs + 2 * T + 128, vs + 5 * T - 1, vs + 5 * T,
+            vs + 12 * T + 700, vs + 25 * T, vs + 29 * T + 1295, vs + 30 * T, lay.seq_len - 1}
+    for i, (q0, q1, _, _) in enumerate(items.tolist()):
+        rows.add(q0 + (37 * i) % (q1 - q0))
+    rows = sorted(rows)
+    print(f"  {len(rows)} rows ({items.shape[0]} work items)", flush=True)
     want = wo.window_attention_rows(hq, hk, hv, rows, lay.video_start, lay.video_end, lay.num_frames, T, lay.bounds,
                                     w.scale, lay.anchor_frames)
     assert_parity(out.cpu()[rows], want)
