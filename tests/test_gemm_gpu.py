@@ -205,10 +205,12 @@ def test_full_shape_fp8_per_tensor_sampled(device, n):
     # outputs reach |7| (K = 5120 products of N(0,1) x N(0, 0.02^2)), where one bf16 step is 2^-5: the bar
     # is one rounding step of the float64 product (fp32 accumulation order), and max-abs 2e-2 where |want| < 2
     assert cos >= 0.9995, cos
+    # per value: one bf16 ulp of the float64 product, plus 2^-12 for the fp32 accumulation of 5120 products
+    # (outputs near zero carry that absolute noise, many of their own ulps)
     ulp = torch.ldexp(torch.ones_like(want), torch.frexp(want)[1] - 8).clamp_min(2.0 ** -133)
-    steps = (g - want).abs() / ulp
-    print(f"  ulps of the float64 value: max {steps.max().item():.2f}", flush=True)
-    assert steps.max().item() <= 1.0
+    excess = ((g - want).abs() - 2.0 ** -12).clamp_min(0) / ulp
+    print(f"  beyond 2^-12, in ulps of the float64 value: max {excess.max().item():.2f}", flush=True)
+    assert excess.max().item() <= 1.0
     assert (g - want).abs()[want.abs() < 2].max().item() <= 2e-2
 
 
