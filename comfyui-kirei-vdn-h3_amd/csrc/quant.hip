@@ -9,6 +9,7 @@
 // The division is IEEE-correct and e4m3fn rounding is round-to-nearest-even, so the codes
 // equal a CPU `(x / s).clamp(...).to(torch.float8_e4m3fn)` bit for bit.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -104,6 +105,88 @@ __global__ __launch_bounds__(256) void cast_tensor_f8_kernel(const uint16_t *__r
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Allocation-free per-tensor fp8 quantisation (vdnh3_quant_tensor_f8_noalloc). The amax is
+// reduced in two deterministic levels through a file-scope device array instead of a caller
+// workspace: one partial maximum per span of kAmaxSpan elements (one workgroup each), then one
+// workgroup reduces the partials into slot kAmaxPartials, which the cast pass reads. Every slot a
+// call reads is written by that call, so nothing needs clearing; calls that overlap on one GPU
+// share the array and race.
+constexpr int kAmaxSpanChunks = 2048;                  // 16-byte chunks per partial (8 per thread)
+constexpr int64_t kAmaxSpan = 8 * kAmaxSpanChunks;     // 16,384 elements per partial maximum
+constexpr int kAmaxPartials = 16384;                   // n <= kAmaxSpan * kAmaxPartials (268,435,456)
+constexpr int kScratchFloats = kAmaxPartials + 64;     // partials, then the total (64 KiB + 256 B)
+__device__ __align__(256) float scratch[kScratchFloats];
+
+__device__ __forceinline__ float absmax8(u32x4_t v, float m) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    m = fmaxf(m, fabsf(__uint_as_float(v[j] << 16)));
+    m = fmaxf(m, fabsf(__uint_as_float(v[j] & 0xffff0000u)));
+  }
+  return m;
+}
+
+__device__ __forceinline__ float block_max256(float m, float *red) {
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// partial[b] = max |x| over chunks [b * kAmaxSpanChunks, (b + 1) * kAmaxSpanChunks) (clipped to n8)
+__global__ __launch_bounds__(256) void absmax_partial_kernel(const uint16_t *__restrict__ x, int64_t n8,
+                                                             float *__restrict__ partial) {
+  __shared__ float red[4];
+  const int64_t c0 = (int64_t)blockIdx.x * kAmaxSpanChunks;
+  const int64_t c1 = c0 + kAmaxSpanChunks < n8 ? c0 + kAmaxSpanChunks : n8;
+  float m = 0.f;
+  for (int64_t c = c0 + threadIdx.x; c < c1; c += 256) m = absmax8(ld16(x + 8 * c), m);
+  m = block_max256(m, red);
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+// *total = max over partial[0 .. count)
+__global__ __launch_bounds__(256) void absmax_total_kernel(const float *__restrict__ partial, int count,
+                                                           float *__restrict__ total) {
+  __shared__ float red[4];
+  float m = 0.f;
+  for (int i = threadIdx.x; i < count; i += 256) m = fmaxf(m, partial[i]);
+  m = block_max256(m, red);
+  if (threadIdx.x == 0) *total = m;
+}
+
+// Device address of `scratch` on the device `stream` runs on (the current device for the null
+// stream), looked up once per device with that device current: each GPU holds its own copy of the
+// array. The array's name is a host-side handle only; every kernel argument uses this address.
+int scratch_address(hipStream_t stream, float **out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex lock;
+  static float *addr[kMaxDevices] = {};
+  int current = 0;
+  hipError_t err = hipGetDevice(&current);
+  if (err != hipSuccess) return set_error(VDNH3_ERR_RUNTIME, "no current HIP device: %s", hipGetErrorString(err));
+  hipDevice_t dev = current;
+  if (stream != nullptr && (err = hipStreamGetDevice(stream, &dev)) != hipSuccess)
+    return set_error(VDNH3_ERR_RUNTIME, "hipStreamGetDevice failed: %s", hipGetErrorString(err));
+  VDNH3_HOST_CHECK(dev >= 0 && dev < kMaxDevices, VDNH3_ERR_RUNTIME, "device %d is beyond the %d this library tracks",
+                   (int)dev, kMaxDevices);
+  std::lock_guard<std::mutex> guard(lock);
+  if (addr[dev] == nullptr) {
+    if (dev != current && (err = hipSetDevice(dev)) != hipSuccess)
+      return set_error(VDNH3_ERR_RUNTIME, "hipSetDevice(%d) failed: %s", (int)dev, hipGetErrorString(err));
+    void *p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != current) (void)hipSetDevice(current);
+    if (err != hipSuccess || p == nullptr)
+      return set_error(VDNH3_ERR_RUNTIME, "hipGetSymbolAddress(scratch) on device %d failed: %s", (int)dev,
+                       hipGetErrorString(err));
+    addr[dev] = static_cast<float *>(p);
+  }
+  *out = addr[dev];
+  return VDNH3_OK;
+}
+
 }  // namespace
 }  // namespace vdnh3
 
@@ -139,4 +222,31 @@ extern "C" int vdnh3_quant_tensor_f8(const uint16_t *x, int64_t n, uint8_t *q, f
   hipLaunchKernelGGL(absmax_kernel, dim3(blocks), dim3(256), 0, s, x, n8, amax_workspace);
   hipLaunchKernelGGL(cast_tensor_f8_kernel, dim3(blocks), dim3(256), 0, s, x, n8, amax_workspace, q, scale);
   return check_launch("quant_tensor_f8");
+}
+
+extern "C" size_t vdnh3_quant_tensor_f8_noalloc_max_elements(void) {
+  return (size_t)vdnh3::kAmaxSpan * (size_t)vdnh3::kAmaxPartials;
+}
+
+extern "C" int vdnh3_quant_tensor_f8_noalloc(const uint16_t *x, int64_t n, uint8_t *q, float *scale, void *stream) {
+  using namespace vdnh3;
+  VDNH3_HOST_CHECK(x && q && scale && n > 0, VDNH3_ERR_INVALID, "quant_tensor_f8_noalloc: empty or null operand");
+  VDNH3_HOST_CHECK(n % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0,
+                   VDNH3_ERR_INVALID,
+                   "quant_tensor_f8_noalloc: n must be a multiple of 8, x 16-byte and q 8-byte aligned");
+  VDNH3_HOST_CHECK(n <= kAmaxSpan * kAmaxPartials, VDNH3_ERR_INVALID,
+                   "quant_tensor_f8_noalloc: %lld elements exceed the %lld its fixed scratch (%d partial maxima of "
+                   "%lld elements) supports; use vdnh3_quant_tensor_f8 with a workspace",
+                   (long long)n, (long long)(kAmaxSpan * kAmaxPartials), kAmaxPartials, (long long)kAmaxSpan);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float *buf = nullptr;
+  const int rc = scratch_address(s, &buf);
+  if (rc) return rc;
+  const int64_t n8 = n / 8;
+  const int partials = (int)((n8 + kAmaxSpanChunks - 1) / kAmaxSpanChunks);
+  const int blocks = (int)std::min<int64_t>((n8 + 255) / 256, 4096);
+  hipLaunchKernelGGL(absmax_partial_kernel, dim3(partials), dim3(256), 0, s, x, n8, buf);
+  hipLaunchKernelGGL(absmax_total_kernel, dim3(1), dim3(256), 0, s, buf, partials, buf + kAmaxPartials);
+  hipLaunchKernelGGL(cast_tensor_f8_kernel, dim3(blocks), dim3(256), 0, s, x, n8, buf + kAmaxPartials, q, scale);
+  return check_launch("quant_tensor_f8_noalloc");
 }

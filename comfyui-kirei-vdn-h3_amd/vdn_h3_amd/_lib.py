@@ -49,6 +49,8 @@ SIGNATURES = {
                             _vp, _c_int, _vp, _c_int, _c_float, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_quant_rows": (_c_int, [_c_int, _vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _vp]),
     "vdnh3_quant_tensor_f8": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _vp]),
+    "vdnh3_quant_tensor_f8_noalloc": (_c_int, [_vp, _c_i64, _vp, _vp, _vp]),
+    "vdnh3_quant_tensor_f8_noalloc_max_elements": (_c_size, []),
     "vdnh3_frame_stats": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_int, _vp, _c_i64, _c_int,
                                    _c_int, _c_int, _c_int, _vp, _vp, _vp]),
     "vdnh3_short_conv": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _c_int,

@@ -124,6 +124,24 @@ def quantize_tensor_fp8(x: torch.Tensor):
     return q, scale
 
 
+def quantize_tensor_fp8_into(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor):
+    """``quantize_tensor_fp8`` into caller-owned ``q`` (e4m3fn, ``x``'s shape) and ``scale`` (fp32, 1 value),
+    with nothing allocated on the device (``vdnh3_quant_tensor_f8_noalloc``): usable inside a HIP graph
+    capture. ``x`` must be contiguous bf16 with at most ``vdnh3_quant_tensor_f8_noalloc_max_elements()``
+    values. Calls that overlap on one GPU share the library's scratch and race."""
+    if x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError("quantize_tensor_fp8_into expects a contiguous bf16 tensor")
+    if q.dtype != torch.float8_e4m3fn or q.shape != x.shape or not q.is_contiguous():
+        raise ValueError("q must be a contiguous float8_e4m3fn tensor of x's shape")
+    if scale.dtype != torch.float32 or scale.numel() != 1:
+        raise ValueError("scale must be one fp32 value")
+    device = _lib.require_device(x, q, scale)
+    rc = _lib.lib().vdnh3_quant_tensor_f8_noalloc(_lib.ptr(x), x.numel(), _lib.ptr(q), _lib.ptr(scale),
+                                                  _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_quant_tensor_f8_noalloc")
+    return q, scale
+
+
 def gemm_w8a8(a_q, a_scale, b_q, b_scale, *, out_dtype=torch.bfloat16, bias=None, out=None, accumulate=False):
     """``(a_q b_q^T) * a_scale[m] * b_scale[n] (+ bias)`` for int8 or fp8 e4m3fn operands."""
     if a_q.dtype == torch.int8 and b_q.dtype == torch.int8:

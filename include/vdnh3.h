@@ -160,6 +160,18 @@ int vdnh3_quant_rows(int kind, const uint16_t *x, int64_t ldx, int M, int K, uin
 int vdnh3_quant_tensor_f8(const uint16_t *x, int64_t n, uint8_t *q, float *scale, float *amax_workspace,
                           void *stream);
 
+/*
+ * No counterpart in the reference: vdnh3_quant_tensor_f8 for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * codes and scale as vdnh3_quant_tensor_f8, with no workspace argument: the amax is reduced through
+ * a fixed 64 KiB device array inside the library (one per GPU, held until the process ends), one
+ * partial maximum per 16,384 elements, so n may not exceed
+ * vdnh3_quant_tensor_f8_noalloc_max_elements() (268,435,456); larger n returns VDNH3_ERR_INVALID.
+ * Allocates nothing and needs no clearing between calls; calls that overlap on one GPU race.
+ */
+int vdnh3_quant_tensor_f8_noalloc(const uint16_t *x, int64_t n, uint8_t *q, float *scale, void *stream);
+size_t vdnh3_quant_tensor_f8_noalloc_max_elements(void);
+
 /* ------------------------------------------------------------------------------
  * Video Delta Attention branch (reference vdn_h3/branch.py, vdn_h3/runtime.py)
  * All head_dim arguments must be 64 or 128. fp32 matrices are [n][D][D] row-major.

@@ -121,3 +121,18 @@ def test_segment_index_is_built_without_device_reads_and_range_checked():
         bk.rmsnorm_modulate(x, torch.ones(16), 1e-6, table, table, bad)
     with pytest.raises(ValueError, match="out of range"):
         bk.gated_residual(x, table, torch.tensor([0] * 11 + [-1]), x)
+
+
+def test_noalloc_fp8_quantisation_rejects_oversize_tensors_on_the_host(built_lib):
+    """vdnh3_quant_tensor_f8_noalloc's scratch holds 16,384 partial maxima of 16,384 elements: a larger
+    tensor is rejected with VDNH3_ERR_INVALID before any device access (as are null and unaligned operands)."""
+    import ctypes
+
+    limit = built_lib.vdnh3_quant_tensor_f8_noalloc_max_elements()
+    assert limit == 16384 * 16384
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.c_void_p((ctypes.addressof(buf) + 15) // 16 * 16)
+    assert built_lib.vdnh3_quant_tensor_f8_noalloc(p, limit + 8, p, p, None) == 1
+    assert b"exceed" in built_lib.vdnh3_last_error()
+    assert built_lib.vdnh3_quant_tensor_f8_noalloc(None, 8, p, p, None) == 1
+    assert built_lib.vdnh3_quant_tensor_f8_noalloc(p, 12, p, p, None) == 1
