@@ -14,6 +14,7 @@
 // wavefront covers 4 (8) head vectors of one row with fully coalesced 16-byte accesses, and the
 // sum of squares is reduced with lane shuffles inside the lane group.
 #include "common.h"
+#include "qk_norm.h"
 
 namespace vdnh3 {
 namespace {
@@ -71,12 +72,7 @@ __global__ __launch_bounds__(256) void qk_rmsnorm_kernel(const uint16_t *__restr
   float x[8], wf[8], y[8];
   unpack8(ld16(src + 8 * c), x);
   unpack8(ld16(w + 8 * c), wf);
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ss = fmaf(x[j], x[j], ss);
-#pragma unroll
-  for (int o = 1; o < LANES; o <<= 1) ss += __shfl_xor(ss, o);
-  const float r = 1.f / sqrtf(ss / (float)D + (which ? k_eps : q_eps));
+  const float r = rms_factor(group_tree_sum<LANES>(chunk_sumsq(x)), D, which ? k_eps : q_eps);
 #pragma unroll
   for (int j = 0; j < 8; ++j) y[j] = x[j] * r * wf[j];
   if constexpr (ROPE) {
@@ -99,12 +95,7 @@ __global__ __launch_bounds__(256) void qk_rmsnorm_kernel(const uint16_t *__restr
       // the eight 2x2 matrices of pairs i0 .. i0 + 7, 16 bytes each (f00 f01 f10 f11)
       const f32x4_t *f = tab_lds ? tab + i0 : reinterpret_cast<const f32x4_t *>(freqs + row * f_row + 4 * i0);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const f32x4_t m = f[j];
-        const float a = first ? m[0] : m[2], b = first ? m[1] : m[3];  // matrix row 0 or 1
-        // first half: out_i = f00 y_i + f01 y_{i+h}; second half: out_{i+h} = f10 y_i + f11 y_{i+h}
-        y[j] = first ? fmaf(a, y[j], b * o[j]) : fmaf(a, o[j], b * y[j]);
-      }
+      for (int j = 0; j < 8; ++j) y[j] = rope_rotate(y[j], o[j], f[j], first);
     }
   }
   st16(dst + 8 * c, pack8(y));

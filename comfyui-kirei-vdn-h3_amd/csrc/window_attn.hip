@@ -24,6 +24,7 @@
 //   XCD work on the same head and neighbouring query blocks, so their K/V tiles are
 //   shared in that XCD's L2.
 #include "common.h"
+#include "qk_norm.h"
 
 namespace vdnh3 {
 namespace {
@@ -76,6 +77,85 @@ __global__ __launch_bounds__(kThreads) void vt_prepass_kernel(const uint16_t *__
 }
 
 // ---------------------------------------------------------------------------------
+// Fused pre-pass of the normalising attention: the V^T copy of vt_prepass_kernel, and the block's
+// k_norm (RMSNorm over the head dim with k_weight / eps, optionally the split-half RoPE, one bf16
+// rounding: the arithmetic of qk_norm.h) written as a head-major copy kn[head][key][d], zero for
+// keys in [seq, s_pad). One workgroup per (64 keys, head); each key row is normalised by an aligned
+// group of D/8 lanes, one 8-channel chunk per lane.
+template <int D, bool ROPE>
+__global__ __launch_bounds__(kThreads) void kv_prepass_kernel(
+    const uint16_t *__restrict__ k, int64_t k_row, int64_t k_head, const uint16_t *__restrict__ v, int64_t v_row,
+    int64_t v_head, const uint16_t *__restrict__ k_weight, float eps, const float *__restrict__ freqs, int64_t f_row,
+    int rot, uint16_t *__restrict__ vt, uint16_t *__restrict__ kn, int seq, int s_pad) {
+  constexpr int P = D + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64 * P];
+  const int k0 = blockIdx.x * 64, head = blockIdx.y, tid = threadIdx.x;
+  constexpr int CH = D / 8;  // 16-byte chunks per key row
+  for (int c = tid; c < 64 * CH; c += kThreads) {
+    int r = c / CH, col = c % CH, key = k0 + r;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (key < seq) val = *reinterpret_cast<const uint4 *>(v + key * v_row + head * v_head + col * 8);
+    *reinterpret_cast<uint4 *>(&tile[r * P + col * 8]) = val;
+  }
+  // K rows: lane c of each D/8-lane group holds channels [8c, 8c + 8) of one key
+  const int c = tid % CH;
+  float wf[8];
+  {
+    const u32x4_t w = ld16(k_weight + 8 * c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wf[j] = __uint_as_float((j & 1) ? (w[j >> 1] & 0xffff0000u) : (w[j >> 1] << 16));
+  }
+  uint16_t *kdst = kn + ((int64_t)head * s_pad + k0) * D;
+  for (int r = tid / CH; r < 64; r += kThreads / CH) {
+    const int key = k0 + r;
+    float x[8], y[8];
+    const u32x4_t raw = key < seq ? ld16(k + key * k_row + head * k_head + 8 * c) : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = __uint_as_float((j & 1) ? (raw[j >> 1] & 0xffff0000u) : (raw[j >> 1] << 16));
+    const float rr = rms_factor(group_tree_sum<CH>(chunk_sumsq(x)), D, eps);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = x[j] * rr * wf[j];
+    if constexpr (ROPE) {
+      const int half = rot >> 1, step = half >> 3;
+      const bool first = 8 * c < half, rotated = 8 * c < rot;
+      const int lane = __lane_id();
+      const int partner = rotated ? (first ? lane + step : lane - step) : lane;
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = __shfl(y[j], partner);
+      if (rotated && key < seq) {
+        const f32x4_t *f = reinterpret_cast<const f32x4_t *>(freqs + key * f_row) + (first ? 8 * c : 8 * c - half);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = rope_rotate(y[j], o[j], f[j], first);
+      }
+    }
+    if (key >= seq) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = 0.f;
+    }
+    st16(kdst + r * D + 8 * c, u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]),
+                                       pack_bf2(y[6], y[7])});
+  }
+  __syncthreads();
+  uint16_t *dst = vt + (int64_t)head * D * s_pad + k0;
+  for (int cc = tid; cc < D * 8; cc += kThreads) {
+    int d = cc >> 3, pc = cc & 7;  // output positions 8*pc .. 8*pc+7 of row d
+    uint16_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int pp = 8 * pc + j;
+      e[j] = tile[((pp & ~15) + kperm(pp & 15)) * P + d];
+    }
+    uint4 o;
+    o.x = uint32_t(e[0]) | (uint32_t(e[1]) << 16);
+    o.y = uint32_t(e[2]) | (uint32_t(e[3]) << 16);
+    o.z = uint32_t(e[4]) | (uint32_t(e[5]) << 16);
+    o.w = uint32_t(e[6]) | (uint32_t(e[7]) << 16);
+    *reinterpret_cast<uint4 *>(dst + (int64_t)d * s_pad + 8 * pc) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // LDS slots of the staged tiles. Each tile row is split into 16-byte chunks; chunk c of row r
 // is stored at slot c ^ swizzle(r), so that the 16 lanes of one MFMA fragment read (16
 // consecutive rows, one chunk column) hit 16 different 16-byte bank groups.
@@ -106,12 +186,15 @@ __device__ __forceinline__ float other_half(float x) {
 // into four-slot rings, K tiles by group A three tiles ahead and V^T tiles by group B two tiles
 // ahead, each between the MFMAs of the issuing group's MFMA phase (the VALU group issues no
 // memory operations), which hides HBM latency for the tiles that miss L2.
-template <int D>
+// QN = 0: q is used as given; 1: q is normalised on load (the block's q_norm: q_weight, q_eps,
+// the arithmetic of qk_norm.h); 2: normalised and rotated (split-half RoPE with freqs).
+template <int D, int QN>
 __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
     const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const uint16_t *__restrict__ k, int64_t k_row,
     int64_t k_head, const uint16_t *__restrict__ vt, int s_pad, uint16_t *__restrict__ out, int64_t o_row,
     int64_t o_head, const uint16_t *__restrict__ gate, int64_t g_row, int seq, float scale_log2,
-    const int4 *__restrict__ items, int n_items, const int2 *__restrict__ tiles, int per_xcd, int total) {
+    const int4 *__restrict__ items, int n_items, const int2 *__restrict__ tiles, int per_xcd, int total,
+    const uint16_t *__restrict__ q_weight, float q_eps, const float *__restrict__ freqs, int64_t f_row, int rot) {
   constexpr int KC = D / 8;    // 16-byte chunks per K row
   constexpr int NS = D / 16;   // k-steps of the QK^T contraction
   constexpr int NO = D / 32;   // 32-row blocks of O^T
@@ -138,9 +221,59 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
 
   bf16x8_t qf[NS];
   {
+    // lane (l32, g) holds channels 16 s + 8 g + j (j < 8) of its query row: chunk 2 s + g
     const uint16_t *qp = q + (int64_t)qrc * q_row + (int64_t)head * q_head + 8 * g;
+    if constexpr (QN == 0) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qf[s] = as_bf16x8(ld16(qp + 16 * s));
+      for (int s = 0; s < NS; ++s) qf[s] = as_bf16x8(ld16(qp + 16 * s));
+    } else {
+      float y[NS][8], p[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const u32x4_t raw = ld16(qp + 16 * s);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          y[s][j] = __uint_as_float((j & 1) ? (raw[j >> 1] & 0xffff0000u) : (raw[j >> 1] << 16));
+        p[s] = chunk_sumsq(y[s]);
+      }
+      const float rr = rms_factor(halves_tree_sum<NS>(p), D, q_eps);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const u32x4_t w = ld16(q_weight + 16 * s + 8 * g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          y[s][j] = y[s][j] * rr * __uint_as_float((j & 1) ? (w[j >> 1] & 0xffff0000u) : (w[j >> 1] << 16));
+      }
+      if constexpr (QN == 2) {
+        // the rotation partner of channel d (d + h or d - h) may sit in the other half-wave: the
+        // normalised rows go through LDS once (the tile rings are not in use yet): group A's 128 rows
+        // in the K ring, group B's in the V^T ring (each ring holds 128 fp32 rows of D)
+        static_assert(4 * 32 * D * sizeof(float) <= sizeof(Ks) && sizeof(Ks) == sizeof(Vs), "stage fits a ring");
+        float *stage = reinterpret_cast<float *>(group == 0 ? &Ks[0][0] : &Vs[0][0]) + ((wave & 3) * 32 + l32) * D;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) stage[16 * s + 8 * g + j] = y[s][j];
+        __syncthreads();
+        const int half = rot >> 1;
+        const f32x4_t *f = reinterpret_cast<const f32x4_t *>(freqs + qrc * f_row);
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int d = 16 * s + 8 * g + j;
+            if (d < rot) {
+              const bool first = d < half;
+              y[s][j] = rope_rotate(y[s][j], stage[first ? d + half : d - half], f[first ? d : d - half], first);
+            }
+          }
+        __syncthreads();  // the prologue's tile loads reuse this LDS
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        qf[s] = as_bf16x8(u32x4_t{pack_bf2(y[s][0], y[s][1]), pack_bf2(y[s][2], y[s][3]), pack_bf2(y[s][4], y[s][5]),
+                                  pack_bf2(y[s][6], y[s][7])});
+    }
   }
 
   const uint16_t *kbase = k + (int64_t)head * k_head;
@@ -377,26 +510,54 @@ int launch_prepass(const uint16_t *v, int64_t v_row, int64_t v_head, int seq, in
   return check_launch("window vt_prepass");
 }
 
-template <int D>
+// QN: 0 = q as given, 1 = q normalised on load, 2 = normalised and rotated (see window_attn_kernel)
+template <int D, int QN>
 int launch_attn(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row, int64_t k_head,
                 uint16_t *out, int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row, int seq,
                 int heads, float scale, const int32_t *items, int32_t n_items, const int32_t *tiles,
-                const void *workspace, hipStream_t stream) {
+                const void *workspace, hipStream_t stream, const uint16_t *q_weight = nullptr, float q_eps = 0.f,
+                const float *freqs = nullptr, int64_t f_row = 0, int rot = 0) {
   const int s_pad = (seq + 63) / 64 * 64;
   const int total = n_items * heads;
   const int per_xcd = (total + 7) / 8;
-  hipLaunchKernelGGL(window_attn_kernel<D>, dim3(per_xcd * 8), dim3(kThreads), 0, stream, q, q_row, q_head, k,
+  hipLaunchKernelGGL((window_attn_kernel<D, QN>), dim3(per_xcd * 8), dim3(kThreads), 0, stream, q, q_row, q_head, k,
                      k_row, k_head, static_cast<const uint16_t *>(workspace), s_pad, out, o_row, o_head, gate,
                      gate_row, seq, scale * 1.4426950408889634f, reinterpret_cast<const int4 *>(items), n_items,
-                     reinterpret_cast<const int2 *>(tiles), per_xcd, total);
+                     reinterpret_cast<const int2 *>(tiles), per_xcd, total, q_weight, q_eps, freqs, f_row, rot);
   return check_launch("window_attn");
+}
+
+template <int D>
+int launch_kv_prepass(const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *v, int64_t v_row,
+                      int64_t v_head, const uint16_t *k_weight, float eps, const float *freqs, int64_t f_row, int rot,
+                      int seq, int heads, void *workspace, hipStream_t stream) {
+  const int s_pad = (seq + 63) / 64 * 64;
+  uint16_t *vt = static_cast<uint16_t *>(workspace);
+  uint16_t *kn = vt + (size_t)heads * D * s_pad;
+  if (freqs)
+    hipLaunchKernelGGL((kv_prepass_kernel<D, true>), dim3(s_pad / 64, heads), dim3(kThreads), 0, stream, k, k_row,
+                       k_head, v, v_row, v_head, k_weight, eps, freqs, f_row, rot, vt, kn, seq, s_pad);
+  else
+    hipLaunchKernelGGL((kv_prepass_kernel<D, false>), dim3(s_pad / 64, heads), dim3(kThreads), 0, stream, k, k_row,
+                       k_head, v, v_row, v_head, k_weight, eps, freqs, f_row, rot, vt, kn, seq, s_pad);
+  return check_launch("window kv_prepass");
+}
+
+int check_rope(const float *freqs, int64_t f_row, int rot, int head_dim) {
+  if (!freqs) return VDNH3_OK;
+  VDNH3_HOST_CHECK(rot > 0 && rot % 16 == 0 && rot <= head_dim, VDNH3_ERR_INVALID,
+                   "rope: rot_dim must be a positive multiple of 16 and at most head_dim %d, got %d", head_dim, rot);
+  VDNH3_HOST_CHECK(f_row >= 0 && f_row % 4 == 0 && reinterpret_cast<uintptr_t>(freqs) % 16 == 0, VDNH3_ERR_INVALID,
+                   "rope: frequencies must be 16-byte aligned with a row stride multiple of 4");
+  return VDNH3_OK;
 }
 
 int check_common(int seq, int heads, int head_dim, const void *workspace, size_t workspace_bytes) {
   VDNH3_HOST_CHECK(head_dim == 64 || head_dim == 128, VDNH3_ERR_INVALID,
                    "window attention supports head_dim 64 or 128, got %d", head_dim);
   VDNH3_HOST_CHECK(seq > 0 && heads > 0, VDNH3_ERR_INVALID, "seq and heads must be positive");
-  VDNH3_HOST_CHECK(workspace != nullptr, VDNH3_ERR_INVALID, "null workspace");
+  VDNH3_HOST_CHECK(workspace != nullptr && reinterpret_cast<uintptr_t>(workspace) % 16 == 0, VDNH3_ERR_INVALID,
+                   "workspace must be non-null and 16-byte aligned");
   VDNH3_HOST_CHECK(workspace_bytes >= vdnh3_window_workspace_bytes(seq, heads, head_dim), VDNH3_ERR_INVALID,
                    "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
                    vdnh3_window_workspace_bytes(seq, heads, head_dim));
@@ -446,10 +607,10 @@ extern "C" int vdnh3_window_attn_prepared(const uint16_t *q, int64_t q_row, int6
   VDNH3_HOST_CHECK(items != nullptr && tiles != nullptr && n_items > 0, VDNH3_ERR_INVALID, "empty window plan");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (head_dim == 128)
-    return vdnh3::launch_attn<128>(q, q_row, q_head, k, k_row, k_head, out, o_row, o_head, gate, gate_row, seq, heads,
+    return vdnh3::launch_attn<128, 0>(q, q_row, q_head, k, k_row, k_head, out, o_row, o_head, gate, gate_row, seq,
+                                      heads, scale, items, n_items, tiles, workspace, s);
+  return vdnh3::launch_attn<64, 0>(q, q_row, q_head, k, k_row, k_head, out, o_row, o_head, gate, gate_row, seq, heads,
                                    scale, items, n_items, tiles, workspace, s);
-  return vdnh3::launch_attn<64>(q, q_row, q_head, k, k_row, k_head, out, o_row, o_head, gate, gate_row, seq, heads,
-                                scale, items, n_items, tiles, workspace, s);
 }
 
 extern "C" int vdnh3_window_attn_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k,
@@ -462,4 +623,63 @@ extern "C" int vdnh3_window_attn_fwd(const uint16_t *q, int64_t q_row, int64_t q
   if (rc) return rc;
   return vdnh3_window_attn_prepared(q, q_row, q_head, k, k_row, k_head, out, o_row, o_head, gate, gate_row, seq,
                                     heads, head_dim, scale, items, n_items, tiles, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t vdnh3_window_norm_workspace_bytes(int seq, int heads, int head_dim) {
+  return 2 * vdnh3_window_workspace_bytes(seq, heads, head_dim);
+}
+
+extern "C" int vdnh3_window_kv_prepass(const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *v,
+                                       int64_t v_row, int64_t v_head, const uint16_t *k_weight, float k_eps,
+                                       const float *freqs, int64_t freqs_row, int rot_dim, int seq, int heads,
+                                       int head_dim, void *workspace, size_t workspace_bytes, void *stream) {
+  int rc = vdnh3::check_common(seq, heads, head_dim, workspace, workspace_bytes);
+  if (!rc) rc = vdnh3::check_vec(k, k_row, k_head, "k");
+  if (!rc) rc = vdnh3::check_vec(v, v_row, v_head, "v");
+  if (!rc) rc = vdnh3::check_vec(k_weight, 0, 0, "k_weight");
+  if (!rc) rc = vdnh3::check_rope(freqs, freqs_row, rot_dim, head_dim);
+  if (rc) return rc;
+  VDNH3_HOST_CHECK(workspace_bytes >= vdnh3_window_norm_workspace_bytes(seq, heads, head_dim), VDNH3_ERR_INVALID,
+                   "workspace of %zu bytes is smaller than the %zu the normalising attention needs", workspace_bytes,
+                   vdnh3_window_norm_workspace_bytes(seq, heads, head_dim));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return head_dim == 128 ? vdnh3::launch_kv_prepass<128>(k, k_row, k_head, v, v_row, v_head, k_weight, k_eps, freqs,
+                                                         freqs_row, rot_dim, seq, heads, workspace, s)
+                         : vdnh3::launch_kv_prepass<64>(k, k_row, k_head, v, v_row, v_head, k_weight, k_eps, freqs,
+                                                        freqs_row, rot_dim, seq, heads, workspace, s);
+}
+
+extern "C" int vdnh3_window_attn_qnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *q_weight,
+                                       float q_eps, const float *freqs, int64_t freqs_row, int rot_dim, uint16_t *out,
+                                       int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row, int seq,
+                                       int heads, int head_dim, float scale, const int32_t *items, int32_t n_items,
+                                       const int32_t *tiles, const void *workspace, size_t workspace_bytes,
+                                       void *stream) {
+  int rc = vdnh3::check_common(seq, heads, head_dim, workspace, workspace_bytes);
+  if (!rc) rc = vdnh3::check_vec(q, q_row, q_head, "q");
+  if (!rc) rc = vdnh3::check_vec(q_weight, 0, 0, "q_weight");
+  if (!rc) rc = vdnh3::check_rope(freqs, freqs_row, rot_dim, head_dim);
+  if (rc) return rc;
+  VDNH3_HOST_CHECK(workspace_bytes >= vdnh3_window_norm_workspace_bytes(seq, heads, head_dim), VDNH3_ERR_INVALID,
+                   "workspace of %zu bytes is smaller than the %zu the normalising attention needs", workspace_bytes,
+                   vdnh3_window_norm_workspace_bytes(seq, heads, head_dim));
+  VDNH3_HOST_CHECK(out != nullptr && o_row % 4 == 0 && o_head % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0,
+                   VDNH3_ERR_INVALID, "out must be 8-byte aligned with strides that are multiples of 4 elements");
+  VDNH3_HOST_CHECK(items != nullptr && tiles != nullptr && n_items > 0, VDNH3_ERR_INVALID, "empty window plan");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int s_pad = (seq + 63) / 64 * 64;
+  // the normalised keys follow the V^T copy in the workspace: [heads][s_pad][head_dim]
+  const uint16_t *kn = static_cast<const uint16_t *>(workspace) + (size_t)heads * head_dim * s_pad;
+  const int64_t kn_row = head_dim, kn_head = (int64_t)s_pad * head_dim;
+#define VDNH3_QNORM(D, QN)                                                                                          \
+  return vdnh3::launch_attn<D, QN>(q, q_row, q_head, kn, kn_row, kn_head, out, o_row, o_head, gate, gate_row, seq, \
+                                   heads, scale, items, n_items, tiles, workspace, s, q_weight, q_eps, freqs,      \
+                                   freqs_row, rot_dim)
+  if (head_dim == 128) {
+    if (freqs) VDNH3_QNORM(128, 2);
+    VDNH3_QNORM(128, 1);
+  }
+  if (freqs) VDNH3_QNORM(64, 2);
+  VDNH3_QNORM(64, 1);
+#undef VDNH3_QNORM
 }

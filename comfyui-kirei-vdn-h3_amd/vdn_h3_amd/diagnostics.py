@@ -4,8 +4,9 @@ Mirrors the role of ``DiagnosticsRecorder`` (``vdn_h3/diagnostics.py:26-174``): 
 recorder costs nothing; an enabled one records a start / end event pair on the current
 stream around each named scope and resolves all pending pairs with one device
 synchronisation in ``flush`` / ``snapshot``. Stage names follow the reference
-(``attention.qkv``, ``attention.rope_norm``, ``attention.softmax``, ``attention.out_proj``,
-``attention.linear_branch``).
+(``attention.qkv``, ``attention.softmax``, ``attention.out_proj``, ``attention.linear_branch``;
+the reference's ``attention.rope_norm`` runs inside ``attention.softmax`` here, whose
+``attention.softmax.kv_prepass`` / ``.kernel`` sub-stages time its two kernels).
 """
 
 from __future__ import annotations

@@ -7,9 +7,11 @@ layout contract (the request-local ``VDNLayout``; without one the original forwa
 and the same exception types. Per call, on the caller's current stream:
 
   qkv = attn.qkv_proj(x)                         raw q / k / v views [S, H, D]
-  q, k = q_norm(q_raw), k_norm(k_raw) [+ RoPE]   one HIP pass into a separate buffer
   g = sigmoid(x W_g^T + b_g)                     [S, H], GEMM with a sigmoid epilogue
-  flat = bf16(window_attention(q, k, v) * g)     one HIP kernel, the gate in its epilogue
+  k' = k_norm(k_raw) [+ RoPE], V^T copy          one HIP pre-pass into the attention workspace
+  flat = bf16(window_attention(q_norm(q_raw) [+ RoPE], k', v) * g)
+                                                 one HIP kernel: q normalised on load, the gate
+                                                 in its epilogue
   out = attn.out_proj(flat)
   out[video] += to_out_linear(branch(x, q_raw, k_raw, v))   GEMM epilogue accumulates into out
 
@@ -18,7 +20,8 @@ the sum is the same bf16 addition, ``bf16(out + bf16(delta))``. A full-cover lay
 dense attention and no branch (``:422``, ``:495-499``). The path is inference-only
 (``torch.no_grad`` / ``inference_mode``). With ``rope_freqs`` the q/k pass also applies the
 split-half rotary embedding (``vdn_h3/hybrid.py:274-292``; ``rope_table`` gives the layout),
-with the q_norm epsilon for both, as the reference does.
+with the q_norm epsilon for both, as the reference does. ``normalise_qk`` is the same q/k pass as a
+standalone op (the fused path gives the same bits).
 """
 
 from __future__ import annotations
@@ -37,6 +40,7 @@ from . import window as _window
 from .branch import cholesky_runtime_scope
 from .diagnostics import DiagnosticsRecorder
 from .layout import current_layout, publish_layout
+from .window import rope_table
 
 _LOG = logging.getLogger("vdn_h3_amd")
 _STATE_PATCH = "diffusion_model._vdn_h3_state"
@@ -141,26 +145,6 @@ class VDNState:
         return self
 
     close = release
-
-
-def rope_table(rope_freqs: torch.Tensor, seq: int, head_dim: int, device) -> tuple[torch.Tensor, int, int]:
-    """``(table, row_stride, rot_dim)`` of ``rope_freqs`` for ``vdnh3_qk_rmsnorm_rope``.
-
-    ``rope_freqs`` holds one 2x2 matrix per (row, pair): shape ``[..., rot_dim/2, 2, 2]`` whose
-    leading dims hold one entry per row (``seq`` in total, e.g. ``[1, seq, 1, ...]``) or one entry
-    shared by every row; ``rot_dim = 2 * rope_freqs.shape[-3]`` (``vdn_h3/hybrid.py:283``).
-    """
-    if rope_freqs.ndim < 3 or tuple(rope_freqs.shape[-2:]) != (2, 2):
-        raise ValueError(f"rope_freqs must end in [rot_dim/2, 2, 2], got {tuple(rope_freqs.shape)}")
-    half = int(rope_freqs.shape[-3])
-    rot = 2 * half
-    if rot % 16 or rot > head_dim:
-        raise ValueError(f"rope rot_dim {rot} must be a multiple of 16 and at most head_dim {head_dim}")
-    rows = rope_freqs.numel() // (4 * half)
-    if rows not in (1, seq):
-        raise ValueError(f"rope_freqs holds {rows} row entries; expected 1 or {seq}")
-    table = rope_freqs.reshape(rows, half, 2, 2).to(device=device, dtype=torch.float32).contiguous()
-    return table, (0 if rows == 1 else 4 * half), rot
 
 
 def normalise_qk(q_raw: torch.Tensor, k_raw: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
@@ -285,19 +269,19 @@ class _VDNBlockForward:
         with scope("attention.qkv", device):
             q_raw, k_raw, value = _split_qkv(attn.qkv_proj(x), heads, head_dim)
         (qw, q_eps), (kw, k_eps) = (_norm_weight_eps(m, head_dim, device) for m in (attn.q_norm, attn.k_norm))
-        with scope("attention.rope_norm", device):
-            # split-half RoPE takes q_norm's epsilon for both (vdn_h3/hybrid.py:284-291)
-            query, key = normalise_qk(q_raw, k_raw, qw, kw, q_eps, rope_freqs=rope_freqs,
-                                      k_eps=q_eps if rope_freqs is not None else k_eps)
+        if rope_freqs is not None:
+            k_eps = q_eps  # split-half RoPE takes q_norm's epsilon for both (vdn_h3/hybrid.py:284-291)
         with scope("attention.gate", device):
             gate, proj_rows = self._gate(x, weights, with_branch)
         plan = self._plan(layout, device)
         with scope("attention.softmax", device):
-            attended = _window.window_softmax_hip(
-                query, key, value, layout.video_start, layout.video_end, layout.num_frames,
-                layout.tokens_per_frame, layout.bounds, head_dim ** -0.5, layout.anchor_frames, gate=gate, plan=plan,
+            # q_norm / k_norm (+ RoPE) run inside the attention: the keys in its pre-pass, each query
+            # row as the kernel loads it; the branch reads the raw q / k
+            attended = _window.window_softmax_normed(
+                q_raw, k_raw, value, qw, kw, q_eps, k_eps, layout.video_start, layout.video_end,
+                layout.num_frames, layout.tokens_per_frame, layout.bounds, head_dim ** -0.5, layout.anchor_frames,
+                rope_freqs=rope_freqs, gate=gate, plan=plan,
                 diagnostics=state.diagnostics if state.diagnostics.enabled else None)
-        del query, key
         with scope("attention.out_proj", device):
             out = attn.out_proj(attended.view(layout.seq_len, heads * head_dim))
         del attended

@@ -9,6 +9,8 @@ Mirrors the public surface of ``vdn_h3/window.py``:
   meaning and ``ValueError`` behaviour of ``window_softmax_grouped`` / ``_flex`` /
   ``_flash2`` / ``_decomposed`` (``:277-313``, ``:694-723``, ``:839-861``); those four names
   are kept as aliases of the one exact HIP kernel;
+* ``window_softmax_normed``: the same op taking the raw q / k with the block's q_norm / k_norm
+  (and RoPE) fused in (``vdn_h3/hybrid.py:271-302``);
 * ``WindowAttentionCache`` (``:77-138``) holds the per-model tile plans;
 * ``resolve_attention_backend`` (``:581-673``) resolves every request to ``"hip"``.
 
@@ -19,6 +21,7 @@ from __future__ import annotations
 
 import ctypes
 from collections import OrderedDict
+from contextlib import nullcontext
 from dataclasses import dataclass
 from typing import Any
 
@@ -161,31 +164,32 @@ def _kernel_operand(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
-def window_softmax_hip(query, key, value, video_start, video_end, num_frames, tokens_per_frame, bounds, scale,
-                       anchor_frames="none", cache: WindowAttentionCache | None = None, *, gate=None,
-                       out: torch.Tensor | None = None, plan: WindowPlan | None = None, diagnostics=None):
-    """Exact window softmax attention on the GPU; returns a new ``[S, H, D]`` bf16 tensor.
+def rope_table(rope_freqs: torch.Tensor, seq: int, head_dim: int, device) -> tuple[torch.Tensor, int, int]:
+    """``(table, row_stride, rot_dim)`` of ``rope_freqs`` for the kernels' split-half RoPE.
 
-    ``gate`` (optional, ``[S, H]`` or ``[S, H, 1]``) fuses the per-head softmax gate into the
-    epilogue: the result is then ``bf16(bf16(O) * gate)``. Inputs are not modified.
-    ``diagnostics`` (a ``DiagnosticsRecorder``) times the V^T pre-pass and the attention kernel
-    as the stages ``attention.softmax.vt_prepass`` / ``attention.softmax.kernel``.
+    ``rope_freqs`` holds one 2x2 matrix per (row, pair): shape ``[..., rot_dim/2, 2, 2]`` whose
+    leading dims hold one entry per row (``seq`` in total, e.g. ``[1, seq, 1, ...]``) or one entry
+    shared by every row; ``rot_dim = 2 * rope_freqs.shape[-3]`` (``vdn_h3/hybrid.py:283``).
     """
-    if query.ndim != 3 or query.shape != key.shape or query.shape != value.shape:
-        raise ValueError("query, key and value must share shape [sequence, heads, dim]")
-    device = _lib.require_device(query, key, value, gate, out)
-    if query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
-        raise TypeError("window_softmax_hip computes in bf16; got "
-                        f"{query.dtype}/{key.dtype}/{value.dtype}")
-    seq, heads, dim = query.shape
+    if rope_freqs.ndim < 3 or tuple(rope_freqs.shape[-2:]) != (2, 2):
+        raise ValueError(f"rope_freqs must end in [rot_dim/2, 2, 2], got {tuple(rope_freqs.shape)}")
+    half = int(rope_freqs.shape[-3])
+    rot = 2 * half
+    if rot % 16 or rot > head_dim:
+        raise ValueError(f"rope rot_dim {rot} must be a multiple of 16 and at most head_dim {head_dim}")
+    rows = rope_freqs.numel() // (4 * half)
+    if rows not in (1, seq):
+        raise ValueError(f"rope_freqs holds {rows} row entries; expected 1 or {seq}")
+    table = rope_freqs.reshape(rows, half, 2, 2).to(device=device, dtype=torch.float32).contiguous()
+    return table, (0 if rows == 1 else 4 * half), rot
+
+
+def _attention_operands(shape, device, plan, cache, geometry, gate, out):
+    """``(plan, gate, gate_row, out)`` for one call: the tile plan (cached or built), the gate as a
+    bf16 ``[S, H]`` view with unit head stride, and the output buffer (new or checked)."""
+    seq, heads, dim = shape
     if plan is None:
-        if cache is not None:
-            plan = cache.plan(seq, video_start, video_end, num_frames, tokens_per_frame, bounds, anchor_frames,
-                              device)
-        else:
-            plan = make_plan(seq, video_start, video_end, num_frames, tokens_per_frame, bounds, anchor_frames,
-                             device)
-    q, k, v = _kernel_operand(query), _kernel_operand(key), _kernel_operand(value)
+        plan = (cache.plan(*geometry, device) if cache is not None else make_plan(*geometry, device))
     if out is None:
         out = torch.empty((seq, heads, dim), dtype=torch.bfloat16, device=device)
     elif out.shape != (seq, heads, dim) or out.dtype != torch.bfloat16 or out.stride(2) != 1:
@@ -198,6 +202,32 @@ def window_softmax_hip(query, key, value, video_start, video_end, num_frames, to
         if gate.stride(1) != 1:
             gate = gate.contiguous()
         g_row = gate.stride(0)
+    return plan, gate, g_row, out
+
+
+def _check_qkv(query, key, value, name):
+    if query.ndim != 3 or query.shape != key.shape or query.shape != value.shape:
+        raise ValueError("query, key and value must share shape [sequence, heads, dim]")
+    if query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
+        raise TypeError(f"{name} computes in bf16; got {query.dtype}/{key.dtype}/{value.dtype}")
+
+
+def window_softmax_hip(query, key, value, video_start, video_end, num_frames, tokens_per_frame, bounds, scale,
+                       anchor_frames="none", cache: WindowAttentionCache | None = None, *, gate=None,
+                       out: torch.Tensor | None = None, plan: WindowPlan | None = None, diagnostics=None):
+    """Exact window softmax attention on the GPU; returns a new ``[S, H, D]`` bf16 tensor.
+
+    ``gate`` (optional, ``[S, H]`` or ``[S, H, 1]``) fuses the per-head softmax gate into the
+    epilogue: the result is then ``bf16(bf16(O) * gate)``. Inputs are not modified.
+    ``diagnostics`` (a ``DiagnosticsRecorder``) times the V^T pre-pass and the attention kernel
+    as the stages ``attention.softmax.vt_prepass`` / ``attention.softmax.kernel``.
+    """
+    _check_qkv(query, key, value, "window_softmax_hip")
+    device = _lib.require_device(query, key, value, gate, out)
+    seq, heads, dim = query.shape
+    geometry = (seq, video_start, video_end, num_frames, tokens_per_frame, bounds, anchor_frames)
+    plan, gate, g_row, out = _attention_operands(query.shape, device, plan, cache, geometry, gate, out)
+    q, k, v = _kernel_operand(query), _kernel_operand(key), _kernel_operand(value)
     lib = _lib.lib()
     ws_bytes = lib.vdnh3_window_workspace_bytes(seq, heads, dim)
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
@@ -221,6 +251,52 @@ def window_softmax_hip(query, key, value, video_start, video_end, num_frames, to
             _lib.ptr(plan.items), plan.n_items, _lib.ptr(plan.tiles), _lib.ptr(workspace), ws_bytes, sh)
     _lib.check(rc, "window_softmax_hip")
     return out
+
+
+def window_softmax_normed(q_raw, k_raw, value, q_weight, k_weight, q_eps, k_eps, video_start, video_end,
+                          num_frames, tokens_per_frame, bounds, scale, anchor_frames="none",
+                          cache: WindowAttentionCache | None = None, *, rope_freqs=None, gate=None,
+                          out: torch.Tensor | None = None, plan: WindowPlan | None = None, diagnostics=None):
+    """``window_softmax_hip(q_norm(q_raw), k_norm(k_raw), value)`` with the block's q/k RMSNorm (and,
+    with ``rope_freqs``, the split-half RoPE) fused into the attention (``vdn_h3/hybrid.py:271-302``).
+
+    The keys are normalised once by the pre-pass that also writes the V^T copy; each query row is
+    normalised as the attention kernel loads it. The result has the same bits as the separate q/k
+    pass followed by ``window_softmax_hip``. ``q_eps`` / ``k_eps`` are the two norms' epsilons (with
+    RoPE the reference takes ``q_eps`` for both: pass it as ``k_eps``). ``diagnostics`` times the
+    stages ``attention.softmax.kv_prepass`` / ``attention.softmax.kernel``.
+    """
+    _check_qkv(q_raw, k_raw, value, "window_softmax_normed")
+    device = _lib.require_device(q_raw, k_raw, value, q_weight, k_weight, gate, out)
+    seq, heads, dim = q_raw.shape
+    wq = q_weight.to(torch.bfloat16).contiguous()
+    wk = k_weight.to(torch.bfloat16).contiguous()
+    if wq.numel() != dim or wk.numel() != dim:
+        raise ValueError(f"q/k norm weights must have {dim} entries")
+    table, f_row, rot = (None, 0, 0) if rope_freqs is None else rope_table(rope_freqs, seq, dim, device)
+    geometry = (seq, video_start, video_end, num_frames, tokens_per_frame, bounds, anchor_frames)
+    plan, gate, g_row, out = _attention_operands(q_raw.shape, device, plan, cache, geometry, gate, out)
+    q, k, v = _kernel_operand(q_raw), _kernel_operand(k_raw), _kernel_operand(value)
+    lib = _lib.lib()
+    ws_bytes = lib.vdnh3_window_norm_workspace_bytes(seq, heads, dim)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    sh = _lib.stream_handle(device)
+    with _maybe_scope(diagnostics, "attention.softmax.kv_prepass", device):
+        rc = lib.vdnh3_window_kv_prepass(
+            _lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(v), v.stride(0), v.stride(1), _lib.ptr(wk), float(k_eps),
+            _lib.ptr(table), f_row, rot, seq, heads, dim, _lib.ptr(workspace), ws_bytes, sh)
+    _lib.check(rc, "window_softmax_normed")
+    with _maybe_scope(diagnostics, "attention.softmax.kernel", device):
+        rc = lib.vdnh3_window_attn_qnorm(
+            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(wq), float(q_eps), _lib.ptr(table), f_row, rot,
+            _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(gate), g_row, seq, heads, dim, float(scale),
+            _lib.ptr(plan.items), plan.n_items, _lib.ptr(plan.tiles), _lib.ptr(workspace), ws_bytes, sh)
+    _lib.check(rc, "window_softmax_normed")
+    return out
+
+
+def _maybe_scope(diagnostics, name, device):
+    return nullcontext() if diagnostics is None else diagnostics.scope(name, device)
 
 
 # The reference's exact backends all resolve to the one HIP kernel on MI355X.
