@@ -8,9 +8,11 @@ seeded data, random-init weights.
 
 Workload ``block`` (default): one hybrid attention block, the patched ``attn.forward``, at the
 full shape: 512 text rows + 31 frames x 1296 tokens = 40 688 rows, hidden 5120, 40 heads x
-128, chunk 5, radius 1, anchors both. A step is one block forward: W8A8 int8 qkv projection,
-q/k RMSNorm, softmax gate, window attention (gate fused), W8A8 out projection, and the VDN
-branch (29 inner frames) with its int8 to_out_linear accumulated into the output.
+128, chunk 5, radius 1, anchors both, a per-row split-half RoPE table (``--rope off`` drops it).
+A step is one block forward: W8A8 int8 qkv projection, softmax gate, window attention (q/k
+RMSNorm + RoPE fused into its pre-pass and query load, the gate into its epilogue), W8A8 out
+projection, and the VDN branch (29 inner frames) with its int8 to_out_linear accumulated into
+the output.
 ``value`` is the block's algorithmic work per second (int8 OPs + bf16/fp32 FLOPs, listed per
 stage in ``config.work_per_step``); ``roofline`` is the window attention kernel (the dominant
 kernel), timed with HIP events on the stream it runs on; ``stages_ms`` are per-stage event
@@ -60,6 +62,9 @@ def _parse():
     ap.add_argument("--short-conv", default="k,v",
                     help="branch short-convolution targets of the block / branch workloads (the released "
                          "checkpoints convolve k and v); '' for none")
+    ap.add_argument("--rope", default="on", choices=["on", "off"],
+                    help="block / stack workloads: hand every block a per-row split-half RoPE table "
+                         "(rot_dim = head_dim), as a DiT does, or no rope_freqs")
     ap.add_argument("--cpu-sample-rows", type=int, default=2304,
                     help="query rows of the CPU-oracle baseline sample (0 disables it)")
     ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "traffic.json"),
@@ -131,7 +136,7 @@ def bench_window(args, torch, device):
                    "tokens_per_frame": lay.tokens_per_frame, "text_rows": lay.text_len, "chunk": w.chunk,
                    "radius": w.radius, "anchor_frames": lay.anchor_frames,
                    "allowed_pairs_per_head": plan.pairs_per_head, "flop_per_step": flops},
-        "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128>", "achieved": round(attn_tflops, 2),
+        "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128,%d>" % (2 if freqs is not None else 1), "achieved": round(attn_tflops, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
                      "kernel_ms": round(attn_ms, 4), "traffic": _traffic(args.traffic_json, "window_attn_kernel")},
         "breakdown_ms": {"vt_prepass": round(ms_step - attn_ms, 4), "window_attn": round(attn_ms, 4)},
@@ -182,6 +187,11 @@ def _short_conv(args):
     return tuple(t for t in args.short_conv.split(",") if t)
 
 
+def _rope_desc(args, dim):
+    return (f"split-half RoPE, rot_dim {dim}, per-row table (fused into the attention's q/k RMSNorm)"
+            if args.rope == "on" else "none")
+
+
 def block_flops(lay, heads, dim, hidden, pairs_per_head, short_conv=()):
     """Algorithmic work of one hybrid block (int8 OPs of the W8A8 GEMMs + bf16/fp32 FLOPs), by stage."""
     s, inner = lay.seq_len, heads * dim
@@ -213,16 +223,17 @@ def bench_block(args, torch, device):
     conv = _short_conv(args)
     state, (forward,) = synth.hybrid_stack(1, heads, dim, hidden, device, short_conv=conv, precision="int8")
     state.diagnostics.enabled = True
+    freqs = synth.rope_freqs(lay.seq_len, dim, device) if args.rope == "on" else None
     stream = torch.cuda.current_stream(device)
     with torch.no_grad(), forward_scope(lay):
         for _ in range(args.warmup):
-            forward(x)
+            forward(x, rope_freqs=freqs)
         torch.cuda.synchronize()
         state.diagnostics.clear()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0.record(stream)
         for _ in range(args.steps):
-            forward(x)
+            forward(x, rope_freqs=freqs)
         t1.record(stream)
         torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
@@ -246,10 +257,11 @@ def bench_block(args, torch, device):
                    "tokens_per_frame": lay.tokens_per_frame, "text_rows": lay.text_len, "chunk": w.chunk,
                    "radius": w.radius, "anchor_frames": lay.anchor_frames,
                    "projections": "W8A8 int8 qkv/out/to_out_linear (per-token x per-channel)",
+                   "rope": _rope_desc(args, dim),
                    "branch_short_conv": ",".join(conv) or "none",
                    "allowed_pairs_per_head": plan.pairs_per_head, "work_per_step": work,
                    "work_total": total},
-        "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128>", "achieved": round(attn_tflops, 2),
+        "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128,%d>" % (2 if freqs is not None else 1), "achieved": round(attn_tflops, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
                      "kernel_ms": round(attn_ms, 4), "traffic": _traffic(args.traffic_json, "window_attn_kernel")},
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
@@ -276,15 +288,16 @@ def bench_stack(args, torch, device):
     conv = _short_conv(args)
     state, forwards = synth.hybrid_stack(blocks, heads, dim, hidden, device, short_conv=conv, precision="int8")
     x0 = synth.randn((lay.seq_len, hidden), 0, device=device, dtype=torch.bfloat16)
+    freqs = synth.rope_freqs(lay.seq_len, dim, device) if args.rope == "on" else None
     stream = torch.cuda.current_stream(device)
     with torch.no_grad(), forward_scope(lay):
-        synth.denoise_pass(forwards, x0.clone(), args.warmup)
+        synth.denoise_pass(forwards, x0.clone(), args.warmup, rope_freqs=freqs)
         torch.cuda.synchronize()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
         x = x0.clone()
         ev[0].record(stream)
         for i in range(args.steps):
-            x = synth.denoise_pass(forwards, x, 1)
+            x = synth.denoise_pass(forwards, x, 1, rope_freqs=freqs)
             ev[i + 1].record(stream)
         torch.cuda.synchronize()
     step_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
@@ -303,7 +316,7 @@ def bench_stack(args, torch, device):
         "dtype": "int8+bf16",
         "config": {"workload": "stack_50blocks_s40688_h40_d128_hidden5120_int8proj", "blocks": blocks,
                    "denoising_steps": args.steps, "seq_len": lay.seq_len, "heads": heads, "head_dim": dim,
-                   "hidden": hidden, "branch_short_conv": ",".join(conv) or "none",
+                   "hidden": hidden, "branch_short_conv": ",".join(conv) or "none", "rope": _rope_desc(args, dim),
                    "residual": "x <- x + block(rms_norm(x)) per block (bf16, torch rms_norm)", "work_per_block": per_block},
         "total_ms": round(total_ms, 2),
         "step_ms": [round(v, 3) for v in step_ms],

@@ -42,7 +42,7 @@ __host__ __device__ constexpr int kperm(int p) { return 8 * ((p & 7) >> 2) + 4 *
 // ---------------------------------------------------------------------------------
 // Pre-pass: V [seq, heads, D] (strided view) -> vt[head][d][s_pad], keys in kperm order
 // inside each 16-key group, zero beyond seq.
-// grid (s_pad / 64, heads), 256 threads.
+// grid (s_pad / 64, heads), kThreads threads.
 template <int D>
 __global__ __launch_bounds__(kThreads) void vt_prepass_kernel(const uint16_t *__restrict__ v, int64_t v_row,
                                                               int64_t v_head, uint16_t *__restrict__ vt,
@@ -77,81 +77,137 @@ __global__ __launch_bounds__(kThreads) void vt_prepass_kernel(const uint16_t *__
 }
 
 // ---------------------------------------------------------------------------------
-// Fused pre-pass of the normalising attention: the V^T copy of vt_prepass_kernel, and the block's
-// k_norm (RMSNorm over the head dim with k_weight / eps, optionally the split-half RoPE, one bf16
-// rounding: the arithmetic of qk_norm.h) written as a head-major copy kn[head][key][d], zero for
-// keys in [seq, s_pad). One workgroup per (64 keys, head); each key row is normalised by an aligned
-// group of D/8 lanes, one 8-channel chunk per lane.
-template <int D, bool ROPE>
-__global__ __launch_bounds__(kThreads) void kv_prepass_kernel(
-    const uint16_t *__restrict__ k, int64_t k_row, int64_t k_head, const uint16_t *__restrict__ v, int64_t v_row,
-    int64_t v_head, const uint16_t *__restrict__ k_weight, float eps, const float *__restrict__ freqs, int64_t f_row,
-    int rot, uint16_t *__restrict__ vt, uint16_t *__restrict__ kn, int seq, int s_pad) {
-  constexpr int P = D + 8;
-  __shared__ __attribute__((aligned(16))) uint16_t tile[64 * P];
-  const int k0 = blockIdx.x * 64, head = blockIdx.y, tid = threadIdx.x;
-  constexpr int CH = D / 8;  // 16-byte chunks per key row
-  for (int c = tid; c < 64 * CH; c += kThreads) {
-    int r = c / CH, col = c % CH, key = k0 + r;
-    uint4 val = make_uint4(0, 0, 0, 0);
-    if (key < seq) val = *reinterpret_cast<const uint4 *>(v + key * v_row + head * v_head + col * 8);
-    *reinterpret_cast<uint4 *>(&tile[r * P + col * 8]) = val;
-  }
-  // K rows: lane c of each D/8-lane group holds channels [8c, 8c + 8) of one key
-  const int c = tid % CH;
-  float wf[8];
-  {
-    const u32x4_t w = ld16(k_weight + 8 * c);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) wf[j] = __uint_as_float((j & 1) ? (w[j >> 1] & 0xffff0000u) : (w[j >> 1] << 16));
-  }
-  uint16_t *kdst = kn + ((int64_t)head * s_pad + k0) * D;
-  for (int r = tid / CH; r < 64; r += kThreads / CH) {
-    const int key = k0 + r;
-    float x[8], y[8];
-    const u32x4_t raw = key < seq ? ld16(k + key * k_row + head * k_head + 8 * c) : u32x4_t{0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = __uint_as_float((j & 1) ? (raw[j >> 1] & 0xffff0000u) : (raw[j >> 1] << 16));
-    const float rr = rms_factor(group_tree_sum<CH>(chunk_sumsq(x)), D, eps);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = x[j] * rr * wf[j];
+// The block's q_norm / k_norm (RMSNorm over the head dim, with ROPE the split-half rotation, one
+// bf16 rounding: the arithmetic of qk_norm.h) of the 64 rows [k0, k0 + 64) of one head at a
+// time, written head-major (row r at dst + r * D), zero for rows at or past seq. Each row is
+// normalised by an aligned group of D/8 lanes, one 8-channel chunk per lane. A lane loads the RoPE
+// matrix rows its chunk uses once (the constructor) and reuses them for every head (run): row 0
+// (f00, f01) below half, row 1 (f10, f11) above.
+template <int D, bool ROPE, int THREADS>
+struct RowNorm {
+  static constexpr int CH = D / 8, ROWS = THREADS / CH, ITER = 64 / ROWS;
+  static_assert(64 % ROWS == 0, "whole row groups per pass");
+  int c, r0, half, k0, seq;
+  bool first, rotated;
+  float2 fm[ITER][ROPE ? 8 : 1];
+
+  __device__ __forceinline__ RowNorm(const float *__restrict__ freqs, int64_t f_row, int rot, int k0_, int seq_,
+                                     int tid)
+      : c(tid % CH), r0(tid / CH), half(rot >> 1), k0(k0_), seq(seq_) {
+    first = 8 * c < half;
+    rotated = ROPE && 8 * c < rot;
     if constexpr (ROPE) {
-      const int half = rot >> 1, step = half >> 3;
-      const bool first = 8 * c < half, rotated = 8 * c < rot;
-      const int lane = __lane_id();
-      const int partner = rotated ? (first ? lane + step : lane - step) : lane;
-      float o[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = __shfl(y[j], partner);
-      if (rotated && key < seq) {
-        const f32x4_t *f = reinterpret_cast<const f32x4_t *>(freqs + key * f_row) + (first ? 8 * c : 8 * c - half);
+      for (int it = 0; it < ITER; ++it) {
+        const int key = k0 + r0 + it * ROWS;
+        if (rotated && key < seq) {
+          const float *f = freqs + key * f_row + 4 * (first ? 8 * c : 8 * c - half) + (first ? 0 : 2);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = rope_rotate(y[j], o[j], f[j], first);
+          for (int j = 0; j < 8; ++j) fm[it][j] = *reinterpret_cast<const float2 *>(f + 4 * j);
+        }
       }
     }
-    if (key >= seq) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = 0.f;
-    }
-    st16(kdst + r * D + 8 * c, u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]),
-                                       pack_bf2(y[6], y[7])});
   }
-  __syncthreads();
-  uint16_t *dst = vt + (int64_t)head * D * s_pad + k0;
-  for (int cc = tid; cc < D * 8; cc += kThreads) {
-    int d = cc >> 3, pc = cc & 7;  // output positions 8*pc .. 8*pc+7 of row d
-    uint16_t e[8];
+
+  __device__ __forceinline__ void run(const uint16_t *__restrict__ x, int64_t x_row, int64_t x_head,
+                                      const uint16_t *__restrict__ weight, float eps, uint16_t *__restrict__ dst,
+                                      int head) const {
+    float wf[8];
+    {
+      const u32x4_t w = ld16(weight + 8 * c);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int pp = 8 * pc + j;
-      e[j] = tile[((pp & ~15) + kperm(pp & 15)) * P + d];
+      for (int j = 0; j < 8; ++j) wf[j] = __uint_as_float((j & 1) ? (w[j >> 1] & 0xffff0000u) : (w[j >> 1] << 16));
     }
-    uint4 o;
-    o.x = uint32_t(e[0]) | (uint32_t(e[1]) << 16);
-    o.y = uint32_t(e[2]) | (uint32_t(e[3]) << 16);
-    o.z = uint32_t(e[4]) | (uint32_t(e[5]) << 16);
-    o.w = uint32_t(e[6]) | (uint32_t(e[7]) << 16);
-    *reinterpret_cast<uint4 *>(dst + (int64_t)d * s_pad + 8 * pc) = o;
+    u32x4_t raw[ITER];
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+      const int key = k0 + r0 + it * ROWS;
+      raw[it] = key < seq ? ld16(x + key * x_row + head * x_head + 8 * c) : u32x4_t{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+      const int r = r0 + it * ROWS;
+      const bool live = k0 + r < seq;
+      float xf[8], y[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        xf[j] = __uint_as_float((j & 1) ? (raw[it][j >> 1] & 0xffff0000u) : (raw[it][j >> 1] << 16));
+      const float rr = rms_factor(group_tree_sum<CH>(chunk_sumsq(xf)), D, eps);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = xf[j] * rr * wf[j];
+      if constexpr (ROPE) {
+        // the partner chunk (8c +- half) is lane c +- half / 8 of the same row group
+        const int lane = __lane_id(), step = half >> 3;
+        const int partner = rotated ? (first ? lane + step : lane - step) : lane;
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = __shfl(y[j], partner);
+        if (rotated && live) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float2 m = fm[it][j];
+            y[j] = rope_rotate(y[j], o[j], f32x4_t{m.x, m.y, m.x, m.y}, first);
+          }
+        }
+      }
+      if (!live) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = 0.f;
+      }
+      st16(dst + r * D + 8 * c, u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]),
+                                        pack_bf2(y[6], y[7])});
+    }
+  }
+};
+
+constexpr int kPrepassHeads = 8;  // heads per pre-pass workgroup (they share its rows' RoPE matrices)
+
+// Pre-pass of the normalising attention, for the 64 rows [k0, k0 + 64) of up to kPrepassHeads
+// heads: the V^T copy of vt_prepass_kernel, the normalised keys kn[head][key][d] and, when q is
+// given, the normalised queries qn[head][row][d] (RowNorm). V tiles alternate between two LDS
+// buffers, so one barrier per head orders the tile's writes before its transposed reads, and
+// the reads of a buffer before its next writes.
+template <int D, bool ROPE>
+__global__ __launch_bounds__(kThreads) void qkv_prepass_kernel(
+    const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const uint16_t *__restrict__ q_weight, float q_eps,
+    const uint16_t *__restrict__ k, int64_t k_row, int64_t k_head, const uint16_t *__restrict__ k_weight, float k_eps,
+    const uint16_t *__restrict__ v, int64_t v_row, int64_t v_head, const float *__restrict__ freqs, int64_t f_row,
+    int rot, uint16_t *__restrict__ vt, uint16_t *__restrict__ kn, uint16_t *__restrict__ qn, int seq, int s_pad,
+    int heads) {
+  constexpr int P = D + 8;
+  constexpr int CH = D / 8;  // 16-byte chunks per row
+  __shared__ __attribute__((aligned(16))) uint16_t tile[2][64 * P];
+  const int h0 = blockIdx.x * kPrepassHeads, h1 = min(heads, h0 + kPrepassHeads);
+  const int k0 = blockIdx.y * 64, tid = threadIdx.x;
+  const RowNorm<D, ROPE, kThreads> norm(freqs, f_row, rot, k0, seq, tid);
+  for (int head = h0; head < h1; ++head) {
+    uint16_t *buf = tile[head & 1];
+    for (int cc = tid; cc < 64 * CH; cc += kThreads) {
+      int r = cc / CH, col = cc % CH, key = k0 + r;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (key < seq) val = *reinterpret_cast<const uint4 *>(v + key * v_row + head * v_head + col * 8);
+      *reinterpret_cast<uint4 *>(&buf[r * P + col * 8]) = val;
+    }
+    const int64_t off = ((int64_t)head * s_pad + k0) * D;
+    norm.run(k, k_row, k_head, k_weight, k_eps, kn + off, head);
+    if (q) norm.run(q, q_row, q_head, q_weight, q_eps, qn + off, head);
+    __syncthreads();
+    uint16_t *dst = vt + (int64_t)head * D * s_pad + k0;
+    for (int cc = tid; cc < D * 8; cc += kThreads) {
+      int d = cc >> 3, pc = cc & 7;  // output positions 8*pc .. 8*pc+7 of row d
+      uint16_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        int pp = 8 * pc + j;
+        e[j] = buf[((pp & ~15) + kperm(pp & 15)) * P + d];
+      }
+      uint4 o;
+      o.x = uint32_t(e[0]) | (uint32_t(e[1]) << 16);
+      o.y = uint32_t(e[2]) | (uint32_t(e[3]) << 16);
+      o.z = uint32_t(e[4]) | (uint32_t(e[5]) << 16);
+      o.w = uint32_t(e[6]) | (uint32_t(e[7]) << 16);
+      *reinterpret_cast<uint4 *>(dst + (int64_t)d * s_pad + 8 * pc) = o;
+    }
   }
 }
 
@@ -186,15 +242,15 @@ __device__ __forceinline__ float other_half(float x) {
 // into four-slot rings, K tiles by group A three tiles ahead and V^T tiles by group B two tiles
 // ahead, each between the MFMAs of the issuing group's MFMA phase (the VALU group issues no
 // memory operations), which hides HBM latency for the tiles that miss L2.
-// QN = 0: q is used as given; 1: q is normalised on load (the block's q_norm: q_weight, q_eps,
-// the arithmetic of qk_norm.h); 2: normalised and rotated (split-half RoPE with freqs).
-template <int D, int QN>
+// QNORM: q is normalised as it is loaded (the block's q_norm with q_weight / q_eps, the arithmetic
+// of qk_norm.h); otherwise q is used as given.
+template <int D, bool QNORM>
 __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
     const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const uint16_t *__restrict__ k, int64_t k_row,
     int64_t k_head, const uint16_t *__restrict__ vt, int s_pad, uint16_t *__restrict__ out, int64_t o_row,
     int64_t o_head, const uint16_t *__restrict__ gate, int64_t g_row, int seq, float scale_log2,
     const int4 *__restrict__ items, int n_items, const int2 *__restrict__ tiles, int per_xcd, int total,
-    const uint16_t *__restrict__ q_weight, float q_eps, const float *__restrict__ freqs, int64_t f_row, int rot) {
+    const uint16_t *__restrict__ q_weight, float q_eps) {
   constexpr int KC = D / 8;    // 16-byte chunks per K row
   constexpr int NS = D / 16;   // k-steps of the QK^T contraction
   constexpr int NO = D / 32;   // 32-row blocks of O^T
@@ -223,7 +279,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   {
     // lane (l32, g) holds channels 16 s + 8 g + j (j < 8) of its query row: chunk 2 s + g
     const uint16_t *qp = q + (int64_t)qrc * q_row + (int64_t)head * q_head + 8 * g;
-    if constexpr (QN == 0) {
+    if constexpr (!QNORM) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) qf[s] = as_bf16x8(ld16(qp + 16 * s));
     } else {
@@ -243,31 +299,6 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           y[s][j] = y[s][j] * rr * __uint_as_float((j & 1) ? (w[j >> 1] & 0xffff0000u) : (w[j >> 1] << 16));
-      }
-      if constexpr (QN == 2) {
-        // the rotation partner of channel d (d + h or d - h) may sit in the other half-wave: the
-        // normalised rows go through LDS once (the tile rings are not in use yet): group A's 128 rows
-        // in the K ring, group B's in the V^T ring (each ring holds 128 fp32 rows of D)
-        static_assert(4 * 32 * D * sizeof(float) <= sizeof(Ks) && sizeof(Ks) == sizeof(Vs), "stage fits a ring");
-        float *stage = reinterpret_cast<float *>(group == 0 ? &Ks[0][0] : &Vs[0][0]) + ((wave & 3) * 32 + l32) * D;
-#pragma unroll
-        for (int s = 0; s < NS; ++s)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) stage[16 * s + 8 * g + j] = y[s][j];
-        __syncthreads();
-        const int half = rot >> 1;
-        const f32x4_t *f = reinterpret_cast<const f32x4_t *>(freqs + qrc * f_row);
-#pragma unroll
-        for (int s = 0; s < NS; ++s)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int d = 16 * s + 8 * g + j;
-            if (d < rot) {
-              const bool first = d < half;
-              y[s][j] = rope_rotate(y[s][j], stage[first ? d + half : d - half], f[first ? d : d - half], first);
-            }
-          }
-        __syncthreads();  // the prologue's tile loads reuse this LDS
       }
 #pragma unroll
       for (int s = 0; s < NS; ++s)
@@ -510,37 +541,40 @@ int launch_prepass(const uint16_t *v, int64_t v_row, int64_t v_head, int seq, in
   return check_launch("window vt_prepass");
 }
 
-// QN: 0 = q as given, 1 = q normalised on load, 2 = normalised and rotated (see window_attn_kernel)
-template <int D, int QN>
+// QNORM: q is normalised on load with q_weight / q_eps (see window_attn_kernel)
+template <int D, bool QNORM>
 int launch_attn(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row, int64_t k_head,
                 uint16_t *out, int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row, int seq,
                 int heads, float scale, const int32_t *items, int32_t n_items, const int32_t *tiles,
-                const void *workspace, hipStream_t stream, const uint16_t *q_weight = nullptr, float q_eps = 0.f,
-                const float *freqs = nullptr, int64_t f_row = 0, int rot = 0) {
+                const void *workspace, hipStream_t stream, const uint16_t *q_weight = nullptr, float q_eps = 0.f) {
   const int s_pad = (seq + 63) / 64 * 64;
   const int total = n_items * heads;
   const int per_xcd = (total + 7) / 8;
-  hipLaunchKernelGGL((window_attn_kernel<D, QN>), dim3(per_xcd * 8), dim3(kThreads), 0, stream, q, q_row, q_head, k,
+  hipLaunchKernelGGL((window_attn_kernel<D, QNORM>), dim3(per_xcd * 8), dim3(kThreads), 0, stream, q, q_row, q_head, k,
                      k_row, k_head, static_cast<const uint16_t *>(workspace), s_pad, out, o_row, o_head, gate,
                      gate_row, seq, scale * 1.4426950408889634f, reinterpret_cast<const int4 *>(items), n_items,
-                     reinterpret_cast<const int2 *>(tiles), per_xcd, total, q_weight, q_eps, freqs, f_row, rot);
+                     reinterpret_cast<const int2 *>(tiles), per_xcd, total, q_weight, q_eps);
   return check_launch("window_attn");
 }
 
 template <int D>
-int launch_kv_prepass(const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *v, int64_t v_row,
-                      int64_t v_head, const uint16_t *k_weight, float eps, const float *freqs, int64_t f_row, int rot,
-                      int seq, int heads, void *workspace, hipStream_t stream) {
+int launch_qkv_prepass(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *q_weight, float q_eps,
+                       const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *k_weight, float k_eps,
+                       const uint16_t *v, int64_t v_row, int64_t v_head, const float *freqs, int64_t f_row, int rot,
+                       int seq, int heads, void *workspace, hipStream_t stream) {
   const int s_pad = (seq + 63) / 64 * 64;
-  uint16_t *vt = static_cast<uint16_t *>(workspace);
-  uint16_t *kn = vt + (size_t)heads * D * s_pad;
+  const size_t region = (size_t)heads * D * s_pad;
+  uint16_t *vt = static_cast<uint16_t *>(workspace), *kn = vt + region, *qn = vt + 2 * region;
+  const dim3 grid((heads + kPrepassHeads - 1) / kPrepassHeads, s_pad / 64);
   if (freqs)
-    hipLaunchKernelGGL((kv_prepass_kernel<D, true>), dim3(s_pad / 64, heads), dim3(kThreads), 0, stream, k, k_row,
-                       k_head, v, v_row, v_head, k_weight, eps, freqs, f_row, rot, vt, kn, seq, s_pad);
+    hipLaunchKernelGGL((qkv_prepass_kernel<D, true>), grid, dim3(kThreads), 0, stream, q, q_row, q_head, q_weight,
+                       q_eps, k, k_row, k_head, k_weight, k_eps, v, v_row, v_head, freqs, f_row, rot, vt, kn, qn, seq,
+                       s_pad, heads);
   else
-    hipLaunchKernelGGL((kv_prepass_kernel<D, false>), dim3(s_pad / 64, heads), dim3(kThreads), 0, stream, k, k_row,
-                       k_head, v, v_row, v_head, k_weight, eps, freqs, f_row, rot, vt, kn, seq, s_pad);
-  return check_launch("window kv_prepass");
+    hipLaunchKernelGGL((qkv_prepass_kernel<D, false>), grid, dim3(kThreads), 0, stream, q, q_row, q_head, q_weight,
+                       q_eps, k, k_row, k_head, k_weight, k_eps, v, v_row, v_head, freqs, f_row, rot, vt, kn, qn, seq,
+                       s_pad, heads);
+  return check_launch("window qkv_prepass");
 }
 
 int check_rope(const float *freqs, int64_t f_row, int rot, int head_dim) {
@@ -607,9 +641,9 @@ extern "C" int vdnh3_window_attn_prepared(const uint16_t *q, int64_t q_row, int6
   VDNH3_HOST_CHECK(items != nullptr && tiles != nullptr && n_items > 0, VDNH3_ERR_INVALID, "empty window plan");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (head_dim == 128)
-    return vdnh3::launch_attn<128, 0>(q, q_row, q_head, k, k_row, k_head, out, o_row, o_head, gate, gate_row, seq,
+    return vdnh3::launch_attn<128, false>(q, q_row, q_head, k, k_row, k_head, out, o_row, o_head, gate, gate_row, seq,
                                       heads, scale, items, n_items, tiles, workspace, s);
-  return vdnh3::launch_attn<64, 0>(q, q_row, q_head, k, k_row, k_head, out, o_row, o_head, gate, gate_row, seq, heads,
+  return vdnh3::launch_attn<64, false>(q, q_row, q_head, k, k_row, k_head, out, o_row, o_head, gate, gate_row, seq, heads,
                                    scale, items, n_items, tiles, workspace, s);
 }
 
@@ -625,44 +659,50 @@ extern "C" int vdnh3_window_attn_fwd(const uint16_t *q, int64_t q_row, int64_t q
                                     heads, head_dim, scale, items, n_items, tiles, workspace, workspace_bytes, stream);
 }
 
-extern "C" size_t vdnh3_window_norm_workspace_bytes(int seq, int heads, int head_dim) {
-  return 2 * vdnh3_window_workspace_bytes(seq, heads, head_dim);
+extern "C" size_t vdnh3_window_norm_workspace_bytes(int seq, int heads, int head_dim, int with_queries) {
+  return (with_queries ? 3 : 2) * vdnh3_window_workspace_bytes(seq, heads, head_dim);
 }
 
-extern "C" int vdnh3_window_kv_prepass(const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *v,
-                                       int64_t v_row, int64_t v_head, const uint16_t *k_weight, float k_eps,
-                                       const float *freqs, int64_t freqs_row, int rot_dim, int seq, int heads,
-                                       int head_dim, void *workspace, size_t workspace_bytes, void *stream) {
+extern "C" int vdnh3_window_qkv_prepass(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *q_weight,
+                                        float q_eps, const uint16_t *k, int64_t k_row, int64_t k_head,
+                                        const uint16_t *k_weight, float k_eps, const uint16_t *v, int64_t v_row,
+                                        int64_t v_head, const float *freqs, int64_t freqs_row, int rot_dim, int seq,
+                                        int heads, int head_dim, void *workspace, size_t workspace_bytes,
+                                        void *stream) {
   int rc = vdnh3::check_common(seq, heads, head_dim, workspace, workspace_bytes);
   if (!rc) rc = vdnh3::check_vec(k, k_row, k_head, "k");
   if (!rc) rc = vdnh3::check_vec(v, v_row, v_head, "v");
   if (!rc) rc = vdnh3::check_vec(k_weight, 0, 0, "k_weight");
+  if (!rc && q) rc = vdnh3::check_vec(q, q_row, q_head, "q");
+  if (!rc && q) rc = vdnh3::check_vec(q_weight, 0, 0, "q_weight");
   if (!rc) rc = vdnh3::check_rope(freqs, freqs_row, rot_dim, head_dim);
   if (rc) return rc;
-  VDNH3_HOST_CHECK(workspace_bytes >= vdnh3_window_norm_workspace_bytes(seq, heads, head_dim), VDNH3_ERR_INVALID,
-                   "workspace of %zu bytes is smaller than the %zu the normalising attention needs", workspace_bytes,
-                   vdnh3_window_norm_workspace_bytes(seq, heads, head_dim));
+  const size_t need = vdnh3_window_norm_workspace_bytes(seq, heads, head_dim, q != nullptr);
+  VDNH3_HOST_CHECK(workspace_bytes >= need, VDNH3_ERR_INVALID,
+                   "workspace of %zu bytes is smaller than the %zu the pre-pass writes", workspace_bytes, need);
+  VDNH3_HOST_CHECK((seq + 63) / 64 <= 65535, VDNH3_ERR_INVALID, "the pre-pass supports at most %d rows, got %d",
+                   65535 * 64, seq);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return head_dim == 128 ? vdnh3::launch_kv_prepass<128>(k, k_row, k_head, v, v_row, v_head, k_weight, k_eps, freqs,
-                                                         freqs_row, rot_dim, seq, heads, workspace, s)
-                         : vdnh3::launch_kv_prepass<64>(k, k_row, k_head, v, v_row, v_head, k_weight, k_eps, freqs,
-                                                        freqs_row, rot_dim, seq, heads, workspace, s);
+  return head_dim == 128 ? vdnh3::launch_qkv_prepass<128>(q, q_row, q_head, q_weight, q_eps, k, k_row, k_head,
+                                                          k_weight, k_eps, v, v_row, v_head, freqs, freqs_row, rot_dim,
+                                                          seq, heads, workspace, s)
+                         : vdnh3::launch_qkv_prepass<64>(q, q_row, q_head, q_weight, q_eps, k, k_row, k_head,
+                                                         k_weight, k_eps, v, v_row, v_head, freqs, freqs_row, rot_dim,
+                                                         seq, heads, workspace, s);
 }
 
 extern "C" int vdnh3_window_attn_qnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *q_weight,
-                                       float q_eps, const float *freqs, int64_t freqs_row, int rot_dim, uint16_t *out,
-                                       int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row, int seq,
-                                       int heads, int head_dim, float scale, const int32_t *items, int32_t n_items,
-                                       const int32_t *tiles, const void *workspace, size_t workspace_bytes,
-                                       void *stream) {
+                                       float q_eps, uint16_t *out, int64_t o_row, int64_t o_head, const uint16_t *gate,
+                                       int64_t gate_row, int seq, int heads, int head_dim, float scale,
+                                       const int32_t *items, int32_t n_items, const int32_t *tiles,
+                                       const void *workspace, size_t workspace_bytes, void *stream) {
   int rc = vdnh3::check_common(seq, heads, head_dim, workspace, workspace_bytes);
   if (!rc) rc = vdnh3::check_vec(q, q_row, q_head, "q");
   if (!rc) rc = vdnh3::check_vec(q_weight, 0, 0, "q_weight");
-  if (!rc) rc = vdnh3::check_rope(freqs, freqs_row, rot_dim, head_dim);
   if (rc) return rc;
-  VDNH3_HOST_CHECK(workspace_bytes >= vdnh3_window_norm_workspace_bytes(seq, heads, head_dim), VDNH3_ERR_INVALID,
-                   "workspace of %zu bytes is smaller than the %zu the normalising attention needs", workspace_bytes,
-                   vdnh3_window_norm_workspace_bytes(seq, heads, head_dim));
+  VDNH3_HOST_CHECK(workspace_bytes >= vdnh3_window_norm_workspace_bytes(seq, heads, head_dim, 0), VDNH3_ERR_INVALID,
+                   "workspace of %zu bytes is smaller than the %zu the normalising attention reads", workspace_bytes,
+                   vdnh3_window_norm_workspace_bytes(seq, heads, head_dim, 0));
   VDNH3_HOST_CHECK(out != nullptr && o_row % 4 == 0 && o_head % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0,
                    VDNH3_ERR_INVALID, "out must be 8-byte aligned with strides that are multiples of 4 elements");
   VDNH3_HOST_CHECK(items != nullptr && tiles != nullptr && n_items > 0, VDNH3_ERR_INVALID, "empty window plan");
@@ -671,15 +711,9 @@ extern "C" int vdnh3_window_attn_qnorm(const uint16_t *q, int64_t q_row, int64_t
   // the normalised keys follow the V^T copy in the workspace: [heads][s_pad][head_dim]
   const uint16_t *kn = static_cast<const uint16_t *>(workspace) + (size_t)heads * head_dim * s_pad;
   const int64_t kn_row = head_dim, kn_head = (int64_t)s_pad * head_dim;
-#define VDNH3_QNORM(D, QN)                                                                                          \
-  return vdnh3::launch_attn<D, QN>(q, q_row, q_head, kn, kn_row, kn_head, out, o_row, o_head, gate, gate_row, seq, \
-                                   heads, scale, items, n_items, tiles, workspace, s, q_weight, q_eps, freqs,      \
-                                   freqs_row, rot_dim)
-  if (head_dim == 128) {
-    if (freqs) VDNH3_QNORM(128, 2);
-    VDNH3_QNORM(128, 1);
-  }
-  if (freqs) VDNH3_QNORM(64, 2);
-  VDNH3_QNORM(64, 1);
-#undef VDNH3_QNORM
+  if (head_dim == 128)
+    return vdnh3::launch_attn<128, true>(q, q_row, q_head, kn, kn_row, kn_head, out, o_row, o_head, gate, gate_row,
+                                         seq, heads, scale, items, n_items, tiles, workspace, s, q_weight, q_eps);
+  return vdnh3::launch_attn<64, true>(q, q_row, q_head, kn, kn_row, kn_head, out, o_row, o_head, gate, gate_row, seq,
+                                      heads, scale, items, n_items, tiles, workspace, s, q_weight, q_eps);
 }

@@ -45,12 +45,12 @@ SIGNATURES = {
     "vdnh3_window_attn_prepared": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64,
                                             _vp, _c_i64, _c_int, _c_int, _c_int, _c_float,
                                             _vp, _c_i32, _vp, _vp, _c_size, _vp]),
-    "vdnh3_window_norm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
-    "vdnh3_window_kv_prepass": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_float, _vp, _c_i64,
-                                         _c_int, _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
-    "vdnh3_window_attn_qnorm": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_float, _vp, _c_i64, _c_int, _vp, _c_i64,
-                                         _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _c_float,
-                                         _vp, _c_i32, _vp, _vp, _c_size, _vp]),
+    "vdnh3_window_norm_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "vdnh3_window_qkv_prepass": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_float, _vp, _c_i64, _c_i64, _vp, _c_float,
+                                          _vp, _c_i64, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                          _vp, _c_size, _vp]),
+    "vdnh3_window_attn_qnorm": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_float, _vp, _c_i64, _c_i64, _vp, _c_i64,
+                                         _c_int, _c_int, _c_int, _c_float, _vp, _c_i32, _vp, _vp, _c_size, _vp]),
     "vdnh3_gemm": (_c_int, [_c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int,
                             _vp, _c_int, _vp, _c_int, _c_float, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_quant_rows": (_c_int, [_c_int, _vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _vp]),

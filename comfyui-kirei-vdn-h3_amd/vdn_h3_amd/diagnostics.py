@@ -6,7 +6,7 @@ stream around each named scope and resolves all pending pairs with one device
 synchronisation in ``flush`` / ``snapshot``. Stage names follow the reference
 (``attention.qkv``, ``attention.softmax``, ``attention.out_proj``, ``attention.linear_branch``;
 the reference's ``attention.rope_norm`` runs inside ``attention.softmax`` here, whose
-``attention.softmax.kv_prepass`` / ``.kernel`` sub-stages time its two kernels).
+``attention.softmax.qkv_prepass`` / ``.kernel`` sub-stages time its two kernels).
 """
 
 from __future__ import annotations

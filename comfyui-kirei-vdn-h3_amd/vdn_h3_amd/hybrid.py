@@ -9,9 +9,9 @@ and the same exception types. Per call, on the caller's current stream:
   qkv = attn.qkv_proj(x)                         raw q / k / v views [S, H, D]
   g = sigmoid(x W_g^T + b_g)                     [S, H], GEMM with a sigmoid epilogue
   k' = k_norm(k_raw) [+ RoPE], V^T copy          one HIP pre-pass into the attention workspace
-  flat = bf16(window_attention(q_norm(q_raw) [+ RoPE], k', v) * g)
-                                                 one HIP kernel: q normalised on load, the gate
-                                                 in its epilogue
+       [with RoPE also q' = q_norm(q_raw) + RoPE]
+  flat = bf16(window_attention(q', k', v) * g)   one HIP kernel, the gate in its epilogue; without
+                                                 RoPE it normalises q_raw as it loads it
   out = attn.out_proj(flat)
   out[video] += to_out_linear(branch(x, q_raw, k_raw, v))   GEMM epilogue accumulates into out
 

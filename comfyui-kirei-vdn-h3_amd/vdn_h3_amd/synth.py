@@ -164,15 +164,28 @@ def hybrid_stack(blocks: int, heads: int, head_dim: int, hidden: int, device, *,
     return state, [make_vdn_forward(attn, state, i) for i, attn in enumerate(attns)]
 
 
-def denoise_pass(forwards, x: torch.Tensor, steps: int, on_block=None) -> torch.Tensor:
+def rope_freqs(seq: int, head_dim: int, device="cpu", base: float = 10000.0) -> torch.Tensor:
+    """Split-half RoPE matrices ``[1, seq, 1, head_dim / 2, 2, 2]`` (fp32) for row positions 0..seq-1:
+    pair i of row r rotates by ``r * base^(-2i / head_dim)``, ``[[cos, -sin], [sin, cos]]`` -- the
+    per-row table a DiT hands each block as ``rope_freqs`` (rot_dim = head_dim)."""
+    half = head_dim // 2
+    inv = base ** (-torch.arange(half, dtype=torch.float64) * 2.0 / head_dim)
+    theta = torch.arange(seq, dtype=torch.float64)[:, None] * inv[None, :]
+    c, s = torch.cos(theta), torch.sin(theta)
+    m = torch.stack([torch.stack([c, -s], -1), torch.stack([s, c], -1)], -2).to(torch.float32)
+    return m.reshape(1, seq, 1, half, 2, 2).to(device)
+
+
+def denoise_pass(forwards, x: torch.Tensor, steps: int, on_block=None, rope_freqs=None) -> torch.Tensor:
     """``steps`` passes of ``x <- x + block(rms_norm(x))`` over every block (a pre-norm residual, as H3's
     blocks normalise their input: random-init blocks fed the raw stream would grow it per block).
-    ``on_block(step, index, block_input, block_output)`` sees every block call."""
+    ``on_block(step, index, block_input, block_output)`` sees every block call; ``rope_freqs`` is handed
+    to every block."""
     hidden = x.shape[-1]
     for step in range(steps):
         for index, forward in enumerate(forwards):
             h = torch.nn.functional.rms_norm(x, (hidden,), eps=1e-6)
-            y = forward(h)
+            y = forward(h, rope_freqs=rope_freqs)
             if on_block is not None:
                 on_block(step, index, h, y)
             x = x + y

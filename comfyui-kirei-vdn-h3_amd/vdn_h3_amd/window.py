@@ -260,11 +260,13 @@ def window_softmax_normed(q_raw, k_raw, value, q_weight, k_weight, q_eps, k_eps,
     """``window_softmax_hip(q_norm(q_raw), k_norm(k_raw), value)`` with the block's q/k RMSNorm (and,
     with ``rope_freqs``, the split-half RoPE) fused into the attention (``vdn_h3/hybrid.py:271-302``).
 
-    The keys are normalised once by the pre-pass that also writes the V^T copy; each query row is
-    normalised as the attention kernel loads it. The result has the same bits as the separate q/k
-    pass followed by ``window_softmax_hip``. ``q_eps`` / ``k_eps`` are the two norms' epsilons (with
-    RoPE the reference takes ``q_eps`` for both: pass it as ``k_eps``). ``diagnostics`` times the
-    stages ``attention.softmax.kv_prepass`` / ``attention.softmax.kernel``.
+    The keys are normalised (and rotated) once, by the pre-pass that also writes the V^T copy.
+    Without RoPE each query row is normalised as the attention kernel loads it; with RoPE the
+    pre-pass normalises and rotates the queries too (a rotation inside the attention kernel would
+    re-read the table for every head and query block). Either way the result has the same bits as
+    the separate q/k pass followed by ``window_softmax_hip``. ``q_eps`` / ``k_eps`` are the two
+    norms' epsilons (with RoPE the reference takes ``q_eps`` for both: pass it as ``k_eps``).
+    ``diagnostics`` times the stages ``attention.softmax.qkv_prepass`` / ``attention.softmax.kernel``.
     """
     _check_qkv(q_raw, k_raw, value, "window_softmax_normed")
     device = _lib.require_device(q_raw, k_raw, value, q_weight, k_weight, gate, out)
@@ -278,19 +280,32 @@ def window_softmax_normed(q_raw, k_raw, value, q_weight, k_weight, q_eps, k_eps,
     plan, gate, g_row, out = _attention_operands(q_raw.shape, device, plan, cache, geometry, gate, out)
     q, k, v = _kernel_operand(q_raw), _kernel_operand(k_raw), _kernel_operand(value)
     lib = _lib.lib()
-    ws_bytes = lib.vdnh3_window_norm_workspace_bytes(seq, heads, dim)
+    rotate = table is not None
+    ws_bytes = lib.vdnh3_window_norm_workspace_bytes(seq, heads, dim, int(rotate))
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     sh = _lib.stream_handle(device)
-    with _maybe_scope(diagnostics, "attention.softmax.kv_prepass", device):
-        rc = lib.vdnh3_window_kv_prepass(
-            _lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(v), v.stride(0), v.stride(1), _lib.ptr(wk), float(k_eps),
+    with _maybe_scope(diagnostics, "attention.softmax.qkv_prepass", device):
+        rc = lib.vdnh3_window_qkv_prepass(
+            _lib.ptr(q) if rotate else None, q.stride(0), q.stride(1), _lib.ptr(wq), float(q_eps),
+            _lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(wk), float(k_eps), _lib.ptr(v), v.stride(0), v.stride(1),
             _lib.ptr(table), f_row, rot, seq, heads, dim, _lib.ptr(workspace), ws_bytes, sh)
     _lib.check(rc, "window_softmax_normed")
     with _maybe_scope(diagnostics, "attention.softmax.kernel", device):
-        rc = lib.vdnh3_window_attn_qnorm(
-            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(wq), float(q_eps), _lib.ptr(table), f_row, rot,
-            _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(gate), g_row, seq, heads, dim, float(scale),
-            _lib.ptr(plan.items), plan.n_items, _lib.ptr(plan.tiles), _lib.ptr(workspace), ws_bytes, sh)
+        if rotate:
+            # regions 2 (queries) and 1 (keys) of the workspace, [heads][s_pad][dim]
+            region = lib.vdnh3_window_workspace_bytes(seq, heads, dim)
+            head_stride = region // (2 * heads)
+            base = workspace.data_ptr()
+            rc = lib.vdnh3_window_attn_prepared(
+                ctypes.c_void_p(base + 2 * region), dim, head_stride, ctypes.c_void_p(base + region), dim,
+                head_stride, _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(gate), g_row, seq, heads, dim,
+                float(scale), _lib.ptr(plan.items), plan.n_items, _lib.ptr(plan.tiles), _lib.ptr(workspace),
+                ws_bytes, sh)
+        else:
+            rc = lib.vdnh3_window_attn_qnorm(
+                _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(wq), float(q_eps),
+                _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(gate), g_row, seq, heads, dim, float(scale),
+                _lib.ptr(plan.items), plan.n_items, _lib.ptr(plan.tiles), _lib.ptr(workspace), ws_bytes, sh)
     _lib.check(rc, "window_softmax_normed")
     return out
 

@@ -118,26 +118,31 @@ int vdnh3_window_attn_prepared(const uint16_t *q, int64_t q_row, int64_t q_head,
  * The attention with the block's q_norm / k_norm fused in (vdn_h3/hybrid.py:271-292 followed by
  * the window softmax of vdn_h3/hybrid.py:295-302): q and k are passed raw, as the qkv projection
  * wrote them, and normalised with the arithmetic of vdnh3_qk_rmsnorm / vdnh3_qk_rmsnorm_rope, so
- * that the result has the same bits as those two calls followed by vdnh3_window_attn_prepared.
- *   vdnh3_window_norm_workspace_bytes: the workspace both phases share (the V^T copy, then the
- *     normalised keys [heads][seq rounded up to 64][head_dim]), 16-byte aligned.
- *   vdnh3_window_kv_prepass: writes the V^T copy and the normalised (and, with freqs, rotated)
- *     keys into `workspace`, RMSNorm with k_weight / k_eps.
- *   vdnh3_window_attn_qnorm: normalises (and rotates) q with q_weight / q_eps as it loads it, and
- *     runs the attention against the keys and V^T copy in `workspace`.
- * freqs / freqs_row / rot_dim: the RoPE table of vdnh3_qk_rmsnorm_rope, or freqs = NULL for none.
- * With RoPE the reference uses the q_norm epsilon for the keys too: pass k_eps = q_eps.
+ * that the result has the same bits as those calls followed by vdnh3_window_attn_prepared.
+ * The workspace holds up to three regions of vdnh3_window_workspace_bytes(seq, heads, head_dim)
+ * bytes each, all [heads][seq rounded up to 64][head_dim] bf16: 0 the V^T copy, 1 the normalised
+ * keys, 2 the normalised queries (zero rows past seq).
+ *   vdnh3_window_norm_workspace_bytes: 2 regions, 3 with_queries; 16-byte aligned.
+ *   vdnh3_window_qkv_prepass: writes regions 0 and 1 (keys: k_weight / k_eps) and, when q is not
+ *     NULL, region 2 (queries: q_weight / q_eps). With freqs (the RoPE table of
+ *     vdnh3_qk_rmsnorm_rope, or NULL) the normalised vectors are rotated; the reference then uses
+ *     the q_norm epsilon for both: pass k_eps = q_eps.
+ *   vdnh3_window_attn_qnorm: the attention from raw q, normalised as the kernel loads it (q_weight,
+ *     q_eps), against regions 0 and 1 (a pre-pass with q = NULL and no freqs). With RoPE, run the
+ *     pre-pass with q and pass regions 2 and 1 as q and k to vdnh3_window_attn_prepared (q_row =
+ *     k_row = head_dim, q_head = k_head = seq rounded up to 64 times head_dim): a rotation in the
+ *     attention kernel would re-read the table for every head and query block.
  */
-size_t vdnh3_window_norm_workspace_bytes(int seq, int heads, int head_dim);
-int vdnh3_window_kv_prepass(const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *v, int64_t v_row,
-                            int64_t v_head, const uint16_t *k_weight, float k_eps, const float *freqs,
-                            int64_t freqs_row, int rot_dim, int seq, int heads, int head_dim, void *workspace,
-                            size_t workspace_bytes, void *stream);
+size_t vdnh3_window_norm_workspace_bytes(int seq, int heads, int head_dim, int with_queries);
+int vdnh3_window_qkv_prepass(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *q_weight, float q_eps,
+                             const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *k_weight, float k_eps,
+                             const uint16_t *v, int64_t v_row, int64_t v_head, const float *freqs,
+                             int64_t freqs_row, int rot_dim, int seq, int heads, int head_dim, void *workspace,
+                             size_t workspace_bytes, void *stream);
 int vdnh3_window_attn_qnorm(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *q_weight, float q_eps,
-                            const float *freqs, int64_t freqs_row, int rot_dim, uint16_t *out, int64_t o_row,
-                            int64_t o_head, const uint16_t *gate, int64_t gate_row, int seq, int heads, int head_dim,
-                            float scale, const int32_t *items, int32_t n_items, const int32_t *tiles,
-                            const void *workspace, size_t workspace_bytes, void *stream);
+                            uint16_t *out, int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row,
+                            int seq, int heads, int head_dim, float scale, const int32_t *items, int32_t n_items,
+                            const int32_t *tiles, const void *workspace, size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------------------
  * Projections (reference vdn_h3/projection.py, vdn_h3/fp8.py, the block's qkv/out GEMMs)

@@ -43,36 +43,40 @@ CASES = [(128, None, False), (64, None, False), (128, 128, False), (128, 64, Tru
 
 
 @pytest.mark.parametrize("dim,rot,shared", CASES)
-def test_kv_prepass_matches_qk_pass(device, dim, rot, shared):
+@pytest.mark.parametrize("with_queries", [False, True])
+def test_qkv_prepass_matches_qk_pass(device, dim, rot, shared, with_queries):
     from vdn_h3_amd import _lib
     from vdn_h3_amd.hybrid import normalise_qk
     from vdn_h3_amd.window import rope_table
 
-    seq, heads, eps = 1000, 3, 1e-5
-    print(f"case kv_prepass D={dim} rot={rot} shared={shared}", flush=True)
+    seq, heads, q_eps, k_eps = 1000, 3, 1e-6, 1e-5
+    if rot is not None:  # with RoPE the q/k pass takes one epsilon for both
+        q_eps = k_eps
+    print(f"case qkv_prepass D={dim} rot={rot} shared={shared} queries={with_queries}", flush=True)
     q, k, v, wq, wk = _inputs(seq, heads, dim, 300 + dim + (rot or 0), device)
     freqs = None if rot is None else _freqs(1 if shared else seq, rot, 7).to(device)
-    # (with RoPE the q/k pass takes one epsilon for both)
-    _, want_k = normalise_qk(q, k, wq, wk, 1e-6 if freqs is None else eps, rope_freqs=freqs, k_eps=eps)
+    want_q, want_k = normalise_qk(q, k, wq, wk, q_eps, rope_freqs=freqs, k_eps=k_eps)
     lib = _lib.lib()
-    ws_bytes = lib.vdnh3_window_norm_workspace_bytes(seq, heads, dim)
+    ws_bytes = lib.vdnh3_window_norm_workspace_bytes(seq, heads, dim, int(with_queries))
     ws = torch.full((ws_bytes,), 0x5A, dtype=torch.uint8, device=device)  # junk: the pass must write every byte
     table, f_row, rot_dim = (None, 0, 0) if freqs is None else rope_table(freqs, seq, dim, device)
-    rc = lib.vdnh3_window_kv_prepass(_lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(v), v.stride(0), v.stride(1),
-                                     _lib.ptr(wk), eps, _lib.ptr(table), f_row, rot_dim, seq, heads, dim,
-                                     _lib.ptr(ws), ws_bytes, _lib.stream_handle(device))
-    _lib.check(rc, "vdnh3_window_kv_prepass")
-    vt_ref = torch.empty(lib.vdnh3_window_workspace_bytes(seq, heads, dim), dtype=torch.uint8, device=device)
+    rc = lib.vdnh3_window_qkv_prepass(_lib.ptr(q) if with_queries else None, q.stride(0), q.stride(1), _lib.ptr(wq),
+                                      q_eps, _lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(wk), k_eps, _lib.ptr(v),
+                                      v.stride(0), v.stride(1), _lib.ptr(table), f_row, rot_dim, seq, heads, dim,
+                                      _lib.ptr(ws), ws_bytes, _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_window_qkv_prepass")
+    region = lib.vdnh3_window_workspace_bytes(seq, heads, dim)
+    vt_ref = torch.empty(region, dtype=torch.uint8, device=device)
     _lib.check(lib.vdnh3_window_vt_prepass(_lib.ptr(v), v.stride(0), v.stride(1), seq, heads, dim, _lib.ptr(vt_ref),
-                                           vt_ref.numel(), _lib.stream_handle(device)), "vdnh3_window_vt_prepass")
+                                           region, _lib.stream_handle(device)), "vdnh3_window_vt_prepass")
     torch.cuda.synchronize()
     s_pad = (seq + 63) // 64 * 64
-    half = ws_bytes // 2
-    assert torch.equal(ws[:half].cpu(), vt_ref.cpu())
-    kn = ws[half:].view(torch.bfloat16).view(heads, s_pad, dim)
-    assert torch.equal(kn[:, :seq].permute(1, 0, 2).cpu().view(torch.int16),
-                       want_k.cpu().view(torch.int16))
-    assert not kn[:, seq:].float().abs().sum().item()
+    assert ws_bytes == (3 if with_queries else 2) * region
+    assert torch.equal(ws[:region].cpu(), vt_ref.cpu())
+    for r, want in ((1, want_k), (2, want_q))[:2 if with_queries else 1]:
+        got = ws[r * region:(r + 1) * region].view(torch.bfloat16).view(heads, s_pad, dim)
+        assert torch.equal(got[:, :seq].permute(1, 0, 2).cpu().view(torch.int16), want.cpu().view(torch.int16)), r
+        assert not got[:, seq:].float().abs().sum().item(), r
 
 
 def _geometry(frames=13, per_frame=64, text=16):
@@ -140,14 +144,16 @@ def test_normed_rejects_bad_arguments(device):
     with pytest.raises(ValueError, match="rot_dim"):
         window.window_softmax_normed(q, k, v, wq, wk, 1e-6, 1e-6, *args, rope_freqs=_freqs(seq, 24, 1).to(device))
     lib = _lib.lib()
-    ws_bytes = lib.vdnh3_window_norm_workspace_bytes(seq, heads, dim)
+    ws_bytes = lib.vdnh3_window_norm_workspace_bytes(seq, heads, dim, 0)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     sh = _lib.stream_handle(device)
-    # a workspace that only holds the V^T copy, and one that is not 16-byte aligned
-    rc = lib.vdnh3_window_kv_prepass(_lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(v), v.stride(0), v.stride(1),
-                                     _lib.ptr(wk), 1e-6, None, 0, 0, seq, heads, dim, _lib.ptr(ws), ws_bytes // 2, sh)
-    assert rc != 0
-    rc = lib.vdnh3_window_kv_prepass(_lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(v), v.stride(0), v.stride(1),
-                                     _lib.ptr(wk), 1e-6, None, 0, 0, seq, heads, dim, ctypes.c_void_p(ws.data_ptr() + 8),
-                                     ws_bytes - 16, sh)
-    assert rc != 0
+
+    def prepass(q_ptr, ws_ptr, nbytes):
+        return lib.vdnh3_window_qkv_prepass(q_ptr, q.stride(0), q.stride(1), _lib.ptr(wq), 1e-6, _lib.ptr(k),
+                                            k.stride(0), k.stride(1), _lib.ptr(wk), 1e-6, _lib.ptr(v), v.stride(0),
+                                            v.stride(1), None, 0, 0, seq, heads, dim, ws_ptr, nbytes, sh)
+
+    assert prepass(None, _lib.ptr(ws), ws_bytes // 2) != 0  # holds the V^T copy only
+    assert prepass(None, ctypes.c_void_p(ws.data_ptr() + 8), ws_bytes - 16) != 0  # not 16-byte aligned
+    assert prepass(_lib.ptr(q), _lib.ptr(ws), ws_bytes) != 0  # no room for the queries
+    assert "smaller" in _lib.last_error()
