@@ -239,9 +239,9 @@ __device__ __forceinline__ float other_half(float x) {
 //   VALU phase of tile t :  P(t) = exp2(scale S(t) - m), row max / sum, O rescale   (softmax)
 // Group A runs tile t's MFMA phase in phase 2t and its VALU phase in 2t+1; group B one phase
 // later. K(t) and V(t-1) are read in phases 2t and 2t+1 only; tiles are loaded direct to LDS
-// into four-slot rings, K tiles by group A three tiles ahead and V^T tiles by group B two tiles
-// ahead, each between the MFMAs of the issuing group's MFMA phase (the VALU group issues no
-// memory operations), which hides HBM latency for the tiles that miss L2.
+// into four-slot rings, three tiles ahead: K tiles by group A and V^T tiles by group B, each at
+// the start of the issuing group's VALU phase, so the MFMA stream carries no memory instruction
+// and a tile that misses L2 has three tiles' time to land.
 // QNORM: q is normalised as it is loaded (the block's q_norm with q_weight / q_eps, the arithmetic
 // of qk_norm.h); otherwise q is used as given.
 template <int D, bool QNORM>
@@ -369,7 +369,8 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   // MFMA stream carries no memory instruction: in its VALU phase of tile t, group A issues
   // K(t+kRing-1) (phase 2t+1) over K(t-1), last read in phase 2t-1, and group B issues
   // V(t+kRing-1) (phase 2t+2) over V(t-1), last read in phase 2t+1. In each phase the slot
-  // being written differs from the K and V slots the MFMA group reads. Past the end the tile index is clamped to T-1: such loads rewrite
+  // being written differs from the K and V slots the MFMA group reads. Past the end the tile
+  // index is clamped to T-1: such loads rewrite
   // slots that no real tile reads any more, and every VALU phase issues the same count, so each
   // group's vmcnt wait at the end of odd phases is exact.
   // prologue: K(0..kRing-2) by group A, V(0..kRing-3) by group B, all landed; V(-1), the V^T
