@@ -56,7 +56,7 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="block", choices=["block", "stack", "window", "hbm_copy", "branch",
                                                              "gemm_i8_qkv", "gemm_i8_out", "gemm_f8_qkv",
-                                                             "gemm_f8_out", "gdn", "dit", "rope"],
+                                                             "gemm_f8_out", "gdn", "dit", "rope", "mfma_peak"],
                     help="hbm_copy: a plain 1 GiB device copy, the reference point for scaling rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes")
     ap.add_argument("--short-conv", default="k,v",
@@ -548,6 +548,65 @@ def bench_rope(args, torch, device):
 CPU_THREADS = 16   # the GPU box's CPU share for one GPU
 
 
+def bench_mfma_peak(args, torch, device):
+    """Sustained MFMA rate of the part (vdnh3_mfma_peak): register-resident fragments, independent
+    accumulators, 2 workgroups of 4 wavefronts per CU; random operands (what the kernels see:
+    bf16 N(0,1), int8 uniform in [-127, 127], e4m3 codes of N(0,1)) and zero operands. The rate on
+    random operands is the ceiling the kernels' rates are read against besides the datasheet peak."""
+    from vdn_h3_amd import _lib
+
+    lib = _lib.lib()
+    sh = _lib.stream_handle(device)
+    stream = torch.cuda.current_stream(device)
+    n = 8 * 64 * 32  # bytes per operand buffer
+    gen = torch.Generator().manual_seed(20261202)
+    rand = {
+        0: torch.randn(n // 2, generator=gen).to(torch.bfloat16).view(torch.uint8),
+        1: torch.randint(-127, 128, (n,), generator=gen, dtype=torch.int8).view(torch.uint8),
+        2: torch.randn(n, generator=gen).to(torch.float8_e4m3fn).view(torch.uint8),
+    }
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    blocks = 2 * cus  # one round: two workgroups per CU for the whole run
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=device)
+    peaks = {0: PEAK_BF16_TFLOPS, 1: PEAK_I8_TOPS, 2: PEAK_F8_TFLOPS}
+    names = {0: "bf16_32x32x16", 1: "int8_32x32x32", 2: "fp8_e4m3_32x32x64"}
+    rates = {}
+    for kind in (0, 1, 2):
+        iters = {0: 40000, 1: 40000, 2: 20000}[kind]  # 10-20 ms per launch
+        ops = lib.vdnh3_mfma_peak_ops(kind, iters, blocks)
+        for data in ("random", "zero"):
+            src = rand[kind] if data == "random" else torch.zeros(n, dtype=torch.uint8)
+            a = src.to(device)
+            b = src.roll(4096).to(device)
+            run = lambda: _lib.check(lib.vdnh3_mfma_peak(kind, _lib.ptr(a), _lib.ptr(b), iters, blocks,  # noqa: E731
+                                                         _lib.ptr(out), sh), "mfma_peak")
+            for _ in range(max(1, args.warmup)):
+                run()
+            times = []
+            for _ in range(max(3, args.steps)):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                run()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1))
+            times.sort()
+            ms = times[len(times) // 2]
+            tops = ops / (ms * 1e-3) / 1e12
+            rates[f"{names[kind]}_{data}"] = {"T_per_s": round(tops, 1), "frac_of_peak": round(tops / peaks[kind], 4),
+                                              "ms": round(ms, 4)}
+    bf = rates["bf16_32x32x16_random"]["T_per_s"]
+    return {
+        "metric": "sustained MFMA rate (register-resident operands)",
+        "value": bf,
+        "unit": "TFLOP/s",
+        "ms_per_step": rates["bf16_32x32x16_random"]["ms"],
+        "dtype": "bf16/int8/fp8",
+        "config": {"workload": "mfma_peak", "blocks": blocks, "waves_per_cu": 8, "mfmas_per_wave_iter": 8},
+        "rates": rates,
+    }
+
+
 def _cpu_description():
     """``(model name, physical cores)`` from /proc/cpuinfo (``platform.machine()`` / None if unreadable)."""
     model, cores, phys = None, set(), None
@@ -702,6 +761,8 @@ def main():
         result = bench_dit(args, torch, device)
     elif args.workload == "rope":
         result = bench_rope(args, torch, device)
+    elif args.workload == "mfma_peak":
+        result = bench_mfma_peak(args, torch, device)
     else:
         result = bench_window(args, torch, device)
     line = {

@@ -92,6 +92,8 @@ SIGNATURES = {
     "vdnh3_swiglu": (_c_int, [_vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp]),
     "vdnh3_swiglu_quant_rows": (_c_int, [_c_int, _vp, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _vp]),
     "vdnh3_head_gate": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _vp]),
+    "vdnh3_mfma_peak": (_c_int, [_c_int, _vp, _vp, _c_int, _c_int, _vp, _vp]),
+    "vdnh3_mfma_peak_ops": (ctypes.c_double, [_c_int, _c_int, _c_int]),
 }
 
 _lock = threading.Lock()

@@ -425,6 +425,21 @@ int vdnh3_swiglu_quant_rows(int kind, const uint16_t *h, int64_t h_row, int rows
 /* Fill rows x cols of a bf16 matrix with a constant (anchor-frame rows of the branch output). */
 int vdnh3_fill_rows_bf16(uint16_t *p, int64_t ld, int rows, int cols, float value, void *stream);
 
+/* ------------------------------------------------------------------------------
+ * Calibration (no counterpart in the reference): the sustained MFMA rate of the part on
+ * caller-supplied operand bits, the ceiling the kernels' rates are read against besides the
+ * datasheet peak (the part is power-limited, so the rate depends on how many bits toggle).
+ * ------------------------------------------------------------------------------ */
+
+/* Runs `blocks` workgroups of 4 wavefronts, each issuing iters x 8 independent MFMAs of `kind`
+ * (0 bf16 32x32x16, 1 int8 32x32x32, 2 fp8 e4m3 32x32x64) on register-resident fragments:
+ * a and b hold 8 x 64 lanes x 32 bytes each (32-byte aligned; bf16 and int8 use the first 16
+ * bytes of each lane's 32). out receives blocks x 256 floats (a checksum that keeps the work live). */
+int vdnh3_mfma_peak(int kind, const void *a, const void *b, int iters, int blocks, float *out, void *stream);
+
+/* Operations (2 per multiply-add) one vdnh3_mfma_peak call performs. */
+double vdnh3_mfma_peak_ops(int kind, int iters, int blocks);
+
 #ifdef __cplusplus
 }
 #endif
