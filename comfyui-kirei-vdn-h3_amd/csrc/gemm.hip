@@ -8,10 +8,12 @@
 // (vdn_h3/fp8.py:254-262) and the W8A8 int8 projection with per-token x per-channel scales
 // (the ComfyUI-native qkv_proj / out_proj of vdn_h3/hybrid.py:263, :535).
 //
-// Tiling: a workgroup of 4 wavefronts (one per SIMD) computes a 256x256 tile of C; wavefront w
-// owns rows 128 * (w / 2) .. +128 and columns 128 * (w % 2) .. +128 as 4 x 4 blocks of 32x32
-// MFMA accumulators (eight 16-byte LDS fragment reads feed sixteen independent MFMAs per
-// k-step; the accumulators live in AGPRs). K advances in
+// Tiling: a workgroup of 8 wavefronts (two per SIMD, so that one wavefront's MFMAs issue while
+// the other waits on LDS or the barrier) computes a 256x256 tile of C; wavefront w owns rows
+// 128 * (w / 4) .. +128 and columns 64 * (w % 4) .. +64 as 4 x 2 blocks of 32x32 MFMA accumulators
+// (six 16-byte LDS fragment reads feed eight independent MFMAs per k-step). The 4-wavefront form
+// (128 x 128 per wavefront, one per SIMD) is kept behind VDNH3_GEMM_WAVES=4; the 8-wavefront form
+// measured 2-8% faster on the int8 and fp8 projection shapes. K advances in
 // stages of 64 bytes per row (32 bf16, 64 int8 or 64 fp8 elements):
 //   bf16: v_mfma_f32_32x32x16_bf16, 2 k-steps of 32 bytes per stage
 //   int8: v_mfma_i32_32x32x32_i8,   2 k-steps of 32 bytes
@@ -38,7 +40,16 @@ constexpr int kGemmBM = 256, kGemmBN = 256;
 constexpr int kGemmKB = 128;    // K bytes per row that the host requires K * element size to be a multiple of
 constexpr int kGemmSK = 64;     // K bytes per row of one pipeline stage
 constexpr int kGemmStages = 5;  // LDS ring slots (5 x 32 KB: all 160 KB)
-constexpr int kGemmThreads = 256;
+#ifndef VDNH3_GEMM_WAVES
+#define VDNH3_GEMM_WAVES 8
+#endif
+constexpr int kGemmWaves = VDNH3_GEMM_WAVES;  // wavefronts per workgroup: 4 (one per SIMD) or 8 (two)
+static_assert(kGemmWaves == 4 || kGemmWaves == 8, "4 or 8 wavefronts per GEMM workgroup");
+constexpr int kGemmThreads = 64 * kGemmWaves;
+// a wavefront owns 128 rows x (32 kGemmNJ) columns of the tile: 2 x 2 wavefronts of 128 x 128
+// or 2 x 4 wavefronts of 128 x 64
+constexpr int kGemmNJ = 16 / kGemmWaves;
+constexpr int kGemmLoads = 32 / kGemmWaves;  // 16-byte stage loads per thread and stage (A and B)
 constexpr int kGemmGroupM = 8;                             // tile rows per grouping band
 
 enum GemmKind { kBF16 = 0, kI8 = 1, kF8 = 2 };
@@ -80,8 +91,10 @@ struct Frag {
 // block leaves as one contiguous run. The staged words are the raw accumulator bits (int32
 // for int8 operands, fp32 otherwise). ACT (sigmoid) and ACCUM are not combined by any caller
 // (the launcher keeps them apart).
-constexpr int kEpiStride = 136;
+constexpr int kEpiStride = 32 * kGemmNJ + 8;
 constexpr int kEpiWaveWords = 32 * kEpiStride;
+constexpr int kEpiLanesPerRow = 8 * kGemmNJ;         // four columns per lane
+constexpr int kEpiRowsPerPass = 64 / kEpiLanesPerRow;  // rows one pass of the wavefront covers
 
 // Per-lane epilogue operands, loaded at the start of the kernel so that their latency hides
 // behind the main loop: the scales of rows mb + lane and mb + 64 + lane of the wavefront's
@@ -99,7 +112,7 @@ __device__ __forceinline__ EpiOperands load_epi_operands(const GemmEpi &epi, int
     const int m = min(mb + 64 * h + lane, M - 1);
     o.row_scale[h] = epi.a_scale ? epi.a_scale[epi.a_scale_n == 1 ? 0 : m] : 1.f;
   }
-  const int n = nb + 4 * (lane & 31);
+  const int n = nb + 4 * (lane % kEpiLanesPerRow);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int nk = min(n + k, N - 1);
@@ -112,11 +125,11 @@ __device__ __forceinline__ EpiOperands load_epi_operands(const GemmEpi &epi, int
 }
 
 template <int OUT, bool ACT, bool ACCUM, bool INT_ACC, typename Acc>
-__device__ __forceinline__ void store_block(const Acc (&acc)[4][4], uint32_t *stage, const GemmEpi &epi,
+__device__ __forceinline__ void store_block(const Acc (&acc)[4][kGemmNJ], uint32_t *stage, const GemmEpi &epi,
                                             const EpiOperands &eo, void *C, int64_t ldc, int M, int N, int mb,
                                             int nb, int lane) {
   const int l32 = lane & 31, g = lane >> 5;
-  const int c0 = 4 * l32, n = nb + c0;
+  const int c0 = 4 * (lane % kEpiLanesPerRow), pr = lane / kEpiLanesPerRow, n = nb + c0;
   const bool vec = epi.vec && n < N;  // the host sets vec only when N % 4 == 0 and C allows 4-wide stores
   using old_t = typename std::conditional<OUT == kOutF32, f32x4_t, u32x2_t>::type;
   const bool round_linear = epi.round_linear;
@@ -125,7 +138,7 @@ __device__ __forceinline__ void store_block(const Acc (&acc)[4][4], uint32_t *st
   for (int i = 0; i < 4; ++i) {
     // stage rows 32 i .. +32 of the block
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < kGemmNJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         // element copied out first: __builtin_bit_cast of a vector-element lvalue reads
@@ -135,15 +148,15 @@ __device__ __forceinline__ void store_block(const Acc (&acc)[4][4], uint32_t *st
         stage[(8 * (r >> 2) + 4 * g + (r & 3)) * kEpiStride + 32 * j + l32] = w;
       }
     asm volatile("" ::: "memory");  // LDS operations of one wavefront complete in order
-    // rows 2 it + g of the round in chunks of four; when accumulating, a chunk's old values
-    // are loaded together before any of its stores
+    // rows kEpiRowsPerPass it + pr of the round in chunks of four passes; when accumulating, a
+    // chunk's old values are loaded together before any of its stores
 #pragma unroll 1
-    for (int c4 = 0; c4 < 4; ++c4) {
+    for (int c4 = 0; c4 < 32 / kEpiRowsPerPass / 4; ++c4) {
       old_t old[4];
       if constexpr (ACCUM) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int m = mb + 32 * i + 2 * (4 * c4 + q) + g;
+          const int m = mb + 32 * i + kEpiRowsPerPass * (4 * c4 + q) + pr;
           old[q] = old_t{};
           if (vec && m < M) {
             const int64_t off = (int64_t)m * ldc + n;
@@ -152,19 +165,19 @@ __device__ __forceinline__ void store_block(const Acc (&acc)[4][4], uint32_t *st
           }
         }
       }
-      // the chunk's staged rows and row scales (row 32 i + 2 it + g of the block: scale held by
-      // lane (32 i + 2 it + g) % 64, entry i / 2), read before any of its arithmetic
+      // the chunk's staged rows and row scales (row 32 i + row of the block: scale held by
+      // lane (32 i + row) % 64, entry i / 2), read before any of its arithmetic
       u32x4_t wq[4];
       float asq[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int row = 2 * (4 * c4 + q) + g;
+        const int row = kEpiRowsPerPass * (4 * c4 + q) + pr;
         wq[q] = *reinterpret_cast<const u32x4_t *>(stage + row * kEpiStride + c0);
         asq[q] = __shfl(eo.row_scale[i >> 1], 32 * (i & 1) + row);
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int m = mb + 32 * i + 2 * (4 * c4 + q) + g;
+        const int m = mb + 32 * i + kEpiRowsPerPass * (4 * c4 + q) + pr;
         if (m >= M || n >= N) continue;
         const int64_t off = (int64_t)m * ldc + n;
         const u32x4_t w = wq[q];
@@ -254,35 +267,37 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
 
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+  constexpr int kWavesN = kGemmWaves / 2;  // wavefront columns of the tile
+  const int wm = (wave / kWavesN) * 128, wn = (wave % kWavesN) * (32 * kGemmNJ);
   const int mb = m0 + wm, nb = n0 + wn;
   const EpiOperands eo = load_epi_operands(epi, M, N, mb, nb, lane);
 
   // Stage loads. A stage is 64 bytes of K for the tile's 256 A rows and 256 B rows (16 KB
   // each); LDS position P (16-byte units) of an operand's stage is row P / 4, slot P % 4 and
-  // holds chunk slot ^ swz(row) of that row. Load instruction q (0..3) of a wavefront covers
-  // positions 256 q + tid, i.e. rows 64 q + tid / 4. Rows past M (N) read the last row; their
-  // results are not stored.
+  // holds chunk slot ^ swz(row) of that row. Load instruction q (0 .. kGemmLoads / 2 - 1) of an
+  // operand covers positions kGemmThreads q + tid, i.e. rows (kGemmThreads / 4) q + tid / 4.
+  // Rows past M (N) read the last row; their results are not stored.
   // The source of a load is a wave-uniform base (the tile's first row, advanced by the stage)
   // plus a per-lane 32-bit byte offset that stays the same for every stage (the host checks
   // that 256 rows of A and B span less than 4 GB).
+  constexpr int kHalf = kGemmLoads / 2, kRowsPerLoad = kGemmThreads / 4;
   const int lrow = tid >> 2;
-  const int lchunk = gemm_slot(lrow, tid & 3);
-  uint32_t a_off[4], b_off[4];
+  const int lchunk = gemm_slot(lrow, tid & 3);  // the swizzle only sees row bits below kRowsPerLoad
+  uint32_t a_off[kHalf], b_off[kHalf];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    a_off[q] = (uint32_t)((min(m0 + 64 * q + lrow, M - 1) - m0) * lda_b + lchunk * 16);
-    b_off[q] = (uint32_t)((min(n0 + 64 * q + lrow, N - 1) - n0) * ldb_b + lchunk * 16);
+  for (int q = 0; q < kHalf; ++q) {
+    a_off[q] = (uint32_t)((min(m0 + kRowsPerLoad * q + lrow, M - 1) - m0) * lda_b + lchunk * 16);
+    b_off[q] = (uint32_t)((min(n0 + kRowsPerLoad * q + lrow, N - 1) - n0) * ldb_b + lchunk * 16);
   }
   const uint8_t *a_tile = A + (int64_t)m0 * lda_b, *b_tile = B + (int64_t)n0 * ldb_b;
-  // load q (0..7) of stage st into ring slot `slot`: A rows 64 q .. +64 (q < 4), else B rows
-  // 64 (q - 4) .. +64
+  // load q (0 .. kGemmLoads - 1) of stage st into ring slot `slot`: A for q < kHalf, else B
   const uint32_t lds_wave = lds_address(&smem[0][0][0]) + wave * 64 * 16;
   auto load_part = [&](int st, int slot, int q) __device__ {
     const int64_t off = (int64_t)st * kGemmSK;
-    const int i = q & 3;
-    const uint32_t dst = lds_wave + (uint32_t)(((q >> 2) * kGemmStages + slot) * STAGE_BYTES + i * kGemmThreads * 16);
-    global_to_lds16_sbase((q >= 4 ? b_tile : a_tile) + off, q >= 4 ? b_off[i] : a_off[i], dst);
+    const int i = q % kHalf;
+    const uint32_t dst =
+        lds_wave + (uint32_t)(((q / kHalf) * kGemmStages + slot) * STAGE_BYTES + i * kGemmThreads * 16);
+    global_to_lds16_sbase((q >= kHalf ? b_tile : a_tile) + off, q >= kHalf ? b_off[i] : a_off[i], dst);
   };
 
   // fragment byte offsets inside an operand's stage (rows 32 i + l32 share l32's swizzle):
@@ -296,48 +311,48 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
   }
 
   using acc_t = typename std::conditional<KIND == kI8, i32x16_t, f32x16_t>::type;
-  acc_t acc[4][4];
+  acc_t acc[4][kGemmNJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
+    for (int j = 0; j < kGemmNJ; ++j) acc[i][j] = acc_t{};
 
   // k-steps per stage: 32 bytes per lane group for bf16 / int8, 64 for fp8
   constexpr int KS = KIND == kF8 ? 1 : 2;
   using frag_t = typename Frag<KIND>::type;
-  frag_t fa[2][4], fb[2][4];
+  frag_t fa[2][4], fb[2][kGemmNJ];
   // fragments of k-step ks of the stage in `slot` into buffer `buf`
   auto read_frags = [&](int slot, int ks, int buf) __device__ {
     __builtin_amdgcn_sched_barrier(0);
     const uint8_t *at = smem[0][slot] + wm * kGemmSK;
     const uint8_t *bt = smem[1][slot] + wn * kGemmSK;
+    auto rd = [&](const uint8_t *base, int i) __device__ {
+      if constexpr (KIND == kF8) {
+        const u32x4_t lo = ld16(base + i * 32 * kGemmSK + foff[0]);
+        const u32x4_t hi = ld16(base + i * 32 * kGemmSK + foff[1]);
+        return frag_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      } else {
+        return frag_t(ld16(base + i * 32 * kGemmSK + foff[ks]));
+      }
+    };
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if constexpr (KIND == kF8) {
-        const u32x4_t alo = ld16(at + i * 32 * kGemmSK + foff[0]);
-        const u32x4_t ahi = ld16(at + i * 32 * kGemmSK + foff[1]);
-        const u32x4_t blo = ld16(bt + i * 32 * kGemmSK + foff[0]);
-        const u32x4_t bhi = ld16(bt + i * 32 * kGemmSK + foff[1]);
-        fa[buf][i] = i32x8_t{(int)alo.x, (int)alo.y, (int)alo.z, (int)alo.w, (int)ahi.x, (int)ahi.y, (int)ahi.z, (int)ahi.w};
-        fb[buf][i] = i32x8_t{(int)blo.x, (int)blo.y, (int)blo.z, (int)blo.w, (int)bhi.x, (int)bhi.y, (int)bhi.z, (int)bhi.w};
-      } else {
-        fa[buf][i] = ld16(at + i * 32 * kGemmSK + foff[ks]);
-        fb[buf][i] = ld16(bt + i * 32 * kGemmSK + foff[ks]);
-      }
+      fa[buf][i] = rd(at, i);
+      if (i < kGemmNJ) fb[buf][i] = rd(bt, i);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // the 16 MFMAs of one k-step; with `dma`, stage loads q0 .. q0 + 8 / KS - 1 of stage ld_st
+  // the 4 kGemmNJ MFMAs of one k-step; with `dma`, stage loads q0 .. q0 + kGemmLoads / KS - 1 of stage ld_st
   // sit between them, evenly spaced; `reads` (the next k-step's fragment reads) follows the
   // second MFMA, so that any LDS wait before the first ones covers only older reads
   auto mfmas = [&](int buf, bool dma, int ld_st, int ld_slot, int q0, auto reads) __device__ {
-    constexpr int kLoads = 8 / KS, kEvery = 16 / kLoads;
+    constexpr int kLoads = kGemmLoads / KS, kEvery = 4 * kGemmNJ / kLoads;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (i == 0 && j == 2) reads();
-        if (dma && (4 * i + j) % kEvery == 0) load_part(ld_st, ld_slot, q0 + (4 * i + j) / kEvery);
+      for (int j = 0; j < kGemmNJ; ++j) {
+        if (kGemmNJ * i + j == 2) reads();
+        if (dma && (kGemmNJ * i + j) % kEvery == 0) load_part(ld_st, ld_slot, q0 + (kGemmNJ * i + j) / kEvery);
         // fixed issue order: each stage load sits between two MFMAs
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (KIND == kF8)
@@ -367,11 +382,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int buf = (P * KS + ks) & 1;
-      const int q0 = ks * (8 / KS);
+      const int q0 = ks * (kGemmLoads / KS);
       if (ks + 1 < KS) {
         mfmas(buf, decltype(dma)::value, s + 4, ld_slot, q0, [&]() __device__ { read_frags(slot, ks + 1, buf ^ 1); });
       } else if constexpr (decltype(next)::value) {
-        if (decltype(dma)::value) wait_vm_lds<16 + 4 * (KS - 1)>();
+        if (decltype(dma)::value) wait_vm_lds<2 * kGemmLoads + kGemmLoads / KS * (KS - 1)>();
         else wait_vm_lds<0>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of stage s are done
         bare_barrier();
@@ -389,10 +404,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
   for (int st = 0; st < 4; ++st) {
     if (st < nst) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) load_part(st, st, q);
+      for (int q = 0; q < kGemmLoads; ++q) load_part(st, st, q);
     }
   }
-  if (nst >= 4) wait_vm_lds<24>();
+  if (nst >= 4) wait_vm_lds<3 * kGemmLoads>();
   else wait_vm_lds<0>();
   bare_barrier();
   read_frags(0, 0, 0);

@@ -230,6 +230,76 @@ __device__ __forceinline__ float other_half(float x) {
   return __uint_as_float(lane < 32 ? r[1] : r[0]);
 }
 
+// The Q^T fragments of a wavefront: lane (l32, g) holds channels 16 s + 8 g + j (j < 8) of its
+// query row qrc, chunk 2 s + g. QNORM: q is normalised as it is loaded (the block's q_norm with
+// q_weight / q_eps, the arithmetic of qk_norm.h); otherwise q is used as given.
+template <int D, bool QNORM>
+__device__ __forceinline__ void load_q_frags(const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, int qrc,
+                                             int head, int g, const uint16_t *__restrict__ q_weight, float q_eps,
+                                             bf16x8_t (&qf)[D / 16]) {
+  constexpr int NS = D / 16;
+  const uint16_t *qp = q + (int64_t)qrc * q_row + (int64_t)head * q_head + 8 * g;
+  if constexpr (!QNORM) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[s] = as_bf16x8(ld16(qp + 16 * s));
+  } else {
+    float y[NS][8], p[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const u32x4_t raw = ld16(qp + 16 * s);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        y[s][j] = __uint_as_float((j & 1) ? (raw[j >> 1] & 0xffff0000u) : (raw[j >> 1] << 16));
+      p[s] = chunk_sumsq(y[s]);
+    }
+    const float rr = rms_factor(halves_tree_sum<NS>(p), D, q_eps);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const u32x4_t w = ld16(q_weight + 16 * s + 8 * g);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        y[s][j] = y[s][j] * rr * __uint_as_float((j & 1) ? (w[j >> 1] & 0xffff0000u) : (w[j >> 1] << 16));
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      qf[s] = as_bf16x8(u32x4_t{pack_bf2(y[s][0], y[s][1]), pack_bf2(y[s][2], y[s][3]), pack_bf2(y[s][4], y[s][5]),
+                                pack_bf2(y[s][6], y[s][7])});
+  }
+}
+
+// The output rows of a wavefront: O = O^T / l (l summed over the two half-waves), rounded to bf16,
+// times the row's gate when one is given (the gate fused into the attention epilogue).
+template <int D>
+__device__ __forceinline__ void store_rows(const f32x16_t (&oacc)[D / 32], float l_run, int qr, int q1,
+                                           const uint16_t *__restrict__ gate, int64_t g_row, int head,
+                                           uint16_t *__restrict__ out, int64_t o_row, int64_t o_head, int g) {
+  constexpr int NO = D / 32;
+  l_run += other_half(l_run);
+  const float inv = 1.f / l_run;
+  if (qr < q1) {
+    float gv = 1.f;
+    if (gate) gv = bf2f(gate[(int64_t)qr * g_row + head]);
+    uint16_t *op = out + (int64_t)qr * o_row + (int64_t)head * o_head;
+#pragma unroll
+    for (int m = 0; m < NO; ++m)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        float v0 = round_bf(oacc[m][4 * i4 + 0] * inv), v1 = round_bf(oacc[m][4 * i4 + 1] * inv);
+        float v2 = round_bf(oacc[m][4 * i4 + 2] * inv), v3 = round_bf(oacc[m][4 * i4 + 3] * inv);
+        if (gate) {
+          v0 *= gv;
+          v1 *= gv;
+          v2 *= gv;
+          v3 *= gv;
+        }
+        uint2 w;
+        w.x = pack_bf2(v0, v1);
+        w.y = pack_bf2(v2, v3);
+        *reinterpret_cast<uint2 *>(op + 32 * m + 8 * i4 + 4 * g) = w;
+      }
+  }
+}
+
 // ---------------------------------------------------------------------------------
 // Two-group ping-pong over the key tiles t = 0..T-1 of a work item (256 query rows of one head).
 // Waves 0-3 (group A) and 4-7 (group B) each own 32 query rows; wave w and w + 4 share a SIMD.
@@ -276,36 +346,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   const bool rows_live = q0 + wave * 32 < q1;
 
   bf16x8_t qf[NS];
-  {
-    // lane (l32, g) holds channels 16 s + 8 g + j (j < 8) of its query row: chunk 2 s + g
-    const uint16_t *qp = q + (int64_t)qrc * q_row + (int64_t)head * q_head + 8 * g;
-    if constexpr (!QNORM) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) qf[s] = as_bf16x8(ld16(qp + 16 * s));
-    } else {
-      float y[NS][8], p[NS];
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const u32x4_t raw = ld16(qp + 16 * s);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          y[s][j] = __uint_as_float((j & 1) ? (raw[j >> 1] & 0xffff0000u) : (raw[j >> 1] << 16));
-        p[s] = chunk_sumsq(y[s]);
-      }
-      const float rr = rms_factor(halves_tree_sum<NS>(p), D, q_eps);
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const u32x4_t w = ld16(q_weight + 16 * s + 8 * g);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          y[s][j] = y[s][j] * rr * __uint_as_float((j & 1) ? (w[j >> 1] & 0xffff0000u) : (w[j >> 1] << 16));
-      }
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-        qf[s] = as_bf16x8(u32x4_t{pack_bf2(y[s][0], y[s][1]), pack_bf2(y[s][2], y[s][3]), pack_bf2(y[s][4], y[s][5]),
-                                  pack_bf2(y[s][6], y[s][7])});
-    }
-  }
+  load_q_frags<D, QNORM>(q, q_row, q_head, qrc, head, g, q_weight, q_eps, qf);
 
   const uint16_t *kbase = k + (int64_t)head * k_head;
   const uint16_t *vbase = vt + (int64_t)head * D * s_pad;
@@ -507,30 +548,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   }
 
   wait_vm_lds<0>();  // no tile load may land in LDS after the workgroup ends
-  l_run += other_half(l_run);
-  const float inv = 1.f / l_run;
-  if (qr < q1) {
-    float gv = 1.f;
-    if (gate) gv = bf2f(gate[(int64_t)qr * g_row + head]);
-    uint16_t *op = out + (int64_t)qr * o_row + (int64_t)head * o_head;
-#pragma unroll
-    for (int m = 0; m < NO; ++m)
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        float v0 = round_bf(oacc[m][4 * i4 + 0] * inv), v1 = round_bf(oacc[m][4 * i4 + 1] * inv);
-        float v2 = round_bf(oacc[m][4 * i4 + 2] * inv), v3 = round_bf(oacc[m][4 * i4 + 3] * inv);
-        if (gate) {
-          v0 *= gv;
-          v1 *= gv;
-          v2 *= gv;
-          v3 *= gv;
-        }
-        uint2 w;
-        w.x = pack_bf2(v0, v1);
-        w.y = pack_bf2(v2, v3);
-        *reinterpret_cast<uint2 *>(op + 32 * m + 8 * i4 + 4 * g) = w;
-      }
-  }
+  store_rows<D>(oacc, l_run, qr, q1, gate, g_row, head, out, o_row, o_head, g);
 }
 
 template <int D>
