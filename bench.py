@@ -136,7 +136,7 @@ def bench_window(args, torch, device):
                    "tokens_per_frame": lay.tokens_per_frame, "text_rows": lay.text_len, "chunk": w.chunk,
                    "radius": w.radius, "anchor_frames": lay.anchor_frames,
                    "allowed_pairs_per_head": plan.pairs_per_head, "flop_per_step": flops},
-        "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128,%d>" % (2 if freqs is not None else 1), "achieved": round(attn_tflops, 2),
+        "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128,false>", "achieved": round(attn_tflops, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
                      "kernel_ms": round(attn_ms, 4), "traffic": _traffic(args.traffic_json, "window_attn_kernel")},
         "breakdown_ms": {"vt_prepass": round(ms_step - attn_ms, 4), "window_attn": round(attn_ms, 4)},
@@ -261,7 +261,7 @@ def bench_block(args, torch, device):
                    "branch_short_conv": ",".join(conv) or "none",
                    "allowed_pairs_per_head": plan.pairs_per_head, "work_per_step": work,
                    "work_total": total},
-        "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128,%d>" % (2 if freqs is not None else 1), "achieved": round(attn_tflops, 2),
+        "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128,%s>" % ("false" if freqs is not None else "true"), "achieved": round(attn_tflops, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
                      "kernel_ms": round(attn_ms, 4), "traffic": _traffic(args.traffic_json, "window_attn_kernel")},
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
