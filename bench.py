@@ -16,13 +16,16 @@ the output.
 ``value`` is the block's algorithmic work per second (int8 OPs + bf16/fp32 FLOPs, listed per
 stage in ``config.work_per_step``); ``roofline`` is the window attention kernel (the dominant
 kernel), timed with HIP events on the stream it runs on; ``stages_ms`` are per-stage event
-timings of the same timed steps.
+timings of the same timed steps. ``roofline_vs_sustained_mfma`` sets the same kernel rate against
+the part's sustained MFMA rate on random operands (``--workload mfma_peak``), measured after the
+timed region: the datasheet ``peak`` assumes a clock the power limit allows only on operands that
+barely toggle.
 
 Other workloads: ``stack`` (50 blocks x ``--steps`` denoising steps, ``x <- x + block(rms_norm(x))``; use
 ``--steps 8 --warmup 1`` for the 8-step pass), ``window`` (attention alone), ``branch`` (VDN branch alone),
 ``gemm_{i8,f8}_{qkv,out}`` (W8A8 GEMMs alone), ``gdn`` (token-level chunk-64 Gated DeltaNet), ``dit``
 (the DiT block pointwise passes), ``rope`` (q/k RMSNorm + RoPE),
-``hbm_copy`` (counter calibration).
+``hbm_copy`` (counter calibration), ``mfma_peak`` (sustained MFMA rates, the ceiling calibration).
 ``cpu_baseline`` times the fp32 CPU oracle on the host cores (16 threads, the box's CPU share) on bounded
 samples (1 warm-up, median of 3): for ``block``, the window attention on sampled query rows, the projections
 on sampled rows and the VDN branch on 7 of its 29 inner frames, combined at the block's per-part work.
@@ -140,6 +143,7 @@ def bench_window(args, torch, device):
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
                      "kernel_ms": round(attn_ms, 4), "traffic": _traffic(args.traffic_json, "window_attn_kernel")},
         "breakdown_ms": {"vt_prepass": round(ms_step - attn_ms, 4), "window_attn": round(attn_ms, 4)},
+        "roofline_vs_sustained_mfma": ceiling_entry(torch, device, 0, attn_tflops),
     }
     if args.cpu_sample_rows > 0:
         result["cpu_baseline"] = cpu_baseline_window(torch, qkv, w, lay, args.cpu_sample_rows)
@@ -274,6 +278,7 @@ def bench_block(args, torch, device):
                                  "frac_bf16_peak": round(attn_tflops / PEAK_BF16_TFLOPS, 4)},
         },
         "linear_to_softmax_ratio": round(stages["attention.linear_branch"] / stages["attention.softmax"], 4),
+        "roofline_vs_sustained_mfma": ceiling_entry(torch, device, 0, attn_tflops),
     }
 
 
@@ -361,6 +366,7 @@ def bench_gemm(args, torch, device):
                      "traffic": _traffic(args.traffic_json, f"gemm_nt_kernel<{kind_name}>:{which}")},
         "breakdown_ms": {"activation_quant": round(quant_ms, 4), "gemm": round(gemm_ms, 4),
                          "activation_quant_GBs": round(qbytes / (quant_ms * 1e-3) / 1e9, 1)},
+        "roofline_vs_sustained_mfma": ceiling_entry(torch, device, 1 if kind_name == "i8" else 2, tops),
     }
 
 
@@ -548,11 +554,15 @@ def bench_rope(args, torch, device):
 CPU_THREADS = 16   # the GPU box's CPU share for one GPU
 
 
-def bench_mfma_peak(args, torch, device):
-    """Sustained MFMA rate of the part (vdnh3_mfma_peak): register-resident fragments, independent
-    accumulators, 2 workgroups of 4 wavefronts per CU; random operands (what the kernels see:
-    bf16 N(0,1), int8 uniform in [-127, 127], e4m3 codes of N(0,1)) and zero operands. The rate on
-    random operands is the ceiling the kernels' rates are read against besides the datasheet peak."""
+MFMA_KINDS = {0: ("bf16_32x32x16", PEAK_BF16_TFLOPS), 1: ("int8_32x32x32", PEAK_I8_TOPS),
+              2: ("fp8_e4m3_32x32x64", PEAK_F8_TFLOPS)}
+
+
+def mfma_rate(torch, device, kind, data="random", reps=3, warmup=1):
+    """Sustained MFMA rate (T(FL)OP/s, median of ``reps`` launches of 10-20 ms) of ``kind`` (0 bf16,
+    1 int8, 2 fp8 e4m3) on register-resident operands (vdnh3_mfma_peak): random operands (what the
+    kernels see: bf16 N(0,1), int8 uniform in [-127, 127], e4m3 codes of N(0,1)) or zeros, two
+    workgroups of 4 wavefronts per CU, independent accumulators."""
     from vdn_h3_amd import _lib
 
     lib = _lib.lib()
@@ -560,49 +570,66 @@ def bench_mfma_peak(args, torch, device):
     stream = torch.cuda.current_stream(device)
     n = 8 * 64 * 32  # bytes per operand buffer
     gen = torch.Generator().manual_seed(20261202)
-    rand = {
-        0: torch.randn(n // 2, generator=gen).to(torch.bfloat16).view(torch.uint8),
-        1: torch.randint(-127, 128, (n,), generator=gen, dtype=torch.int8).view(torch.uint8),
-        2: torch.randn(n, generator=gen).to(torch.float8_e4m3fn).view(torch.uint8),
-    }
+    if data == "zero":
+        src = torch.zeros(n, dtype=torch.uint8)
+    elif kind == 0:
+        src = torch.randn(n // 2, generator=gen).to(torch.bfloat16).view(torch.uint8)
+    elif kind == 1:
+        src = torch.randint(-127, 128, (n,), generator=gen, dtype=torch.int8).view(torch.uint8)
+    else:
+        src = torch.randn(n, generator=gen).to(torch.float8_e4m3fn).view(torch.uint8)
     cus = torch.cuda.get_device_properties(device).multi_processor_count
     blocks = 2 * cus  # one round: two workgroups per CU for the whole run
     out = torch.empty(blocks * 256, dtype=torch.float32, device=device)
-    peaks = {0: PEAK_BF16_TFLOPS, 1: PEAK_I8_TOPS, 2: PEAK_F8_TFLOPS}
-    names = {0: "bf16_32x32x16", 1: "int8_32x32x32", 2: "fp8_e4m3_32x32x64"}
+    iters = {0: 40000, 1: 40000, 2: 20000}[kind]
+    ops = lib.vdnh3_mfma_peak_ops(kind, iters, blocks)
+    a, b = src.to(device), src.roll(4096).to(device)
+
+    def run():
+        _lib.check(lib.vdnh3_mfma_peak(kind, _lib.ptr(a), _lib.ptr(b), iters, blocks, _lib.ptr(out), sh), "mfma_peak")
+
+    for _ in range(warmup):
+        run()
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    times.sort()
+    ms = times[len(times) // 2]
+    return ops / (ms * 1e-3) / 1e12, ms
+
+
+def ceiling_entry(torch, device, kind, achieved):
+    """The kernel's rate against the part's sustained random-operand MFMA rate of the same kind,
+    measured after the timed region (the datasheet ``roofline.peak`` assumes a clock the part holds
+    only on operands that barely toggle)."""
+    rate, _ = mfma_rate(torch, device, kind)
+    return {"mfma": MFMA_KINDS[kind][0], "operands": "random", "rate": round(rate, 1),
+            "achieved": round(achieved, 2), "frac": round(achieved / rate, 4),
+            "source": "vdnh3_mfma_peak (bench.py --workload mfma_peak)"}
+
+
+def bench_mfma_peak(args, torch, device):
+    """Sustained MFMA rate of the part for every MFMA kind on random and zero operands: the ceiling
+    the kernels' rates are read against besides the datasheet peak."""
     rates = {}
-    for kind in (0, 1, 2):
-        iters = {0: 40000, 1: 40000, 2: 20000}[kind]  # 10-20 ms per launch
-        ops = lib.vdnh3_mfma_peak_ops(kind, iters, blocks)
+    for kind, (name, peak) in MFMA_KINDS.items():
         for data in ("random", "zero"):
-            src = rand[kind] if data == "random" else torch.zeros(n, dtype=torch.uint8)
-            a = src.to(device)
-            b = src.roll(4096).to(device)
-            run = lambda: _lib.check(lib.vdnh3_mfma_peak(kind, _lib.ptr(a), _lib.ptr(b), iters, blocks,  # noqa: E731
-                                                         _lib.ptr(out), sh), "mfma_peak")
-            for _ in range(max(1, args.warmup)):
-                run()
-            times = []
-            for _ in range(max(3, args.steps)):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                run()
-                e1.record(stream)
-                torch.cuda.synchronize()
-                times.append(e0.elapsed_time(e1))
-            times.sort()
-            ms = times[len(times) // 2]
-            tops = ops / (ms * 1e-3) / 1e12
-            rates[f"{names[kind]}_{data}"] = {"T_per_s": round(tops, 1), "frac_of_peak": round(tops / peaks[kind], 4),
-                                              "ms": round(ms, 4)}
-    bf = rates["bf16_32x32x16_random"]["T_per_s"]
+            tops, ms = mfma_rate(torch, device, kind, data, reps=max(3, args.steps), warmup=max(1, args.warmup))
+            rates[f"{name}_{data}"] = {"T_per_s": round(tops, 1), "frac_of_peak": round(tops / peak, 4),
+                                       "ms": round(ms, 4)}
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
     return {
         "metric": "sustained MFMA rate (register-resident operands)",
-        "value": bf,
+        "value": rates["bf16_32x32x16_random"]["T_per_s"],
         "unit": "TFLOP/s",
         "ms_per_step": rates["bf16_32x32x16_random"]["ms"],
         "dtype": "bf16/int8/fp8",
-        "config": {"workload": "mfma_peak", "blocks": blocks, "waves_per_cu": 8, "mfmas_per_wave_iter": 8},
+        "config": {"workload": "mfma_peak", "blocks": 2 * cus, "waves_per_cu": 8, "mfmas_per_wave_iter": 8},
         "rates": rates,
     }
 
