@@ -244,7 +244,9 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
 }
 
 // One workgroup = head h, state rows (dv) 32 sl .. 32 sl + 31; wave w holds the state block of
-// dk columns 32 w .. 32 w + 31 as one 32x32 MFMA accumulator (fp32).
+// dk columns 32 w .. 32 w + 31 as one 32x32 MFMA accumulator (fp32). s_init and s_final may be the
+// same buffer: a workgroup reads its slice of s_init before anything else and writes the same slice
+// of s_final last.
 //
 // A chunk's operands reach LDS by direct-to-LDS loads (global_load_lds_dwordx4) into one of
 // two slots, issued one chunk ahead; no register staging, and the only wait is an explicit
@@ -262,7 +264,7 @@ template <int D>
 __global__ __launch_bounds__(256) void gdn_scan_kernel(
     const uint16_t *__restrict__ Wi, const uint16_t *__restrict__ Ui, const uint16_t *__restrict__ Qi,
     const uint16_t *__restrict__ Ki, const uint16_t *__restrict__ Pi, const float *__restrict__ Gi, int n_chunks,
-    int T, int heads, const float *__restrict__ s_init, float *__restrict__ s_final, uint16_t *__restrict__ out,
+    int T, int heads, const float *s_init, float *s_final, uint16_t *__restrict__ out,
     int64_t o_row, int64_t o_head) {
   static_assert(D == 128, "the scan keeps one 32-column state block per wave: head_dim 128");
   constexpr int C = kGdnC, KP = D + 8, CP = C + 8, OP = 32 + 8;
@@ -407,12 +409,32 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
 }  // namespace
 }  // namespace vdnh3
 
+namespace vdnh3 {
+namespace {
+#ifndef VDNH3_GDN_SEGMENT_BYTES
+#define VDNH3_GDN_SEGMENT_BYTES (2048ll << 20)
+#endif
+// Workspace bytes of one (chunk, head): W, U~, Q^, K^T^ ([64][D] bf16 each), P ([64][64] bf16), G (64 fp32).
+int64_t gdn_chunk_head_bytes(int head_dim) {
+  return 4 * (int64_t)kGdnC * head_dim * 2 + (int64_t)kGdnC * kGdnC * 2 + (int64_t)kGdnC * 4;
+}
+// The sequence runs in segments of this many chunks, so that the workspace stays at about
+// VDNH3_GDN_SEGMENT_BYTES (2 GiB: one segment up to ~57k tokens at 40 heads) however long the sequence.
+// Segments small enough to stay in the 256 MB last-level cache between prep and scan were measured
+// slower (2.49-3.0 ms against 2.41 at 40,688 x 40 x 128): the scan's wait is not HBM latency.
+int64_t gdn_segment_chunks(int64_t chunks, int heads, int head_dim) {
+  const int64_t seg = VDNH3_GDN_SEGMENT_BYTES / (heads * gdn_chunk_head_bytes(head_dim));
+  return seg < 1 ? 1 : (seg > chunks ? chunks : seg);
+}
+}  // namespace
+}  // namespace vdnh3
+
 extern "C" size_t vdnh3_gdn_workspace_bytes(int tokens, int heads, int head_dim) {
   if (tokens <= 0 || heads <= 0 || head_dim <= 0) return 0;
   const int64_t chunks = (tokens + vdnh3::kGdnC - 1) / vdnh3::kGdnC;
-  const int64_t per = 4 * (int64_t)vdnh3::kGdnC * head_dim * 2 + (int64_t)vdnh3::kGdnC * vdnh3::kGdnC * 2 +
-                      (int64_t)vdnh3::kGdnC * 4;
-  return (size_t)(chunks * heads * per);
+  const int64_t seg = vdnh3::gdn_segment_chunks(chunks, heads, head_dim);
+  // one segment's workspace, then the fp32 state carried between segments ([heads][D][D])
+  return (size_t)(seg * heads * vdnh3::gdn_chunk_head_bytes(head_dim) + (int64_t)heads * head_dim * head_dim * 4);
 }
 
 extern "C" int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k,
@@ -437,19 +459,33 @@ extern "C" int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_h
                    VDNH3_ERR_INVALID, "gdn: out must be 16-byte aligned with strides multiple of 8");
   constexpr int D = 128;
   const int chunks = (tokens + kGdnC - 1) / kGdnC;
-  const int64_t n = (int64_t)chunks * heads;
+  const int seg = (int)gdn_segment_chunks(chunks, heads, D);
+  const int64_t n = (int64_t)seg * heads;
   uint16_t *W = static_cast<uint16_t *>(workspace);
   uint16_t *U = W + n * GdnWs<D>::W;
   uint16_t *Qh = U + n * GdnWs<D>::U;
   uint16_t *Kt = Qh + n * GdnWs<D>::Q;
   uint16_t *P = Kt + n * GdnWs<D>::K;
   float *G = reinterpret_cast<float *>(P + n * GdnWs<D>::P);
+  float *carry = G + n * GdnWs<D>::G;  // [heads][D][D] fp32 state between segments (16-byte aligned)
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(heads, chunks), dim3(256), 0, s, q, q_row, q_head, k, k_row, k_head,
-                     v, v_row, v_head, beta, beta_row, log_decay, decay_row, tokens, heads, W, U, Qh, Kt, P, G);
-  int rc = check_launch("gdn_prep");
-  if (rc) return rc;
-  hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(heads, D / 32), dim3(256), 0, s, W, U, Qh, Kt, P, G, chunks, tokens,
-                     heads, initial_state, final_state, out, o_row, o_head);
-  return check_launch("gdn_scan");
+  // Segment by segment: the segment's tokens form an independent sequence whose initial state is the
+  // state the previous segment ended with (the chunk form restarts exactly at a chunk boundary). Each
+  // scan workgroup reads its state slice before it writes the same slice, so the carry is updated in place.
+  for (int c0 = 0; c0 < chunks; c0 += seg) {
+    const int nc = seg < chunks - c0 ? seg : chunks - c0;
+    const int64_t t0 = (int64_t)c0 * kGdnC;
+    const int nt = (int)(tokens - t0 < (int64_t)nc * kGdnC ? tokens - t0 : (int64_t)nc * kGdnC);
+    const bool first = c0 == 0, last = c0 + nc >= chunks;
+    hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(heads, nc), dim3(256), 0, s, q + t0 * q_row, q_row, q_head,
+                       k + t0 * k_row, k_row, k_head, v + t0 * v_row, v_row, v_head, beta + t0 * beta_row, beta_row,
+                       log_decay + t0 * decay_row, decay_row, nt, heads, W, U, Qh, Kt, P, G);
+    int rc = check_launch("gdn_prep");
+    if (rc) return rc;
+    hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(heads, D / 32), dim3(256), 0, s, W, U, Qh, Kt, P, G, nc, nt, heads,
+                       first ? initial_state : carry, last ? final_state : carry, out + t0 * o_row, o_row, o_head);
+    rc = check_launch("gdn_scan");
+    if (rc) return rc;
+  }
+  return VDNH3_OK;
 }

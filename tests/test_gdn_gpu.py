@@ -56,6 +56,27 @@ def test_gdn_matches_recurrence(device, tokens, heads, decay, init):
     assert s_err <= 1e-2 * s_want.abs().max().item(), s_err
 
 
+def test_gdn_split_at_chunk_boundary_is_bit_identical(device):
+    """A sequence run as two calls, the second starting at a chunk boundary from the first call's final
+    state, gives the same bits as one call: the restart the library's segmented long-sequence path makes
+    (a segment is an independent sequence whose initial state is the state the previous one ended with)."""
+    from vdn_h3_amd.gdn import chunk_gated_delta_rule
+
+    tokens, heads, split = 1000, 3, 384  # split at chunk 6 of 16; the tail ends in a partial chunk
+    print(f"case gdn split T={tokens} H={heads} at {split}", flush=True)
+    q, k, v, beta, lg = _inputs(tokens, heads, 11, 0.05)
+    s0 = torch.randn(heads, 128, 128, generator=torch.Generator().manual_seed(8)) * 0.1
+    dq, dk, dv, db, dg, ds0 = (t.to(device) for t in (q, k, v, beta, lg, s0))
+    whole, s_whole = chunk_gated_delta_rule(dq, dk, dv, db, dg, initial_state=ds0, output_final_state=True)
+    head, s_mid = chunk_gated_delta_rule(dq[:split], dk[:split], dv[:split], db[:split], dg[:split],
+                                         initial_state=ds0, output_final_state=True)
+    tail, s_tail = chunk_gated_delta_rule(dq[split:], dk[split:], dv[split:], db[split:], dg[split:],
+                                          initial_state=s_mid, output_final_state=True)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat([head, tail]).cpu(), whole.cpu())
+    assert torch.equal(s_tail.cpu(), s_whole.cpu())
+
+
 def test_gdn_full_shape_sampled_heads(device):
     """40,688 tokens x 40 heads (the chunk-64 benchmark shape); heads 0 and 39 against the oracle."""
     from vdn_h3_amd.gdn import chunk_gated_delta_rule
