@@ -68,6 +68,9 @@ def _parse():
     ap.add_argument("--rope", default="on", choices=["on", "off"],
                     help="block / stack workloads: hand every block a per-row split-half RoPE table "
                          "(rot_dim = head_dim), as a DiT does, or no rope_freqs")
+    ap.add_argument("--branch-execution", default="serial", choices=["serial", "parallel"],
+                    help="block / stack workloads: the VDN branch after the attention on the same stream "
+                         "(serial) or beside it on a second stream, joined at to_out_linear (parallel)")
     ap.add_argument("--cpu-sample-rows", type=int, default=2304,
                     help="query rows of the CPU-oracle baseline sample (0 disables it)")
     ap.add_argument("--traffic-json", default=str(ROOT / "profiles" / "traffic.json"),
@@ -225,7 +228,8 @@ def bench_block(args, torch, device):
     heads, dim, hidden = w.heads, w.head_dim, 5120
     x = synth.randn((lay.seq_len, hidden), 0, device=device, dtype=torch.bfloat16)
     conv = _short_conv(args)
-    state, (forward,) = synth.hybrid_stack(1, heads, dim, hidden, device, short_conv=conv, precision="int8")
+    state, (forward,) = synth.hybrid_stack(1, heads, dim, hidden, device, short_conv=conv, precision="int8",
+                                           branch_execution=args.branch_execution)
     state.diagnostics.enabled = True
     freqs = synth.rope_freqs(lay.seq_len, dim, device) if args.rope == "on" else None
     stream = torch.cuda.current_stream(device)
@@ -262,7 +266,7 @@ def bench_block(args, torch, device):
                    "radius": w.radius, "anchor_frames": lay.anchor_frames,
                    "projections": "W8A8 int8 qkv/out/to_out_linear (per-token x per-channel)",
                    "rope": _rope_desc(args, dim),
-                   "branch_short_conv": ",".join(conv) or "none",
+                   "branch_short_conv": ",".join(conv) or "none", "branch_execution": args.branch_execution,
                    "allowed_pairs_per_head": plan.pairs_per_head, "work_per_step": work,
                    "work_total": total},
         "roofline": {"bound": "mfma", "kernel": "window_attn_kernel<128,%s>" % ("false" if freqs is not None else "true"), "achieved": round(attn_tflops, 2),
@@ -277,7 +281,9 @@ def bench_block(args, torch, device):
             "window_attention": {"achieved_TFLOPs": round(attn_tflops, 1),
                                  "frac_bf16_peak": round(attn_tflops / PEAK_BF16_TFLOPS, 4)},
         },
-        "linear_to_softmax_ratio": round(stages["attention.linear_branch"] / stages["attention.softmax"], 4),
+        "linear_to_softmax_ratio": round((stages["attention.linear_branch"]
+                                          + stages.get("attention.branch_projection", 0.0))
+                                         / stages["attention.softmax"], 4),
         "roofline_vs_sustained_mfma": ceiling_entry(torch, device, 0, attn_tflops),
     }
 
@@ -291,7 +297,8 @@ def bench_stack(args, torch, device):
     lay = w.layout
     heads, dim, hidden, blocks = w.heads, w.head_dim, 5120, 50
     conv = _short_conv(args)
-    state, forwards = synth.hybrid_stack(blocks, heads, dim, hidden, device, short_conv=conv, precision="int8")
+    state, forwards = synth.hybrid_stack(blocks, heads, dim, hidden, device, short_conv=conv, precision="int8",
+                                         branch_execution=args.branch_execution)
     x0 = synth.randn((lay.seq_len, hidden), 0, device=device, dtype=torch.bfloat16)
     freqs = synth.rope_freqs(lay.seq_len, dim, device) if args.rope == "on" else None
     stream = torch.cuda.current_stream(device)
@@ -322,6 +329,7 @@ def bench_stack(args, torch, device):
         "config": {"workload": "stack_50blocks_s40688_h40_d128_hidden5120_int8proj", "blocks": blocks,
                    "denoising_steps": args.steps, "seq_len": lay.seq_len, "heads": heads, "head_dim": dim,
                    "hidden": hidden, "branch_short_conv": ",".join(conv) or "none", "rope": _rope_desc(args, dim),
+                   "branch_execution": args.branch_execution,
                    "residual": "x <- x + block(rms_norm(x)) per block (bf16, torch rms_norm)", "work_per_block": per_block},
         "total_ms": round(total_ms, 2),
         "step_ms": [round(v, 3) for v in step_ms],

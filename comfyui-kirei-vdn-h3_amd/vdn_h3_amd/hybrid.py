@@ -66,17 +66,25 @@ def _block_weight_maps(branches: Sequence[Any], weight_maps) -> list:
     raise ValueError(f"{len(maps)} weight maps were given for {len(branches)} branches")
 
 
+# How the VDN branch runs beside the window attention (vdn_h3/nodes.py:26): "serial" on the caller's
+# stream after the attention, "parallel" on a second stream of the same device from the qkv projection
+# on, joined at the to_out_linear accumulation.
+BRANCH_EXECUTION_MODES = ("serial", "parallel")
+
+
 class VDNState:
     """Runtime state of one patched model: config, per-block branches and weights, plan cache."""
 
     def __init__(self, name: str, config: Mapping[str, Any], branches: Sequence[Any], num_heads: int,
                  head_dim: int, *, attention_backend: str = "hip", weight_maps=None, inference: bool = True,
                  projection_precision: str = "bf16", projection_info: Any = None, diagnostics: bool = False,
-                 block_fusion: bool = False, **_runtime):
+                 block_fusion: bool = False, branch_execution: str = "serial", **_runtime):
         if attention_backend not in _window.ATTENTION_BACKENDS:
             raise ValueError(f"unsupported attention backend {attention_backend!r}")
         if projection_precision not in _projection.PROJECTION_PRECISIONS:
             raise ValueError(f"unsupported projection precision {projection_precision!r}")
+        if branch_execution not in BRANCH_EXECUTION_MODES:
+            raise ValueError(f"unknown branch execution mode {branch_execution!r}")
         self.name = str(name)
         self.config = dict(config)
         self.cfg = self.config
@@ -91,7 +99,8 @@ class VDNState:
         self.forwards = 0
         self.last_attention_backend = None
         self.last_layout = None
-        self.branch_execution = "serial"
+        self.branch_execution = branch_execution
+        self._branch_streams: dict[Any, torch.cuda.Stream] = {}
         self.diagnostics = DiagnosticsRecorder(diagnostics)
         self.block_fusion = bool(block_fusion)
         self._maps = _block_weight_maps(self.branches, weight_maps)
@@ -134,7 +143,18 @@ class VDNState:
             raise RuntimeError("VDN projection state contains neither BF16 nor quantized weight")
         return weights, lambda rows, **kw: _projection.project(rows, weights, **kw)
 
+    def branch_stream(self, device) -> torch.cuda.Stream:
+        """The stream of the parallel branch execution on ``device`` (default priority), one per device."""
+        device = torch.device(device)
+        stream = self._branch_streams.get(device)
+        if stream is None:
+            stream = self._branch_streams[device] = torch.cuda.Stream(device=device)
+        return stream
+
     def release(self):
+        for stream in self._branch_streams.values():
+            stream.synchronize()
+        self._branch_streams.clear()
         self._resident.clear()
         self.__dict__.pop("_gate_branch_cache", None)
         self.window_cache.release()
@@ -274,6 +294,11 @@ class _VDNBlockForward:
         with scope("attention.gate", device):
             gate, proj_rows = self._gate(x, weights, with_branch)
         plan = self._plan(layout, device)
+        pending = None
+        if with_branch and state.branch_execution == "parallel" and hasattr(self.branch, "branch_rows"):
+            # the branch reads only x, the raw q / k / v and its projections, none of which the attention
+            # below writes: it runs on a second stream and joins at the to_out_linear accumulation
+            pending = self._start_branch(x, q_raw, k_raw, value, layout, weights, proj_rows)
         with scope("attention.softmax", device):
             # q_norm / k_norm (+ RoPE) run inside the attention: the keys in its pre-pass, each query
             # row as the kernel loads it; the branch reads the raw q / k
@@ -285,27 +310,58 @@ class _VDNBlockForward:
         with scope("attention.out_proj", device):
             out = attn.out_proj(attended.view(layout.seq_len, heads * head_dim))
         del attended
-        if with_branch:
+        if pending is not None:
+            self._finish_branch(out, layout, *pending)
+        elif with_branch:
             self._add_branch(out, x, q_raw, k_raw, value, layout, weights, proj_rows)
         return out
 
-    def _add_branch(self, out, x, q_raw, k_raw, value, layout, weights, proj_rows):
-        """``out[video] += to_out_linear(branch)``, accumulated by the projection GEMM's epilogue."""
+    def _branch_args(self, x, q_raw, k_raw, value, layout, weights, proj_rows):
         video = slice(layout.video_start, layout.video_end)
         text = slice(layout.text_start, layout.text_start + layout.text_len)
         use_text = bool(getattr(self.branch, "enable_text_state",
                                 self.state.config.get("enable_text_state", False)))
         branch_weights, projector = self.state.projection_view(weights)
-        extra = {}
+        kwargs = dict(frame_size=layout.frame_size, text_x=x[text] if use_text else None,
+                      text_k_raw=k_raw[text] if use_text else None, text_v_raw=value[text] if use_text else None,
+                      skip_ends=(layout.anchor_frames == "both"))
         if proj_rows is not None:
-            extra = {"proj_rows": proj_rows[video], "text_proj_rows": proj_rows[text] if use_text else None}
+            kwargs.update(proj_rows=proj_rows[video], text_proj_rows=proj_rows[text] if use_text else None)
+        args = (branch_weights, x[video], q_raw[video], k_raw[video], value[video], layout.num_frames,
+                layout.tokens_per_frame, layout.bounds)
+        return args, kwargs, projector
+
+    def _start_branch(self, x, q_raw, k_raw, value, layout, weights, proj_rows):
+        """The branch up to its gated readout rows, on the state's branch stream (the reference's
+        ``branch_execution="parallel"``, ``vdn_h3/parallel.py:79-247``). Returns what the join needs."""
+        main = torch.cuda.current_stream(x.device)
+        side = self.state.branch_stream(x.device)
+        side.wait_stream(main)  # qkv, the gate GEMM's beta / down-projection rows
+        args, kwargs, projector = self._branch_args(x, q_raw, k_raw, value, layout, weights, proj_rows)
+        with torch.cuda.stream(side):
+            with self.state.diagnostics.scope("attention.linear_branch", x.device):
+                rows, sl = self.branch.branch_rows(*args, **kwargs)
+            done = torch.cuda.Event()
+            done.record(side)
+        return rows, sl, projector, done
+
+    def _finish_branch(self, out, layout, rows, sl, projector, done):
+        """``out[video][sl] += to_out_linear(rows)`` on the caller's stream once the branch stream is done."""
+        main = torch.cuda.current_stream(out.device)
+        main.wait_event(done)
+        if rows is None:
+            return
+        rows.record_stream(main)  # allocated on the branch stream, read here
+        video = out[layout.video_start:layout.video_end]
+        with self.state.diagnostics.scope("attention.branch_projection", out.device):
+            projector(rows, out=video[sl], accumulate=True)
+
+    def _add_branch(self, out, x, q_raw, k_raw, value, layout, weights, proj_rows):
+        """``out[video] += to_out_linear(branch)``, accumulated by the projection GEMM's epilogue."""
+        args, kwargs, projector = self._branch_args(x, q_raw, k_raw, value, layout, weights, proj_rows)
         with self.state.diagnostics.scope("attention.linear_branch", x.device):
-            self.branch.projected_delta(
-                branch_weights, x[video], q_raw[video], k_raw[video], value[video], layout.num_frames,
-                layout.tokens_per_frame, layout.bounds, frame_size=layout.frame_size,
-                text_x=x[text] if use_text else None, text_k_raw=k_raw[text] if use_text else None,
-                text_v_raw=value[text] if use_text else None, skip_ends=(layout.anchor_frames == "both"),
-                inference=True, projector=projector, out=out[video], accumulate=True, **extra)
+            self.branch.projected_delta(*args, inference=True, projector=projector,
+                                        out=out[layout.video_start:layout.video_end], accumulate=True, **kwargs)
 
 
 def make_vdn_forward(attn: Any, state: VDNState, block_index: int):

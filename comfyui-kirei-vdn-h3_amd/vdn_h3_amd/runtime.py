@@ -212,25 +212,41 @@ class OptimizedLinearBranch:
             out = torch.empty((original_rows, hidden), dtype=torch.bfloat16, device=xv.device)
         elif out.shape != (original_rows, hidden):
             raise ValueError(f"out must be [{original_rows}, {hidden}]")
+        flat, rows = self.branch_rows(weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds,
+                                      frame_size=frame_size, text_x=text_x, text_k_raw=text_k_raw,
+                                      text_v_raw=text_v_raw, skip_ends=skip_ends, proj_rows=proj_rows,
+                                      text_proj_rows=text_proj_rows)
+        if flat is None:
+            return out if accumulate else _b.fill_rows(out)
+        if not accumulate and rows != slice(0, original_rows):
+            _b.fill_rows(out[:rows.start])
+            _b.fill_rows(out[rows.stop:])
+        proj(flat, out=out[rows], accumulate=accumulate)
+        return out
+
+    def branch_rows(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, *,
+                    frame_size=None, text_x=None, text_k_raw=None, text_v_raw=None, skip_ends=False,
+                    proj_rows=None, text_proj_rows=None):
+        """``(rows, sl)``: the branch's gated readout ``[n, heads * head_dim]`` bf16, the input of
+        ``to_out_linear``, and the slice of ``xv``'s rows it belongs to; ``(None, None)`` when no row
+        carries a delta (``skip_ends`` with at most two frames). ``projected_delta`` is
+        ``to_out_linear`` of these rows, with zero rows elsewhere; the block's parallel branch execution
+        computes them on a second stream and projects them after the attention."""
+        self._check(xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds)
         t = tokens_per_frame
         if skip_ends:
             if num_frames <= 2:
-                return out if accumulate else _b.fill_rows(out)
+                return None, None
             inner = slice(t, (num_frames - 1) * t)
-            if not accumulate:
-                _b.fill_rows(out[:t])
-                _b.fill_rows(out[(num_frames - 1) * t:])
             flat = self._readout_flat(weights, xv[inner], q_raw[inner], k_raw[inner], v_raw[inner],
                                       num_frames - 2, t, [(lo - 1, hi - 1) for lo, hi in bounds[1:-1]], text_x,
                                       text_k_raw, text_v_raw, frame_size,
                                       proj_rows=None if proj_rows is None else proj_rows[inner],
                                       text_proj_rows=text_proj_rows)
-            proj(flat, out=out[inner], accumulate=accumulate)
-            return out
+            return flat, inner
         flat = self._readout_flat(weights, xv, q_raw, k_raw, v_raw, num_frames, t, bounds, text_x, text_k_raw,
                                   text_v_raw, frame_size, proj_rows=proj_rows, text_proj_rows=text_proj_rows)
-        proj(flat, out=out, accumulate=accumulate)
-        return out
+        return flat, slice(0, num_frames * t)
 
 
 __all__ = ["OptimizedLinearBranch"]

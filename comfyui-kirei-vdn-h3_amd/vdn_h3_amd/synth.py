@@ -142,9 +142,10 @@ def attention_module(heads: int, head_dim: int, hidden: int, device, seed: int, 
 
 
 def hybrid_stack(blocks: int, heads: int, head_dim: int, hidden: int, device, *, short_conv=("k", "v"),
-                 precision: str = "int8", config=None, first_seed: int = 1000):
+                 precision: str = "int8", config=None, first_seed: int = 1000, branch_execution: str = "serial"):
     """``(state, forwards)``: ``blocks`` random-init VDN-H3 hybrid attention blocks (block i seeded from
-    ``first_seed * (i + 1)``), branch and projections prepared for ``precision``, one ``VDNState``."""
+    ``first_seed * (i + 1)``), branch and projections prepared for ``precision``, one ``VDNState``
+    (``branch_execution`` "serial" or "parallel", the VDN branch on a second stream)."""
     from . import projection
     from .hybrid import VDNState, make_vdn_forward
     from .runtime import OptimizedLinearBranch
@@ -160,7 +161,8 @@ def hybrid_stack(blocks: int, heads: int, head_dim: int, hidden: int, device, *,
     branches = [OptimizedLinearBranch(bw, heads, head_dim, short_conv=short_conv) for bw in maps]
     cfg = {"enable_softmax_gate": True, "linear_enabled": True, "enable_text_state": True}
     cfg.update(config or {})
-    state = VDNState("hybrid-stack", cfg, branches, heads, head_dim, projection_precision=precision)
+    state = VDNState("hybrid-stack", cfg, branches, heads, head_dim, projection_precision=precision,
+                     branch_execution=branch_execution)
     return state, [make_vdn_forward(attn, state, i) for i, attn in enumerate(attns)]
 
 

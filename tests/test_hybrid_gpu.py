@@ -45,15 +45,15 @@ def _attn(aw, heads, dim, device, precision="bf16"):
         k_norm=SimpleNamespace(weight=aw["k_norm.weight"].to(device), eps=1e-6))
 
 
-def _block(aw, bw, heads, dim, device, precision="bf16", config=None):
+def _block(aw, bw, heads, dim, device, precision="bf16", config=None, branch_execution="serial", short_conv=()):
     from vdn_h3_amd.hybrid import VDNState, make_vdn_forward
     from vdn_h3_amd.runtime import OptimizedLinearBranch
 
     attn = _attn(aw, heads, dim, device, precision)
-    branch = OptimizedLinearBranch(bw, heads, dim, short_conv=(), enable_text_state=True)
+    branch = OptimizedLinearBranch(bw, heads, dim, short_conv=short_conv, enable_text_state=True)
     cfg = {"enable_softmax_gate": True, "linear_enabled": True, "enable_text_state": True}
     cfg.update(config or {})
-    state = VDNState("test", cfg, [branch], heads, dim)
+    state = VDNState("test", cfg, [branch], heads, dim, branch_execution=branch_execution)
     return make_vdn_forward(attn, state, 0), state
 
 
@@ -136,6 +136,32 @@ def test_block_int8_projections_vs_oracle(device):
                           project_out=int8_project(aw["out_proj.weight"]),
                           branch_projector=int8_project(bw["to_out_linear.weight"]))
     _parity(out, want, "block int8 vs oracle")
+
+
+@pytest.mark.parametrize("anchors", ["both", "none"])
+def test_parallel_branch_execution_is_bit_identical(device, anchors):
+    """branch_execution="parallel" (the branch on a second stream, joined at the to_out_linear
+    accumulation) gives the serial block's bits, with anchor rows skipped or not, int8 projections and
+    the k/v short convolutions; twice in a row, so the second call reuses the branch stream."""
+    from vdn_h3_amd import projection, synth
+    from vdn_h3_amd.layout import text_first_layout
+
+    print(f"case hybrid block parallel branch execution anchors={anchors}", flush=True)
+    heads, dim, hidden = 4, 128, 512
+    _, x, aw, _ = _synthetic(13, (16, 16), 64, heads, dim, hidden, seed=9)
+    layout = text_first_layout(64, 13, (16, 16), anchor_frames=anchors)
+    bw = synth.branch_weights(heads, dim, hidden, seed=109, short_conv=("k", "v"))
+    dbw = {k: v.to(device) for k, v in bw.items()}
+    (qbw,), _ = projection.prepare_projection_maps([dbw], device, "int8")
+    outs = {}
+    for mode in ("serial", "parallel"):
+        forward, state = _block(aw, qbw, heads, dim, device, precision="int8", branch_execution=mode,
+                                short_conv=("k", "v"))
+        outs[mode] = [_run(forward, x.to(device), layout).cpu() for _ in range(2)]
+        state.release()
+    assert torch.equal(outs["serial"][0], outs["serial"][1])
+    for got in outs["parallel"]:
+        assert torch.equal(got, outs["serial"][0])
 
 
 def test_gate_off_and_branch_off(device):
