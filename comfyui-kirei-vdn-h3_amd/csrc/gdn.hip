@@ -127,13 +127,17 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
   }
   __syncthreads();
 
-  // T = (I + A)^-1 (unit lower triangular) by 16 x 16 blocks, in fp32. T[i][j] (i > j) is kept
-  // transposed in the upper triangle of As (at As[j][i]), A stays in the lower one. The diagonal
-  // blocks come from forward substitution (wave I, lane c: column c of block I); the blocks
+  // T = (I + A)^-1 (unit lower triangular) by 16 x 16 blocks, in fp32. T[i][j] (block of i at or
+  // below the block of j) is kept transposed in As at As[j][i]: the blocks below the diagonal in
+  // the upper triangle, the diagonal blocks whole (unit diagonal, zeros above it) in place of A's
+  // diagonal blocks, which only their own solve reads. The diagonal blocks come from forward
+  // substitution (wave I, lane c: column c of block I, stored as row 16 I + c of As); the blocks
   // below follow by distance d = I - J from the diagonal:
   //   X = sum_{K=J}^{I-1} A_IK T_KJ,   T_IJ = -T_II X
-  // with X in the (now free) P staging area.
-  auto t_at = [&](int i, int j) __device__ { return As[j * AP + i]; };  // T[i][j], i > j
+  // so X[r][c] is the dot product of As rows 16 I + r (A) and 16 J + c (T^T) over columns
+  // 16 J .. 16 I - 1, and X sits in the (now free) Q staging area. Every load is unconditional:
+  // no branch keeps the compiler from issuing them early.
+  auto t_at = [&](int i, int j) __device__ { return As[j * AP + i]; };  // T[i][j], block(i) >= block(j)
   if (lane < 16) {
     const int I = wave, cc = lane;
     float t[16];
@@ -143,10 +147,13 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
 #pragma unroll
       for (int m = 0; m < r; ++m) acc = fmaf(As[(16 * I + r) * AP + 16 * I + m], t[m], acc);
       t[r] = r == cc ? 1.f : (r < cc ? 0.f : -acc);
-      if (r > cc) As[(16 * I + cc) * AP + 16 * I + r] = t[r];
     }
+    // after every read of the block (program order within the wave)
+    f32x4_t *row = reinterpret_cast<f32x4_t *>(As + (16 * I + cc) * AP + 16 * I);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) row[q] = f32x4_t{t[4 * q], t[4 * q + 1], t[4 * q + 2], t[4 * q + 3]};
   }
-  float *Xs = reinterpret_cast<float *>(Ps);  // [block][16][16]
+  float *Xs = reinterpret_cast<float *>(Qs);  // [block][16][16]
   const int br = tid >> 4, bc = tid & 15;     // this thread's element of every 16 x 16 block
 #pragma unroll
   for (int d = 1; d < 4; ++d) {
@@ -154,16 +161,16 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
 #pragma unroll
     for (int b = 0; b < 4 - d; ++b) {
       const int I = d + b, J = b;
+      const f32x4_t *ra = reinterpret_cast<const f32x4_t *>(As + (16 * I + br) * AP + 16 * J);
+      const f32x4_t *rt = reinterpret_cast<const f32x4_t *>(As + (16 * J + bc) * AP + 16 * J);
       float x = 0.f;
 #pragma unroll
-      for (int K = J; K < I; ++K) {
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-          float tv;  // T[16 K + m][16 J + bc]
-          if (K > J) tv = t_at(16 * K + m, 16 * J + bc);
-          else tv = m == bc ? 1.f : (m > bc ? t_at(16 * J + m, 16 * J + bc) : 0.f);
-          x = fmaf(As[(16 * I + br) * AP + 16 * K + m], tv, x);
-        }
+      for (int q = 0; q < 4 * d; ++q) {
+        const f32x4_t a4 = ra[q], t4 = rt[q];
+        x = fmaf(a4[0], t4[0], x);
+        x = fmaf(a4[1], t4[1], x);
+        x = fmaf(a4[2], t4[2], x);
+        x = fmaf(a4[3], t4[3], x);
       }
       Xs[(b * 16 + br) * 16 + bc] = x;
     }
@@ -173,8 +180,10 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
       const int I = d + b, J = b;
       float y = Xs[(b * 16 + br) * 16 + bc];
 #pragma unroll
-      for (int m = 0; m < 15; ++m)
-        if (m < br) y = fmaf(t_at(16 * I + br, 16 * I + m), Xs[(b * 16 + m) * 16 + bc], y);
+      for (int m = 0; m < 15; ++m) {
+        const float tm = t_at(16 * I + br, 16 * I + m);  // T_II[br][m], the unit diagonal left out
+        y = fmaf(m < br ? tm : 0.f, Xs[(b * 16 + m) * 16 + bc], y);
+      }
       As[(16 * J + bc) * AP + 16 * I + br] = -y;
     }
   }
@@ -190,7 +199,8 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
       const int j = 8 * jc + jj;
-      const float tv = j == i ? 1.f : (j < i ? t_at(i, j) : 0.f);
+      const float ta = t_at(i, j);  // A[j][i] when block(j) > block(i): read always, then dropped
+      const float tv = (j >> 4) > (i >> 4) ? 0.f : ta;
       v8[jj] = tv * Bs[j];
       w[jj] = v8[jj] * Eg[j];
     }
