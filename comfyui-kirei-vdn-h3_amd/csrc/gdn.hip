@@ -11,11 +11,11 @@
 // gdn_prep_kernel (grid heads x chunks, fully parallel): K K^T and Q K^T on bf16 MFMA; the
 // inverse T = (I + A)^-1 in fp32 by 16 x 16 blocks, then W = T diag(b e^G) K and U~ = T diag(b) V
 // on bf16 MFMA (T's scaled columns rounded to bf16); writes W, U~, Q^ = e^G Q,
-// K^T^ = (e^{G_C - G} K)^T, P = Q K^T o D (bf16) and G (fp32) for each chunk, every output
-// through LDS as 16-byte stores.
+// K^ = e^{G_C - G} K, P = Q K^T o D (bf16, each in the fragment order of the scan wavefront
+// that reads it) and G (fp32) for each chunk, as 16-byte stores.
 // gdn_scan_kernel (grid heads x dv/32, sequential over chunks): one workgroup carries a 32-row
 // slice of the state in MFMA accumulators (fp32); per chunk U = U~ - W S^T, O = Q^ S^T + P U and
-// S = e^{G_C} S + U^T K^, with the next chunk's operands loaded straight into LDS during the step.
+// S = e^{G_C} S + U^T K^, each wavefront loading its operands into registers two chunks ahead.
 #include "common.h"
 
 namespace vdnh3 {
@@ -27,6 +27,19 @@ template <int D>
 struct GdnWs {  // per (chunk, head) workspace element counts
   static constexpr int64_t W = (int64_t)kGdnC * D, U = W, Q = W, K = W, P = (int64_t)kGdnC * kGdnC, G = kGdnC;
 };
+
+// The workspace holds each block in the fragment order of the scan wavefront that reads it, so
+// that a wavefront's 16-byte fragment pieces lie in lane order (1 KB per load instruction):
+//  - W, Q^ (A operands, 8 k-steps) and P (4 k-steps): piece p of the block is lane p % 64 of
+//    k-step (p / 64) % steps of row block p / (64 steps): row 32 (p / (64 steps)) + p % 32,
+//    columns 16 ((p / 64) % steps) + 8 ((p / 32) % 2) .. + 7;
+//  - K^ = e^{G_C - G} K (B operand of state block w): piece ((w, s), lane) holds tokens
+//    16 s + 8 (lane / 32) .. + 7 of column 32 w + lane % 32;
+//  - U~ (state slice sl, row block tb, half j): piece ((sl, tb, j), lane) holds, at element
+//    4 i + e, row 32 tb + 8 (2 j + i) + 4 (lane / 32) + e of column 32 sl + lane % 32 (the layout
+//    of a 32x32 MFMA accumulator, elements 8 j .. 8 j + 7).
+__device__ __forceinline__ int gdn_a_row(int p, int steps = 8) { return 32 * (p / (64 * steps)) + (p & 31); }
+__device__ __forceinline__ int gdn_a_col(int p, int steps = 8) { return 16 * ((p >> 6) % steps) + 8 * ((p >> 5) & 1); }
 
 template <int D>
 __global__ __launch_bounds__(256) void gdn_prep_kernel(
@@ -94,16 +107,16 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
   }
   __syncthreads();
 
-  // Q^ = e^G Q (rows), K^T^ = (e^{G_C - G} K)^T ([D][C]) and P: 16-byte stores, before the
-  // solve overwrites Ks
+  // Q^ = e^G Q, K^ = e^{G_C - G} K and P in the scan's fragment order (gdn_a_row): 16-byte
+  // stores in piece order, before the solve overwrites Ks
   {
     uint16_t *qc = Qo + ch * GdnWs<D>::Q, *kc = Ko + ch * GdnWs<D>::K, *pc = Po + ch * GdnWs<D>::P;
 #pragma unroll
     for (int u = 0; u < C * CH / 256; ++u) {
-      const int e = tid + 256 * u, r = e / CH, cc = e - r * CH;
-      const u32x4_t x = ld16(Qs + r * KP + 8 * cc);
+      const int p = tid + 256 * u, r = gdn_a_row(p), k0 = gdn_a_col(p);
+      const u32x4_t x = ld16(Qs + r * KP + k0);
       const float sc = Eg[r];
-      st16(qc + r * D + 8 * cc,
+      st16(qc + 8 * p,
            u32x4_t{pack_bf2(bf2f((uint16_t)x[0]) * sc, bf2f((uint16_t)(x[0] >> 16)) * sc),
                    pack_bf2(bf2f((uint16_t)x[1]) * sc, bf2f((uint16_t)(x[1] >> 16)) * sc),
                    pack_bf2(bf2f((uint16_t)x[2]) * sc, bf2f((uint16_t)(x[2] >> 16)) * sc),
@@ -115,13 +128,14 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
       float y[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] = bf2f(Ks[(8 * tc + j) * KP + d]) * Ec[8 * tc + j];
-      st16(kc + d * C + 8 * tc,
+      // K^ as the B operand of wave d / 32: piece (d / 32, tc / 2, lane 32 (tc & 1) + d % 32)
+      st16(kc + 8 * ((((d >> 5) * 4 + (tc >> 1)) << 6) + 32 * (tc & 1) + (d & 31)),
            u32x4_t{pack_bf2(y[0], y[1]), pack_bf2(y[2], y[3]), pack_bf2(y[4], y[5]), pack_bf2(y[6], y[7])});
     }
 #pragma unroll
     for (int u = 0; u < C * (C / 8) / 256; ++u) {
-      const int e = tid + 256 * u, r = e >> 3, cc = e & 7;
-      st16(pc + r * C + 8 * cc, ld16(Ps + r * PP + 8 * cc));
+      const int p = tid + 256 * u, r = gdn_a_row(p, C / 16), j0 = gdn_a_col(p, C / 16);
+      st16(pc + 8 * p, ld16(Ps + r * PP + j0));
     }
     if (tid < C) Go[ch * GdnWs<D>::G + tid] = Gs[tid];
   }
@@ -232,92 +246,89 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
         au[mb] = mfma_bf16_32x32x16(as_bf16x8(ld16(Tu + off)), bv, au[mb]);
       }
     }
-    __syncthreads();  // every read of Ks / Vs is done: W and U~ replace them
+    // U~ leaves from the accumulators: wave w's block is the scan's state slice w, and its
+    // accumulator element 8 j + e of row block mb is exactly piece ((w, mb, j), lane) element e
+    uint16_t *uc = Uo + ch * GdnWs<D>::U;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f32x16_t &a = au[mb];
+        st16(uc + 8 * ((((wave * 2 + mb) * 2 + j) << 6) + lane),
+             u32x4_t{pack_bf2(a[8 * j], a[8 * j + 1]), pack_bf2(a[8 * j + 2], a[8 * j + 3]),
+                     pack_bf2(a[8 * j + 4], a[8 * j + 5]), pack_bf2(a[8 * j + 6], a[8 * j + 7])});
+      }
+    __syncthreads();  // every read of Ks is done: W replaces it
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = 32 * mb + 8 * (i >> 2) + 4 * gl + (i & 3);
         Ks[r * KP + 32 * wave + l32] = f2bf(aw[mb][i]);
-        Vs[r * KP + 32 * wave + l32] = f2bf(au[mb][i]);
       }
   }
   __syncthreads();
   {
-    uint16_t *wc = Wo + ch * GdnWs<D>::W, *uc = Uo + ch * GdnWs<D>::U;
+    uint16_t *wc = Wo + ch * GdnWs<D>::W;
 #pragma unroll
-    for (int u = 0; u < 2 * C * CH / 256; ++u) {
-      const int e = tid + 256 * u, which = e / (C * CH), x = e - which * (C * CH), r = x / CH, cc = x - r * CH;
-      st16((which ? uc : wc) + r * D + 8 * cc, ld16((which ? Vs : Ks) + r * KP + 8 * cc));
+    for (int u = 0; u < C * CH / 256; ++u) {
+      const int p = tid + 256 * u;
+      st16(wc + 8 * p, ld16(Ks + gdn_a_row(p) * KP + gdn_a_col(p)));
     }
   }
 }
 
-// One workgroup = head h, state rows (dv) 32 sl .. 32 sl + 31; wave w holds the state block of
-// dk columns 32 w .. 32 w + 31 as one 32x32 MFMA accumulator (fp32). s_init and s_final may be the
-// same buffer: a workgroup reads its slice of s_init before anything else and writes the same slice
-// of s_final last.
+// One workgroup = head h, state rows (dv) 32 sl .. 32 sl + 31, four wavefronts: waves 0, 1 form
+// tokens 32 w .. 32 w + 31 of U = U~ - W S^T, waves 2, 3 tokens 32 (w - 2) .. of O = Q^ S^T + P U,
+// and wave w carries the state block of dk columns 32 w .. 32 w + 31 as one 32x32 MFMA
+// accumulator (fp32), S = e^{G_C} S + U^T K^. s_init and s_final may be the same buffer: a
+// workgroup reads its slice of s_init before anything else and writes the same slice of s_final
+// last.
 //
-// A chunk's operands reach LDS by direct-to-LDS loads (global_load_lds_dwordx4) into one of
-// two slots, issued one chunk ahead; no register staging, and the only wait is an explicit
-// vmcnt(0) at the end of each step. A slot is [W | Q^ | K^T^ | P | U~ slice | G], unpadded;
-// 16-byte chunk c of row r sits at chunk position c ^ swizzle(r) (16 chunks per row: r & 15;
-// 8 per row: (r >> 1) & 7), so the 16 lanes of an MFMA fragment read 16 different bank groups.
-// Wave instruction i (0..59, i = 4 u + wave) fills slot bytes 1024 i .. 1024 i + 1023; lane L
-// loads the source chunk that lands at piece 64 i + L. The outputs of chunk c go to LDS (Os)
-// in step c and to global memory at the start of step c + 1 (one 16-byte store per thread).
-constexpr int kScanSlotBytes = 3 * 64 * 128 * 2 + 64 * 64 * 2 + 64 * 32 * 2 + 64 * 4;  // 61,696
-__device__ __forceinline__ int swz16(int r, int c) { return c ^ (r & 15); }
-__device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }
-
+// Every wavefront reads only its own part of a chunk's operands (half of W or of Q^ and P, its
+// U~ rows, its K^ block), stored in its fragment order, so each wavefront loads them straight
+// into registers (1 KB per load instruction), two chunks ahead: a ring of three register sets,
+// which keeps two chunks' loads in flight behind the step that computes. The state's bf16 copy
+// (Sb) and U (Ut, transposed) are exchanged through LDS; the outputs of chunk c go to LDS (Os) in
+// step c and to global memory at the start of step c + 1 (one 16-byte store per thread).
 template <int D>
 __global__ __launch_bounds__(256) void gdn_scan_kernel(
-    const uint16_t *__restrict__ Wi, const uint16_t *__restrict__ Ui, const uint16_t *__restrict__ Qi,
-    const uint16_t *__restrict__ Ki, const uint16_t *__restrict__ Pi, const float *__restrict__ Gi, int n_chunks,
+    const u32x4_t *__restrict__ Wi, const u32x4_t *__restrict__ Ui, const u32x4_t *__restrict__ Qi,
+    const u32x4_t *__restrict__ Ki, const u32x4_t *__restrict__ Pi, const float *__restrict__ Gi, int n_chunks,
     int T, int heads, const float *s_init, float *s_final, uint16_t *__restrict__ out,
     int64_t o_row, int64_t o_head) {
   static_assert(D == 128, "the scan keeps one 32-column state block per wave: head_dim 128");
   constexpr int C = kGdnC, KP = D + 8, CP = C + 8, OP = 32 + 8;
-  constexpr int OFF_Q = 64 * 128 * 2, OFF_K = 2 * OFF_Q, OFF_P = 3 * OFF_Q, OFF_U = OFF_P + 64 * 64 * 2,
-                OFF_G = OFF_U + 64 * 32 * 2;
-  static_assert(OFF_G + 256 == kScanSlotBytes, "slot layout");
-  __shared__ __attribute__((aligned(1024))) uint8_t slots[2 * kScanSlotBytes];
   __shared__ __attribute__((aligned(16))) uint16_t Sb[32 * KP], Ut[32 * CP], Os[C * OP];
   const int h = blockIdx.x, sl = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, gl = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, gl = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), tb = wave & 1;
+  const bool u_wave = wave < 2;
 
-  // per-lane source byte offsets of the 15 wave instructions inside a chunk's blocks (the same
-  // for every chunk), and the region each instruction reads
-  uint32_t src_off[15];
-#pragma unroll
-  for (int u = 0; u < 15; ++u) {
-    const int i = 4 * u + wave;
-    if (u < 8) {  // W (u 0-3) or Q^ (u 4-7): 64 x 128, 16 chunks per row
-      const int q = 64 * (i & 15) + lane, r = q >> 4;
-      src_off[u] = (uint32_t)(r * 128 + 8 * swz16(r, q & 15)) * 2;
-    } else if (u < 12) {  // K^T^: 128 x 64, 8 chunks per row
-      const int q = 64 * (i - 32) + lane, r = q >> 3;
-      src_off[u] = (uint32_t)(r * 64 + 8 * swz8(r, q & 7)) * 2;
-    } else if (u < 14) {  // P: 64 x 64
-      const int q = 64 * (i - 48) + lane, r = q >> 3;
-      src_off[u] = (uint32_t)(r * 64 + 8 * swz8(r, q & 7)) * 2;
-    } else {  // U~ columns 32 sl .. 32 sl + 31 of 64 rows: 4 chunks per row, no swizzle
-      const int q = 64 * (i - 56) + lane, r = q >> 2;
-      src_off[u] = (uint32_t)(r * 128 + 32 * sl + 8 * (q & 3)) * 2;
-    }
-  }
-  const uint32_t slots_lds = lds_address(slots);
-  auto dma = [&](int c, int slot) __device__ {
+  // one chunk's operands of this wavefront: a = W (u waves) or Q^ (o waves) for its 32 tokens,
+  // p = U~ (u waves, 2 pieces) or P (o waves, 4), k = K^ of its state block, g = G of lane
+  struct Frags {
+    u32x4_t a[D / 16], p[C / 16], k[C / 16];
+    float g;
+  };
+  // Every wave issues the same load sequence (no branch: the compiler then tracks each register
+  // set's loads exactly); the u waves' p[2], p[3] repeat their two U~ pieces and go unused.
+  const u32x4_t *a_src = (u_wave ? Wi : Qi) + (tb * (D / 16) << 6) + lane;
+  const u32x4_t *p_src = u_wave ? Ui + (((sl * 2 + tb) * 2) << 6) + lane : Pi + (tb * (C / 16) << 6) + lane;
+  const u32x4_t *k_src = Ki + (wave * (C / 16) << 6) + lane;
+  const int64_t p_chunk = u_wave ? GdnWs<D>::U / 8 : GdnWs<D>::P / 8;  // 16-byte pieces per block
+  const int p_step = u_wave ? 1 : 3;                                   // piece s at 64 (s & p_step)
+  auto load = [&](int c, Frags &f) __device__ {
+    c = c < n_chunks ? c : n_chunks - 1;  // past the end: the last chunk again, never used
     const int64_t ch = (int64_t)c * heads + h;
-    const uint32_t base = slots_lds + (uint32_t)(slot * kScanSlotBytes);
+    const int64_t o16 = ch * (GdnWs<D>::W / 8);  // 16-byte pieces per W / U~ / Q^ / K^ block
 #pragma unroll
-    for (int u = 0; u < 15; ++u) {
-      const uint16_t *src = u < 4 ? Wi + ch * GdnWs<D>::W : u < 8 ? Qi + ch * GdnWs<D>::Q
-                          : u < 12 ? Ki + ch * GdnWs<D>::K : u < 14 ? Pi + ch * GdnWs<D>::P : Ui + ch * GdnWs<D>::U;
-      global_to_lds16_sbase(src, src_off[u], base + (uint32_t)((4 * u + wave) * 1024));
-    }
-    if (wave == 0 && lane < 16)  // G: 64 fp32
-      global_to_lds16_sbase(Gi + ch * GdnWs<D>::G, (uint32_t)lane * 16u, base + OFF_G);
+    for (int s = 0; s < D / 16; ++s) f.a[s] = a_src[o16 + 64 * s];
+#pragma unroll
+    for (int s = 0; s < C / 16; ++s) f.p[s] = p_src[ch * p_chunk + 64 * (s & p_step)];
+#pragma unroll
+    for (int s = 0; s < C / 16; ++s) f.k[s] = k_src[o16 + 64 * s];
+    f.g = Gi[ch * GdnWs<D>::G + lane];  // a vector load: its wait is a vmcnt like the others
   };
 
   // state block of this wave: S[v = 32 sl + row][k = 32 wave + l32]
@@ -336,6 +347,11 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
       Sb[vr * KP + 32 * wave + l32] = f2bf(st[i]);
     }
   };
+  // this wave's LDS writes are done, then the barrier
+  auto lds_barrier = [&]() __device__ {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    bare_barrier();
+  };
   // outputs of chunk c (in Os) to global memory: thread = (token tid / 4, 8 dv columns)
   auto store_o = [&](int c) __device__ {
     const int tk = tid >> 2, pc = tid & 3, tok = c * C + tk;
@@ -343,69 +359,63 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
     if (tok < T) st16(out + (int64_t)tok * o_row + (int64_t)h * o_head + 32 * sl + 8 * pc, val);
   };
 
-  // fragment element offsets inside a slot (bf16 units)
-  int wfo[D / 16], pfo[C / 16], kfo[C / 16];
-  const int tb = wave & 1;
-#pragma unroll
-  for (int s = 0; s < D / 16; ++s) {
-    const int r = 32 * tb + l32;
-    wfo[s] = (wave < 2 ? 0 : OFF_Q / 2) + r * 128 + 8 * swz16(r, 2 * s + gl);
-  }
-#pragma unroll
-  for (int s = 0; s < C / 16; ++s) {
-    const int r = 32 * tb + l32, d = 32 * wave + l32;
-    pfo[s] = OFF_P / 2 + r * 64 + 8 * swz8(r, 2 * s + gl);
-    kfo[s] = OFF_K / 2 + d * 64 + 8 * swz8(d, 2 * s + gl);
-  }
-
-  write_sb();
-  dma(0, 0);
-  wait_vm_lds<0>();
-  bare_barrier();
-  for (int c = 0; c < n_chunks; ++c) {
-    const uint16_t *sb = reinterpret_cast<const uint16_t *>(slots + (c & 1) * kScanSlotBytes);
-    const float *gsl = reinterpret_cast<const float *>(slots + (c & 1) * kScanSlotBytes + OFF_G);
+  auto step = [&](int c, const Frags &f, Frags &ahead) __device__ {
     if (c > 0) store_o(c - 1);
-    if (c + 1 < n_chunks) dma(c + 1, (c + 1) & 1);
+    load(c + 2, ahead);
     // (a) waves 0, 1: U = U~ - W S^T for tokens 32 w ..; waves 2, 3: O = Q^ S^T for tokens 32 (w - 2) ..
     f32x16_t acc = {};
 #pragma unroll
     for (int s = 0; s < D / 16; ++s)
-      acc = mfma_bf16_32x32x16(as_bf16x8(ld16(sb + wfo[s])), as_bf16x8(ld16(Sb + l32 * KP + 16 * s + 8 * gl)), acc);
-    if (wave < 2) {
+      acc = mfma_bf16_32x32x16(as_bf16x8(f.a[s]), as_bf16x8(ld16(Sb + l32 * KP + 16 * s + 8 * gl)), acc);
+    if (u_wave) {
       // U[tok][dv] = U~ - acc; stored transposed (Ut[dv][tok]), four consecutive tokens per write
-      const uint16_t *ul = sb + OFF_U / 2;
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const int tok = 32 * tb + 8 * i4 + 4 * gl;
-        float u[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) u[e] = bf2f(ul[(tok + e) * 32 + l32]) - acc[4 * i4 + e];
-        *reinterpret_cast<u32x2_t *>(Ut + l32 * CP + tok) = u32x2_t{pack_bf2(u[0], u[1]), pack_bf2(u[2], u[3])};
+        const u32x4_t &up = f.p[i4 >> 1];
+        const uint32_t w0 = up[2 * (i4 & 1)], w1 = up[2 * (i4 & 1) + 1];
+        const float u0 = bf2f((uint16_t)w0) - acc[4 * i4], u1 = bf2f((uint16_t)(w0 >> 16)) - acc[4 * i4 + 1];
+        const float u2 = bf2f((uint16_t)w1) - acc[4 * i4 + 2], u3 = bf2f((uint16_t)(w1 >> 16)) - acc[4 * i4 + 3];
+        *reinterpret_cast<u32x2_t *>(Ut + l32 * CP + tok) = u32x2_t{pack_bf2(u0, u1), pack_bf2(u2, u3)};
       }
     }
-    bare_barrier();  // Ut complete; every read of Sb and of the Os of chunk c - 1 is done
+    lds_barrier();  // Ut complete; every read of Sb and of the Os of chunk c - 1 is done
     // (b) waves 2, 3: O += P U into Os; every wave: S = e^{G_C} S + U^T K^, then its bf16 copy
-    if (wave >= 2) {
+    if (!u_wave) {
 #pragma unroll
       for (int s = 0; s < C / 16; ++s)
-        acc = mfma_bf16_32x32x16(as_bf16x8(ld16(sb + pfo[s])), as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)),
-                                 acc);
+        acc = mfma_bf16_32x32x16(as_bf16x8(f.p[s]), as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)), acc);
 #pragma unroll
       for (int i = 0; i < 16; ++i) Os[(32 * tb + 8 * (i >> 2) + 4 * gl + (i & 3)) * OP + l32] = f2bf(acc[i]);
     }
     {
-      const float decay = expf(gsl[C - 1]);
+      const float decay = expf(__builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f.g), C - 1)));
 #pragma unroll
       for (int i = 0; i < 16; ++i) st[i] *= decay;
 #pragma unroll
       for (int s = 0; s < C / 16; ++s)
-        st = mfma_bf16_32x32x16(as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)), as_bf16x8(ld16(sb + kfo[s])), st);
+        st = mfma_bf16_32x32x16(as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)), as_bf16x8(f.k[s]), st);
     }
     write_sb();
-    wait_vm_lds<0>();  // the next chunk's operands have landed; this wave's LDS writes are done
-    bare_barrier();
+    lds_barrier();
+  };
+
+  Frags f0, f1, f2;
+  load(0, f0);
+  asm volatile("" ::: "memory");  // chunk 0's loads all issue before chunk 1's, as in the loop
+  load(1, f1);
+  write_sb();
+  lds_barrier();
+  // three chunks per trip, so every register set has a fixed name: chunk c in f[c % 3]
+  int c = 0;
+  for (; c + 3 <= n_chunks; c += 3) {
+    step(c, f0, f2);
+    step(c + 1, f1, f0);
+    step(c + 2, f2, f1);
   }
+  if (c < n_chunks) step(c, f0, f2);
+  if (c + 1 < n_chunks) step(c + 1, f1, f0);
   store_o(n_chunks - 1);
   if (s_final) {
 #pragma unroll
@@ -414,6 +424,7 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
       s_final[((int64_t)h * D + 32 * sl + vr) * D + 32 * wave + l32] = st[i];
     }
   }
+  wait_vm_lds<0>();  // the loads of the two chunks past the end land before the wave ends
 }
 
 }  // namespace
@@ -492,7 +503,9 @@ extern "C" int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_h
                        log_decay + t0 * decay_row, decay_row, nt, heads, W, U, Qh, Kt, P, G);
     int rc = check_launch("gdn_prep");
     if (rc) return rc;
-    hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(heads, D / 32), dim3(256), 0, s, W, U, Qh, Kt, P, G, nc, nt, heads,
+    const auto pieces = [](const uint16_t *b) { return reinterpret_cast<const u32x4_t *>(b); };
+    hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(heads, D / 32), dim3(256), 0, s, pieces(W), pieces(U), pieces(Qh),
+                       pieces(Kt), pieces(P), G, nc, nt, heads,
                        first ? initial_state : carry, last ? final_state : carry, out + t0 * o_row, o_row, o_head);
     rc = check_launch("gdn_scan");
     if (rc) return rc;
