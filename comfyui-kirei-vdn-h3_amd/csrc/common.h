@@ -96,6 +96,11 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ f32x16_t mfma_bf16_32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+// 16x16x32 bf16 -> fp32. Lane l holds A[m = l%16][k = 8*(l/16) + j], B[k = 8*(l/16) + j][n = l%16]
+// for j = 0..7, and C[m = 4*(l/16) + i][n = l%16] for i = 0..3.
+__device__ __forceinline__ f32x4_t mfma_bf16_16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 

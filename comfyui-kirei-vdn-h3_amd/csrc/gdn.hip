@@ -18,6 +18,8 @@
 // S = e^{G_C} S + U^T K^, each wavefront loading its operands into registers two chunks ahead.
 #include "common.h"
 
+#include <mutex>
+
 namespace vdnh3 {
 namespace {
 
@@ -29,17 +31,17 @@ struct GdnWs {  // per (chunk, head) workspace element counts
 };
 
 // The workspace holds each block in the fragment order of the scan wavefront that reads it, so
-// that a wavefront's 16-byte fragment pieces lie in lane order (1 KB per load instruction):
-//  - W, Q^ (A operands, 8 k-steps) and P (4 k-steps): piece p of the block is lane p % 64 of
-//    k-step (p / 64) % steps of row block p / (64 steps): row 32 (p / (64 steps)) + p % 32,
-//    columns 16 ((p / 64) % steps) + 8 ((p / 32) % 2) .. + 7;
-//  - K^ = e^{G_C - G} K (B operand of state block w): piece ((w, s), lane) holds tokens
+// that a wavefront's 16-byte fragment pieces lie in lane order (1 KB per load instruction). Scan
+// wavefront w forms U and O for tokens 16 w .. 16 w + 15 on 16x16x32 MFMAs and carries the state
+// block of dk columns 32 w .. 32 w + 31 on 32x32x16 MFMAs:
+//  - W, Q^ (8 bf16 columns of 128: 4 k-steps) and P (64 columns: 2 k-steps), A operands: piece
+//    p = (w steps + s) 64 + lane holds row 16 w + lane % 16, columns 32 s + 8 (lane / 16) .. + 7;
+//  - K^ = e^{G_C - G} K, B operand of state block w: piece (w 4 + s) 64 + lane holds tokens
 //    16 s + 8 (lane / 32) .. + 7 of column 32 w + lane % 32;
-//  - U~ (state slice sl, row block tb, half j): piece ((sl, tb, j), lane) holds, at element
-//    4 i + e, row 32 tb + 8 (2 j + i) + 4 (lane / 32) + e of column 32 sl + lane % 32 (the layout
-//    of a 32x32 MFMA accumulator, elements 8 j .. 8 j + 7).
-__device__ __forceinline__ int gdn_a_row(int p, int steps = 8) { return 32 * (p / (64 * steps)) + (p & 31); }
-__device__ __forceinline__ int gdn_a_col(int p, int steps = 8) { return 16 * ((p >> 6) % steps) + 8 * ((p >> 5) & 1); }
+//  - U~ for state slice sl in the 16x16 accumulator layout: piece (sl 4 + w) 64 + lane holds, at
+//    element 4 nb + i, row 16 w + 4 (lane / 16) + i of column 32 sl + 16 nb + lane % 16.
+__device__ __forceinline__ int gdn_a_row(int p, int steps) { return 16 * (p / (64 * steps)) + (p & 15); }
+__device__ __forceinline__ int gdn_a_col(int p, int steps) { return 32 * ((p >> 6) % steps) + 8 * ((p >> 4) & 3); }
 
 template <int D>
 __global__ __launch_bounds__(256) void gdn_prep_kernel(
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
     uint16_t *qc = Qo + ch * GdnWs<D>::Q, *kc = Ko + ch * GdnWs<D>::K, *pc = Po + ch * GdnWs<D>::P;
 #pragma unroll
     for (int u = 0; u < C * CH / 256; ++u) {
-      const int p = tid + 256 * u, r = gdn_a_row(p), k0 = gdn_a_col(p);
+      const int p = tid + 256 * u, r = gdn_a_row(p, D / 32), k0 = gdn_a_col(p, D / 32);
       const u32x4_t x = ld16(Qs + r * KP + k0);
       const float sc = Eg[r];
       st16(qc + 8 * p,
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
     }
 #pragma unroll
     for (int u = 0; u < C * (C / 8) / 256; ++u) {
-      const int p = tid + 256 * u, r = gdn_a_row(p, C / 16), j0 = gdn_a_col(p, C / 16);
+      const int p = tid + 256 * u, r = gdn_a_row(p, C / 32), j0 = gdn_a_col(p, C / 32);
       st16(pc + 8 * p, ld16(Ps + r * PP + j0));
     }
     if (tid < C) Go[ch * GdnWs<D>::G + tid] = Gs[tid];
@@ -246,51 +248,46 @@ __global__ __launch_bounds__(256) void gdn_prep_kernel(
         au[mb] = mfma_bf16_32x32x16(as_bf16x8(ld16(Tu + off)), bv, au[mb]);
       }
     }
-    // U~ leaves from the accumulators: wave w's block is the scan's state slice w, and its
-    // accumulator element 8 j + e of row block mb is exactly piece ((w, mb, j), lane) element e
-    uint16_t *uc = Uo + ch * GdnWs<D>::U;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const f32x16_t &a = au[mb];
-        st16(uc + 8 * ((((wave * 2 + mb) * 2 + j) << 6) + lane),
-             u32x4_t{pack_bf2(a[8 * j], a[8 * j + 1]), pack_bf2(a[8 * j + 2], a[8 * j + 3]),
-                     pack_bf2(a[8 * j + 4], a[8 * j + 5]), pack_bf2(a[8 * j + 6], a[8 * j + 7])});
-      }
-    __syncthreads();  // every read of Ks is done: W replaces it
+    __syncthreads();  // every read of Ks / Vs is done: W and U~ replace them
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = 32 * mb + 8 * (i >> 2) + 4 * gl + (i & 3);
         Ks[r * KP + 32 * wave + l32] = f2bf(aw[mb][i]);
+        Vs[r * KP + 32 * wave + l32] = f2bf(au[mb][i]);
       }
   }
   __syncthreads();
   {
-    uint16_t *wc = Wo + ch * GdnWs<D>::W;
+    uint16_t *wc = Wo + ch * GdnWs<D>::W, *uc = Uo + ch * GdnWs<D>::U;
 #pragma unroll
     for (int u = 0; u < C * CH / 256; ++u) {
       const int p = tid + 256 * u;
-      st16(wc + 8 * p, ld16(Ks + gdn_a_row(p) * KP + gdn_a_col(p)));
+      st16(wc + 8 * p, ld16(Ks + gdn_a_row(p, D / 32) * KP + gdn_a_col(p, D / 32)));
+      // U~ piece p = (sl 4 + w) 64 + L: column 32 sl + 16 nb + L % 16 at rows 16 w + 4 (L / 16) + i
+      const int L = p & 63, r0 = 16 * ((p >> 6) & 3) + 4 * (L >> 4), c0 = 32 * (p >> 8) + (L & 15);
+      uint16_t e[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) e[x] = Vs[(r0 + (x & 3)) * KP + c0 + 16 * (x >> 2)];
+      st16(uc + 8 * p, u32x4_t{e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                               e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16});
     }
   }
 }
 
-// One workgroup = head h, state rows (dv) 32 sl .. 32 sl + 31, four wavefronts: waves 0, 1 form
-// tokens 32 w .. 32 w + 31 of U = U~ - W S^T, waves 2, 3 tokens 32 (w - 2) .. of O = Q^ S^T + P U,
-// and wave w carries the state block of dk columns 32 w .. 32 w + 31 as one 32x32 MFMA
-// accumulator (fp32), S = e^{G_C} S + U^T K^. s_init and s_final may be the same buffer: a
-// workgroup reads its slice of s_init before anything else and writes the same slice of s_final
-// last.
+// One workgroup = head h, state rows (dv) 32 sl .. 32 sl + 31, four wavefronts alike: wave w forms
+// tokens 16 w .. 16 w + 15 of U = U~ - W S^T and of O = Q^ S^T + P U on 16x16x32 MFMAs, and
+// carries the state block of dk columns 32 w .. 32 w + 31 as one 32x32 MFMA accumulator (fp32),
+// S = e^{G_C} S + U^T K^. s_init and s_final may be the same buffer: a workgroup reads its slice
+// of s_init before anything else and writes the same slice of s_final last.
 //
-// Every wavefront reads only its own part of a chunk's operands (half of W or of Q^ and P, its
-// U~ rows, its K^ block), stored in its fragment order, so each wavefront loads them straight
-// into registers (1 KB per load instruction), two chunks ahead: a ring of three register sets,
-// which keeps two chunks' loads in flight behind the step that computes. The state's bf16 copy
-// (Sb) and U (Ut, transposed) are exchanged through LDS; the outputs of chunk c go to LDS (Os) in
-// step c and to global memory at the start of step c + 1 (one 16-byte store per thread).
+// Every wavefront reads only its own part of a chunk's operands (its 16 rows of W, Q^, P and U~,
+// its K^ block), stored in its fragment order, so each wavefront loads them straight into
+// registers (1 KB per load instruction), two chunks ahead: a ring of three register sets, which
+// keeps two chunks' loads in flight behind the step that computes. The state's bf16 copy (Sb) and
+// U (Ut, transposed) are exchanged through LDS; the outputs of chunk c go to LDS (Os) in step c
+// and to global memory at the start of step c + 1 (one 16-byte store per thread).
 template <int D>
 __global__ __launch_bounds__(256) void gdn_scan_kernel(
     const u32x4_t *__restrict__ Wi, const u32x4_t *__restrict__ Ui, const u32x4_t *__restrict__ Qi,
@@ -301,34 +298,32 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
   constexpr int C = kGdnC, KP = D + 8, CP = C + 8, OP = 32 + 8;
   __shared__ __attribute__((aligned(16))) uint16_t Sb[32 * KP], Ut[32 * CP], Os[C * OP];
   const int h = blockIdx.x, sl = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, gl = lane >> 5;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), tb = wave & 1;
-  const bool u_wave = wave < 2;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, gl = lane >> 5;  // 32x32 fragment coordinates
+  const int l16 = lane & 15, g4 = lane >> 4;  // 16x16 fragment coordinates
 
-  // one chunk's operands of this wavefront: a = W (u waves) or Q^ (o waves) for its 32 tokens,
-  // p = U~ (u waves, 2 pieces) or P (o waves, 4), k = K^ of its state block, g = G of lane
+  // one chunk's operands of this wavefront; g = G of lane (a vector load, so its wait is a vmcnt)
   struct Frags {
-    u32x4_t a[D / 16], p[C / 16], k[C / 16];
+    u32x4_t w[D / 32], q[D / 32], p[C / 32], u, k[C / 16];
     float g;
   };
-  // Every wave issues the same load sequence (no branch: the compiler then tracks each register
-  // set's loads exactly); the u waves' p[2], p[3] repeat their two U~ pieces and go unused.
-  const u32x4_t *a_src = (u_wave ? Wi : Qi) + (tb * (D / 16) << 6) + lane;
-  const u32x4_t *p_src = u_wave ? Ui + (((sl * 2 + tb) * 2) << 6) + lane : Pi + (tb * (C / 16) << 6) + lane;
+  const u32x4_t *w_src = Wi + (wave * (D / 32) << 6) + lane, *q_src = Qi + (wave * (D / 32) << 6) + lane;
+  const u32x4_t *p_src = Pi + (wave * (C / 32) << 6) + lane, *u_src = Ui + ((sl * 4 + wave) << 6) + lane;
   const u32x4_t *k_src = Ki + (wave * (C / 16) << 6) + lane;
-  const int64_t p_chunk = u_wave ? GdnWs<D>::U / 8 : GdnWs<D>::P / 8;  // 16-byte pieces per block
-  const int p_step = u_wave ? 1 : 3;                                   // piece s at 64 (s & p_step)
   auto load = [&](int c, Frags &f) __device__ {
     c = c < n_chunks ? c : n_chunks - 1;  // past the end: the last chunk again, never used
     const int64_t ch = (int64_t)c * heads + h;
-    const int64_t o16 = ch * (GdnWs<D>::W / 8);  // 16-byte pieces per W / U~ / Q^ / K^ block
+    const int64_t o16 = ch * (GdnWs<D>::W / 8), p16 = ch * (GdnWs<D>::P / 8);  // 16-byte pieces
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) f.a[s] = a_src[o16 + 64 * s];
+    for (int s = 0; s < D / 32; ++s) f.w[s] = w_src[o16 + 64 * s];
 #pragma unroll
-    for (int s = 0; s < C / 16; ++s) f.p[s] = p_src[ch * p_chunk + 64 * (s & p_step)];
+    for (int s = 0; s < D / 32; ++s) f.q[s] = q_src[o16 + 64 * s];
+#pragma unroll
+    for (int s = 0; s < C / 32; ++s) f.p[s] = p_src[p16 + 64 * s];
+    f.u = u_src[o16];
 #pragma unroll
     for (int s = 0; s < C / 16; ++s) f.k[s] = k_src[o16 + 64 * s];
-    f.g = Gi[ch * GdnWs<D>::G + lane];  // a vector load: its wait is a vmcnt like the others
+    f.g = Gi[ch * GdnWs<D>::G + lane];
   };
 
   // state block of this wave: S[v = 32 sl + row][k = 32 wave + l32]
@@ -362,32 +357,28 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
   auto step = [&](int c, const Frags &f, Frags &ahead) __device__ {
     if (c > 0) store_o(c - 1);
     load(c + 2, ahead);
-    // (a) waves 0, 1: U = U~ - W S^T for tokens 32 w ..; waves 2, 3: O = Q^ S^T for tokens 32 (w - 2) ..
-    f32x16_t acc = {};
+    // (a) tokens 16 w .. 16 w + 15, state rows 16 nb .. 16 nb + 15: W S^T and Q^ S^T share the
+    // B fragments (S^T from Sb)
+    f32x4_t ua[2] = {}, oa[2] = {};
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s)
-      acc = mfma_bf16_32x32x16(as_bf16x8(f.a[s]), as_bf16x8(ld16(Sb + l32 * KP + 16 * s + 8 * gl)), acc);
-    if (u_wave) {
-      // U[tok][dv] = U~ - acc; stored transposed (Ut[dv][tok]), four consecutive tokens per write
+    for (int s = 0; s < D / 32; ++s)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int tok = 32 * tb + 8 * i4 + 4 * gl;
-        const u32x4_t &up = f.p[i4 >> 1];
-        const uint32_t w0 = up[2 * (i4 & 1)], w1 = up[2 * (i4 & 1) + 1];
-        const float u0 = bf2f((uint16_t)w0) - acc[4 * i4], u1 = bf2f((uint16_t)(w0 >> 16)) - acc[4 * i4 + 1];
-        const float u2 = bf2f((uint16_t)w1) - acc[4 * i4 + 2], u3 = bf2f((uint16_t)(w1 >> 16)) - acc[4 * i4 + 3];
-        *reinterpret_cast<u32x2_t *>(Ut + l32 * CP + tok) = u32x2_t{pack_bf2(u0, u1), pack_bf2(u2, u3)};
+      for (int nb = 0; nb < 2; ++nb) {
+        const bf16x8_t b = as_bf16x8(ld16(Sb + (16 * nb + l16) * KP + 32 * s + 8 * g4));
+        ua[nb] = mfma_bf16_16x16x32(as_bf16x8(f.w[s]), b, ua[nb]);
+        oa[nb] = mfma_bf16_16x16x32(as_bf16x8(f.q[s]), b, oa[nb]);
       }
+    // U[tok][dv] = U~ - W S^T, stored transposed (Ut[dv][tok]): four consecutive tokens per write
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const uint32_t w0 = f.u[2 * nb], w1 = f.u[2 * nb + 1];
+      const float u0 = bf2f((uint16_t)w0) - ua[nb][0], u1 = bf2f((uint16_t)(w0 >> 16)) - ua[nb][1];
+      const float u2 = bf2f((uint16_t)w1) - ua[nb][2], u3 = bf2f((uint16_t)(w1 >> 16)) - ua[nb][3];
+      *reinterpret_cast<u32x2_t *>(Ut + (16 * nb + l16) * CP + 16 * wave + 4 * g4) =
+          u32x2_t{pack_bf2(u0, u1), pack_bf2(u2, u3)};
     }
     lds_barrier();  // Ut complete; every read of Sb and of the Os of chunk c - 1 is done
-    // (b) waves 2, 3: O += P U into Os; every wave: S = e^{G_C} S + U^T K^, then its bf16 copy
-    if (!u_wave) {
-#pragma unroll
-      for (int s = 0; s < C / 16; ++s)
-        acc = mfma_bf16_32x32x16(as_bf16x8(f.p[s]), as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)), acc);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) Os[(32 * tb + 8 * (i >> 2) + 4 * gl + (i & 3)) * OP + l32] = f2bf(acc[i]);
-    }
+    // (b) the state first (it is the chain into the next chunk), then O += P U into Os
     {
       const float decay = expf(__builtin_bit_cast(
           float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f.g), C - 1)));
@@ -398,6 +389,16 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
         st = mfma_bf16_32x32x16(as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)), as_bf16x8(f.k[s]), st);
     }
     write_sb();
+#pragma unroll
+    for (int s = 0; s < C / 32; ++s)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        oa[nb] = mfma_bf16_16x16x32(as_bf16x8(f.p[s]),
+                                    as_bf16x8(ld16(Ut + (16 * nb + l16) * CP + 32 * s + 8 * g4)), oa[nb]);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Os[(16 * wave + 4 * g4 + i) * OP + 16 * nb + l16] = f2bf(oa[nb][i]);
     lds_barrier();
   };
 
@@ -435,17 +436,75 @@ namespace {
 #ifndef VDNH3_GDN_SEGMENT_BYTES
 #define VDNH3_GDN_SEGMENT_BYTES (2048ll << 20)
 #endif
-// Workspace bytes of one (chunk, head): W, U~, Q^, K^T^ ([64][D] bf16 each), P ([64][64] bf16), G (64 fp32).
+#ifndef VDNH3_GDN_PIPE_SEGMENTS
+#define VDNH3_GDN_PIPE_SEGMENTS 8
+#endif
+constexpr int64_t kGdnPipeMinChunks = 32;  // a pipelined segment is at least this many chunks
+// Workspace bytes of one (chunk, head): W, U~, Q^, K^ ([64][D] bf16 each), P ([64][64] bf16), G (64 fp32).
 int64_t gdn_chunk_head_bytes(int head_dim) {
   return 4 * (int64_t)kGdnC * head_dim * 2 + (int64_t)kGdnC * kGdnC * 2 + (int64_t)kGdnC * 4;
 }
-// The sequence runs in segments of this many chunks, so that the workspace stays at about
-// VDNH3_GDN_SEGMENT_BYTES (2 GiB: one segment up to ~57k tokens at 40 heads) however long the sequence.
-// Segments small enough to stay in the 256 MB last-level cache between prep and scan were measured
-// slower (2.49-3.0 ms against 2.41 at 40,688 x 40 x 128): the scan's wait is not HBM latency.
+// Chunks per segment. A sequence of fewer than 2 kGdnPipeMinChunks chunks runs as one segment;
+// a longer one in about VDNH3_GDN_PIPE_SEGMENTS segments (at least kGdnPipeMinChunks chunks each)
+// whose prep and scan overlap on two streams, through two workspace buffers of at most
+// VDNH3_GDN_SEGMENT_BYTES / 2 each, so the workspace stays bounded however long the sequence.
 int64_t gdn_segment_chunks(int64_t chunks, int heads, int head_dim) {
-  const int64_t seg = VDNH3_GDN_SEGMENT_BYTES / (heads * gdn_chunk_head_bytes(head_dim));
-  return seg < 1 ? 1 : (seg > chunks ? chunks : seg);
+  int64_t cap = VDNH3_GDN_SEGMENT_BYTES / 2 / (heads * gdn_chunk_head_bytes(head_dim));
+  cap = cap < 1 ? 1 : cap;
+  if (chunks < 2 * kGdnPipeMinChunks && chunks <= cap) return chunks;
+  int64_t seg = (chunks + VDNH3_GDN_PIPE_SEGMENTS - 1) / VDNH3_GDN_PIPE_SEGMENTS;
+  seg = seg < kGdnPipeMinChunks ? kGdnPipeMinChunks : seg;
+  return seg < cap ? seg : cap;
+}
+// Workspace buffers: two when the sequence runs in more than one segment.
+int gdn_buffers(int64_t chunks, int64_t seg) { return seg < chunks ? 2 : 1; }
+
+// Per-device side stream (default priority) and events of the prep / scan pipeline, made on first
+// use with that device current. Every call re-records the same events, so calls on one device
+// hold the pipe's lock while they enqueue.
+struct GdnPipe {
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, prep_done[2] = {}, scan_done[2] = {};
+  std::mutex lock;
+};
+int gdn_pipe(hipStream_t stream, GdnPipe **out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex table_lock;
+  static GdnPipe pipes[kMaxDevices];
+  int current = 0;
+  hipError_t err = hipGetDevice(&current);
+  if (err != hipSuccess) return set_error(VDNH3_ERR_RUNTIME, "no current HIP device: %s", hipGetErrorString(err));
+  hipDevice_t dev = current;
+  if (stream != nullptr && (err = hipStreamGetDevice(stream, &dev)) != hipSuccess)
+    return set_error(VDNH3_ERR_RUNTIME, "hipStreamGetDevice failed: %s", hipGetErrorString(err));
+  VDNH3_HOST_CHECK(dev >= 0 && dev < kMaxDevices, VDNH3_ERR_RUNTIME, "device %d is beyond the %d this library tracks",
+                   (int)dev, kMaxDevices);
+  std::lock_guard<std::mutex> guard(table_lock);
+  GdnPipe &p = pipes[dev];
+  if (p.side == nullptr) {
+    if (dev != current && (err = hipSetDevice(dev)) != hipSuccess)
+      return set_error(VDNH3_ERR_RUNTIME, "hipSetDevice(%d) failed: %s", (int)dev, hipGetErrorString(err));
+    hipStream_t side = nullptr;
+    hipEvent_t ev[5] = {};
+    err = hipStreamCreateWithFlags(&side, hipStreamNonBlocking);
+    for (int i = 0; i < 5 && err == hipSuccess; ++i) err = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
+    if (dev != current) (void)hipSetDevice(current);
+    if (err != hipSuccess) {
+      for (hipEvent_t e : ev)
+        if (e) (void)hipEventDestroy(e);
+      if (side) (void)hipStreamDestroy(side);
+      return set_error(VDNH3_ERR_RUNTIME, "gdn: side stream / events on device %d: %s", (int)dev,
+                       hipGetErrorString(err));
+    }
+    p.fork = ev[0];
+    p.prep_done[0] = ev[1];
+    p.prep_done[1] = ev[2];
+    p.scan_done[0] = ev[3];
+    p.scan_done[1] = ev[4];
+    p.side = side;
+  }
+  *out = &p;
+  return VDNH3_OK;
 }
 }  // namespace
 }  // namespace vdnh3
@@ -454,8 +513,9 @@ extern "C" size_t vdnh3_gdn_workspace_bytes(int tokens, int heads, int head_dim)
   if (tokens <= 0 || heads <= 0 || head_dim <= 0) return 0;
   const int64_t chunks = (tokens + vdnh3::kGdnC - 1) / vdnh3::kGdnC;
   const int64_t seg = vdnh3::gdn_segment_chunks(chunks, heads, head_dim);
-  // one segment's workspace, then the fp32 state carried between segments ([heads][D][D])
-  return (size_t)(seg * heads * vdnh3::gdn_chunk_head_bytes(head_dim) + (int64_t)heads * head_dim * head_dim * 4);
+  // one or two segment buffers, then the fp32 state carried between segments ([heads][D][D])
+  return (size_t)(vdnh3::gdn_buffers(chunks, seg) * seg * heads * vdnh3::gdn_chunk_head_bytes(head_dim) +
+                  (int64_t)heads * head_dim * head_dim * 4);
 }
 
 extern "C" int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k,
@@ -481,34 +541,83 @@ extern "C" int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_h
   constexpr int D = 128;
   const int chunks = (tokens + kGdnC - 1) / kGdnC;
   const int seg = (int)gdn_segment_chunks(chunks, heads, D);
+  const int segments = (chunks + seg - 1) / seg;
   const int64_t n = (int64_t)seg * heads;
-  uint16_t *W = static_cast<uint16_t *>(workspace);
-  uint16_t *U = W + n * GdnWs<D>::W;
-  uint16_t *Qh = U + n * GdnWs<D>::U;
-  uint16_t *Kt = Qh + n * GdnWs<D>::Q;
-  uint16_t *P = Kt + n * GdnWs<D>::K;
-  float *G = reinterpret_cast<float *>(P + n * GdnWs<D>::P);
-  float *carry = G + n * GdnWs<D>::G;  // [heads][D][D] fp32 state between segments (16-byte aligned)
+  // buffer b: [W | U~ | Q^ | K^ | P | G] of one segment
+  struct Buf {
+    uint16_t *W, *U, *Q, *K, *P;
+    float *G;
+  } buf[2];
+  const int64_t buf_bytes = n * gdn_chunk_head_bytes(D);
+  for (int b = 0; b < gdn_buffers(chunks, seg); ++b) {
+    uint16_t *base = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + b * buf_bytes);
+    buf[b].W = base;
+    buf[b].U = buf[b].W + n * GdnWs<D>::W;
+    buf[b].Q = buf[b].U + n * GdnWs<D>::U;
+    buf[b].K = buf[b].Q + n * GdnWs<D>::Q;
+    buf[b].P = buf[b].K + n * GdnWs<D>::K;
+    buf[b].G = reinterpret_cast<float *>(buf[b].P + n * GdnWs<D>::P);
+  }
+  // [heads][D][D] fp32 state between segments (16-byte aligned)
+  float *carry = reinterpret_cast<float *>(static_cast<char *>(workspace) + gdn_buffers(chunks, seg) * buf_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Segment by segment: the segment's tokens form an independent sequence whose initial state is the
-  // state the previous segment ended with (the chunk form restarts exactly at a chunk boundary). Each
-  // scan workgroup reads its state slice before it writes the same slice, so the carry is updated in place.
-  for (int c0 = 0; c0 < chunks; c0 += seg) {
-    const int nc = seg < chunks - c0 ? seg : chunks - c0;
-    const int64_t t0 = (int64_t)c0 * kGdnC;
-    const int nt = (int)(tokens - t0 < (int64_t)nc * kGdnC ? tokens - t0 : (int64_t)nc * kGdnC);
-    const bool first = c0 == 0, last = c0 + nc >= chunks;
-    hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(heads, nc), dim3(256), 0, s, q + t0 * q_row, q_row, q_head,
+  // Segment i covers chunks i seg ..: its tokens form an independent sequence whose initial state is
+  // the state segment i - 1 ended with (the chunk form restarts exactly at a chunk boundary). Each scan
+  // workgroup reads its state slice before it writes the same slice, so the carry is updated in place.
+  auto span = [&](int i, int64_t *t0, int *nc, int *nt) {
+    const int c0 = i * seg;
+    *nc = seg < chunks - c0 ? seg : chunks - c0;
+    *t0 = (int64_t)c0 * kGdnC;
+    *nt = (int)(tokens - *t0 < (int64_t)*nc * kGdnC ? tokens - *t0 : (int64_t)*nc * kGdnC);
+  };
+  auto prep = [&](int i, hipStream_t st) -> int {
+    int64_t t0;
+    int nc, nt;
+    span(i, &t0, &nc, &nt);
+    const Buf &b = buf[i & 1];
+    hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(heads, nc), dim3(256), 0, st, q + t0 * q_row, q_row, q_head,
                        k + t0 * k_row, k_row, k_head, v + t0 * v_row, v_row, v_head, beta + t0 * beta_row, beta_row,
-                       log_decay + t0 * decay_row, decay_row, nt, heads, W, U, Qh, Kt, P, G);
-    int rc = check_launch("gdn_prep");
-    if (rc) return rc;
-    const auto pieces = [](const uint16_t *b) { return reinterpret_cast<const u32x4_t *>(b); };
-    hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(heads, D / 32), dim3(256), 0, s, pieces(W), pieces(U), pieces(Qh),
-                       pieces(Kt), pieces(P), G, nc, nt, heads,
-                       first ? initial_state : carry, last ? final_state : carry, out + t0 * o_row, o_row, o_head);
-    rc = check_launch("gdn_scan");
-    if (rc) return rc;
+                       log_decay + t0 * decay_row, decay_row, nt, heads, b.W, b.U, b.Q, b.K, b.P, b.G);
+    return check_launch("gdn_prep");
+  };
+  auto scan = [&](int i, hipStream_t st) -> int {
+    int64_t t0;
+    int nc, nt;
+    span(i, &t0, &nc, &nt);
+    const Buf &b = buf[i & 1];
+    const auto pieces = [](const uint16_t *x) { return reinterpret_cast<const u32x4_t *>(x); };
+    hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(heads, D / 32), dim3(256), 0, st, pieces(b.W), pieces(b.U),
+                       pieces(b.Q), pieces(b.K), pieces(b.P), b.G, nc, nt, heads,
+                       i == 0 ? initial_state : carry, i == segments - 1 ? final_state : carry, out + t0 * o_row,
+                       o_row, o_head);
+    return check_launch("gdn_scan");
+  };
+  int rc = prep(0, s);
+  if (rc) return rc;
+  if (segments == 1) return scan(0, s);
+  // Two or more segments: the prep of segment i + 1 runs on the side stream while segment i scans
+  // on the caller's stream (a scan leaves most of each CU free). Buffer i % 2 holds segment i: the
+  // side stream waits for the scan that last read a buffer before its prep overwrites it, and the
+  // caller's stream waits for a segment's prep before scanning it. The last scan waits for the last
+  // prep, so every side-stream operation is joined back into the caller's stream.
+  GdnPipe *pp = nullptr;
+  if ((rc = gdn_pipe(s, &pp))) return rc;
+  std::lock_guard<std::mutex> guard(pp->lock);
+  auto ok = [](hipError_t e, const char *what) -> int {
+    return e == hipSuccess ? VDNH3_OK : set_error(VDNH3_ERR_RUNTIME, "gdn: %s: %s", what, hipGetErrorString(e));
+  };
+  if ((rc = ok(hipEventRecord(pp->fork, s), "fork record"))) return rc;
+  if ((rc = ok(hipStreamWaitEvent(pp->side, pp->fork, 0), "fork wait"))) return rc;
+  for (int i = 0; i < segments; ++i) {
+    const int b = i & 1;
+    if (i + 1 < segments) {
+      if (i >= 1 && (rc = ok(hipStreamWaitEvent(pp->side, pp->scan_done[b ^ 1], 0), "scan wait"))) return rc;
+      if ((rc = prep(i + 1, pp->side))) return rc;
+      if ((rc = ok(hipEventRecord(pp->prep_done[b ^ 1], pp->side), "prep record"))) return rc;
+    }
+    if (i >= 1 && (rc = ok(hipStreamWaitEvent(s, pp->prep_done[b], 0), "prep wait"))) return rc;
+    if ((rc = scan(i, s))) return rc;
+    if ((rc = ok(hipEventRecord(pp->scan_done[b], s), "scan record"))) return rc;
   }
   return VDNH3_OK;
 }
