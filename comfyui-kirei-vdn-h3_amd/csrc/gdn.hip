@@ -296,7 +296,8 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
     int64_t o_row, int64_t o_head) {
   static_assert(D == 128, "the scan keeps one 32-column state block per wave: head_dim 128");
   constexpr int C = kGdnC, KP = D + 8, CP = C + 8, OP = 32 + 8;
-  __shared__ __attribute__((aligned(16))) uint16_t Sb[32 * KP], Ut[32 * CP], Os[C * OP];
+  // Ut and Os hold two chunks each: P U of chunk c and its outputs are finished in step c + 1
+  __shared__ __attribute__((aligned(16))) uint16_t Sb[32 * KP], Ut[2][32 * CP], Os[2][C * OP];
   const int h = blockIdx.x, sl = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, gl = lane >> 5;  // 32x32 fragment coordinates
@@ -347,59 +348,77 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     bare_barrier();
   };
-  // outputs of chunk c (in Os) to global memory: thread = (token tid / 4, 8 dv columns)
+  // outputs of chunk c (in Os[c & 1]) to global memory: thread = (token tid / 4, 8 dv columns)
   auto store_o = [&](int c) __device__ {
     const int tk = tid >> 2, pc = tid & 3, tok = c * C + tk;
-    const u32x4_t val = ld16(Os + tk * OP + 8 * pc);
+    const u32x4_t val = ld16(Os[c & 1] + tk * OP + 8 * pc);
     if (tok < T) st16(out + (int64_t)tok * o_row + (int64_t)h * o_head + 32 * sl + 8 * pc, val);
   };
 
+  // O of chunk c - 1 between its two halves: Q^ S^T (step c - 1), P U (step c)
+  f32x4_t oprev[2] = {};
+  // P U of the chunk whose P fragments are p and whose U is in Ut[b], onto oprev
+  auto pu = [&](const u32x4_t (&p)[C / 32], int b) __device__ {
+#pragma unroll
+    for (int s = 0; s < C / 32; ++s)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        oprev[nb] = mfma_bf16_16x16x32(as_bf16x8(p[s]),
+                                       as_bf16x8(ld16(Ut[b] + (16 * nb + l16) * CP + 32 * s + 8 * g4)), oprev[nb]);
+  };
+  auto write_o = [&](int b) __device__ {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Os[b][(16 * wave + 4 * g4 + i) * OP + 16 * nb + l16] = f2bf(oprev[nb][i]);
+  };
+
+  // Step c computes chunk c from register set f; `ahead` holds chunk c - 1 until it is reloaded
+  // with chunk c + 2. The U chain (W S^T, U, Ut, the state update, Sb) is the critical path, so
+  // its MFMAs issue first; O's products follow it in the MFMA pipe and O of chunk c - 1 is
+  // completed and written here, off that chain.
   auto step = [&](int c, const Frags &f, Frags &ahead) __device__ {
-    if (c > 0) store_o(c - 1);
-    load(c + 2, ahead);
-    // (a) tokens 16 w .. 16 w + 15, state rows 16 nb .. 16 nb + 15: W S^T and Q^ S^T share the
-    // B fragments (S^T from Sb)
-    f32x4_t ua[2] = {}, oa[2] = {};
+    const int b = c & 1;
+    if (c > 1) store_o(c - 2);
+    // (a) tokens 16 w .. 16 w + 15, state rows 16 nb .. 16 nb + 15: U = U~ - W S^T (S^T from Sb)
+    f32x4_t ua[2] = {}, ocur[2] = {};
 #pragma unroll
     for (int s = 0; s < D / 32; ++s)
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const bf16x8_t b = as_bf16x8(ld16(Sb + (16 * nb + l16) * KP + 32 * s + 8 * g4));
-        ua[nb] = mfma_bf16_16x16x32(as_bf16x8(f.w[s]), b, ua[nb]);
-        oa[nb] = mfma_bf16_16x16x32(as_bf16x8(f.q[s]), b, oa[nb]);
-      }
+      for (int nb = 0; nb < 2; ++nb)
+        ua[nb] = mfma_bf16_16x16x32(as_bf16x8(f.w[s]),
+                                    as_bf16x8(ld16(Sb + (16 * nb + l16) * KP + 32 * s + 8 * g4)), ua[nb]);
+    if (c > 0) pu(ahead.p, b ^ 1);
+    load(c + 2, ahead);
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        ocur[nb] = mfma_bf16_16x16x32(as_bf16x8(f.q[s]),
+                                      as_bf16x8(ld16(Sb + (16 * nb + l16) * KP + 32 * s + 8 * g4)), ocur[nb]);
     // U[tok][dv] = U~ - W S^T, stored transposed (Ut[dv][tok]): four consecutive tokens per write
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       const uint32_t w0 = f.u[2 * nb], w1 = f.u[2 * nb + 1];
       const float u0 = bf2f((uint16_t)w0) - ua[nb][0], u1 = bf2f((uint16_t)(w0 >> 16)) - ua[nb][1];
       const float u2 = bf2f((uint16_t)w1) - ua[nb][2], u3 = bf2f((uint16_t)(w1 >> 16)) - ua[nb][3];
-      *reinterpret_cast<u32x2_t *>(Ut + (16 * nb + l16) * CP + 16 * wave + 4 * g4) =
+      *reinterpret_cast<u32x2_t *>(Ut[b] + (16 * nb + l16) * CP + 16 * wave + 4 * g4) =
           u32x2_t{pack_bf2(u0, u1), pack_bf2(u2, u3)};
     }
-    lds_barrier();  // Ut complete; every read of Sb and of the Os of chunk c - 1 is done
-    // (b) the state first (it is the chain into the next chunk), then O += P U into Os
-    {
-      const float decay = expf(__builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f.g), C - 1)));
+    if (c > 0) write_o(b ^ 1);
+    lds_barrier();  // Ut[b] and Os[b ^ 1] complete; every read of Sb and of Os[b] is done
+    // (b) S = e^{G_C} S + U^T K^, then its bf16 copy
+    const float decay = expf(__builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f.g), C - 1)));
 #pragma unroll
-      for (int i = 0; i < 16; ++i) st[i] *= decay;
+    for (int i = 0; i < 16; ++i) st[i] *= decay;
 #pragma unroll
-      for (int s = 0; s < C / 16; ++s)
-        st = mfma_bf16_32x32x16(as_bf16x8(ld16(Ut + l32 * CP + 16 * s + 8 * gl)), as_bf16x8(f.k[s]), st);
-    }
+    for (int s = 0; s < C / 16; ++s)
+      st = mfma_bf16_32x32x16(as_bf16x8(ld16(Ut[b] + l32 * CP + 16 * s + 8 * gl)), as_bf16x8(f.k[s]), st);
     write_sb();
-#pragma unroll
-    for (int s = 0; s < C / 32; ++s)
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-        oa[nb] = mfma_bf16_16x16x32(as_bf16x8(f.p[s]),
-                                    as_bf16x8(ld16(Ut + (16 * nb + l16) * CP + 32 * s + 8 * g4)), oa[nb]);
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Os[(16 * wave + 4 * g4 + i) * OP + 16 * nb + l16] = f2bf(oa[nb][i]);
     lds_barrier();
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) oprev[nb] = ocur[nb];
   };
 
   Frags f0, f1, f2;
@@ -417,6 +436,11 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(
   }
   if (c < n_chunks) step(c, f0, f2);
   if (c + 1 < n_chunks) step(c + 1, f1, f0);
+  // the last chunk's P U: the loads past the end left every register set holding the last chunk
+  if (n_chunks > 1) store_o(n_chunks - 2);
+  pu(f0.p, (n_chunks - 1) & 1);
+  write_o((n_chunks - 1) & 1);
+  lds_barrier();
   store_o(n_chunks - 1);
   if (s_final) {
 #pragma unroll
