@@ -77,6 +77,55 @@ def test_gdn_split_at_chunk_boundary_is_bit_identical(device):
     assert torch.equal(s_tail.cpu(), s_whole.cpu())
 
 
+def test_gdn_pipelined_segments_match_chained_calls(device):
+    """A sequence long enough to run in pipelined segments (the prep of segment i + 1 on the library's
+    side stream beside the scan of segment i, through two workspace buffers, so segment 2 reuses the
+    buffer of segment 0) gives the same bits as the same segments run as separate one-segment calls
+    chained through their final states."""
+    from vdn_h3_amd.gdn import chunk_gated_delta_rule
+
+    tokens, heads = 64 * 70 - 17, 3  # 70 chunks: segments of 32, 32 and 6 chunks, the last one partial
+    print(f"case gdn pipelined T={tokens} H={heads}", flush=True)
+    q, k, v, beta, lg = _inputs(tokens, heads, 12, 0.05)
+    s0 = torch.randn(heads, 128, 128, generator=torch.Generator().manual_seed(9)) * 0.1
+    dq, dk, dv, db, dg, ds0 = (t.to(device) for t in (q, k, v, beta, lg, s0))
+    whole, s_whole = chunk_gated_delta_rule(dq, dk, dv, db, dg, initial_state=ds0, output_final_state=True)
+    parts, state = [], ds0
+    for a, b in ((0, 64 * 32), (64 * 32, 64 * 64), (64 * 64, tokens)):
+        o, state = chunk_gated_delta_rule(dq[a:b], dk[a:b], dv[a:b], db[a:b], dg[a:b], initial_state=state,
+                                          output_final_state=True)
+        parts.append(o)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat(parts).cpu(), whole.cpu())
+    assert torch.equal(state.cpu(), s_whole.cpu())
+
+
+def test_gdn_pipelined_call_replays_in_a_graph(device):
+    """The pipelined call captured in a graph (the side stream joins the capture through the call's fork
+    event and is joined back by the last scan's wait) replays to the eager result, three replays with
+    eager work and synchronisations between them."""
+    from vdn_h3_amd.gdn import chunk_gated_delta_rule
+
+    tokens, heads = 64 * 70, 2
+    print(f"case gdn graph T={tokens} H={heads}", flush=True)
+    q, k, v, beta, lg = (t.to(device) for t in _inputs(tokens, heads, 13, 0.05))
+    eager, s_eager = chunk_gated_delta_rule(q, k, v, beta, lg, output_final_state=True)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out, s_out = chunk_gated_delta_rule(q, k, v, beta, lg, output_final_state=True)
+    for r in range(3):
+        out.zero_()
+        s_out.zero_()
+        noise = torch.randn(1 << 20, device=device).sum()  # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        assert torch.equal(out, eager), f"replay {r}: output"
+        assert torch.equal(s_out, s_eager), f"replay {r}: final state"
+
+
 def test_gdn_full_shape_sampled_heads(device):
     """40,688 tokens x 40 heads (the chunk-64 benchmark shape); heads 0 and 39 against the oracle."""
     from vdn_h3_amd.gdn import chunk_gated_delta_rule
