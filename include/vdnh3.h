@@ -381,8 +381,13 @@ int vdnh3_head_gate(const uint16_t *o, int64_t o_row, int64_t o_head, const uint
  * q, k, v: [tokens, heads, 128] bf16 views (element (t, h, d) at p[t*row + h*head + d]);
  * beta, log_decay: fp32 (element (t, h) at p[t*row + h]); out: bf16 like q; initial_state /
  * final_state: fp32 [heads][128][128] (dv rows, dk columns) or NULL (zero start / not written).
- * workspace: vdnh3_gdn_workspace_bytes(tokens, heads, 128) bytes, 16-byte aligned (the operands of
- * one segment of at most ~2 GiB plus the fp32 state carried between segments).
+ * workspace: vdnh3_gdn_workspace_bytes(tokens, heads, 128) bytes, 16-byte aligned (two segment
+ * buffers of at most ~1 GiB each, one for a sequence under 64 chunks, plus the fp32 state carried
+ * between segments). A sequence of 64 chunks or more runs in segments whose prep overlaps the
+ * previous segment's scan on a side stream the library owns (one per device, default priority,
+ * created on the first such call): the call forks it from `stream` with an event and joins it back
+ * before its last kernel, so all of its work is ordered on `stream` and it can be captured in a
+ * graph. Calls on one device serialise their enqueue on a host lock.
  * ------------------------------------------------------------------------------ */
 size_t vdnh3_gdn_workspace_bytes(int tokens, int heads, int head_dim);
 int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
