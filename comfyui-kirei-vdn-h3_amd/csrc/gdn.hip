@@ -632,16 +632,22 @@ extern "C" int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_h
   };
   if ((rc = ok(hipEventRecord(pp->fork, s), "fork record"))) return rc;
   if ((rc = ok(hipStreamWaitEvent(pp->side, pp->fork, 0), "fork wait"))) return rc;
+  // on a failure after the fork, the caller's stream still waits for what the side stream holds
+  // (best effort), so that no side-stream work outlives the call's ordering on `stream`
+  auto fail = [&](int code) {
+    if (hipEventRecord(pp->fork, pp->side) == hipSuccess) (void)hipStreamWaitEvent(s, pp->fork, 0);
+    return code;
+  };
   for (int i = 0; i < segments; ++i) {
     const int b = i & 1;
     if (i + 1 < segments) {
-      if (i >= 1 && (rc = ok(hipStreamWaitEvent(pp->side, pp->scan_done[b ^ 1], 0), "scan wait"))) return rc;
-      if ((rc = prep(i + 1, pp->side))) return rc;
-      if ((rc = ok(hipEventRecord(pp->prep_done[b ^ 1], pp->side), "prep record"))) return rc;
+      if (i >= 1 && (rc = ok(hipStreamWaitEvent(pp->side, pp->scan_done[b ^ 1], 0), "scan wait"))) return fail(rc);
+      if ((rc = prep(i + 1, pp->side))) return fail(rc);
+      if ((rc = ok(hipEventRecord(pp->prep_done[b ^ 1], pp->side), "prep record"))) return fail(rc);
     }
-    if (i >= 1 && (rc = ok(hipStreamWaitEvent(s, pp->prep_done[b], 0), "prep wait"))) return rc;
-    if ((rc = scan(i, s))) return rc;
-    if ((rc = ok(hipEventRecord(pp->scan_done[b], s), "scan record"))) return rc;
+    if (i >= 1 && (rc = ok(hipStreamWaitEvent(s, pp->prep_done[b], 0), "prep wait"))) return fail(rc);
+    if ((rc = scan(i, s))) return fail(rc);
+    if ((rc = ok(hipEventRecord(pp->scan_done[b], s), "scan record"))) return fail(rc);
   }
   return VDNH3_OK;
 }
