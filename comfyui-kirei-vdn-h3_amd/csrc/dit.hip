@@ -68,50 +68,99 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
   return s;
 }
 
-// One 256-thread workgroup per row, 8 channels per thread per pass; the row stays in registers
-// between the sum of squares and the output (hidden <= 8 * 256 * kRowChunks).
+// 8 channels per thread per pass of a 256-thread workgroup; a row stays in registers between the
+// sum of squares and the output (hidden <= 8 * 256 * kRowChunks).
 constexpr int kRowChunks = 4;
+constexpr int kNormGroups = 768;  // workgroups of rmsnorm_modulate: three per CU (132 VGPRs)
 
+// A workgroup walks a contiguous block of rows: the weight row stays in registers (packed bf16),
+// and so do the segment's 1 + scale and shift (bf16, as the reference rounds them) while
+// consecutive rows share a segment; the next row's x is in flight while the current row is reduced
+// and written, with one barrier per row (two reduction slots). A thread's chunks and the reduction
+// order are those of a one-row workgroup, so every row gets the same bits either way.
 __global__ __launch_bounds__(256) void rmsnorm_modulate_kernel(
     const uint16_t *__restrict__ x, int64_t x_row, const uint16_t *__restrict__ w, float eps,
     const void *__restrict__ scale, const void *__restrict__ shift, int64_t mod_row, int mod_bf16,
-    const int32_t *__restrict__ idx, int table_rows, uint16_t *__restrict__ out, int64_t out_row, int hidden) {
-  __shared__ float red[4];
-  const int64_t row = blockIdx.x;
-  const uint16_t *xr = x + row * x_row;
-  const int chunks = hidden / 8;
-  float v[kRowChunks][8];
-  float ss = 0.f;
+    const int32_t *__restrict__ idx, int table_rows, uint16_t *__restrict__ out, int64_t out_row, int hidden,
+    int rows, int rows_per_group) {
+  __shared__ float red[2][4];
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_group;
+  const int64_t r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
+  const int chunks = hidden / 8, tid = threadIdx.x;
+  u32x4_t wv[kRowChunks], opsc[kRowChunks], shv[kRowChunks], xa[kRowChunks], xb[kRowChunks];
 #pragma unroll
   for (int u = 0; u < kRowChunks; ++u) {
-    const int c = threadIdx.x + 256 * u;
-    if (c < chunks) {
-      unpack8f(ld16(xr + 8 * c), v[u]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss = fmaf(v[u][j], v[u][j], ss);
-    }
+    const int c = tid + 256 * u;
+    wv[u] = c < chunks ? ld16(w + 8 * c) : u32x4_t{0, 0, 0, 0};
+    opsc[u] = shv[u] = u32x4_t{0, 0, 0, 0};
   }
-  const float r = 1.f / sqrtf(block_sum(ss, red) / (float)hidden + eps);
-  // a segment index outside the modulation table reads row 0 and writes a NaN row instead of
-  // reading past the table
-  const int seg = idx[row];
-  const bool seg_ok = (unsigned)seg < (unsigned)table_rows;
-  const int64_t mrow = (int64_t)(seg_ok ? seg : 0) * mod_row;
+  int cur = -1;  // the segment whose modulation the registers hold (none yet)
+  bool cur_ok = false;
+  auto load_x = [&](int64_t row, u32x4_t (&xv)[kRowChunks]) __device__ {
 #pragma unroll
-  for (int u = 0; u < kRowChunks; ++u) {
-    const int c = threadIdx.x + 256 * u;
-    if (c >= chunks) continue;
-    float wf[8], sc[8], sh[8], y[8];
-    unpack8f(ld16(w + 8 * c), wf);
-    load_mod8(scale, mrow + 8 * c, mod_bf16, sc);
-    load_mod8(shift, mrow + 8 * c, mod_bf16, sh);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float n = round_bf(v[u][j] * r * wf[j]);  // F.rms_norm, one rounding
-      const float p = round_bf(n * round_bf(1.f + sc[j]));
-      y[j] = seg_ok ? p + sh[j] : __builtin_nanf("");
+    for (int u = 0; u < kRowChunks; ++u) {
+      const int c = tid + 256 * u;
+      if (c < chunks) xv[u] = ld16(x + row * x_row + 8 * c);
     }
-    st16(out + row * out_row + 8 * c, pack8f(y));
+  };
+  auto process = [&](int64_t row, const u32x4_t (&xv)[kRowChunks], float *slot) __device__ {
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < kRowChunks; ++u) {
+      if (tid + 256 * u < chunks) {
+        float v[8];
+        unpack8f(xv[u], v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
+      }
+    }
+    // a segment index outside the modulation table reads row 0 and writes a NaN row instead of
+    // reading past the table
+    const int seg = idx[row];
+    if (seg != cur || cur < 0) {
+      cur = seg;
+      cur_ok = (unsigned)seg < (unsigned)table_rows;
+      const int64_t mrow = (int64_t)(cur_ok ? seg : 0) * mod_row;
+#pragma unroll
+      for (int u = 0; u < kRowChunks; ++u) {
+        const int c = tid + 256 * u;
+        if (c >= chunks) continue;
+        float sc[8], sh[8];
+        load_mod8(scale, mrow + 8 * c, mod_bf16, sc);
+        load_mod8(shift, mrow + 8 * c, mod_bf16, sh);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sc[j] = 1.f + sc[j];
+        opsc[u] = pack8f(sc);  // bf16(1 + scale), the reference's rounding
+        shv[u] = pack8f(sh);   // already bf16 values: exact
+      }
+    }
+    const float r = 1.f / sqrtf(block_sum(ss, slot) / (float)hidden + eps);
+#pragma unroll
+    for (int u = 0; u < kRowChunks; ++u) {
+      const int c = tid + 256 * u;
+      if (c >= chunks) continue;
+      float v[8], wf[8], o[8], sh[8], y[8];
+      unpack8f(xv[u], v);  // the row is still in registers, packed
+      unpack8f(wv[u], wf);
+      unpack8f(opsc[u], o);
+      unpack8f(shv[u], sh);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float n = round_bf(v[j] * r * wf[j]);  // F.rms_norm, one rounding
+        const float p = round_bf(n * o[j]);
+        y[j] = cur_ok ? p + sh[j] : __builtin_nanf("");
+      }
+      st16(out + row * out_row + 8 * c, pack8f(y));
+    }
+  };
+  // two rows per trip, so both x buffers have fixed names
+  load_x(r0, xa);
+  for (int64_t row = r0; row < r1; row += 2) {
+    if (row + 1 < r1) load_x(row + 1, xb);
+    process(row, xa, red[0]);
+    if (row + 1 >= r1) break;
+    if (row + 2 < r1) load_x(row + 2, xa);
+    process(row + 1, xb, red[1]);
   }
 }
 
@@ -286,8 +335,10 @@ extern "C" int vdnh3_rmsnorm_modulate(const uint16_t *x, int64_t x_row, const ui
   if (rc) return rc;
   VDNH3_HOST_CHECK(idx != nullptr && table_rows > 0, VDNH3_ERR_INVALID,
                    "rmsnorm_modulate: null segment index or empty modulation table");
-  hipLaunchKernelGGL(vdnh3::rmsnorm_modulate_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream), x,
-                     x_row, weight, eps, scale, shift, mod_row, mod_bf16, idx, table_rows, out, out_row, hidden);
+  const int per = (rows + vdnh3::kNormGroups - 1) / vdnh3::kNormGroups, groups = (rows + per - 1) / per;
+  hipLaunchKernelGGL(vdnh3::rmsnorm_modulate_kernel, dim3(groups), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     x, x_row, weight, eps, scale, shift, mod_row, mod_bf16, idx, table_rows, out, out_row, hidden,
+                     rows, per);
   return vdnh3::check_launch("rmsnorm_modulate");
 }
 
