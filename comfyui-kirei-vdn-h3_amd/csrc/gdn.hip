@@ -34,7 +34,7 @@ struct GdnWs {  // per (chunk, head) workspace element counts
 // that a wavefront's 16-byte fragment pieces lie in lane order (1 KB per load instruction). Scan
 // wavefront w forms U and O for tokens 16 w .. 16 w + 15 on 16x16x32 MFMAs and carries the state
 // block of dk columns 32 w .. 32 w + 31 on 32x32x16 MFMAs:
-//  - W, Q^ (8 bf16 columns of 128: 4 k-steps) and P (64 columns: 2 k-steps), A operands: piece
+//  - W, Q^ (128 columns: 4 k-steps of 32) and P (64 columns: 2 k-steps), A operands: piece
 //    p = (w steps + s) 64 + lane holds row 16 w + lane % 16, columns 32 s + 8 (lane / 16) .. + 7;
 //  - K^ = e^{G_C - G} K, B operand of state block w: piece (w 4 + s) 64 + lane holds tokens
 //    16 s + 8 (lane / 32) .. + 7 of column 32 w + lane % 32;
