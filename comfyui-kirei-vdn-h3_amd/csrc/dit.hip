@@ -12,6 +12,8 @@
 // torch ops in bf16: every op's result is rounded to bf16 (rms_norm once, then 1 + scale,
 // the product, the sum; silu, then the product), so a CPU evaluation of the same expressions
 // gives the same bits.
+#include <type_traits>
+
 #include "common.h"
 
 namespace vdnh3 {
@@ -224,24 +226,29 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const uint16_t *__res
     for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(a[j]));
   }
   amax = wave_max(amax);
-  const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f);
+  const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f), r = 1.f / s;
   if (lane == 0) scale[row] = s;
   uint8_t *qr = q + (int64_t)row * q_row;
-  for (int c = lane; c < chunks; c += 64) {
-    float a[8];
-    swiglu8(hr, ffn, c, a);
-    uint32_t lo = 0, hi = 0;
+  // the codes of a / s (quant_div for a finite amax, the division otherwise)
+  auto sweep = [&](auto exact) __device__ {
+    for (int c = lane; c < chunks; c += 64) {
+      float a[8];
+      swiglu8(hr, ffn, c, a);
+      uint32_t lo = 0, hi = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float e = a[j] / s;
-      const uint32_t code = KIND == 1 ? i8_code(e) : e4m3_code(fminf(fmaxf(e, -kF8Max), kF8Max));
-      if (j < 4)
-        lo |= code << (8 * j);
-      else
-        hi |= code << (8 * (j - 4));
+      for (int j = 0; j < 8; ++j) {
+        const float e = decltype(exact)::value ? a[j] / s : quant_div(a[j], s, r);
+        const uint32_t code = KIND == 1 ? i8_code(e) : e4m3_code(fminf(fmaxf(e, -kF8Max), kF8Max));
+        if (j < 4)
+          lo |= code << (8 * j);
+        else
+          hi |= code << (8 * (j - 4));
+      }
+      *reinterpret_cast<u32x2_t *>(qr + 8 * c) = u32x2_t{lo, hi};
     }
-    *reinterpret_cast<u32x2_t *>(qr + 8 * c) = u32x2_t{lo, hi};
-  }
+  };
+  if (__builtin_isfinite(amax)) sweep(std::false_type{});
+  else sweep(std::true_type{});
 }
 
 // One workgroup of kQuantThreads threads per row for ffn <= 8 * kQuantThreads * kQuantChunks (16,384):
@@ -285,27 +292,32 @@ __global__ __launch_bounds__(kQuantThreads) void swiglu_quant_row_kernel(const u
     a[u] = pack8f(av);  // exact: av holds bf16 values
   }
   amax = block_max<kQuantThreads / 64>(amax, red);
-  const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f);
+  const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f), r = 1.f / s;
   if (threadIdx.x == 0) scale[row] = s;
   uint8_t *qr = q + row * q_row;
+  // the codes of a / s (quant_div for a finite amax, the division otherwise)
+  auto sweep = [&](auto exact) __device__ {
 #pragma unroll
-  for (int u = 0; u < kQuantChunks; ++u) {
-    const int c = threadIdx.x + kQuantThreads * u;
-    if (c >= chunks) continue;
-    float av[8];
-    unpack8f(a[u], av);
-    uint32_t lo = 0, hi = 0;
+    for (int u = 0; u < kQuantChunks; ++u) {
+      const int c = threadIdx.x + kQuantThreads * u;
+      if (c >= chunks) continue;
+      float av[8];
+      unpack8f(a[u], av);
+      uint32_t lo = 0, hi = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float e = av[j] / s;
-      const uint32_t code = KIND == 1 ? i8_code(e) : e4m3_code(fminf(fmaxf(e, -kF8Max), kF8Max));
-      if (j < 4)
-        lo |= code << (8 * j);
-      else
-        hi |= code << (8 * (j - 4));
+      for (int j = 0; j < 8; ++j) {
+        const float e = decltype(exact)::value ? av[j] / s : quant_div(av[j], s, r);
+        const uint32_t code = KIND == 1 ? i8_code(e) : e4m3_code(fminf(fmaxf(e, -kF8Max), kF8Max));
+        if (j < 4)
+          lo |= code << (8 * j);
+        else
+          hi |= code << (8 * (j - 4));
+      }
+      *reinterpret_cast<u32x2_t *>(qr + 8 * c) = u32x2_t{lo, hi};
     }
-    *reinterpret_cast<u32x2_t *>(qr + 8 * c) = u32x2_t{lo, hi};
-  }
+  };
+  if (__builtin_isfinite(amax)) sweep(std::false_type{});
+  else sweep(std::true_type{});
 }
 
 int check_vec8(const void *p, int64_t row, const char *name, int esize = 2) {

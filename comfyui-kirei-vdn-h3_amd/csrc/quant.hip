@@ -6,10 +6,13 @@
 //   tensor fp8: one scale for the whole tensor, amax by a grid reduction then a cast pass
 //               (vdn_h3/fp8.py:56-71 `_absmax_kernel` + `_cast_scaled_kernel`, :114-126)
 //
-// The division is IEEE-correct and e4m3fn rounding is round-to-nearest-even, so the codes
-// equal a CPU `(x / s).clamp(...).to(torch.float8_e4m3fn)` bit for bit.
+// The quotient x / s is the multiply-and-correct quant_div (whose codes equal those of the
+// correctly rounded division for every bf16 x with |x| <= amax) or, for a non-finite amax, the
+// IEEE division; e4m3fn rounding is round-to-nearest-even, so the codes equal a CPU
+// `(x / s).clamp(...).to(torch.float8_e4m3fn)` bit for bit.
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -36,15 +39,19 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restr
     }
   }
   amax = wave_max(amax);
-  const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f);
+  const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f), r = 1.f / s;
   if (lane == 0) scale[row] = s;
   uint8_t *qr = q + (int64_t)row * ldq;
+  // the codes of x / s (quant_div for a finite amax, the division otherwise)
+  auto sweep = [&](auto exact) __device__ {
   for (int c = lane; c < chunks; c += 64) {
     const u32x4_t v = ld16(xr + 8 * c);
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float e0 = __uint_as_float(v[j] << 16) / s, e1 = __uint_as_float(v[j] & 0xffff0000u) / s;
+      const float x0 = __uint_as_float(v[j] << 16), x1 = __uint_as_float(v[j] & 0xffff0000u);
+      const float e0 = decltype(exact)::value ? x0 / s : quant_div(x0, s, r);
+      const float e1 = decltype(exact)::value ? x1 / s : quant_div(x1, s, r);
       uint32_t c0, c1;
       if (KIND == 1) {
         c0 = i8_code(e0);
@@ -61,6 +68,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restr
     }
     *reinterpret_cast<u32x2_t *>(qr + 8 * c) = u32x2_t{lo, hi};
   }
+  };
+  if (__builtin_isfinite(amax)) sweep(std::false_type{});
+  else sweep(std::true_type{});
 }
 
 __global__ void fill_f32_kernel(float *p, float v) { *p = v; }
@@ -90,19 +100,25 @@ __global__ __launch_bounds__(256) void absmax_kernel(const uint16_t *__restrict_
 __global__ __launch_bounds__(256) void cast_tensor_f8_kernel(const uint16_t *__restrict__ x, int64_t n8,
                                                              const float *__restrict__ amax, uint8_t *__restrict__ q,
                                                              float *__restrict__ scale) {
-  const float s = fmaxf(*amax / kF8Max, 1e-12f);
+  const float a = *amax, s = fmaxf(a / kF8Max, 1e-12f), r = 1.f / s;
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
-  for (int64_t c = blockIdx.x * 256 + threadIdx.x; c < n8; c += (int64_t)gridDim.x * 256) {
-    const u32x4_t v = ld16(x + 8 * c);
-    uint32_t w[2] = {0, 0};
+  // the codes of x / s (quant_div for a finite amax, the division otherwise)
+  auto sweep = [&](auto exact) __device__ {
+    for (int64_t c = blockIdx.x * 256 + threadIdx.x; c < n8; c += (int64_t)gridDim.x * 256) {
+      const u32x4_t v = ld16(x + 8 * c);
+      uint32_t w[2] = {0, 0};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float e0 = fminf(fmaxf(__uint_as_float(v[j] << 16) / s, -kF8Max), kF8Max);
-      const float e1 = fminf(fmaxf(__uint_as_float(v[j] & 0xffff0000u) / s, -kF8Max), kF8Max);
-      w[j >> 1] |= (e4m3_code(e0) | (e4m3_code(e1) << 8)) << (16 * (j & 1));
+      for (int j = 0; j < 4; ++j) {
+        const float x0 = __uint_as_float(v[j] << 16), x1 = __uint_as_float(v[j] & 0xffff0000u);
+        const float e0 = fminf(fmaxf(decltype(exact)::value ? x0 / s : quant_div(x0, s, r), -kF8Max), kF8Max);
+        const float e1 = fminf(fmaxf(decltype(exact)::value ? x1 / s : quant_div(x1, s, r), -kF8Max), kF8Max);
+        w[j >> 1] |= (e4m3_code(e0) | (e4m3_code(e1) << 8)) << (16 * (j & 1));
+      }
+      *reinterpret_cast<u32x2_t *>(q + 8 * c) = u32x2_t{w[0], w[1]};
     }
-    *reinterpret_cast<u32x2_t *>(q + 8 * c) = u32x2_t{w[0], w[1]};
-  }
+  };
+  if (__builtin_isfinite(a)) sweep(std::false_type{});
+  else sweep(std::true_type{});
 }
 
 // ---------------------------------------------------------------------------------
