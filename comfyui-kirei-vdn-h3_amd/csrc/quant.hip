@@ -19,9 +19,36 @@
 namespace vdnh3 {
 namespace {
 
-// One wavefront per row (4 rows per 256-thread workgroup). Two sweeps over the row: amax,
-// then quantise (the second sweep is served from L2).
-template <int KIND>
+__device__ __forceinline__ float absmax8(u32x4_t v, float m) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    m = fmaxf(m, fabsf(__uint_as_float(v[j] << 16)));
+    m = fmaxf(m, fabsf(__uint_as_float(v[j] & 0xffff0000u)));
+  }
+  return m;
+}
+
+// The int8 (KIND 1) or e4m3fn (KIND 2) codes of the eight bf16 values of v divided by s, bytes
+// in element order: quant_div with r = 1 / s, or the IEEE division when EXACT (non-finite amax).
+template <int KIND, bool EXACT>
+__device__ __forceinline__ u32x2_t codes8(u32x4_t v, float s, float r) {
+  uint32_t w[2] = {0, 0};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float x0 = __uint_as_float(v[j] << 16), x1 = __uint_as_float(v[j] & 0xffff0000u);
+    const float e0 = EXACT ? x0 / s : quant_div(x0, s, r), e1 = EXACT ? x1 / s : quant_div(x1, s, r);
+    const uint32_t c0 = KIND == 1 ? i8_code(e0) : e4m3_code(fminf(fmaxf(e0, -kF8Max), kF8Max));
+    const uint32_t c1 = KIND == 1 ? i8_code(e1) : e4m3_code(fminf(fmaxf(e1, -kF8Max), kF8Max));
+    w[j >> 1] |= (c0 | (c1 << 8)) << (16 * (j & 1));
+  }
+  return u32x2_t{w[0], w[1]};
+}
+
+// One wavefront per row (4 rows per 256-thread workgroup). NCH > 0 (K <= 512 NCH): each lane
+// loads its (up to NCH) 16-byte chunks of the row at once and keeps them in registers from the
+// amax to the codes, so the row is read once with all its loads in flight. NCH == 0 (longer
+// rows): two sweeps, the amax and then the codes (the second sweep served from L2).
+template <int KIND, int NCH>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx, int M, int K,
                                                          uint8_t *__restrict__ q, int64_t ldq,
                                                          float *__restrict__ scale) {
@@ -29,48 +56,53 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t *__restr
   if (row >= M) return;
   const uint16_t *xr = x + (int64_t)row * ldx;
   const int chunks = K / 8;
+  u32x4_t xv[NCH > 0 ? NCH : 1];
   float amax = 0.f;
-  for (int c = lane; c < chunks; c += 64) {
-    const u32x4_t v = ld16(xr + 8 * c);
+  if constexpr (NCH > 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[j] << 16)));
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[j] & 0xffff0000u)));
+    for (int u = 0; u < NCH; ++u) {
+      const int c = lane + 64 * u;
+      xv[u] = c < chunks ? ld16(xr + 8 * c) : u32x4_t{0, 0, 0, 0};  // zeros leave the amax alone
     }
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) amax = absmax8(xv[u], amax);
+  } else {
+    for (int c = lane; c < chunks; c += 64) amax = absmax8(ld16(xr + 8 * c), amax);
   }
   amax = wave_max(amax);
   const float s = fmaxf(amax / (KIND == 1 ? kI8Max : kF8Max), 1e-12f), r = 1.f / s;
   if (lane == 0) scale[row] = s;
   uint8_t *qr = q + (int64_t)row * ldq;
-  // the codes of x / s (quant_div for a finite amax, the division otherwise)
   auto sweep = [&](auto exact) __device__ {
-  for (int c = lane; c < chunks; c += 64) {
-    const u32x4_t v = ld16(xr + 8 * c);
-    uint32_t lo = 0, hi = 0;
+    constexpr bool E = decltype(exact)::value;
+    if constexpr (NCH > 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float x0 = __uint_as_float(v[j] << 16), x1 = __uint_as_float(v[j] & 0xffff0000u);
-      const float e0 = decltype(exact)::value ? x0 / s : quant_div(x0, s, r);
-      const float e1 = decltype(exact)::value ? x1 / s : quant_div(x1, s, r);
-      uint32_t c0, c1;
-      if (KIND == 1) {
-        c0 = i8_code(e0);
-        c1 = i8_code(e1);
-      } else {
-        c0 = e4m3_code(fminf(fmaxf(e0, -kF8Max), kF8Max));
-        c1 = e4m3_code(fminf(fmaxf(e1, -kF8Max), kF8Max));
+      for (int u = 0; u < NCH; ++u) {
+        const int c = lane + 64 * u;
+        if (c < chunks) *reinterpret_cast<u32x2_t *>(qr + 8 * c) = codes8<KIND, E>(xv[u], s, r);
       }
-      const uint32_t pair = c0 | (c1 << 8);
-      if (j < 2)
-        lo |= pair << (16 * j);
-      else
-        hi |= pair << (16 * (j - 2));
+    } else {
+      for (int c = lane; c < chunks; c += 64)
+        *reinterpret_cast<u32x2_t *>(qr + 8 * c) = codes8<KIND, E>(ld16(xr + 8 * c), s, r);
     }
-    *reinterpret_cast<u32x2_t *>(qr + 8 * c) = u32x2_t{lo, hi};
-  }
   };
   if (__builtin_isfinite(amax)) sweep(std::false_type{});
   else sweep(std::true_type{});
+}
+
+// The register-resident form with the fewest chunks per lane that holds the row (K <= 2048, 5120,
+// 8192; more chunks cost registers and occupancy), else the two-sweep form.
+template <int KIND>
+void launch_quant_rows(dim3 grid, hipStream_t s, const uint16_t *x, int64_t ldx, int M, int K, uint8_t *q, int64_t ldq,
+                       float *scale) {
+  if (K <= 512 * 4)
+    hipLaunchKernelGGL((quant_rows_kernel<KIND, 4>), grid, dim3(256), 0, s, x, ldx, M, K, q, ldq, scale);
+  else if (K <= 512 * 10)
+    hipLaunchKernelGGL((quant_rows_kernel<KIND, 10>), grid, dim3(256), 0, s, x, ldx, M, K, q, ldq, scale);
+  else if (K <= 512 * 16)
+    hipLaunchKernelGGL((quant_rows_kernel<KIND, 16>), grid, dim3(256), 0, s, x, ldx, M, K, q, ldq, scale);
+  else
+    hipLaunchKernelGGL((quant_rows_kernel<KIND, 0>), grid, dim3(256), 0, s, x, ldx, M, K, q, ldq, scale);
 }
 
 __global__ void fill_f32_kernel(float *p, float v) { *p = v; }
@@ -102,20 +134,9 @@ __global__ __launch_bounds__(256) void cast_tensor_f8_kernel(const uint16_t *__r
                                                              float *__restrict__ scale) {
   const float a = *amax, s = fmaxf(a / kF8Max, 1e-12f), r = 1.f / s;
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
-  // the codes of x / s (quant_div for a finite amax, the division otherwise)
   auto sweep = [&](auto exact) __device__ {
-    for (int64_t c = blockIdx.x * 256 + threadIdx.x; c < n8; c += (int64_t)gridDim.x * 256) {
-      const u32x4_t v = ld16(x + 8 * c);
-      uint32_t w[2] = {0, 0};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float x0 = __uint_as_float(v[j] << 16), x1 = __uint_as_float(v[j] & 0xffff0000u);
-        const float e0 = fminf(fmaxf(decltype(exact)::value ? x0 / s : quant_div(x0, s, r), -kF8Max), kF8Max);
-        const float e1 = fminf(fmaxf(decltype(exact)::value ? x1 / s : quant_div(x1, s, r), -kF8Max), kF8Max);
-        w[j >> 1] |= (e4m3_code(e0) | (e4m3_code(e1) << 8)) << (16 * (j & 1));
-      }
-      *reinterpret_cast<u32x2_t *>(q + 8 * c) = u32x2_t{w[0], w[1]};
-    }
+    for (int64_t c = blockIdx.x * 256 + threadIdx.x; c < n8; c += (int64_t)gridDim.x * 256)
+      *reinterpret_cast<u32x2_t *>(q + 8 * c) = codes8<2, decltype(exact)::value>(ld16(x + 8 * c), s, r);
   };
   if (__builtin_isfinite(a)) sweep(std::false_type{});
   else sweep(std::true_type{});
@@ -133,15 +154,6 @@ constexpr int64_t kAmaxSpan = 8 * kAmaxSpanChunks;     // 16,384 elements per pa
 constexpr int kAmaxPartials = 16384;                   // n <= kAmaxSpan * kAmaxPartials (268,435,456)
 constexpr int kScratchFloats = kAmaxPartials + 64;     // partials, then the total (64 KiB + 256 B)
 __device__ __align__(256) float scratch[kScratchFloats];
-
-__device__ __forceinline__ float absmax8(u32x4_t v, float m) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    m = fmaxf(m, fabsf(__uint_as_float(v[j] << 16)));
-    m = fmaxf(m, fabsf(__uint_as_float(v[j] & 0xffff0000u)));
-  }
-  return m;
-}
 
 __device__ __forceinline__ float block_max256(float m, float *red) {
   m = wave_max(m);
@@ -218,9 +230,9 @@ extern "C" int vdnh3_quant_rows(int kind, const uint16_t *x, int64_t ldx, int M,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((M + 3) / 4);
   if (kind == 1)
-    hipLaunchKernelGGL(quant_rows_kernel<1>, grid, dim3(256), 0, s, x, ldx, M, K, q, ldq, scale);
+    launch_quant_rows<1>(grid, s, x, ldx, M, K, q, ldq, scale);
   else
-    hipLaunchKernelGGL(quant_rows_kernel<2>, grid, dim3(256), 0, s, x, ldx, M, K, q, ldq, scale);
+    launch_quant_rows<2>(grid, s, x, ldx, M, K, q, ldq, scale);
   return check_launch("quant_rows");
 }
 
