@@ -119,6 +119,15 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_
 // 16-byte vector load / store (addresses must be 16-byte aligned).
 __device__ __forceinline__ u32x4_t ld16(const void *p) { return *reinterpret_cast<const u32x4_t *>(p); }
 __device__ __forceinline__ void st16(void *p, u32x4_t v) { *reinterpret_cast<u32x4_t *>(p) = v; }
+// the same to global memory with the non-temporal hint: the data streams through L2 without
+// displacing lines that other workgroups are still reading
+__device__ __forceinline__ void st16_stream(void *p, u32x4_t v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t *>(p));
+}
+// 16-byte global load with the non-temporal hint, for data read once
+__device__ __forceinline__ u32x4_t ld16_stream(const void *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+}
 
 // ---- direct-to-LDS tile loads and explicit waits ---------------------------------------
 // s_waitcnt with vmcnt <= N, lgkmcnt = 0 (expcnt left alone), gfx9 encoding of the immediate.
