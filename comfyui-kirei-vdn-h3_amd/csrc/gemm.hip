@@ -124,12 +124,17 @@ __device__ __forceinline__ EpiOperands load_epi_operands(const GemmEpi &epi, int
   return o;
 }
 
-// Output stores are non-temporal (the `nt` hint): the output streams through each XCD's L2 at
-// 128 KB per tile, which would otherwise evict the A and B panels that the XCD's other
-// workgroups are still reading (6-8% of the int8 / fp8 projection time, bit-identical output).
+// Output stores, and the loads of the old values when accumulating, are non-temporal (the `nt`
+// hint): the output streams through each XCD's L2 at 128 KB per tile, which would otherwise
+// evict the A and B panels that the XCD's other workgroups are still reading (6-8% of the int8 /
+// fp8 projection time, 2% more for the accumulating to_out_linear; bit-identical output).
 template <typename V, typename P>
 __device__ __forceinline__ void stream_store(V v, P *p) {
   __builtin_nontemporal_store(v, reinterpret_cast<V *>(p));
+}
+template <typename V, typename P>
+__device__ __forceinline__ V stream_load(const P *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const V *>(p));
 }
 
 template <int OUT, bool ACT, bool ACCUM, bool INT_ACC, typename Acc>
@@ -168,8 +173,8 @@ __device__ __forceinline__ void store_block(const Acc (&acc)[4][kGemmNJ], uint32
           old[q] = old_t{};
           if (vec && m < M) {
             const int64_t off = (int64_t)m * ldc + n;
-            if constexpr (OUT == kOutF32) old[q] = *reinterpret_cast<const f32x4_t *>(static_cast<float *>(C) + off);
-            else old[q] = *reinterpret_cast<const u32x2_t *>(static_cast<uint16_t *>(C) + off);
+            if constexpr (OUT == kOutF32) old[q] = stream_load<f32x4_t>(static_cast<float *>(C) + off);
+            else old[q] = stream_load<u32x2_t>(static_cast<uint16_t *>(C) + off);
           }
         }
       }
