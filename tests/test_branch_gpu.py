@@ -1,6 +1,6 @@
 """Parity of the HIP Video Delta Attention kernels with the CPU oracle (GPU).
 
-Bars (north star: delta-rule outputs within max-abs 2e-2 and cosine >= 0.9995 of the fp32
+Bars (the block parity bar: delta-rule outputs within max-abs 2e-2 and cosine >= 0.9995 of the fp32
 reference path): per-stage checks are tighter where the arithmetic allows - A to fp32
 rounding, B / bf16 outputs to one or two bf16 steps, the factor and scans to ~1e-4
 relative (fp32 Cholesky and MFMA summation order).

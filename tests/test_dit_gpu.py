@@ -3,7 +3,7 @@
 The pointwise passes follow the reference's bf16 ops, so they are compared element by element
 (bit-exact where every input of an op is exact, otherwise within one bf16 step where the fp32
 statistics of the RMSNorm or the exponential of SiLU may round a midpoint differently); the
-whole block against the north-star bar (max-abs 2e-2, cosine >= 0.9995).
+whole block against the block parity bar (max-abs 2e-2, cosine >= 0.9995).
 """
 
 from __future__ import annotations

@@ -184,7 +184,7 @@ def _tile_rows(m, tile=256):
 
 @pytest.mark.parametrize("n", [15360, 5120])
 def test_full_shape_fp8_per_tensor_sampled(device, n):
-    """M=40,688, K=5,120 fp8 e4m3 with per-tensor scales (BASELINE's second W8A8 variant), N=15,360
+    """M=40,688, K=5,120 fp8 e4m3 with per-tensor scales (the reference's fp8 W8A8 variant), N=15,360
     (qkv) and 5,120 (out): one row of every M tile against the dequantised float64 product."""
     from vdn_h3_amd import fp8, synth
 

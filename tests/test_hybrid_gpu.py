@@ -1,6 +1,6 @@
 """Parity of the HIP hybrid attention block (``make_vdn_forward``) with the reference (GPU).
 
-Bars (north star): max-abs 2e-2 and cosine >= 0.9995 against the reference's own
+Bars: max-abs 2e-2 and cosine >= 0.9995 (the block's parity bar) against the reference's own
 ``make_vdn_forward`` output (golden vector) and against the CPU oracle of the block; the
 q/k RMSNorm pass and the standalone softmax gate within one bf16 rounding step.
 """
