@@ -160,7 +160,8 @@ struct RowNorm {
   }
 };
 
-constexpr int kPrepassHeads = 8;  // heads per pre-pass workgroup (they share its rows' RoPE matrices)
+constexpr int kPrepassHeads = 10;  // heads per pre-pass workgroup (they share its rows' RoPE matrices);
+                                   // 10 measured 4% faster than 8 at 40 heads, 4, 5 and 20 no better
 
 // Pre-pass of the normalising attention, for the 64 rows [k0, k0 + 64) of up to kPrepassHeads
 // heads: the V^T copy of vt_prepass_kernel, the normalised keys kn[head][key][d] and, when q is
