@@ -76,7 +76,8 @@ def test_split_sigmoid_epilogue_equals_two_gemms(device):
         L.gemm(L.KIND_BF16, x, wb, act="sigmoid", act_cols=heads + 1)
 
 
-@pytest.mark.parametrize("m,k", [(257, 512), (64, 5120), (33, 1032), (9, 8192), (7, 8200)])
+@pytest.mark.parametrize("m,k", [(257, 512), (64, 5120), (33, 1032), (5, 2048), (5, 2056), (5, 5128),
+                                 (9, 8192), (7, 8200)])
 def test_quant_codes_bit_exact(device, m, k):
     from vdn_h3_amd import linear
 
