@@ -8,7 +8,7 @@
 //   one workgroup = 8 wavefronts = 256 query rows of one head x the key tiles of its run;
 //   each wavefront owns 32 query rows and keeps its Q fragment in registers.
 //   Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16: every lane
-//   then owns one query column (lane % 32) and 16+16 of the 64 keys of a tile, so the row
+//   then owns one query column (lane % 32) and 3 x 16 of the 96 keys of a tile, so the row
 //   max is one cross-lane exchange (lane ^ 32) and the probabilities P^T feed the next
 //   MFMA (O^T += V^T P^T) straight from registers, without an LDS round trip.
 //   V^T is read from a head-major copy made by a pre-pass (one extra 2*S*H*D-byte sweep),
@@ -30,9 +30,9 @@ namespace vdnh3 {
 namespace {
 
 constexpr int kBM = 256;  // query rows per workgroup (8 wavefronts x 32)
-constexpr int kBN = 64;   // keys per tile
+constexpr int kBN = 96;   // keys per tile: 48 MFMAs per wavefront and phase at D = 128
 constexpr int kThreads = 512;
-constexpr int kRing = 4;  // LDS slots per K and V^T ring: tile loads are issued kRing - 1 tiles ahead
+constexpr int kRing = 3;  // LDS slots per K and V^T ring (144 KB at D = 128): loads run kRing - 1 tiles ahead
 constexpr float kLazy = 8.0f;  // log2 of the largest probability a stale running max allows
 
 // LDS position p (0..15) inside a 16-key group holds key offset kperm(p): the order in
@@ -222,6 +222,13 @@ __device__ __forceinline__ int k_slot(int r, int c) {
   else return c ^ ((r >> 1) & 7);               // 8 chunks per 128-byte row
 }
 __device__ __forceinline__ int v_slot(int d, int c) { return c ^ ((d >> 1) & 7); }  // 8 chunks per row
+// the V^T tile's 32-key part (4 chunks per row): the 16 lanes of a fragment read (rows d..d+15)
+// hit 16 different 16-byte bank groups
+__device__ __forceinline__ int vb_slot(int d, int c) { return c ^ ((d >> 2) & 3); }
+
+// Rows of the V^T copy and of the normalised q / k regions: seq rounded up to 192, a multiple of the
+// pre-pass's 64-row blocks and of the attention's key tiles, so a tile never reads past its row.
+__host__ __device__ constexpr int pad_rows(int seq) { return (seq + 191) / 192 * 192; }
 
 
 // The value of lane (l + 32) mod 64, via v_permlane32_swap (gfx950).
@@ -306,13 +313,15 @@ __device__ __forceinline__ void store_rows(const f32x16_t (&oacc)[D / 32], float
 // Waves 0-3 (group A) and 4-7 (group B) each own 32 query rows; wave w and w + 4 share a SIMD.
 // The item runs in barrier-separated phases p = 0 .. 2T+1; in each phase one group works on the
 // matrix cores and the other on the VALU, so the two waves of every SIMD alternate:
-//   MFMA phase of tile t :  O^T += V(t-1)^T P(t-1)^T   and   S(t)^T = K(t) Q^T      (32 MFMAs)
+//   MFMA phase of tile t :  O^T += V(t-1)^T P(t-1)^T   and   S(t)^T = K(t) Q^T      (48 MFMAs)
 //   VALU phase of tile t :  P(t) = exp2(scale S(t) - m), row max / sum, O rescale   (softmax)
 // Group A runs tile t's MFMA phase in phase 2t and its VALU phase in 2t+1; group B one phase
 // later. K(t) and V(t-1) are read in phases 2t and 2t+1 only; tiles are loaded direct to LDS
-// into four-slot rings, three tiles ahead: K tiles by group A and V^T tiles by group B, each at
+// into three-slot rings, two tiles ahead: K tiles by group A and V^T tiles by group B, each at
 // the start of the issuing group's VALU phase, so the MFMA stream carries no memory instruction
-// and a tile that misses L2 has three tiles' time to land.
+// and a tile that misses L2 has two tiles' time to land. A tile is 96 keys: every phase switch
+// (a barrier, the first fragment reads of the MFMA phase) is shared by 48 MFMAs per wavefront, a
+// third fewer switches than with 64-key tiles for the same work.
 // QNORM: q is normalised as it is loaded (the block's q_norm with q_weight / q_eps, the arithmetic
 // of qk_norm.h); otherwise q is used as given.
 template <int D, bool QNORM>
@@ -325,7 +334,12 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   constexpr int KC = D / 8;    // 16-byte chunks per K row
   constexpr int NS = D / 16;   // k-steps of the QK^T contraction
   constexpr int NO = D / 32;   // 32-row blocks of O^T
+  constexpr int NKB = kBN / 32;  // 32-key blocks of S^T
+  constexpr int NT = kBN / 16;   // k-steps of the PV contraction
   constexpr int KT = kBN * D, VT = D * kBN;  // elements per tile
+  // a V^T tile in LDS: keys 0..63 as [D][8 chunks] (v_slot), then keys 64..95 as [D][4 chunks] (vb_slot)
+  constexpr int VA = D * 64;
+  static_assert(kBN == 96, "the V^T tile layout is a 64-key part and a 32-key part");
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kRing][KT];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kRing][VT];
 
@@ -351,24 +365,33 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
 
   const uint16_t *kbase = k + (int64_t)head * k_head;
   const uint16_t *vbase = vt + (int64_t)head * D * s_pad;
-  // Tile loads, by one group of 256 threads: LDS position P of a K tile is (row P / KC, slot
-  // P % KC) and holds chunk slot ^ swizzle(row) of that key row (likewise for V^T with 8 chunks
-  // per d-row). Thread chunk i covers row kr0 + i * kBN / KCG; the swizzle depends on the row
-  // only through bits that are the same for every i. Rows past seq read row seq - 1 (their
-  // scores are masked).
-  constexpr int KCG = kBN * KC / 256, VCG = D * 8 / 256;  // 16-byte chunks per thread and tile
+  // Tile loads, by one group of 256 threads: thread chunk i fills LDS position P = 256 i + gtid
+  // (16-byte units) of the tile. In a K tile, P is (row P / KC, slot P % KC) and holds chunk
+  // slot ^ swizzle(row) of that key row; row kr0 + i * 256 / KC has the same swizzle for every i.
+  // In a V^T tile, P < 8 D is (d, slot) of the 64-key part, the rest (d, slot) of the 32-key part.
+  // Rows past seq read row seq - 1 (their scores are masked).
+  constexpr int KCG = kBN * KC / 256, VCG = D * (kBN / 8) / 256;  // 16-byte chunks per thread and tile
   static_assert(KCG >= 1 && VCG >= 1 && KCG == VCG, "both groups issue the same number of loads");
   const int gtid = tid & 255, gw = wave & 3;
-  const int kr0 = gtid / KC, vd0 = gtid >> 3;
+  const int kr0 = gtid / KC;
   const int kslot = k_slot<D>(kr0, gtid % KC) * 8;
   // per-lane byte offsets of this group's chunks inside a tile's source rows (K rows for group
   // A, V^T rows for group B) and the tile's LDS base of this wavefront: an issue is a scalar
   // tile base, a scalar M0 and the load
   uint32_t doff[KCG];
 #pragma unroll
-  for (int i = 0; i < KCG; ++i)
-    doff[i] = 2u * (group == 0 ? (uint32_t)((kr0 + i * (kBN / KCG)) * (int)k_row + kslot)
-                               : (uint32_t)((vd0 + i * (D / VCG)) * s_pad + v_slot(vd0, gtid & 7) * 8));
+  for (int i = 0; i < KCG; ++i) {
+    const int P = 256 * i + gtid;
+    uint32_t vo;
+    if (P < D * 8) {
+      const int d = P >> 3;
+      vo = (uint32_t)(d * s_pad + v_slot(d, P & 7) * 8);
+    } else {
+      const int d = (P - D * 8) >> 2;
+      vo = (uint32_t)(d * s_pad + 64 + vb_slot(d, P & 3) * 8);
+    }
+    doff[i] = 2u * (group == 0 ? (uint32_t)((kr0 + i * (256 / KC)) * (int)k_row + kslot) : vo);
+  }
   const uint32_t lds_dma = __builtin_amdgcn_readfirstlane(
       (group == 0 ? lds_address(&Ks[0][0]) : lds_address(&Vs[0][0])) + gw * 64 * 16);
   constexpr uint32_t kTileBytes = KT * 2;
@@ -383,7 +406,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
     if (group == 0 && ks + kBN > seq) {  // uniform: taken for the last tile of the sequence only
 #pragma unroll
       for (int i = 0; i < KCG; ++i)
-        off[i] = 2u * (uint32_t)((min(ks + kr0 + i * (kBN / KCG), seq - 1) - ks) * (int)k_row + kslot);
+        off[i] = 2u * (uint32_t)((min(ks + kr0 + i * (256 / KC), seq - 1) - ks) * (int)k_row + kslot);
     }
 #pragma unroll
     for (int i = 0; i < KCG; ++i)
@@ -392,18 +415,19 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
 
   // Fragment offsets inside a tile (elements). The swizzles depend on the row only through
   // l32 (r = 32 kb + l32, d = 32 m + l32), so the 32-row blocks differ by constant offsets.
-  int kfo[NS], vfo[4];
+  int kfo[NS], vfo[NT];
 #pragma unroll
   for (int st = 0; st < NS; ++st) kfo[st] = (l32 * KC + k_slot<D>(l32, 2 * st + g)) * 8;
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) vfo[tt] = (l32 * 8 + v_slot(l32, 2 * tt + g)) * 8;
+  for (int tt = 0; tt < NT; ++tt)
+    vfo[tt] = tt < 4 ? (l32 * 8 + v_slot(l32, 2 * tt + g)) * 8 : VA + (l32 * 4 + vb_slot(l32, 2 * (tt - 4) + g)) * 8;
 
-  f32x16_t oacc[NO], sacc[2];
+  f32x16_t oacc[NO], sacc[NKB];
 #pragma unroll
   for (int m = 0; m < NO; ++m) oacc[m] = f32x16_t{};
-  bf16x8_t pb[4];
+  bf16x8_t pb[NT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) pb[j] = bf16x8_t{};
+  for (int j = 0; j < NT; ++j) pb[j] = bf16x8_t{};
   float m_run = -INFINITY, l_run = 0.f;
 
   // Rings: K(tau) and V(tau) live in slot tau % kRing. K(t) and V(t-1) are read in phases 2t
@@ -421,9 +445,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
 #pragma unroll
   for (int j = 0; j < kRing - 1; ++j)
     if (j < kRing - 2 || group == 0) tile_dma(tiles[toff + min(j, T - 1)].x, j);
-#pragma unroll
-  for (int i = 0; i < VT / 8 / kThreads; ++i)
-    st16(Vs[kRing - 1] + (i * kThreads + tid) * 8, u32x4_t{0, 0, 0, 0});
+  for (int i = tid; i < VT / 8; i += kThreads) st16(Vs[kRing - 1] + i * 8, u32x4_t{0, 0, 0, 0});
   wait_vm_lds<0>();
   bare_barrier();
 
@@ -444,19 +466,22 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
         // descriptors of this group's next VALU phase (tile t_mfma)
         dma_ks = tiles[toff + min(t_mfma + kRing - 1, T - 1)].x;
       } else {
-      // MFMA phase of tile t: O^T += V(t-1)^T P(t-1)^T, S(t)^T = K(t) Q^T (16 + 16 MFMAs at D = 128).
+      // MFMA phase of tile t: O^T += V(t-1)^T P(t-1)^T, S(t)^T = K(t) Q^T (24 + 24 MFMAs at D = 128).
       // t = 0 has no PV and t = T no QK: those phases run on a zero tile / discard the scores,
       // so the phase is one branch-free block. Fragment reads run eight MFMAs ahead.
       const int t = t_mfma;
-      const uint16_t *vtile = Vs[(t + kRing - 1) & (kRing - 1)];
-      const uint16_t *ktile = Ks[t & (kRing - 1)];
-      // MFMA i < NP: PV block m = i % NO, k-step tt = i / NO; i >= NP: QK block kb = (i - NP) % 2,
-      // k-step st = (i - NP) / 2. Consecutive MFMAs update different accumulators, so none waits
+      const uint16_t *vtile = Vs[(t + kRing - 1) % kRing];
+      const uint16_t *ktile = Ks[t % kRing];
+      // MFMA i < NP: PV block m = i % NO, k-step tt = i / NO; i >= NP: QK block kb = (i - NP) % NKB,
+      // k-step st = (i - NP) / NKB. Consecutive MFMAs update different accumulators, so none waits
       // for the result of the one before it.
-      constexpr int NP = NO * 4, NM = NP + 2 * NS;
+      constexpr int NP = NO * NT, NM = NP + NKB * NS;
       auto frag = [&](int i) __device__ {
-        return i < NP ? ld16(vtile + (i % NO) * 32 * kBN + vfo[i / NO])
-                      : ld16(ktile + ((i - NP) & 1) * 32 * D + kfo[(i - NP) >> 1]);
+        if (i < NP) {
+          const int m = i % NO, tt = i / NO;
+          return ld16(vtile + (tt < 4 ? m * 32 * 64 : m * 32 * 32) + vfo[tt]);
+        }
+        return ld16(ktile + ((i - NP) % NKB) * 32 * D + kfo[(i - NP) / NKB]);
       };
       // the MFMA wave of each SIMD issues ahead of the VALU wave sharing it
       __builtin_amdgcn_s_setprio(1);
@@ -470,7 +495,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
         if (i < NP) {
           oacc[i % NO] = mfma_bf16_32x32x16(as_bf16x8(a), pb[i / NO], oacc[i % NO]);
         } else {
-          const int kb = (i - NP) & 1, st = (i - NP) >> 1;
+          const int kb = (i - NP) % NKB, st = (i - NP) / NKB;
           if (st == 0) sacc[kb] = f32x16_t{};
           sacc[kb] = mfma_bf16_32x32x16(as_bf16x8(a), qf[st], sacc[kb]);
         }
@@ -483,35 +508,35 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
       mask = t < T ? tiles[toff + t].y : 0;
       }
     } else {
-      // VALU phase of tile t: first this group's tile loads (three tiles ahead), then the softmax
+      // VALU phase of tile t: first this group's tile loads (two tiles ahead), then the softmax
       // in base 2, one query per lane. The running max m_run moves only when this tile's max
       // exceeds it by more than 2^kLazy: probabilities stay below 2^kLazy (exact softmax either
       // way, a common shift cancels in O / l) and most tiles skip the rescale.
-      tile_dma(dma_ks, (t_valu + kRing - 1) & (kRing - 1));
+      tile_dma(dma_ks, (t_valu + kRing - 1) % kRing);
       const bool work = rows_live && p >= 1 + group && t_valu < T;
       if (work) {
         const int lo = mask & 0xffff, hi = mask >> 16;
         if (lo > 0 || hi < kBN) {
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
               const int ko = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
               if (ko < lo || ko >= hi) sacc[kb][i] = -INFINITY;
             }
         }
-        // tile row max over the lane's 32 scores as a tree of three-input maxima (16 v_max3),
-        // then the other half-wave's value through v_permlane32_swap (no LDS round trip)
-        float m1[11];
+        // tile row max over the lane's 48 scores as a tree of three-input maxima (16 + 5 + 2
+        // v_max3), then the other half-wave's value through v_permlane32_swap (no LDS round trip)
+        static_assert(NKB == 3, "the max tree is written for 48 scores per lane");
+        float m1[16];
 #pragma unroll
-        for (int i = 0; i < 10; ++i) {
-          const int a = 3 * i, b = 3 * i + 1, c = 3 * i + 2;
-          m1[i] = fmaxf(fmaxf(sacc[a >> 4][a & 15], sacc[b >> 4][b & 15]), sacc[c >> 4][c & 15]);
-        }
-        m1[10] = fmaxf(sacc[1][14], sacc[1][15]);
-        const float m2a = fmaxf(fmaxf(m1[0], m1[1]), m1[2]), m2b = fmaxf(fmaxf(m1[3], m1[4]), m1[5]);
-        const float m2c = fmaxf(fmaxf(m1[6], m1[7]), m1[8]), m2d = fmaxf(m1[9], m1[10]);
-        const float mx = fmaxf(fmaxf(fmaxf(m2a, m2b), m2c), m2d);
+        for (int i = 0; i < 16; ++i)
+          m1[i] = fmaxf(fmaxf(sacc[0][i], sacc[1][i]), sacc[2][i]);
+        float m2[6];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) m2[i] = fmaxf(fmaxf(m1[3 * i], m1[3 * i + 1]), m1[3 * i + 2]);
+        m2[5] = m1[15];
+        const float mx = fmaxf(fmaxf(fmaxf(m2[0], m2[1]), m2[2]), fmaxf(fmaxf(m2[3], m2[4]), m2[5]));
         const float mt = fmaxf(mx, other_half(mx)) * scale_log2;
         const bool grow = mt > m_run + kLazy;
         if (__any(grow)) {
@@ -528,7 +553,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
         const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
         float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; i += 2) {
             const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][i], scale_log2, -m_run));
@@ -555,7 +580,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
 template <int D>
 int launch_prepass(const uint16_t *v, int64_t v_row, int64_t v_head, int seq, int heads, void *workspace,
                    hipStream_t stream) {
-  const int s_pad = (seq + 63) / 64 * 64;
+  const int s_pad = pad_rows(seq);
   hipLaunchKernelGGL(vt_prepass_kernel<D>, dim3(s_pad / 64, heads), dim3(kThreads), 0, stream, v, v_row, v_head,
                      static_cast<uint16_t *>(workspace), seq, s_pad);
   return check_launch("window vt_prepass");
@@ -567,7 +592,7 @@ int launch_attn(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t
                 uint16_t *out, int64_t o_row, int64_t o_head, const uint16_t *gate, int64_t gate_row, int seq,
                 int heads, float scale, const int32_t *items, int32_t n_items, const int32_t *tiles,
                 const void *workspace, hipStream_t stream, const uint16_t *q_weight = nullptr, float q_eps = 0.f) {
-  const int s_pad = (seq + 63) / 64 * 64;
+  const int s_pad = pad_rows(seq);
   const int total = n_items * heads;
   const int per_xcd = (total + 7) / 8;
   hipLaunchKernelGGL((window_attn_kernel<D, QNORM>), dim3(per_xcd * 8), dim3(kThreads), 0, stream, q, q_row, q_head, k,
@@ -582,7 +607,7 @@ int launch_qkv_prepass(const uint16_t *q, int64_t q_row, int64_t q_head, const u
                        const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *k_weight, float k_eps,
                        const uint16_t *v, int64_t v_row, int64_t v_head, const float *freqs, int64_t f_row, int rot,
                        int seq, int heads, void *workspace, hipStream_t stream) {
-  const int s_pad = (seq + 63) / 64 * 64;
+  const int s_pad = pad_rows(seq);
   const size_t region = (size_t)heads * D * s_pad;
   uint16_t *vt = static_cast<uint16_t *>(workspace), *kn = vt + region, *qn = vt + 2 * region;
   const dim3 grid((heads + kPrepassHeads - 1) / kPrepassHeads, s_pad / 64);
@@ -633,7 +658,7 @@ extern "C" int vdnh3_window_block_n(void) { return vdnh3::kBN; }
 
 extern "C" size_t vdnh3_window_workspace_bytes(int seq, int heads, int head_dim) {
   if (seq <= 0 || heads <= 0 || head_dim <= 0) return 0;
-  return size_t(heads) * size_t(head_dim) * size_t((seq + 63) / 64 * 64) * sizeof(uint16_t);
+  return size_t(heads) * size_t(head_dim) * size_t(vdnh3::pad_rows(seq)) * sizeof(uint16_t);
 }
 
 extern "C" int vdnh3_window_vt_prepass(const uint16_t *v, int64_t v_row, int64_t v_head, int seq, int heads,
@@ -700,7 +725,7 @@ extern "C" int vdnh3_window_qkv_prepass(const uint16_t *q, int64_t q_row, int64_
   const size_t need = vdnh3_window_norm_workspace_bytes(seq, heads, head_dim, q != nullptr);
   VDNH3_HOST_CHECK(workspace_bytes >= need, VDNH3_ERR_INVALID,
                    "workspace of %zu bytes is smaller than the %zu the pre-pass writes", workspace_bytes, need);
-  VDNH3_HOST_CHECK((seq + 63) / 64 <= 65535, VDNH3_ERR_INVALID, "the pre-pass supports at most %d rows, got %d",
+  VDNH3_HOST_CHECK(vdnh3::pad_rows(seq) / 64 <= 65535, VDNH3_ERR_INVALID, "the pre-pass supports at most %d rows, got %d",
                    65535 * 64, seq);
   hipStream_t s = static_cast<hipStream_t>(stream);
   return head_dim == 128 ? vdnh3::launch_qkv_prepass<128>(q, q_row, q_head, q_weight, q_eps, k, k_row, k_head,
@@ -727,7 +752,7 @@ extern "C" int vdnh3_window_attn_qnorm(const uint16_t *q, int64_t q_row, int64_t
                    VDNH3_ERR_INVALID, "out must be 8-byte aligned with strides that are multiples of 4 elements");
   VDNH3_HOST_CHECK(items != nullptr && tiles != nullptr && n_items > 0, VDNH3_ERR_INVALID, "empty window plan");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int s_pad = (seq + 63) / 64 * 64;
+  const int s_pad = vdnh3::pad_rows(seq);
   // the normalised keys follow the V^T copy in the workspace: [heads][s_pad][head_dim]
   const uint16_t *kn = static_cast<const uint16_t *>(workspace) + (size_t)heads * head_dim * s_pad;
   const int64_t kn_row = head_dim, kn_head = (int64_t)s_pad * head_dim;

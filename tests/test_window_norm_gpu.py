@@ -70,7 +70,7 @@ def test_qkv_prepass_matches_qk_pass(device, dim, rot, shared, with_queries):
     _lib.check(lib.vdnh3_window_vt_prepass(_lib.ptr(v), v.stride(0), v.stride(1), seq, heads, dim, _lib.ptr(vt_ref),
                                            region, _lib.stream_handle(device)), "vdnh3_window_vt_prepass")
     torch.cuda.synchronize()
-    s_pad = (seq + 63) // 64 * 64
+    s_pad = region // (2 * heads * dim)  # the rows of each workspace region (seq padded)
     assert ws_bytes == (3 if with_queries else 2) * region
     assert torch.equal(ws[:region].cpu(), vt_ref.cpu())
     for r, want in ((1, want_k), (2, want_q))[:2 if with_queries else 1]:
