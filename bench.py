@@ -469,8 +469,7 @@ def bench_gdn(args, torch, device):
     if args.cpu_sample_rows > 0:
         from oracle import gdn_oracle as go
 
-        sel = list(range(heads))
-        sel = list(range(8))
+        sel = list(range(8))  # 8 of the heads: the same work per head, a bounded CPU sample
         hq, hk, hv, hb, hg = (t[:, sel].cpu() for t in (q, k, v, beta, lg))
         dt, runs = _median_seconds(lambda: go.chunked(hq, hk, hv, hb, hg))
         model, physical = _cpu_description()

@@ -318,9 +318,11 @@ def test_projected_delta_qkv_short_conv(device):
 def test_full_shape_branch(device):
     """31 frames x 1296 tokens x 40 heads x 128 (29 inner frames after skip_ends), 512 text rows.
 
-    The oracle runs the whole branch on the CPU. The readout (RMS-normalised, values up to ~6)
-    is compared element-wise within two bf16 steps; the projected delta (O(1) values) at
-    sampled rows against the absolute bar (max-abs 2e-2, cosine >= 0.9995).
+    The oracle runs the whole branch on the CPU. The readout (RMS-normalised, values up to ~6) is
+    compared element-wise: at most 0.5% of values more than two bf16 ulps of the oracle value off and
+    0.15% more than eight, every value within eight ulps of max(|v|, 1), cosine >= 0.9999; the isolation
+    check below pins the path after the statistics tighter. The projected delta (O(1) values) at sampled
+    rows against the absolute bar (max-abs 2e-2, cosine >= 0.9995).
     """
     from vdn_h3_amd import synth
     from vdn_h3_amd.runtime import OptimizedLinearBranch
@@ -370,6 +372,9 @@ def test_full_shape_branch(device):
     cos = torch.nn.functional.cosine_similarity(g32.double().flatten(), w32.double().flatten(), dim=0).item()
     rows = torch.arange(0, 37584, 64)
     want_delta = bo.linear_bf16(want[rows], hw["to_out_linear.weight"])
+    steps1 = (g32 - w32).abs() / torch.maximum(ulp, torch.full_like(ulp, 2.0 ** -7))
+    print(f"readout: ulps of max(|v|, 1): max {steps1.max().item():.1f}, frac > 2 {(steps1 > 2).float().mean():.2e}, "
+          f"frac > 8 {(steps1 > 8).float().mean():.2e}", flush=True)
     print(f"readout: cosine {cos:.7f}, ulps: max {steps.max().item():.1f}, frac > 2 {(steps > 2).float().mean():.2e}, "
           f"frac > 4 {(steps > 4).float().mean():.2e}, frac > 8 {(steps > 8).float().mean():.2e}; "
           f"max abs where |want| < 2: {err_small:.3e}; max |want| {w32.abs().max().item():.2f}", flush=True)
@@ -379,6 +384,8 @@ def test_full_shape_branch(device):
     assert cos >= 0.9999, cos
     assert (steps > 2).float().mean().item() <= 5e-3
     assert (steps > 8).float().mean().item() <= 1.5e-3
+    # every value within 8 ulps of max(|v|, 1): the values far off in their own ulps lie near zero
+    assert steps1.max().item() <= 8
     assert torch.count_nonzero(readout[:tpf]) == 0 and torch.count_nonzero(readout[-tpf:]) == 0
     _parity(delta[tpf:-tpf][rows], want_delta, "full-shape projected delta")
     assert torch.count_nonzero(delta[:tpf]) == 0 and torch.count_nonzero(delta[-tpf:]) == 0

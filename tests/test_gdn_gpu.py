@@ -1,9 +1,9 @@
 """Parity of the chunked Gated DeltaNet kernels with the float64 oracle (GPU).
 
 Not reference parity: the reference has no token-level delta rule (its branch is per frame).
-Bars: cosine >= 0.9995 and max-abs within max(2e-2, 2^-6 * max|o|) (a few bf16 steps of the
-largest output: q, k K^T, W, U~, P and U enter the MFMAs in bf16) for the outputs; the final
-fp32 state within 1e-2 relative to its largest entry.
+Bars (``_check``): cosine >= 0.9995 and every output within 4 bf16 ulps of its row's largest value
+(8 at the full 40,688-token shape), at most 1% of outputs beyond one such ulp; q, k K^T, W, U~, P
+and S^T enter the MFMAs in bf16. The final fp32 state within 1e-2 relative to its largest entry.
 """
 
 from __future__ import annotations
@@ -27,13 +27,26 @@ def _inputs(tokens, heads, seed, decay_scale):
     return q, k, v, beta, lg
 
 
-def _check(got, want, what):
+def _check(got, want, what, row_ulps=4.0):
+    """Cosine >= 0.9995, and every output within ``row_ulps`` bf16 ulps of its row's largest float64 value
+    (the row: the 128 outputs of one token and head), at most 1% of them beyond one such ulp.
+
+    The GPU forms U~, W, P, Q-hat and S^T in bf16 for its MFMAs, so an output carries an error of a few bf16
+    steps of the largest term it sums, whatever its own size: an output near zero in a row of O(1) values
+    is many of its own ulps off (that fraction is printed, not bounded)."""
     g32, w = got.float().cpu().double(), want.double()
-    err = (g32 - w).abs().max().item()
+    diff = (g32 - w).abs()
     cos = F.cosine_similarity(g32.flatten(), w.flatten(), dim=0).item()
-    bar = max(2e-2, 2.0 ** -6 * w.abs().max().item())
-    print(f"{what}: max abs {err:.3e} (bar {bar:.3e}), cosine {cos:.7f}", flush=True)
-    assert torch.isfinite(g32).all() and err <= bar and cos >= 0.9995, what
+    ulp_v = torch.ldexp(torch.ones_like(w), torch.frexp(w)[1] - 8).clamp_min(2.0 ** -133)
+    scale = w.abs().amax(-1, keepdim=True)
+    ulp_row = torch.ldexp(torch.ones_like(scale), torch.frexp(scale)[1] - 8).clamp_min(2.0 ** -133)
+    sv, sr = diff / ulp_v, diff / ulp_row
+    print(f"{what}: max abs {diff.max().item():.3e}, cosine {cos:.7f}; ulps of the row's largest value: max "
+          f"{sr.max().item():.2f} (bar {row_ulps}), frac > 1 {(sr > 1).double().mean():.2e}; ulps of the value: "
+          f"frac > 2 {(sv > 2).double().mean():.2e}, frac > 4 {(sv > 4).double().mean():.2e}", flush=True)
+    assert torch.isfinite(g32).all() and cos >= 0.9995, what
+    assert sr.max().item() <= row_ulps, what
+    assert (sr > 1).double().mean().item() <= 1e-2, what
 
 
 @pytest.mark.parametrize("tokens,heads,decay,init", [(300, 3, 0.05, True), (64, 2, 0.05, False),
@@ -142,4 +155,5 @@ def test_gdn_full_shape_sampled_heads(device):
     torch.cuda.synchronize()
     sel = [0, 39]
     want, _ = go.chunked(q[:, sel].cpu(), k[:, sel].cpu(), v[:, sel].cpu(), beta[:, sel].cpu(), lg[:, sel].cpu())
-    _check(out[:, sel], want, "gdn full shape heads 0, 39")
+    # 636 chunk steps, each through a bf16 S^T: the largest row error seen is 6.2 row-max ulps
+    _check(out[:, sel], want, "gdn full shape heads 0, 39", row_ulps=8.0)
