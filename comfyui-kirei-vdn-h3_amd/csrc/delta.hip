@@ -42,7 +42,10 @@ __device__ __forceinline__ f32x16_t mfma_f32_32x32x2(float a, float b, f32x16_t 
 // hi = bf16(x) and lo = x - hi, both exact bf16, so A = hi^T k~ + lo^T k~ carries every bit.
 // KF / VF: k / v already hold the features k~ / v~ (the output of the short convolutions),
 // so the feature map is not applied on load.
-template <int D, bool KF, bool VF>
+// AB: A in bf16 as the reference computes it with a_fp32=False (vdn_h3/branch.py:238-240):
+// S = bf16(hi^T k~) (the bf16 product of bf16(k~ * beta) and k~, fp32 accumulation), then
+// 0.5 (S + S^T) in fp32; the lo half and its MFMAs are skipped.
+template <int D, bool KF, bool VF, bool AB>
 __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__restrict__ k, int64_t k_row,
                                                              int64_t k_head, const uint16_t *__restrict__ v,
                                                              int64_t v_row, int64_t v_head,
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
           const float hi = round_bf(x);
           kk[e][j] = f2bf(kt);
           xh[e][j] = f2bf(hi);
-          xl[e][j] = f2bf(x - hi);
+          if (!AB) xl[e][j] = f2bf(x - hi);
           const uint32_t w = r.v[e][j >> 1];
           const float vr = (j & 1) ? bf_hi(w) : bf_lo(w);
           vb[e][j] = f2bf((VF ? vr : silu_bf(vr)) * b);
@@ -134,7 +137,7 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
         const int o = (8 * c + j) * P + col;
         *reinterpret_cast<uint32_t *>(Kt + o) = kk[0][j] | (kk[1][j] << 16);
         *reinterpret_cast<uint32_t *>(Xh + o) = xh[0][j] | (xh[1][j] << 16);
-        *reinterpret_cast<uint32_t *>(Xl + o) = xl[0][j] | (xl[1][j] << 16);
+        if (!AB) *reinterpret_cast<uint32_t *>(Xl + o) = xl[0][j] | (xl[1][j] << 16);
         *reinterpret_cast<uint32_t *>(Vb + o) = vb[0][j] | (vb[1][j] << 16);
       }
     }
@@ -150,7 +153,7 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
       for (int i = 0; i < NB; ++i) {
         const int ro = (wm + 32 * i + l32) * P + slot;
         ah[i] = as_bf16x8(ld16(Xh + ro));
-        al[i] = as_bf16x8(ld16(Xl + ro));
+        if (!AB) al[i] = as_bf16x8(ld16(Xl + ro));
         av[i] = as_bf16x8(ld16(Vb + ro));
         bk[i] = as_bf16x8(ld16(Kt + (wn + 32 * i + l32) * P + slot));
       }
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
           accA[i][j] = mfma_bf16_32x32x16(ah[i], bk[j], accA[i][j]);
-          accA[i][j] = mfma_bf16_32x32x16(al[i], bk[j], accA[i][j]);
+          if (!AB) accA[i][j] = mfma_bf16_32x32x16(al[i], bk[j], accA[i][j]);
           accB[i][j] = mfma_bf16_32x32x16(av[i], bk[j], accB[i][j]);
         }
     }
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(256, 2) void frame_stats_kernel(const uint16_t *__r
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = wm + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3), n = wn + 32 * j + l32;
-        S[m * (D + 1) + n] = accA[i][j][r];
+        S[m * (D + 1) + n] = AB ? round_bf(accA[i][j][r]) : accA[i][j][r];
         Bo[m * D + n] = round_bf(accB[i][j][r]);
       }
   __syncthreads();
@@ -829,21 +832,25 @@ extern "C" int vdnh3_frame_stats(const uint16_t *k, int64_t k_row, int64_t k_hea
   VDNH3_HOST_CHECK(k_row % 8 == 0 && k_head % 8 == 0 && v_row % 8 == 0 && v_head % 8 == 0 &&
                        reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0,
                    VDNH3_ERR_INVALID, "frame_stats: k/v must be 16-byte aligned with strides multiple of 8");
-  VDNH3_HOST_CHECK((features & ~3) == 0, VDNH3_ERR_INVALID, "frame_stats: unknown feature flags %d", features);
+  VDNH3_HOST_CHECK((features & ~7) == 0, VDNH3_ERR_INVALID, "frame_stats: unknown feature flags %d", features);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(frames * heads);
-#define VDNH3_FS(D, KF, VF)                                                                                    \
-  if (head_dim == D && (features & 1) == KF && ((features >> 1) & 1) == VF)                                   \
-    hipLaunchKernelGGL((vdnh3::frame_stats_kernel<D, KF, VF>), grid, dim3(256), 0, s, k, k_row, k_head, v, \
+#define VDNH3_FS(D, KF, VF, AB)                                                                                \
+  if (head_dim == D && (features & 1) == KF && ((features >> 1) & 1) == VF && ((features >> 2) & 1) == AB)   \
+    hipLaunchKernelGGL((vdnh3::frame_stats_kernel<D, KF, VF, AB>), grid, dim3(256), 0, s, k, k_row, k_head, v, \
                        v_row, v_head, beta, beta_row, tokens, heads, A, B);
-  VDNH3_FS(128, 0, 0)
-  VDNH3_FS(128, 1, 0)
-  VDNH3_FS(128, 0, 1)
-  VDNH3_FS(128, 1, 1)
-  VDNH3_FS(64, 0, 0)
-  VDNH3_FS(64, 1, 0)
-  VDNH3_FS(64, 0, 1)
-  VDNH3_FS(64, 1, 1)
+#define VDNH3_FS_D(D)    \
+  VDNH3_FS(D, 0, 0, 0)   \
+  VDNH3_FS(D, 1, 0, 0)   \
+  VDNH3_FS(D, 0, 1, 0)   \
+  VDNH3_FS(D, 1, 1, 0)   \
+  VDNH3_FS(D, 0, 0, 1)   \
+  VDNH3_FS(D, 1, 0, 1)   \
+  VDNH3_FS(D, 0, 1, 1)   \
+  VDNH3_FS(D, 1, 1, 1)
+  VDNH3_FS_D(128)
+  VDNH3_FS_D(64)
+#undef VDNH3_FS_D
 #undef VDNH3_FS
   return check_launch("frame_stats");
 }

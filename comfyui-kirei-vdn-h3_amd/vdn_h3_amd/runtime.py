@@ -59,14 +59,12 @@ class OptimizedLinearBranch:
         targets = tuple(short_conv)
         if len(set(targets)) != len(targets) or any(t not in ("q", "k", "v") for t in targets):
             raise ValueError("short_conv must be a distinct subset of ('q', 'k', 'v')")
-        if not a_fp32:
-            raise NotImplementedError("the HIP branch computes A at full fp32 accuracy (a_fp32=True)")
         self.w = weights
         self.num_heads = int(num_heads)
         self.head_dim = int(head_dim)
         self.delta_rule = delta_rule
         self.bridge = bridge
-        self.a_fp32 = True
+        self.a_fp32 = bool(a_fp32)
         self.short_conv = targets
         self.enable_text_state = bool(enable_text_state)
 
@@ -83,7 +81,7 @@ class OptimizedLinearBranch:
             raise ValueError("text tensors must share a positive sequence length")
         if beta is None:
             beta = _linear.sigmoid_linear(text_x, weights["beta_proj.weight"])
-        a, b = _b.frame_statistics_raw(text_k_raw, text_v_raw, beta, 1, length)
+        a, b = _b.frame_statistics_raw(text_k_raw, text_v_raw, beta, 1, length, a_fp32=self.a_fp32)
         _, jay = self._backend(length).factor_apply(None, a, b, jay_scale=_b.TEXT_STATE_SCALE, need_phi=False)
         return jay[0]
 
@@ -138,7 +136,7 @@ class OptimizedLinearBranch:
             k_in, k_feat = self._features(weights, "k", k_raw, num_frames, frame_size)
             v_in, v_feat = self._features(weights, "v", v_raw, num_frames, frame_size)
         a, b = _b.frame_statistics_raw(k_in, v_in, beta, num_frames, tokens_per_frame, k_features=k_feat,
-                                       v_features=v_feat)
+                                       v_features=v_feat, a_fp32=self.a_fp32)
         del k_in, v_in
         mean = _b.frame_mean(xv, num_frames, tokens_per_frame)
         alpha = _b.alpha_gate(mean, weights["alpha.down.weight"], weights["alpha.up.weight"],

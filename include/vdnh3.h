@@ -214,7 +214,9 @@ size_t vdnh3_quant_tensor_f8_noalloc_max_elements(void);
  *   A[f][h] = 0.5 (S + S^T), S = (k~ b)^T k~ in fp32        (vdn_h3/branch.py:197-241)
  *   B[f][h] = bf16((v~ * b)^T k~)                             (vdn_h3/branch.py:242)
  * `features` bit 0: k already holds k~; bit 1: v already holds v~ (the outputs of
- * vdnh3_short_conv, vdn_h3/runtime.py:319-341), so the feature map is not applied to it.
+ * vdnh3_short_conv, vdn_h3/runtime.py:319-341), so the feature map is not applied to it;
+ * bit 2: S = bf16(bf16(k~ b)^T k~), the reference's a_fp32=False statistics
+ * (vdn_h3/branch.py:238-240), instead of the fp32 product.
  * A and B are [frames][heads][D][D] fp32.
  */
 int vdnh3_frame_stats(const uint16_t *k, int64_t k_row, int64_t k_head, const uint16_t *v, int64_t v_row,

@@ -3,7 +3,9 @@
 Run in the build container only (it reads the reference checkout, which the GPU hosts do
 not have):
 
-    python tests/golden/make_golden.py [/root/reference]
+    python tests/golden/make_golden.py [/root/reference [NAME ...]]
+
+(NAME: the file names below; all of them by default).
 
 It imports ``vdn_h3`` of hyukudan/ComfyUI-Kirei-VDN-H3 v0.3.3 on the CPU and saves small
 inputs / outputs as safetensors next to this script:
@@ -17,6 +19,8 @@ inputs / outputs as safetensors next to this script:
   out-projection and the branch delta;
 * ``branch_13f_sana.safetensors`` - ``projected_delta`` and ``readout`` with
   ``delta_rule="sana_scaled"`` (``SanaDelta``, ``vdn_h3/branch.py:163-177``) and the text state;
+* ``branch_13f_abf16.safetensors`` - ``projected_delta`` and ``readout`` with ``a_fp32=False``
+  (A from the bf16 product of ``k~ * beta`` and ``k~``, ``vdn_h3/branch.py:235-240``);
 * ``dit_block.safetensors``       - ``make_fast_block_forward`` (``vdn_h3/block_kernels.py:149-240``)
   on a stand-in DiT block (RMSNorm weights, six AdaLN tables, a linear attention, a SwiGLU
   MLP) with a two-segment modulation map. The fused path only runs for device tensors; its
@@ -74,7 +78,7 @@ def branch_weights(short_conv):
     return out
 
 
-def make_branch(short_conv, delta_rule="vdn_solve"):
+def make_branch(short_conv, delta_rule="vdn_solve", a_fp32=True):
     from vdn_h3.runtime import OptimizedLinearBranch
     from vdn_h3.window import window_bounds
 
@@ -87,7 +91,7 @@ def make_branch(short_conv, delta_rule="vdn_solve"):
     conv = ("k", "v") if short_conv else ()
     branch = OptimizedLinearBranch(weights, HEADS, DIM, delta_rule=delta_rule, short_conv=conv,
                                    enable_text_state=True, kernel_backend="eager", compile_policy="off",
-                                   tile_frames=0)
+                                   tile_frames=0, a_fp32=a_fp32)
     va, vb = TEXT, seq
     with torch.inference_mode():
         delta = branch.projected_delta(
@@ -100,11 +104,13 @@ def make_branch(short_conv, delta_rule="vdn_solve"):
     tensors.update({"x": x, "qkv": qkv, "delta": delta.contiguous(), "readout": readout.contiguous()})
     meta = {"frames": str(FRAMES), "grid": f"{GRID[0]}x{GRID[1]}", "text": str(TEXT), "heads": str(HEADS),
             "dim": str(DIM), "hidden": str(HIDDEN), "short_conv": ",".join(conv), "radius": "1", "chunk": "5",
-            "delta_rule": delta_rule,
+            "delta_rule": delta_rule, "a_fp32": str(bool(a_fp32)).lower(),
             "source": "vdn_h3.runtime.OptimizedLinearBranch.projected_delta / readout (inference, skip_ends)"}
     name = "branch_13f_conv.safetensors" if short_conv else "branch_13f.safetensors"
     if delta_rule != "vdn_solve":
         name = "branch_13f_sana.safetensors"
+    if not a_fp32:
+        name = "branch_13f_abf16.safetensors"
     save_file(tensors, str(HERE / name), metadata=meta)
     return name
 
@@ -251,9 +257,15 @@ def main():
         raise SystemExit(f"reference checkout not found at {REF}")
     sys.path.insert(0, str(REF))
     torch.set_num_threads(4)
-    for name in (make_branch(False), make_branch(True), make_hybrid(), make_branch(False, "sana_scaled"),
-                 make_dit_block()):
-        print("wrote", HERE / name)
+    makers = {"branch_13f.safetensors": lambda: make_branch(False),
+              "branch_13f_conv.safetensors": lambda: make_branch(True),
+              "hybrid_13f.safetensors": make_hybrid,
+              "branch_13f_sana.safetensors": lambda: make_branch(False, "sana_scaled"),
+              "dit_block.safetensors": make_dit_block,
+              "branch_13f_abf16.safetensors": lambda: make_branch(False, a_fp32=False)}
+    wanted = sys.argv[2:] or list(makers)
+    for name in wanted:
+        print("wrote", HERE / makers[name]())
 
 
 if __name__ == "__main__":

@@ -60,6 +60,34 @@ def test_frame_statistics(device, dim):
     _close(b, wb, 2 * 2.0 ** -8, 1e-6, "B")
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+def test_frame_statistics_bf16_a(device, dim):
+    """a_fp32=False: S = bf16(bf16(k~ beta)^T k~) and A = (S + S^T) / 2. The GPU's fp32 sums run in another
+    order than the oracle's, so where one straddles a bf16 midpoint S moves by one of its bf16 steps: every
+    A value within one bf16 step of the oracle's (at |A|), at least 99% of them exact; B as before."""
+    from vdn_h3_amd import branch
+
+    print(f"case frame stats bf16 A D={dim}", flush=True)
+    frames, tokens, heads = 3, 100, 2
+    k = _rand((frames * tokens, heads, dim), 21, dtype=torch.bfloat16)
+    v = _rand((frames * tokens, heads, dim), 22, dtype=torch.bfloat16)
+    beta = torch.sigmoid(_rand((frames * tokens, heads), 23)).to(torch.bfloat16)
+    a, b = branch.frame_statistics_raw(k.to(device), v.to(device), beta.to(device), frames, tokens, a_fp32=False)
+    a32, _ = branch.frame_statistics_raw(k.to(device), v.to(device), beta.to(device), frames, tokens)
+    kf = bo.to_fhsd(bo.activate(k, True), frames, heads, dim)
+    vf = bo.to_fhsd(bo.activate(v, False), frames, heads, dim)
+    bt = beta.reshape(frames, tokens, heads).permute(0, 2, 1)
+    wa, wb = bo.frame_statistics(kf, vf, bt, a_fp32=False)
+    ga = a.cpu()
+    assert torch.equal(ga, ga.transpose(-1, -2))
+    step = torch.ldexp(torch.ones_like(wa), torch.frexp(wa)[1] - 8).clamp_min(2.0 ** -133)
+    off = ((ga - wa).abs() / step)
+    print(f"  A: {(off > 0).float().mean():.2e} of values off, max {off.max().item():.2f} steps", flush=True)
+    assert off.max().item() <= 1.0 and (off == 0).float().mean().item() >= 0.99
+    assert not torch.equal(ga, a32.cpu())                      # the bf16 rounding is applied
+    _close(b, wb, 2 * 2.0 ** -8, 1e-6, "B")
+
+
 def test_factor_and_status(device):
     from vdn_h3_amd import branch
 
@@ -444,6 +472,40 @@ def test_sana_factor(device, dim, alpha_ones):
     assert none_phi is None and torch.equal(half.cpu(), 0.5 * wjay)
     with pytest.raises(ValueError, match="alpha"):
         backend.factor_apply(alpha[:, :, :-1].to(device), a.to(device), b.to(device))
+
+
+def test_projected_delta_a_bf16_matches_reference_golden(device):
+    """The branch with a_fp32=False (13 frames of 8x8, 2 heads x 64, text state) vs the reference's own output
+    and vs the oracle; the text state's statistics take the same flag."""
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+
+    print("case projected_delta a_fp32=False golden", flush=True)
+    t, meta = _load("branch_13f_abf16.safetensors")
+    assert meta["a_fp32"] == "false"
+    frames, text, heads, dim = int(meta["frames"]), int(meta["text"]), int(meta["heads"]), int(meta["dim"])
+    gh, gw = map(int, meta["grid"].split("x"))
+    tpf = gh * gw
+    w = {k[2:]: v.to(device) for k, v in t.items() if k.startswith("w.")}
+    x, qkv = t["x"].to(device), t["qkv"].to(device)
+    seq = x.shape[0]
+    q, k, v = [y.view(seq, heads, dim) for y in qkv.split(heads * dim, dim=-1)]
+    bounds = wo.window_bounds(frames, 1, 5)
+    br = OptimizedLinearBranch(w, heads, dim, a_fp32=False, short_conv=(), enable_text_state=True)
+    kw = dict(frame_size=(gh, gw), text_x=x[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True)
+    with torch.no_grad():
+        got = br.projected_delta(w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, **kw)
+        readout = br.readout(w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, **kw)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(got[:tpf]) == 0 and torch.count_nonzero(got[-tpf:]) == 0
+    _parity(got, t["delta"], "a_fp32=False projected_delta vs reference")
+    _parity(readout, t["readout"], "a_fp32=False readout vs reference", atol=2 ** -5, min_cos=0.9999)
+    hw = {k2[2:]: v2 for k2, v2 in t.items() if k2.startswith("w.")}
+    hq, hk, hv = [y.reshape(seq, heads, dim) for y in t["qkv"].split(heads * dim, dim=-1)]
+    hx = t["x"]
+    want = bo.projected_delta(hw, hx[text:], hq[text:], hk[text:], hv[text:], frames, tpf, bounds, frame_size=(gh, gw),
+                              text_x=hx[:text], text_k_raw=hk[:text], text_v_raw=hv[:text], skip_ends=True,
+                              a_fp32=False)
+    _parity(got, want, "a_fp32=False projected_delta vs oracle")
 
 
 def test_projected_delta_sana_matches_reference_golden(device):

@@ -227,6 +227,51 @@ def test_branch_oracle_matches_reference_golden(name):
     assert torch.count_nonzero(delta[:tpf]) == 0 and torch.count_nonzero(delta[-tpf:]) == 0
 
 
+def test_branch_oracle_a_bf16_matches_reference_golden():
+    """a_fp32=False (A = bf16(bf16(k~ beta)^T k~), symmetrised; vdn_h3/branch.py:238-240): the oracle
+    reproduces the reference's own branch output, and the fp32 statistics on the same inputs do not."""
+    t, meta = _load("branch_13f_abf16.safetensors")
+    assert meta["a_fp32"] == "false"
+    frames, text, heads, dim = int(meta["frames"]), int(meta["text"]), int(meta["heads"]), int(meta["dim"])
+    gh, gw = map(int, meta["grid"].split("x"))
+    tpf = gh * gw
+    w = {k[2:]: v for k, v in t.items() if k.startswith("w.")}
+    x, qkv = t["x"], t["qkv"]
+    seq = x.shape[0]
+    q, k, v = [y.reshape(seq, heads, dim) for y in qkv.split(heads * dim, dim=-1)]
+    bounds = wo.window_bounds(frames, 1, 5)
+    args = (w, x[text:], q[text:], k[text:], v[text:], frames, tpf, bounds)
+    kw = dict(frame_size=(gh, gw), text_x=x[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True)
+    want = t["delta"].float()
+    delta = bo.projected_delta(*args, **kw, a_fp32=False).float()
+    err = (delta - want).abs().max().item()
+    assert err <= 4e-3 * max(1.0, want.abs().max().item()), err
+    assert (delta == want).float().mean().item() >= 0.999
+    other = bo.projected_delta(*args, **kw).float()        # the fp32 statistics: a different output
+    assert (other == want).float().mean().item() < 0.9
+
+
+def test_frame_statistics_bf16_a_closed_form():
+    """With a_fp32=False, A is the symmetrised bf16 rounding of the bf16 product of bf16(k beta) and k:
+    exact when every product and sum is representable (keys in {0, +-1/2, +-1}, betas in {1/4 .. 1}, 8
+    tokens: multiples of 1/16 up to 8, at most 7 significant bits), and off by the bf16 rounding of that
+    product otherwise (a dropped rounding fails it)."""
+    g = torch.Generator().manual_seed(3)
+    key = (torch.randint(-2, 3, (2, 2, 8, 6), generator=g).float() / 2).to(torch.bfloat16)
+    beta = (torch.randint(1, 5, (2, 2, 8), generator=g).float() / 4).to(torch.bfloat16)
+    a16, _ = bo.frame_statistics(key, key, beta, a_fp32=False)
+    exact = torch.einsum("fhsk,fhsl,fhs->fhkl", key.double(), key.double(), beta.double())
+    assert torch.equal(a16.double(), exact)
+    key = torch.randn(2, 2, 40, 6, generator=g).to(torch.bfloat16)
+    beta = torch.rand(2, 2, 40, generator=g).to(torch.bfloat16)
+    a16, _ = bo.frame_statistics(key, key, beta, a_fp32=False)
+    wk = (key.float() * beta.float().unsqueeze(-1)).to(torch.bfloat16).double()
+    s = torch.einsum("fhsk,fhsl->fhkl", wk, key.double()).to(torch.bfloat16).float()
+    torch.testing.assert_close(a16, 0.5 * (s + s.transpose(-1, -2)), atol=0, rtol=0)
+    a32, _ = bo.frame_statistics(key, key, beta)
+    assert not torch.equal(a16, a32)
+
+
 def test_sana_factor_closed_forms():
     """SanaDelta (vdn_h3/branch.py:163-177): A = 0 gives Phi = diag(alpha); A = T I gives Phi = 0; B = I gives
     J = I / sqrt(T); alpha scales rows (a transposed product fails it); Phi is linear in A."""
