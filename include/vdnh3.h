@@ -389,7 +389,10 @@ int vdnh3_head_gate(const uint16_t *o, int64_t o_row, int64_t o_head, const uint
  * previous segment's scan on a side stream the library owns (one per device, default priority,
  * created on the first such call): the call forks it from `stream` with an event and joins it back
  * before its last kernel, so all of its work is ordered on `stream` and it can be captured in a
- * graph. Calls on one device serialise their enqueue on a host lock.
+ * graph, the call that creates the side stream included. Calls on one device serialise their
+ * enqueue on a host lock. While a graph capture that holds such a call is open on one thread, no
+ * other thread may make an eager pipelined call on the same device: the side stream stays in that
+ * capture until it ends, and the eager call's work would join it.
  * ------------------------------------------------------------------------------ */
 size_t vdnh3_gdn_workspace_bytes(int tokens, int heads, int head_dim);
 int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,

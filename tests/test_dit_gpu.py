@@ -64,6 +64,68 @@ def test_rmsnorm_modulate(device, hidden, mod_dtype):
     assert (steps == 0).float().mean().item() >= 0.99
 
 
+@pytest.mark.parametrize("rows,hidden,pattern", [(4001, 192, "random"), (40688, 5120, "runs")])
+def test_rmsnorm_modulate_multi_row_walk(device, rows, hidden, pattern):
+    """More than 768 rows: each of the kernel's workgroups walks a block of consecutive rows (4001 rows: 6
+    per workgroup, 667 workgroups; 40,688: 53 per workgroup, 768 workgroups; both end in an odd-length
+    last block), with two x buffers in flight, alternating reduction slots, and the segment's bf16(1 +
+    scale) and shift cached in registers and reloaded where the index changes inside a block ("random":
+    a new segment on most rows; "runs": segments of 37 rows, so most blocks keep theirs). Against the oracle
+    with the one-row bar, and bit for bit against the same rows run in slices of at most 768 rows, where
+    every workgroup takes a single row."""
+    from vdn_h3_amd import block_kernels as bk
+
+    print(f"case rmsnorm_modulate multi-row rows={rows} hidden={hidden} {pattern}", flush=True)
+    x, w, scale, shift, idx = _case(rows, hidden, 3, 11, torch.float32)
+    if pattern == "runs":
+        g = torch.Generator().manual_seed(12)
+        idx = torch.randint(0, 3, ((rows + 36) // 37,), generator=g).repeat_interleave(37)[:rows]
+    dx, dw, dsc, dsh = x.to(device), w.to(device), scale.to(device), shift.to(device)
+    didx = idx.to(torch.int32).to(device)
+    got = bk.rmsnorm_modulate(dx, dw, 1e-6, dsc, dsh, didx)
+    parts = [bk.rmsnorm_modulate(dx[i:i + 768], dw, 1e-6, dsc, dsh, didx[i:i + 768]) for i in range(0, rows, 768)]
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), torch.cat(parts).cpu())
+    want = do.pre(x, w, 1e-6, scale, shift, idx)
+    prod = do.pre(x, w, 1e-6, scale, torch.zeros_like(shift), idx)
+    steps = _steps_mag(got, want, torch.maximum(want.float().abs(), prod.float().abs()))
+    print(f"  steps > 0: {(steps > 0).sum().item()} of {steps.numel()}, max {steps.max().item()}", flush=True)
+    assert steps.max().item() <= 2, steps.max().item()
+    assert (steps == 0).float().mean().item() >= 0.99
+
+
+def test_out_of_range_device_index_gives_nan_rows(device):
+    """A modulation index held in a device tensor is not range-checked on the host; an index outside the
+    table (2 and -1 for a 2-row table) makes both passes read row 0 and write NaN for exactly those rows,
+    in the single-row and the multi-row walk of rmsnorm_modulate; every other row equals the oracle."""
+    from vdn_h3_amd import block_kernels as bk
+
+    print("case out-of-range device modulation index", flush=True)
+    for rows in (300, 2000):
+        x, w, scale, shift, idx = _case(rows, 256, 2, 13, torch.float32)
+        bad = torch.zeros(rows, dtype=torch.bool)
+        bad[[3, 4, rows // 2, rows - 1]] = True
+        dev_idx = idx.clone()
+        dev_idx[[3, rows // 2]] = 2
+        dev_idx[[4, rows - 1]] = -1
+        didx = dev_idx.to(torch.int32).to(device)
+        got = bk.rmsnorm_modulate(x.to(device), w.to(device), 1e-6, scale.to(device), shift.to(device), didx).cpu()
+        want = do.pre(x, w, 1e-6, scale, shift, idx)
+        assert bool(torch.isnan(got[bad].float()).all())
+        good = ~bad
+        assert not bool(torch.isnan(got[good].float()).any())
+        prod = do.pre(x, w, 1e-6, scale, torch.zeros_like(shift), idx)
+        steps = _steps_mag(got[good], want[good], torch.maximum(want[good].float().abs(), prod[good].float().abs()))
+        assert steps.max().item() <= 2
+        b = torch.randn(x.shape, generator=torch.Generator().manual_seed(14)).to(torch.bfloat16)
+        got_r = bk.gated_residual(x.to(device), scale.to(device), didx, b.to(device)).cpu()
+        want_r = do.post(x, scale, idx, b)
+        assert bool(torch.isnan(got_r[bad].float()).all())
+        assert torch.equal(got_r[good], want_r[good])
+        with pytest.raises(ValueError, match="out of range"):  # a host tensor is checked before the launch
+            bk.rmsnorm_modulate(x.to(device), w.to(device), 1e-6, scale.to(device), shift.to(device), dev_idx)
+
+
 @pytest.mark.parametrize("gate_dtype", [torch.float32, torch.bfloat16])
 def test_gated_residual(device, gate_dtype):
     from vdn_h3_amd import block_kernels as bk

@@ -139,6 +139,57 @@ def test_gdn_pipelined_call_replays_in_a_graph(device):
         assert torch.equal(s_out, s_eager), f"replay {r}: final state"
 
 
+def test_gdn_first_call_captured_in_a_fresh_process(device):
+    """The per-device pipeline stream and events are made by the first pipelined call. Here that call is made
+    inside a graph capture, in a fresh process with no eager call before it; three replays (eager work and
+    synchronisations between them) give the bits of an eager call made afterwards."""
+    import subprocess
+    import sys
+    import textwrap
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    script = textwrap.dedent(f"""
+        import sys
+        sys.path[:0] = [{str(root)!r}, {str(root / "comfyui-kirei-vdn-h3_amd")!r}]
+        import torch
+        import torch.nn.functional as F
+        from vdn_h3_amd.gdn import chunk_gated_delta_rule
+        dev = torch.device("cuda:0")
+        g = torch.Generator().manual_seed(17)
+        t, h = 64 * 70, 2
+        q = torch.randn(t, h, 128, generator=g).to(torch.bfloat16).to(dev)
+        k = F.normalize(torch.randn(t, h, 128, generator=g), dim=-1).to(torch.bfloat16).to(dev)
+        v = torch.randn(t, h, 128, generator=g).to(torch.bfloat16).to(dev)
+        beta = torch.sigmoid(torch.randn(t, h, generator=g)).to(dev)
+        lg = (-F.softplus(torch.randn(t, h, generator=g)) * 0.05).to(dev)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out, s_out = chunk_gated_delta_rule(q, k, v, beta, lg, output_final_state=True)
+        got = []
+        for r in range(3):
+            out.zero_()
+            s_out.zero_()
+            noise = torch.randn(1 << 20, device=dev).sum()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            got.append((out.clone(), s_out.clone()))
+        eager, s_eager = chunk_gated_delta_rule(q, k, v, beta, lg, output_final_state=True)
+        torch.cuda.synchronize()
+        for r, (o, s) in enumerate(got):
+            assert torch.equal(o, eager), f"replay {{r}}: output"
+            assert torch.equal(s, s_eager), f"replay {{r}}: final state"
+        print("first call captured: 3 replays equal the eager call", flush=True)
+    """)
+    print("case gdn first pipelined call inside a capture (child process)", flush=True)
+    proc = subprocess.run([sys.executable, "-u", "-c", script], capture_output=True, text=True, timeout=300)
+    print(proc.stdout[-2000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    assert "3 replays equal the eager call" in proc.stdout
+
+
 def test_gdn_full_shape_sampled_heads(device):
     """40,688 tokens x 40 heads (the chunk-64 benchmark shape); heads 0 and 39 against the oracle."""
     from vdn_h3_amd.gdn import chunk_gated_delta_rule
