@@ -375,7 +375,27 @@ def bench_gemm(args, torch, device):
         "breakdown_ms": {"activation_quant": round(quant_ms, 4), "gemm": round(gemm_ms, 4),
                          "activation_quant_GBs": round(qbytes / (quant_ms * 1e-3) / 1e9, 1)},
         "roofline_vs_sustained_mfma": ceiling_entry(torch, device, 1 if kind_name == "i8" else 2, tops),
+        "library_same_box": library_gemm_rate(torch, device, stream, args, kind_name, xq, xs, wq, ws, ops),
     }
+
+
+def library_gemm_rate(torch, device, stream, args, kind_name, xq, xs, wq, ws, ops):
+    """hipBLASLt on the same operands and box, timed like the kernel above (a comparison, not this library's
+    path): torch._scaled_mm (fp8 per-tensor, bf16 out) or torch._int_mm (int8, int32 accumulators out, no
+    scales applied)."""
+    if kind_name == "i8":
+        fn = lambda: torch._int_mm(xq, wq.t())  # noqa: E731
+        what = "torch._int_mm (hipBLASLt), int32 output, scales not applied"
+    else:
+        sa, sb = xs.reshape(()).float(), ws.reshape(()).float()
+        fn = lambda: torch._scaled_mm(xq.view(torch.float8_e4m3fn), wq.view(torch.float8_e4m3fn).t(),  # noqa: E731
+                                      scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)
+        what = "torch._scaled_mm (hipBLASLt), per-tensor scales, bf16 output"
+    try:
+        ms = _time_steps(torch, stream, args.steps, args.warmup, fn)
+    except RuntimeError as err:  # the library path is a comparison only
+        return {"kernel": what, "error": str(err)[:200]}
+    return {"kernel": what, "ms": round(ms, 4), "TOPs": round(ops / (ms * 1e-3) / 1e12, 1)}
 
 
 def bench_branch(args, torch, device):

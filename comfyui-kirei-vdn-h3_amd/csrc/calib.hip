@@ -49,7 +49,7 @@ __global__ __launch_bounds__(kCalibThreads, 2) void mfma_peak_kernel(const i32x8
         const i32x4_t bv = {b[j][0], b[j][1], b[j][2], b[j][3]};
         iacc[j & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, iacc[j & 3], 0, 0, 0);
       } else {
-        acc[j & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[j], b[j], acc[j & 3], 0, 0, 0, 127, 0, 127);
+        acc[j & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[j], b[j], acc[j & 3], 0, 0, 0, 0, 0, 0);  // unscaled form, as the GEMM
       }
     }
   }

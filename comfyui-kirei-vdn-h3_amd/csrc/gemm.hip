@@ -17,7 +17,7 @@
 // stages of 64 bytes per row (32 bf16, 64 int8 or 64 fp8 elements):
 //   bf16: v_mfma_f32_32x32x16_bf16, 2 k-steps of 32 bytes per stage
 //   int8: v_mfma_i32_32x32x32_i8,   2 k-steps of 32 bytes
-//   fp8 : v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales), 1 k-step of 64 bytes
+//   fp8 : v_mfma_f32_32x32x64_f8f6f4 (no block scales), 1 k-step of 64 bytes
 // Every lane reads its A and B k-slices at the same byte offsets, so the products pair the
 // same k whatever order the instruction assigns to the lane's bytes.
 // Stages are loaded straight into LDS (global_load_lds) through a five-slot ring (160 KB, all
@@ -369,8 +369,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
         // fixed issue order: each stage load sits between two MFMAs
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (KIND == kF8)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0, 127,
-                                                                     0, 127);
+          // scale operands 0 select the unscaled v_mfma_f32_32x32x64_f8f6f4 (no scale VGPRs to read; the
+          // same bits as unit E8M0 scales, 127): 0.6% faster on the projection shapes
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0, 0,
+                                                                     0, 0);
         else if constexpr (KIND == kBF16)
           acc[i][j] = mfma_bf16_32x32x16(as_bf16x8(fa[buf][i]), as_bf16x8(fb[buf][j]), acc[i][j]);
         else
