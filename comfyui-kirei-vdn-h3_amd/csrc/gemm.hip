@@ -20,13 +20,19 @@
 //   fp8 : v_mfma_f32_32x32x64_f8f6f4 (no block scales), 1 k-step of 64 bytes
 // Every lane reads its A and B k-slices at the same byte offsets, so the products pair the
 // same k whatever order the instruction assigns to the lane's bytes.
-// Stages are loaded straight into LDS (global_load_lds) through a five-slot ring (160 KB, all
-// of the CU's LDS): each stage's k-steps issue the loads of the stage four ahead, evenly spaced
-// between their MFMAs, so the loads have three to four stages of MFMA time to land and the
-// address unit sees a steady stream instead of bursts. One barrier per stage, placed before
-// its last k-step, frees a slot and publishes the next stage; fragments are double-buffered
+// Stages are loaded straight into LDS (global_load_lds), in one of two pipelines (GemmPipe):
+//  - bf16 and fp8: stages of 64 bytes per row in a five-slot ring (160 KB, all of the CU's LDS);
+//    each stage's k-steps issue the loads of the stage four ahead, evenly spaced between their
+//    MFMAs, so the loads have three to four stages of MFMA time to land;
+//  - int8: stages of 128 bytes per row (whole 128-byte lines, half the barriers per MFMA) in two
+//    slots (128 KB); stage s issues the loads of stage s + 1 in its first three k-steps (of four),
+//    and the barrier sits before the last one. Against the ring at the projection shapes, bit-
+//    identical: -2.8 to -4.4% (qkv) and -4.0 to -4.7% (out) on two boxes. For fp8 (two k-steps per
+//    stage, so the loads had one k-step to land) the same pipeline, and one with the loads spread
+//    over both k-steps and the barrier after the second, measured from -1.6% to +3.5%: not kept.
+// One barrier per stage frees a slot and publishes the next stage; fragments are double-buffered
 // in registers one k-step ahead, across that barrier too. 16-byte chunk c of stage row r is
-// stored at slot c ^ ((r >> 2) & 3), which makes the 16-lane fragment reads conflict-free.
+// stored at a slot that makes the 16-lane fragment reads conflict-free (gemm_slot).
 // Tiles are ordered so that the 32 workgroups resident on one XCD cover a 4 x 8 block of
 // tiles and share their A and B panels in that XCD's L2.
 #include <type_traits>
@@ -38,8 +44,6 @@ namespace {
 
 constexpr int kGemmBM = 256, kGemmBN = 256;
 constexpr int kGemmKB = 128;    // K bytes per row that the host requires K * element size to be a multiple of
-constexpr int kGemmSK = 64;     // K bytes per row of one pipeline stage
-constexpr int kGemmStages = 5;  // LDS ring slots (5 x 32 KB: all 160 KB)
 #ifndef VDNH3_GEMM_WAVES
 #define VDNH3_GEMM_WAVES 8
 #endif
@@ -49,10 +53,20 @@ constexpr int kGemmThreads = 64 * kGemmWaves;
 // a wavefront owns 128 rows x (32 kGemmNJ) columns of the tile: 2 x 2 wavefronts of 128 x 128
 // or 2 x 4 wavefronts of 128 x 64
 constexpr int kGemmNJ = 16 / kGemmWaves;
-constexpr int kGemmLoads = 32 / kGemmWaves;  // 16-byte stage loads per thread and stage (A and B)
 constexpr int kGemmGroupM = 4;  // tile rows per grouping band (4 measured 1-3% faster than 2, 8 or 16)
 
 enum GemmKind { kBF16 = 0, kI8 = 1, kF8 = 2 };
+
+// The stage pipeline of each operand kind (see the file comment): SK K bytes per row and stage,
+// SLOTS LDS slots, LOADS 16-byte loads per thread and stage (A and B), KS k-steps per stage
+// (32 bytes per lane group for bf16 / int8, 64 for fp8).
+template <int KIND>
+struct GemmPipe {
+  static constexpr int SK = KIND == kI8 ? 128 : 64;
+  static constexpr int SLOTS = SK == 64 ? 5 : 2;
+  static constexpr int LOADS = 2 * kGemmBM * (SK / 16) / kGemmThreads;
+  static constexpr int KS = SK / (KIND == kF8 ? 64 : 32);
+};
 enum OutType { kOutBF16 = 0, kOutF32 = 1, kOutI32 = 2 };
 
 struct GemmEpi {
@@ -73,9 +87,13 @@ struct GemmEpi {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
 
-// LDS slot of 16-byte chunk c of stage row r (4 chunks per 64-byte row): 16 consecutive rows
-// read at one chunk column hit 16 different 16-byte bank groups (row % 4 x 4 slots)
-__host__ __device__ constexpr int gemm_slot(int r, int c) { return c ^ ((r >> 2) & 3); }
+// LDS slot of 16-byte chunk c of stage row r: 16 consecutive rows read at one chunk column hit 16
+// different 16-byte bank groups (4 chunks per 64-byte row: row % 4 x 4 slots; 8 chunks per
+// 128-byte row: row % 2 x 8 slots)
+template <int SK>
+__host__ __device__ constexpr int gemm_slot(int r, int c) {
+  return SK == 64 ? c ^ ((r >> 2) & 3) : c ^ ((r >> 1) & 7);
+}
 
 // MFMA operand reads: one k-step = 32 bytes per row (bf16 / int8, one 16-byte chunk per lane
 // group) or 64 bytes (fp8, two chunks per lane group)
@@ -259,7 +277,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
                                                                    void *__restrict__ C, int64_t ldc, int M, int N,
                                                                    int nkt, GemmEpi epi, int tiles_m, int tiles_n,
                                                                    int per_xcd, int total) {
-  constexpr int STAGE_BYTES = kGemmBM * kGemmSK;  // one 256-row x 64-byte stage of A or B (16 KB)
+  using Pipe = GemmPipe<KIND>;
+  constexpr int kGemmSK = Pipe::SK, kGemmStages = Pipe::SLOTS, kGemmLoads = Pipe::LOADS, KS = Pipe::KS;
+  constexpr int STAGE_BYTES = kGemmBM * kGemmSK;  // one 256-row stage of A or B (16 or 32 KB)
   __shared__ __attribute__((aligned(16))) uint8_t smem[2][kGemmStages][STAGE_BYTES];
   static_assert(4 * kEpiWaveWords * 4 <= (int)sizeof(smem), "epilogue staging must fit the ring");
   auto &As = smem[0];
@@ -285,17 +305,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
   const int mb = m0 + wm, nb = n0 + wn;
   const EpiOperands eo = load_epi_operands(epi, M, N, mb, nb, lane);
 
-  // Stage loads. A stage is 64 bytes of K for the tile's 256 A rows and 256 B rows (16 KB
-  // each); LDS position P (16-byte units) of an operand's stage is row P / 4, slot P % 4 and
-  // holds chunk slot ^ swz(row) of that row. Load instruction q (0 .. kGemmLoads / 2 - 1) of an
-  // operand covers positions kGemmThreads q + tid, i.e. rows (kGemmThreads / 4) q + tid / 4.
+  // Stage loads. A stage is SK bytes of K for the tile's 256 A rows and 256 B rows; LDS position
+  // P (16-byte units) of an operand's stage is row P / CPR, slot P % CPR (CPR = SK / 16 chunks per
+  // row) and holds the chunk gemm_slot maps to that slot. Load instruction q (0 .. kGemmLoads / 2
+  // - 1) of an operand covers positions kGemmThreads q + tid, i.e. rows (kGemmThreads / CPR) q +
+  // tid / CPR.
   // Rows past M (N) read the last row; their results are not stored.
   // The source of a load is a wave-uniform base (the tile's first row, advanced by the stage)
   // plus a per-lane 32-bit byte offset that stays the same for every stage (the host checks
   // that 256 rows of A and B span less than 4 GB).
-  constexpr int kHalf = kGemmLoads / 2, kRowsPerLoad = kGemmThreads / 4;
-  const int lrow = tid >> 2;
-  const int lchunk = gemm_slot(lrow, tid & 3);  // the swizzle only sees row bits below kRowsPerLoad
+  constexpr int CPR = kGemmSK / 16, kHalf = kGemmLoads / 2, kRowsPerLoad = kGemmThreads / CPR;
+  const int lrow = tid / CPR;
+  const int lchunk = gemm_slot<kGemmSK>(lrow, tid % CPR);  // the swizzle only sees row bits below kRowsPerLoad
   uint32_t a_off[kHalf], b_off[kHalf];
 #pragma unroll
   for (int q = 0; q < kHalf; ++q) {
@@ -314,14 +335,17 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
   };
 
   // fragment byte offsets inside an operand's stage (rows 32 i + l32 share l32's swizzle):
-  // bf16 / int8 k-step ks reads chunk 2 ks + g (foff[ks]); fp8 reads chunks 2 g and 2 g + 1
-  // (foff[0], foff[1])
-  int foff[2];
+  // bf16 / int8 k-step ks reads chunk 2 ks + g (foff[ks][0]); fp8 reads chunks 4 ks + 2 g and
+  // 4 ks + 2 g + 1 (foff[ks][0], foff[ks][1])
+  constexpr int NCH = KIND == kF8 ? 2 : 1;
+  int foff[KS][NCH];
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int chunk = KIND == kF8 ? 2 * g + c : 2 * c + g;
-    foff[c] = l32 * kGemmSK + gemm_slot(l32, chunk) * 16;
-  }
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int chunk = KIND == kF8 ? 4 * ks + 2 * g + c : 2 * ks + g;
+      foff[ks][c] = l32 * kGemmSK + gemm_slot<kGemmSK>(l32, chunk) * 16;
+    }
 
   using acc_t = typename std::conditional<KIND == kI8, i32x16_t, f32x16_t>::type;
   acc_t acc[4][kGemmNJ];
@@ -330,8 +354,6 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
 #pragma unroll
     for (int j = 0; j < kGemmNJ; ++j) acc[i][j] = acc_t{};
 
-  // k-steps per stage: 32 bytes per lane group for bf16 / int8, 64 for fp8
-  constexpr int KS = KIND == kF8 ? 1 : 2;
   using frag_t = typename Frag<KIND>::type;
   frag_t fa[2][4], fb[2][kGemmNJ];
   // fragments of k-step ks of the stage in `slot` into buffer `buf`
@@ -341,11 +363,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
     const uint8_t *bt = smem[1][slot] + wn * kGemmSK;
     auto rd = [&](const uint8_t *base, int i) __device__ {
       if constexpr (KIND == kF8) {
-        const u32x4_t lo = ld16(base + i * 32 * kGemmSK + foff[0]);
-        const u32x4_t hi = ld16(base + i * 32 * kGemmSK + foff[1]);
+        const u32x4_t lo = ld16(base + i * 32 * kGemmSK + foff[ks][0]);
+        const u32x4_t hi = ld16(base + i * 32 * kGemmSK + foff[ks][NCH - 1]);
         return frag_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
       } else {
-        return frag_t(ld16(base + i * 32 * kGemmSK + foff[ks]));
+        return frag_t(ld16(base + i * 32 * kGemmSK + foff[ks][0]));
       }
     };
 #pragma unroll
@@ -355,17 +377,22 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // the 4 kGemmNJ MFMAs of one k-step; with `dma`, stage loads q0 .. q0 + kGemmLoads / KS - 1 of stage ld_st
-  // sit between them, evenly spaced; `reads` (the next k-step's fragment reads) follows the
-  // second MFMA, so that any LDS wait before the first ones covers only older reads
-  auto mfmas = [&](int buf, bool dma, int ld_st, int ld_slot, int q0, auto reads) __device__ {
-    constexpr int kLoads = kGemmLoads / KS, kEvery = 4 * kGemmNJ / kLoads;
+  // the 4 kGemmNJ MFMAs of one k-step; stage loads qa .. qb - 1 of stage ld_st sit between them,
+  // evenly spaced (qa, qb are constants once the k-step loops are unrolled); `reads` (the next
+  // k-step's fragment reads) follows the second MFMA, so that any LDS wait before the first ones
+  // covers only older reads
+  auto mfmas = [&](int buf, int ld_st, int ld_slot, int qa, int qb, auto reads) __device__ {
+    constexpr int NM = 4 * kGemmNJ;
+    const int nl = qb - qa;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < kGemmNJ; ++j) {
-        if (kGemmNJ * i + j == 2) reads();
-        if (dma && (kGemmNJ * i + j) % kEvery == 0) load_part(ld_st, ld_slot, q0 + (kGemmNJ * i + j) / kEvery);
+        const int mi = kGemmNJ * i + j;
+        if (mi == 2) reads();
+#pragma unroll
+        for (int q = 0; q < kGemmLoads; ++q)
+          if (q < nl && mi == (q * NM) / nl) load_part(ld_st, ld_slot, qa + q);
         // fixed issue order: each stage load sits between two MFMAs
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (KIND == kF8)
@@ -389,7 +416,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
   // s + 1 has landed, one barrier lets stage s + 1 be read (its first fragments are read
   // during the last k-step) and frees slot s % 5. At that barrier the loads issued after
   // stage s + 1's are those of stages s + 2, s + 3 and the first KS - 1 k-steps of stage s + 4.
-  const int nst = nkt * (kGemmKB / kGemmSK);  // even
+  const int nst = nkt * (kGemmKB / kGemmSK);  // even for the ring
+  if constexpr (kGemmStages == 5) {
   auto run_stage = [&](int s, int slot, auto parity, auto dma, auto next) __device__ {
     constexpr int P = decltype(parity)::value;
     const int ld_slot = slot == 0 ? kGemmStages - 1 : slot - 1;
@@ -397,17 +425,17 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int buf = (P * KS + ks) & 1;
-      const int q0 = ks * (kGemmLoads / KS);
+      const int q0 = ks * (kGemmLoads / KS), q1 = decltype(dma)::value ? q0 + kGemmLoads / KS : q0;
       if (ks + 1 < KS) {
-        mfmas(buf, decltype(dma)::value, s + 4, ld_slot, q0, [&]() __device__ { read_frags(slot, ks + 1, buf ^ 1); });
+        mfmas(buf, s + 4, ld_slot, q0, q1, [&]() __device__ { read_frags(slot, ks + 1, buf ^ 1); });
       } else if constexpr (decltype(next)::value) {
         if (decltype(dma)::value) wait_vm_lds<2 * kGemmLoads + kGemmLoads / KS * (KS - 1)>();
         else wait_vm_lds<0>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of stage s are done
         bare_barrier();
-        mfmas(buf, decltype(dma)::value, s + 4, ld_slot, q0, [&]() __device__ { read_frags(nslot, 0, buf ^ 1); });
+        mfmas(buf, s + 4, ld_slot, q0, q1, [&]() __device__ { read_frags(nslot, 0, buf ^ 1); });
       } else {
-        mfmas(buf, decltype(dma)::value, s + 4, ld_slot, q0, []() __device__ {});
+        mfmas(buf, s + 4, ld_slot, q0, q1, []() __device__ {});
       }
     }
   };
@@ -445,6 +473,44 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_nt_kernel(const uint8_t 
   run_stage(s, slot, std::integral_constant<int, 0>{}, F{}, T{});
   adv();
   run_stage(s, slot, std::integral_constant<int, 1>{}, F{}, F{});
+  } else {
+  // Two slots; stage s lives in slot s % 2 and issues the loads of stage s + 1 into the other slot,
+  // where every wave finished reading stage s - 1 before the barrier of stage s - 1. The loads go
+  // out in k-steps 0 .. KS - 2; before the last k-step (whose fragments were read during the one
+  // before), once stage s + 1 has landed, one barrier publishes it and frees slot s % 2, and the
+  // last k-step reads stage s + 1's first fragments.
+  constexpr int kPer = (kGemmLoads + KS - 2) / (KS - 1);  // loads per k-step
+  static_assert(KS % 2 == 0 && KS > 1, "the fragment buffer parity is the k-step's");
+  auto run_stage = [&](int s, auto next) __device__ {
+    const int slot = s & 1, nslot = slot ^ 1;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int buf = ks & 1;
+      const int qa = decltype(next)::value ? min(ks * kPer, kGemmLoads) : 0;
+      const int qb = decltype(next)::value ? min((ks + 1) * kPer, kGemmLoads) : 0;
+      if (ks + 1 < KS) {
+        mfmas(buf, s + 1, nslot, qa, qb, [&]() __device__ { read_frags(slot, ks + 1, buf ^ 1); });
+      } else if constexpr (decltype(next)::value) {
+        wait_vm_lds<0>();
+        bare_barrier();
+        mfmas(buf, s + 1, nslot, 0, 0, [&]() __device__ { read_frags(nslot, 0, buf ^ 1); });
+      } else {
+        mfmas(buf, s + 1, nslot, 0, 0, []() __device__ {});
+      }
+    }
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+
+  // prologue: stage 0 landed, its first fragments read
+#pragma unroll
+  for (int q = 0; q < kGemmLoads; ++q) load_part(0, 0, q);
+  wait_vm_lds<0>();
+  bare_barrier();
+  read_frags(0, 0, 0);
+  for (int s = 0; s + 1 < nst; ++s) run_stage(s, T{});
+  run_stage(nst - 1, F{});
+  }
 
   // epilogue, specialised on the output type, activation and accumulation (one uniform
   // branch here instead of per-element tests); the ring's LDS is reused for staging
