@@ -11,11 +11,13 @@
 //   then owns one query column (lane % 32) and 3 x 16 of the 96 keys of a tile, so the row
 //   max is one cross-lane exchange (lane ^ 32) and the probabilities P^T feed the next
 //   MFMA (O^T += V^T P^T) straight from registers, without an LDS round trip.
-//   V^T is read from a head-major copy made by a pre-pass (one extra 2*S*H*D-byte sweep),
-//   stored with keys interleaved in 16-key groups so that each lane's 8 MFMA k-values are
-//   one 16-byte LDS read. K and V^T tiles go straight from HBM/L2 to LDS rings
-//   (global_load_lds_dwordx4); the two halves of the workgroup alternate between the matrix
-//   cores and the VALU (see window_attn_kernel).
+//   V^T is read from a copy made by a pre-pass (one extra 2*S*H*D-byte sweep): per head, one
+//   contiguous image per 96-key tile, its 16-byte chunks already in the order and XOR swizzle of
+//   the kernel's LDS tile, with keys interleaved in 16-key groups so that each lane's 8 MFMA
+//   k-values are one 16-byte LDS read. K and V^T tiles go straight from HBM/L2 to LDS rings
+//   (global_load_lds_dwordx4), each wavefront's load of a V^T tile one contiguous kilobyte; the
+//   two halves of the workgroup alternate between the matrix cores and the VALU (see
+//   window_attn_kernel).
 //
 // Scheduling
 //   work items (query block, head) are ordered longest-first per head, and the flat
@@ -40,8 +42,58 @@ constexpr float kLazy = 8.0f;  // log2 of the largest probability a stale runnin
 __host__ __device__ constexpr int kperm(int p) { return 8 * ((p & 7) >> 2) + 4 * (p >> 3) + (p & 3); }
 
 // ---------------------------------------------------------------------------------
-// Pre-pass: V [seq, heads, D] (strided view) -> vt[head][d][s_pad], keys in kperm order
-// inside each 16-key group, zero beyond seq.
+// LDS slots of the staged tiles. Each tile row is split into 16-byte chunks; chunk c of row r
+// is stored at slot c ^ swizzle(r), so that the 16 lanes of one MFMA fragment read (16
+// consecutive rows, one chunk column) hit 16 different 16-byte bank groups.
+template <int D>
+__device__ __forceinline__ int k_slot(int r, int c) {
+  if constexpr (D == 128) return c ^ (r & 15);  // 16 chunks per 256-byte row
+  else return c ^ ((r >> 1) & 7);               // 8 chunks per 128-byte row
+}
+__device__ __forceinline__ int v_slot(int d, int c) { return c ^ ((d >> 1) & 7); }  // 8 chunks per row
+// the V^T tile's 32-key part (4 chunks per row): the 16 lanes of a fragment read (rows d..d+15)
+// hit 16 different 16-byte bank groups
+__device__ __forceinline__ int vb_slot(int d, int c) { return c ^ ((d >> 2) & 3); }
+
+// Rows of the V^T copy and of the normalised q / k regions: seq rounded up to 192, a multiple of the
+// pre-passes' 64-row blocks and of the attention's 96-key tiles, so a tile never reads past its head's
+// region.
+__host__ __device__ constexpr int pad_rows(int seq) { return (seq + 191) / 192 * 192; }
+
+// ---------------------------------------------------------------------------------
+// The V^T copy is a sequence of tile images, one per 96-key tile: the image of keys [ks, ks + 96)
+// of head h starts at element (h * s_pad + ks) * D and holds the tile's 16-byte chunks in LDS
+// order: position P < 8 D is (d = P / 8, slot P % 8) of the 64-key part, holding chunk
+// v_slot(d, slot) of keys [ks, ks + 64) of V^T row d; position 8 D + 4 d + slot of the 32-key part
+// holds chunk vb_slot(d, slot) of keys [ks + 64, ks + 96). Inside a chunk the 8 keys follow kperm
+// within their 16-key group; keys past seq are zero. A tile load is then a contiguous copy.
+// write_vt_image: the image chunks of the 64 keys [k0, k0 + 64) (k0 a multiple of 64) from their V rows
+// staged in LDS (row r at rows + r * P), into the head's images at vt_head. A 64-key block holds whole
+// 16-key groups, so every chunk it writes is complete; it covers one or two tiles.
+template <int D, int P>
+__device__ __forceinline__ void write_vt_image(const uint16_t *rows, int k0, uint16_t *__restrict__ vt_head,
+                                               int tid) {
+  for (int cc = tid; cc < D * 8; cc += kThreads) {
+    const int d = cc >> 3, pc = cc & 7;  // V^T row; chunk pc holds key slots 8 pc .. 8 pc + 7 of the block
+    const int key = k0 + 8 * pc, tile = key / kBN, sb = key - tile * kBN;
+    const int pos = sb < 64 ? 8 * d + v_slot(d, sb >> 3) : 8 * D + 4 * d + vb_slot(d, (sb - 64) >> 3);
+    uint16_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int p = 8 * pc + j;
+      e[j] = rows[((p & ~15) + kperm(p & 15)) * P + d];
+    }
+    uint4 o;
+    o.x = uint32_t(e[0]) | (uint32_t(e[1]) << 16);
+    o.y = uint32_t(e[2]) | (uint32_t(e[3]) << 16);
+    o.z = uint32_t(e[4]) | (uint32_t(e[5]) << 16);
+    o.w = uint32_t(e[6]) | (uint32_t(e[7]) << 16);
+    *reinterpret_cast<uint4 *>(vt_head + (int64_t)tile * (kBN * D) + pos * 8) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Pre-pass: V [seq, heads, D] (strided view) -> the V^T tile images, 64 keys per workgroup.
 // grid (s_pad / 64, heads), kThreads threads.
 template <int D>
 __global__ __launch_bounds__(kThreads) void vt_prepass_kernel(const uint16_t *__restrict__ v, int64_t v_row,
@@ -58,35 +110,22 @@ __global__ __launch_bounds__(kThreads) void vt_prepass_kernel(const uint16_t *__
     *reinterpret_cast<uint4 *>(&tile[r * P + col * 8]) = val;
   }
   __syncthreads();
-  uint16_t *dst = vt + (int64_t)head * D * s_pad + k0;
-  for (int c = tid; c < D * 8; c += kThreads) {
-    int d = c >> 3, pc = c & 7;  // output positions 8*pc .. 8*pc+7 of row d
-    uint16_t e[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int p = 8 * pc + j;
-      e[j] = tile[((p & ~15) + kperm(p & 15)) * P + d];
-    }
-    uint4 o;
-    o.x = uint32_t(e[0]) | (uint32_t(e[1]) << 16);
-    o.y = uint32_t(e[2]) | (uint32_t(e[3]) << 16);
-    o.z = uint32_t(e[4]) | (uint32_t(e[5]) << 16);
-    o.w = uint32_t(e[6]) | (uint32_t(e[7]) << 16);
-    *reinterpret_cast<uint4 *>(dst + (int64_t)d * s_pad + 8 * pc) = o;
-  }
+  write_vt_image<D, P>(tile, k0, vt + (int64_t)head * s_pad * D, tid);
 }
 
 // ---------------------------------------------------------------------------------
 // The block's q_norm / k_norm (RMSNorm over the head dim, with ROPE the split-half rotation, one
-// bf16 rounding: the arithmetic of qk_norm.h) of the 64 rows [k0, k0 + 64) of one head at a
+// bf16 rounding: the arithmetic of qk_norm.h) of the BR rows [k0, k0 + BR) of one head at a
 // time, written head-major (row r at dst + r * D), zero for rows at or past seq. Each row is
-// normalised by an aligned group of D/8 lanes, one 8-channel chunk per lane. A lane loads the RoPE
-// matrix rows its chunk uses once (the constructor) and reuses them for every head (run): row 0
-// (f00, f01) below half, row 1 (f10, f11) above.
-template <int D, bool ROPE, int THREADS>
+// normalised by an aligned group of D/8 lanes, one 8-channel chunk per lane (THREADS / (D/8) rows
+// per pass; with D = 64 the last pass is partly idle). A lane loads the RoPE matrix rows its chunk
+// uses once (the constructor) and reuses them for every head (run): row 0 (f00, f01) below half,
+// row 1 (f10, f11) above.
+template <int D, bool ROPE, int THREADS, int BR>
 struct RowNorm {
-  static constexpr int CH = D / 8, ROWS = THREADS / CH, ITER = 64 / ROWS;
-  static_assert(64 % ROWS == 0, "whole row groups per pass");
+  static constexpr int CH = D / 8, ROWS = THREADS / CH, ITER = (BR + ROWS - 1) / ROWS;
+  // row r0 + it * ROWS lies in the block (a whole row group is in or out)
+  __device__ __forceinline__ bool in_block(int it) const { return BR % ROWS == 0 || r0 + it * ROWS < BR; }
   int c, r0, half, k0, seq;
   bool first, rotated;
   float2 fm[ITER][ROPE ? 8 : 1];
@@ -100,7 +139,7 @@ struct RowNorm {
 #pragma unroll
       for (int it = 0; it < ITER; ++it) {
         const int key = k0 + r0 + it * ROWS;
-        if (rotated && key < seq) {
+        if (rotated && key < seq && in_block(it)) {
           const float *f = freqs + key * f_row + 4 * (first ? 8 * c : 8 * c - half) + (first ? 0 : 2);
 #pragma unroll
           for (int j = 0; j < 8; ++j) fm[it][j] = *reinterpret_cast<const float2 *>(f + 4 * j);
@@ -122,10 +161,11 @@ struct RowNorm {
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
       const int key = k0 + r0 + it * ROWS;
-      raw[it] = key < seq ? ld16(x + key * x_row + head * x_head + 8 * c) : u32x4_t{0, 0, 0, 0};
+      raw[it] = key < seq && in_block(it) ? ld16(x + key * x_row + head * x_head + 8 * c) : u32x4_t{0, 0, 0, 0};
     }
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
+      if (!in_block(it)) continue;
       const int r = r0 + it * ROWS;
       const bool live = k0 + r < seq;
       float xf[8], y[8];
@@ -164,10 +204,10 @@ constexpr int kPrepassHeads = 10;  // heads per pre-pass workgroup (they share i
                                    // 10 measured 4% faster than 8 at 40 heads, 4, 5 and 20 no better
 
 // Pre-pass of the normalising attention, for the 64 rows [k0, k0 + 64) of up to kPrepassHeads
-// heads: the V^T copy of vt_prepass_kernel, the normalised keys kn[head][key][d] and, when q is
-// given, the normalised queries qn[head][row][d] (RowNorm). V tiles alternate between two LDS
-// buffers, so one barrier per head orders the tile's writes before its transposed reads, and
-// the reads of a buffer before its next writes.
+// heads: the V^T image chunks of vt_prepass_kernel, the normalised keys kn[head][key][d] and, when q
+// is given, the normalised queries qn[head][row][d] (RowNorm). V tiles alternate between two LDS
+// buffers, so one barrier per head orders the tile's writes before its transposed reads, and the
+// reads of a buffer before its next writes.
 template <int D, bool ROPE>
 __global__ __launch_bounds__(kThreads) void qkv_prepass_kernel(
     const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const uint16_t *__restrict__ q_weight, float q_eps,
@@ -180,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void qkv_prepass_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t tile[2][64 * P];
   const int h0 = blockIdx.x * kPrepassHeads, h1 = min(heads, h0 + kPrepassHeads);
   const int k0 = blockIdx.y * 64, tid = threadIdx.x;
-  const RowNorm<D, ROPE, kThreads> norm(freqs, f_row, rot, k0, seq, tid);
+  const RowNorm<D, ROPE, kThreads, 64> norm(freqs, f_row, rot, k0, seq, tid);
   for (int head = h0; head < h1; ++head) {
     uint16_t *buf = tile[head & 1];
     for (int cc = tid; cc < 64 * CH; cc += kThreads) {
@@ -193,42 +233,10 @@ __global__ __launch_bounds__(kThreads) void qkv_prepass_kernel(
     norm.run(k, k_row, k_head, k_weight, k_eps, kn + off, head);
     if (q) norm.run(q, q_row, q_head, q_weight, q_eps, qn + off, head);
     __syncthreads();
-    uint16_t *dst = vt + (int64_t)head * D * s_pad + k0;
-    for (int cc = tid; cc < D * 8; cc += kThreads) {
-      int d = cc >> 3, pc = cc & 7;  // output positions 8*pc .. 8*pc+7 of row d
-      uint16_t e[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        int pp = 8 * pc + j;
-        e[j] = buf[((pp & ~15) + kperm(pp & 15)) * P + d];
-      }
-      uint4 o;
-      o.x = uint32_t(e[0]) | (uint32_t(e[1]) << 16);
-      o.y = uint32_t(e[2]) | (uint32_t(e[3]) << 16);
-      o.z = uint32_t(e[4]) | (uint32_t(e[5]) << 16);
-      o.w = uint32_t(e[6]) | (uint32_t(e[7]) << 16);
-      *reinterpret_cast<uint4 *>(dst + (int64_t)d * s_pad + 8 * pc) = o;
-    }
+    write_vt_image<D, P>(buf, k0, vt + (int64_t)head * s_pad * D, tid);
   }
 }
 
-// ---------------------------------------------------------------------------------
-// LDS slots of the staged tiles. Each tile row is split into 16-byte chunks; chunk c of row r
-// is stored at slot c ^ swizzle(r), so that the 16 lanes of one MFMA fragment read (16
-// consecutive rows, one chunk column) hit 16 different 16-byte bank groups.
-template <int D>
-__device__ __forceinline__ int k_slot(int r, int c) {
-  if constexpr (D == 128) return c ^ (r & 15);  // 16 chunks per 256-byte row
-  else return c ^ ((r >> 1) & 7);               // 8 chunks per 128-byte row
-}
-__device__ __forceinline__ int v_slot(int d, int c) { return c ^ ((d >> 1) & 7); }  // 8 chunks per row
-// the V^T tile's 32-key part (4 chunks per row): the 16 lanes of a fragment read (rows d..d+15)
-// hit 16 different 16-byte bank groups
-__device__ __forceinline__ int vb_slot(int d, int c) { return c ^ ((d >> 2) & 3); }
-
-// Rows of the V^T copy and of the normalised q / k regions: seq rounded up to 192, a multiple of the
-// pre-pass's 64-row blocks and of the attention's key tiles, so a tile never reads past its row.
-__host__ __device__ constexpr int pad_rows(int seq) { return (seq + 191) / 192 * 192; }
 
 
 // The value of lane (l + 32) mod 64, via v_permlane32_swap (gfx950).
@@ -368,7 +376,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   // Tile loads, by one group of 256 threads: thread chunk i fills LDS position P = 256 i + gtid
   // (16-byte units) of the tile. In a K tile, P is (row P / KC, slot P % KC) and holds chunk
   // slot ^ swizzle(row) of that key row; row kr0 + i * 256 / KC has the same swizzle for every i.
-  // In a V^T tile, P < 8 D is (d, slot) of the 64-key part, the rest (d, slot) of the 32-key part.
+  // A V^T tile image is already in LDS order: P comes from position P of the image.
   // Rows past seq read row seq - 1 (their scores are masked).
   constexpr int KCG = kBN * KC / 256, VCG = D * (kBN / 8) / 256;  // 16-byte chunks per thread and tile
   static_assert(KCG >= 1 && VCG >= 1 && KCG == VCG, "both groups issue the same number of loads");
@@ -382,15 +390,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
 #pragma unroll
   for (int i = 0; i < KCG; ++i) {
     const int P = 256 * i + gtid;
-    uint32_t vo;
-    if (P < D * 8) {
-      const int d = P >> 3;
-      vo = (uint32_t)(d * s_pad + v_slot(d, P & 7) * 8);
-    } else {
-      const int d = (P - D * 8) >> 2;
-      vo = (uint32_t)(d * s_pad + 64 + vb_slot(d, P & 3) * 8);
-    }
-    doff[i] = 2u * (group == 0 ? (uint32_t)((kr0 + i * (256 / KC)) * (int)k_row + kslot) : vo);
+    doff[i] = 2u * (group == 0 ? (uint32_t)((kr0 + i * (256 / KC)) * (int)k_row + kslot) : (uint32_t)(P * 8));
   }
   const uint32_t lds_dma = __builtin_amdgcn_readfirstlane(
       (group == 0 ? lds_address(&Ks[0][0]) : lds_address(&Vs[0][0])) + gw * 64 * 16);
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(kThreads, 1) void window_attn_kernel(
   // this group's loads of the tile whose first key is ks into ring slot `slot`; the last K tile
   // of the sequence reads rows past seq as row seq - 1 (their scores are masked)
   auto tile_dma = [&](int ks, int slot) __device__ {
-    const uint16_t *base = group == 0 ? kbase + (int64_t)ks * k_row : vbase + ks;
+    const uint16_t *base = group == 0 ? kbase + (int64_t)ks * k_row : vbase + (int64_t)ks * D;
     uint32_t off[KCG];
 #pragma unroll
     for (int i = 0; i < KCG; ++i) off[i] = doff[i];

@@ -73,7 +73,8 @@ int vdnh3_window_plan_build(int seq, int video_start, int video_end, int num_fra
 int vdnh3_window_block_m(void);
 int vdnh3_window_block_n(void);
 
-/* Device workspace (bytes) for vdnh3_window_attn_fwd: the head-major V^T copy. */
+/* Device workspace (bytes) for vdnh3_window_attn_fwd: the V^T copy, per head one contiguous image per
+ * 96-key tile in the attention kernel's LDS order (seq rounded up to 192 rows per head). */
 size_t vdnh3_window_workspace_bytes(int seq, int heads, int head_dim);
 
 /*
@@ -101,7 +102,7 @@ int vdnh3_window_attn_fwd(const uint16_t *q, int64_t q_row, int64_t q_head,
 
 /*
  * The two phases of vdnh3_window_attn_fwd, for callers that time or reuse them:
- * vdnh3_window_vt_prepass writes the head-major V^T copy into `workspace`;
+ * vdnh3_window_vt_prepass writes the V^T tile images into `workspace`;
  * vdnh3_window_attn_prepared runs the attention from q, k and that copy.
  */
 int vdnh3_window_vt_prepass(const uint16_t *v, int64_t v_row, int64_t v_head, int seq, int heads,
@@ -120,8 +121,8 @@ int vdnh3_window_attn_prepared(const uint16_t *q, int64_t q_row, int64_t q_head,
  * wrote them, and normalised with the arithmetic of vdnh3_qk_rmsnorm / vdnh3_qk_rmsnorm_rope, so
  * that the result has the same bits as those calls followed by vdnh3_window_attn_prepared.
  * The workspace holds up to three regions of vdnh3_window_workspace_bytes(seq, heads, head_dim)
- * bytes each, all [heads][seq rounded up to 64][head_dim] bf16: 0 the V^T copy, 1 the normalised
- * keys, 2 the normalised queries (zero rows past seq).
+ * bytes each, all [heads][seq rounded up to 192][head_dim] bf16: 0 the V^T tile images, 1 the
+ * normalised keys, 2 the normalised queries (zero rows past seq).
  *   vdnh3_window_norm_workspace_bytes: 2 regions, 3 with_queries; 16-byte aligned.
  *   vdnh3_window_qkv_prepass: writes regions 0 and 1 (keys: k_weight / k_eps) and, when q is not
  *     NULL, region 2 (queries: q_weight / q_eps). With freqs (the RoPE table of
@@ -130,7 +131,7 @@ int vdnh3_window_attn_prepared(const uint16_t *q, int64_t q_row, int64_t q_head,
  *   vdnh3_window_attn_qnorm: the attention from raw q, normalised as the kernel loads it (q_weight,
  *     q_eps), against regions 0 and 1 (a pre-pass with q = NULL and no freqs). With RoPE, run the
  *     pre-pass with q and pass regions 2 and 1 as q and k to vdnh3_window_attn_prepared (q_row =
- *     k_row = head_dim, q_head = k_head = seq rounded up to 64 times head_dim): a rotation in the
+ *     k_row = head_dim, q_head = k_head = seq rounded up to 192 times head_dim): a rotation in the
  *     attention kernel would re-read the table for every head and query block.
  */
 size_t vdnh3_window_norm_workspace_bytes(int seq, int heads, int head_dim, int with_queries);
