@@ -25,7 +25,8 @@ Other workloads: ``stack`` (50 blocks x ``--steps`` denoising steps, ``x <- x + 
 ``--steps 8 --warmup 1`` for the 8-step pass), ``window`` (attention alone), ``branch`` (VDN branch alone),
 ``gemm_{i8,f8}_{qkv,out}`` (W8A8 GEMMs alone), ``gdn`` (token-level chunk-64 Gated DeltaNet), ``dit``
 (the DiT block pointwise passes), ``rope`` (q/k RMSNorm + RoPE),
-``hbm_copy`` (counter calibration), ``mfma_peak`` (sustained MFMA rates, the ceiling calibration).
+``hbm_copy`` (counter calibration), ``mfma_peak`` (sustained MFMA rates, the ceiling calibration),
+``cpu_configs`` (the fp32 CPU oracle timed per configuration at full size on the host cores, a few minutes).
 ``cpu_baseline`` times the fp32 CPU oracle on the host cores (16 threads, the box's CPU share) on bounded
 samples (1 warm-up, median of 3): for ``block``, the window attention on sampled query rows, the projections
 on sampled rows and the VDN branch on 7 of its 29 inner frames, combined at the block's per-part work.
@@ -59,7 +60,8 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="block", choices=["block", "stack", "window", "hbm_copy", "branch",
                                                              "gemm_i8_qkv", "gemm_i8_out", "gemm_f8_qkv",
-                                                             "gemm_f8_out", "gdn", "dit", "rope", "mfma_peak"],
+                                                             "gemm_f8_out", "gdn", "dit", "rope", "mfma_peak",
+                                                             "cpu_configs"],
                     help="hbm_copy: a plain 1 GiB device copy, the reference point for scaling rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes")
     ap.add_argument("--short-conv", default="k,v",
@@ -778,6 +780,131 @@ def cpu_baseline_block(torch, device, lay, work, conv, n_rows):
                       "a warm-up, combined at the block's per-part work"}
 
 
+def bench_cpu_configs(args, torch, device):
+    """The fp32 CPU oracle timed per benchmark configuration on the host cores, at full size (no sampling):
+    1 warm-up, then the median of 3 (config 2: the warm-up runs on 2304 sampled rows, each full run is about a
+    minute). Nothing here runs on the GPU.
+
+    * config 1 / 1b: one hybrid block forward, 2 heads x 64, hidden 128, 16 text rows + 7 / 13 frames of 8 x 8
+      tokens (7 frames is full cover: dense attention, no branch), ``oracle.hybrid_oracle.vdn_forward``;
+    * config 2: the window attention at 40,688 x 40 x 128, ``oracle.window_oracle.window_attention_rows`` over
+      every row (rows that share a key set batched, 8 heads at a time);
+    * config 3: the VDN branch at the full shape (31 frames x 1296 tokens, skip_ends: 29 inner frames, 40 x
+      128, hidden 5120, text state, k/v short convolutions), ``oracle.branch_oracle.projected_delta``; and the
+      chunk-64 Gated DeltaNet at 40,688 x 40 x 128, ``oracle.gdn_oracle.chunked`` (float64);
+    * config 4: the qkv (N 15,360) and out (N 5,120) projections at M 40,688, K 5,120 as the dequantised fp32
+      ``F.linear`` the reference's projection falls back to on the CPU (``vdn_h3/fp8.py:253-266``).
+    """
+    import torch.nn.functional as F
+
+    from oracle import branch_oracle as bo
+    from oracle import gdn_oracle as go
+    from oracle import hybrid_oracle as ho
+    from oracle import window_oracle as wo
+    from vdn_h3_amd import synth, window
+    from vdn_h3_amd.gdn import gdn_flops
+    from vdn_h3_amd.layout import text_first_layout
+
+    del device
+    model, physical = _cpu_description()
+    parts = {}
+
+    def record(name, work, unit, med, times, sample):
+        parts[name] = {"seconds_median": round(med, 4), "seconds_runs": [round(t, 4) for t in times],
+                       "work": work, "rate": round(work / med / 1e12, 5), "rate_unit": unit, "sample": sample}
+        print(f"cpu_configs: {name}: {med:.3f} s ({work / med / 1e12:.4f} {unit})", file=sys.stderr, flush=True)
+
+    # configs 1 and 1b: the CPU-plumbing block
+    for name, frames in (("config1_block_s464_h2_d64", 7), ("config1b_block_s848_h2_d64_13f", 13)):
+        heads, dim, hidden = 2, 64, 128
+        lay = text_first_layout(16, frames, (8, 8))
+        x = synth.randn((lay.seq_len, hidden), 70, dtype=torch.bfloat16)
+        bw = synth.branch_weights(heads, dim, hidden, seed=170)
+        aw = {"qkv_proj.weight": synth.randn((3 * heads * dim, hidden), 71, dtype=torch.bfloat16, scale=0.02),
+              "out_proj.weight": synth.randn((hidden, heads * dim), 72, dtype=torch.bfloat16, scale=0.02),
+              "q_norm.weight": (1 + 0.1 * synth.randn((dim,), 73)).to(torch.bfloat16),
+              "k_norm.weight": (1 + 0.1 * synth.randn((dim,), 74)).to(torch.bfloat16)}
+        pairs = wo.pair_count(lay.seq_len, lay.video_start, lay.video_end, lay.num_frames, lay.tokens_per_frame,
+                              list(lay.bounds), lay.anchor_frames)
+        flop = window.attention_flops(pairs, heads, dim) + 2.0 * lay.seq_len * hidden * 4 * heads * dim
+        med, times = _median_seconds(lambda: ho.vdn_forward(x, lay, aw, bw, heads, dim))
+        record(name, flop, "TFLOP/s", med, times,
+               f"whole block ({'full cover, dense' if lay.full_cover else 'window + branch'}); work = attention "
+               "+ qkv / out projections")
+
+    # config 2: the window attention at the full shape
+    w = synth.WINDOW_FULL
+    lay = w.layout
+    qkv = synth.fused_qkv(lay.seq_len, w.heads, w.head_dim, seed=0, scale=w.scale)
+    q, k, v = synth.split_qkv(qkv, w.heads, w.head_dim)
+    geo = (lay.video_start, lay.video_end, lay.num_frames, lay.tokens_per_frame, lay.bounds, w.scale,
+           lay.anchor_frames)
+    wo.window_attention_rows(q, k, v, torch.linspace(0, lay.seq_len - 1, 2304).long().tolist(), *geo)
+    rows = list(range(lay.seq_len))
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        wo.window_attention_rows(q, k, v, rows, *geo)
+        times.append(time.perf_counter() - t)
+        print(f"cpu_configs: window full run {len(times)}: {times[-1]:.1f} s", file=sys.stderr, flush=True)
+    pairs = wo.pair_count(lay.seq_len, lay.video_start, lay.video_end, lay.num_frames, lay.tokens_per_frame,
+                          list(lay.bounds), lay.anchor_frames)
+    record("config2_window_s40688_h40_d128", window.attention_flops(pairs, w.heads, w.head_dim), "TFLOP/s",
+           sorted(times)[1], times, "every query row, fp32; warm-up on 2304 sampled rows")
+    del qkv, q, k, v
+
+    # config 3: the VDN branch at the full shape, and the chunk-64 Gated DeltaNet
+    heads, dim, hidden, tpf, text = w.heads, w.head_dim, 5120, lay.tokens_per_frame, lay.text_len
+    frames = lay.num_frames
+    seq = text + frames * tpf
+    conv = ("k", "v")
+    bqkv = synth.fused_qkv(seq, heads, dim, seed=40)
+    bx = synth.randn((seq, hidden), 41, dtype=torch.bfloat16)
+    bw = synth.branch_weights(heads, dim, hidden, short_conv=conv)
+    q, k, v = synth.split_qkv(bqkv, heads, dim)
+    bounds = wo.window_bounds(frames, 1, 5)
+    work = block_flops(lay, heads, dim, hidden, pairs, conv)
+    branch_work = (work["branch_core"] + work["branch_gates"] + work["branch_text_state"]
+                   + work["branch_short_conv"] + work["to_out_linear"])
+    med, times = _median_seconds(lambda: bo.projected_delta(
+        bw, bx[text:], q[text:], k[text:], v[text:], frames, tpf, bounds, frame_size=lay.frame_size,
+        text_x=bx[:text], text_k_raw=k[:text], text_v_raw=v[:text], skip_ends=True, short_conv=conv,
+        fused_conv=True))
+    record("config3_vdn_branch_f31_t1296_h40_d128", branch_work, "TFLOP/s", med, times,
+           "projected_delta, 31 frames (29 inner) x 1296 tokens, text state, k/v short convolutions, "
+           "to_out_linear")
+    del bqkv, bx, q, k, v
+    tokens = lay.seq_len
+    g = torch.Generator().manual_seed(50)
+    gq = torch.randn(tokens, heads, dim, generator=g).to(torch.bfloat16)
+    gk = F.normalize(torch.randn(tokens, heads, dim, generator=g), dim=-1).to(torch.bfloat16)
+    gv = torch.randn(tokens, heads, dim, generator=g).to(torch.bfloat16)
+    gb = torch.sigmoid(torch.randn(tokens, heads, generator=g))
+    gg = -F.softplus(torch.randn(tokens, heads, generator=g))
+    med, times = _median_seconds(lambda: go.chunked(gq, gk, gv, gb, gg))
+    record("config3_gdn_chunk64_t40688_h40_d128", gdn_flops(tokens, heads, dim), "TFLOP/s", med, times,
+           "all tokens and heads, float64 chunk form")
+    del gq, gk, gv
+
+    # config 4: the projections as the CPU fallback computes them
+    x = synth.randn((tokens, hidden), 60, dtype=torch.float32)
+    for name, n in (("config4_qkv_m40688_k5120_n15360", 3 * heads * dim), ("config4_out_m40688_k5120_n5120", hidden)):
+        wt = synth.randn((n, hidden), 61, scale=0.02)
+        med, times = _median_seconds(lambda: F.linear(x, wt))
+        record(name, 2.0 * tokens * hidden * n, "TFLOP/s", med, times, "dequantised fp32 F.linear")
+        del wt
+    return {
+        "metric": "fp32 CPU oracle seconds per benchmark configuration on the host cores",
+        "value": parts["config2_window_s40688_h40_d128"]["rate"],
+        "unit": "TFLOP/s",
+        "ms_per_step": round(1e3 * parts["config2_window_s40688_h40_d128"]["seconds_median"], 1),
+        "dtype": "f32",
+        "config": {"workload": "cpu_configs", "cpu": model, "physical_cores": physical,
+                   "threads": torch.get_num_threads(), "kind": "port"},
+        "parts": parts,
+    }
+
+
 def main():
     args = _parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -817,6 +944,8 @@ def main():
         result = bench_rope(args, torch, device)
     elif args.workload == "mfma_peak":
         result = bench_mfma_peak(args, torch, device)
+    elif args.workload == "cpu_configs":
+        result = bench_cpu_configs(args, torch, device)
     else:
         result = bench_window(args, torch, device)
     line = {

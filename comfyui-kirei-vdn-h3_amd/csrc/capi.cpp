@@ -35,4 +35,4 @@ int check_launch(const char *what) {
 
 extern "C" const char *vdnh3_last_error(void) { return g_last_error.c_str(); }
 
-extern "C" int vdnh3_abi_version(void) { return 101; }
+extern "C" int vdnh3_abi_version(void) { return 102; }

@@ -384,7 +384,9 @@ __global__ void alpha_logsum_kernel(const float *__restrict__ alpha, float *__re
 }
 
 // ---------------------------------------------------------------------------------------
-// readout. grid = frames * heads, 256 threads; wavefronts take 32-token tiles in turn.
+// readout. grid = frame_count * heads, 256 threads; wavefronts take 32-token tiles in turn. The grid
+// covers frames f0 .. f0 + frame_count - 1 of the F frames the banks and bounds describe; the rows of
+// q, the gate and out are those of that range (frame f's tokens at rows (f - f0) T ..).
 //   L_f[v][k] = bf16(before[v][k] * decay_b[k] + after[v][k] * decay_a[k])   (LDS, [v][k])
 //   r^T = L_f q~^T on bf16 MFMA (lane = token, so the RMS over v is in-lane plus one exchange)
 // The normalised, weighted tile y (bf16) goes through a per-wavefront LDS stage so that the
@@ -410,7 +412,7 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
     const uint16_t *__restrict__ q, int64_t q_row, int64_t q_head, const float *__restrict__ prefix,
     const float *__restrict__ suffix, const float *__restrict__ logsum, const float *__restrict__ text,
     const int *__restrict__ bounds, int use_alpha, const uint16_t *__restrict__ norm_w, ReadoutGate gin,
-    uint16_t *__restrict__ out, int64_t out_row, int F, int T, int heads) {
+    uint16_t *__restrict__ out, int64_t out_row, int F, int f0, int T, int heads) {
   constexpr int LP = D + 8, NS = D / 16, NO = D / 32, YP = D + 8, CPR = D / 8;  // CPR: 16-byte chunks per row
   constexpr int RPI = 64 / CPR;                                                  // rows per wave instruction
   __shared__ __attribute__((aligned(16))) uint16_t Ls[D * LP];
@@ -419,7 +421,7 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
   __shared__ float Bg[FG ? D : 1];
   __shared__ float dec[2][D];
   __shared__ __attribute__((aligned(16))) uint16_t Wn[D];
-  const int fh = blockIdx.x, f = fh / heads, h = fh - f * heads;
+  const int fh = blockIdx.x, fl = fh / heads, h = fh - fl * heads, f = f0 + fl;  // fl: frame within the range
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int lo = max(bounds[2 * f], 0), hi = min(bounds[2 * f + 1], F - 1);
   const bool has_b = lo - 1 >= 0, has_a = hi + 1 < F;
@@ -470,14 +472,14 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
 
   // gate hidden rows of a tile (FG): lane = token, like q
   auto h_ptr = [&](int tile) __device__ {
-    const int64_t row = (int64_t)f * T + min(tile * 32 + l32, T - 1);
+    const int64_t row = (int64_t)fl * T + min(tile * 32 + l32, T - 1);
     return gin.hidden + row * gin.hidden_row + 8 * g;
   };
 
   // q tiles: lane = token; the next tile's raw q is loaded after this tile's features
   const int ntiles = (T + 31) / 32;
   auto q_ptr = [&](int tile) __device__ {
-    const int64_t row = (int64_t)f * T + min(tile * 32 + l32, T - 1);
+    const int64_t row = (int64_t)fl * T + min(tile * 32 + l32, T - 1);
     return q + row * q_row + (int64_t)h * q_head + 8 * g;
   };
   u32x4_t raw[NS];
@@ -495,7 +497,7 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
 #pragma unroll
       for (int it = 0; it < 32 / RPI; ++it) {
         const int t = min(tile * 32 + it * RPI + orow, T - 1);
-        gv[it] = ld16(gin.gate + ((int64_t)f * T + t) * gin.gate_row + (int64_t)h * D + 8 * ochunk);
+        gv[it] = ld16(gin.gate + ((int64_t)fl * T + t) * gin.gate_row + (int64_t)h * D + 8 * ochunk);
       }
     }
 
@@ -590,7 +592,7 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
             o[e] = y * gt;
           }
           if (t < T)
-            *reinterpret_cast<u32x2_t *>(out + ((int64_t)f * T + t) * out_row + (int64_t)h * D + v0) =
+            *reinterpret_cast<u32x2_t *>(out + ((int64_t)fl * T + t) * out_row + (int64_t)h * D + v0) =
                 u32x2_t{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
         }
       }
@@ -622,7 +624,7 @@ __global__ __launch_bounds__(256, 2) void readout_kernel(
 #pragma unroll
         for (int w = 0; w < 4; ++w)
           o[w] = pack_bf2(bf_lo(yv[w]) * bf_lo(gv[it][w]), bf_hi(yv[w]) * bf_hi(gv[it][w]));
-        *reinterpret_cast<u32x4_t *>(out + ((int64_t)f * T + t) * out_row + (int64_t)h * D + 8 * ochunk) = o;
+        *reinterpret_cast<u32x4_t *>(out + ((int64_t)fl * T + t) * out_row + (int64_t)h * D + 8 * ochunk) = o;
       }
     }
     asm volatile("" ::: "memory");
@@ -633,13 +635,17 @@ template <bool FG>
 int launch_readout(const uint16_t *q, int64_t q_row, int64_t q_head, int q_features, const float *prefix,
                    const float *suffix, const float *alpha_logsum, const float *text_state, const int32_t *bounds,
                    int use_alpha, const uint16_t *norm_w, const ReadoutGate &gin, uint16_t *out, int64_t out_row,
-                   int frames, int tokens, int heads, int head_dim, hipStream_t s) {
+                   int frames, int first_frame, int frame_count, int tokens, int heads, int head_dim, hipStream_t s) {
   VDNH3_HOST_CHECK(q_features == 0 || q_features == 1, VDNH3_ERR_INVALID, "readout: q_features must be 0 or 1");
-  const dim3 grid(frames * heads);
+  VDNH3_HOST_CHECK(first_frame >= 0 && frame_count > 0 && first_frame <= frames - frame_count, VDNH3_ERR_INVALID,
+                   "readout: frame range [%d, %d + %d) is not inside the %d frames", first_frame, first_frame,
+                   frame_count, frames);
+  const dim3 grid(frame_count * heads);
 #define VDNH3_RO(D, QF)                                                                                          \
   if (head_dim == D && q_features == QF)                                                                         \
     hipLaunchKernelGGL((readout_kernel<D, QF, FG>), grid, dim3(256), 0, s, q, q_row, q_head, prefix, suffix,      \
-                       alpha_logsum, text_state, bounds, use_alpha, norm_w, gin, out, out_row, frames, tokens, heads);
+                       alpha_logsum, text_state, bounds, use_alpha, norm_w, gin, out, out_row, frames, first_frame, \
+                       tokens, heads);
   VDNH3_RO(128, 0)
   VDNH3_RO(128, 1)
   VDNH3_RO(64, 0)
@@ -910,7 +916,7 @@ extern "C" int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, i
                              const float *prefix, const float *suffix, const float *alpha_logsum,
                              const float *text_state, const int32_t *bounds, int use_alpha, const uint16_t *norm_w,
                              const uint16_t *gate, int64_t gate_row, uint16_t *out, int64_t out_row, int frames,
-                             int tokens, int heads, int head_dim, void *stream) {
+                             int first_frame, int frame_count, int tokens, int heads, int head_dim, void *stream) {
   int rc = check_dim(head_dim);
   if (rc) return rc;
   VDNH3_HOST_CHECK(q && prefix && suffix && (alpha_logsum || !use_alpha) && bounds && norm_w && gate && out &&
@@ -924,8 +930,8 @@ extern "C" int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, i
                    VDNH3_ERR_INVALID, "readout: misaligned q / gate / out / norm weight / states");
   const vdnh3::ReadoutGate gin{gate, gate_row, nullptr, 0, nullptr, nullptr};
   return vdnh3::launch_readout<false>(q, q_row, q_head, q_features, prefix, suffix, alpha_logsum, text_state, bounds,
-                                      use_alpha, norm_w, gin, out, out_row, frames, tokens, heads, head_dim,
-                                      static_cast<hipStream_t>(stream));
+                                      use_alpha, norm_w, gin, out, out_row, frames, first_frame, frame_count, tokens,
+                                      heads, head_dim, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int vdnh3_readout_fused_gate(const uint16_t *q, int64_t q_row, int64_t q_head, int q_features,
@@ -933,8 +939,8 @@ extern "C" int vdnh3_readout_fused_gate(const uint16_t *q, int64_t q_row, int64_
                                         const float *text_state, const int32_t *bounds, int use_alpha,
                                         const uint16_t *norm_w, const uint16_t *gate_hidden, int64_t hidden_row,
                                         const uint16_t *gate_up_w, const uint16_t *gate_up_b, uint16_t *out,
-                                        int64_t out_row, int frames, int tokens, int heads, int head_dim,
-                                        void *stream) {
+                                        int64_t out_row, int frames, int first_frame, int frame_count, int tokens,
+                                        int heads, int head_dim, void *stream) {
   int rc = check_dim(head_dim);
   if (rc) return rc;
   VDNH3_HOST_CHECK(q && prefix && suffix && (alpha_logsum || !use_alpha) && bounds && norm_w && gate_hidden &&
@@ -949,8 +955,8 @@ extern "C" int vdnh3_readout_fused_gate(const uint16_t *q, int64_t q_row, int64_
                    VDNH3_ERR_INVALID, "readout: misaligned q / gate hidden / gate weight / out / norm weight / states");
   const vdnh3::ReadoutGate gin{nullptr, 0, gate_hidden, hidden_row, gate_up_w, gate_up_b};
   return vdnh3::launch_readout<true>(q, q_row, q_head, q_features, prefix, suffix, alpha_logsum, text_state, bounds,
-                                     use_alpha, norm_w, gin, out, out_row, frames, tokens, heads, head_dim,
-                                     static_cast<hipStream_t>(stream));
+                                     use_alpha, norm_w, gin, out, out_row, frames, first_frame, frame_count, tokens,
+                                     heads, head_dim, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int vdnh3_frame_mean(const uint16_t *x, int64_t x_row, int frames, int tokens, int hidden, float *out,

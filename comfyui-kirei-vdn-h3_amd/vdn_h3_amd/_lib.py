@@ -67,9 +67,10 @@ SIGNATURES = {
     "vdnh3_sana_factor": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_float, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_delta_scan": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_readout": (_c_int, [_vp, _c_i64, _c_i64, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_i64,
-                               _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp]),
+                               _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "vdnh3_readout_fused_gate": (_c_int, [_vp, _c_i64, _c_i64, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp,
-                                          _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp]),
+                                          _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                          _c_int, _vp]),
     "vdnh3_frame_mean": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _vp, _vp]),
     "vdnh3_linear_f32": (_c_int, [_vp, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_i64, _c_int, _c_int, _c_int,
                                   _vp]),

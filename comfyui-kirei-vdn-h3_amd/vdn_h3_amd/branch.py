@@ -358,13 +358,17 @@ def _device_bounds(bounds, device) -> torch.Tensor:
 
 def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *, text_state=None,
                      bridge="alpha", num_frames, tokens_per_frame, out=None, q_features=False, gate_hidden=None,
-                     gate_up_weight=None, gate_up_bias=None):
+                     gate_up_weight=None, gate_up_bias=None, frame_range=None):
     """Gather, readout and RMSNorm/gate epilogue: ``[F*T, H*D]`` bf16.
 
     ``q_raw`` is the raw query (``L2(SiLU(q))`` is applied on load) unless ``q_features`` says it
     already holds the query features (short-convolution output). With ``gate=None`` the output
     gate ``sigmoid(gate_hidden @ gate_up_weight.T + gate_up_bias)`` (``vdn_h3/branch.py:754-758``,
     ``gate_hidden`` = the down-projection ``[F*T, D]``) is computed inside the readout kernel.
+    ``frame_range=(start, stop)`` reads out only frames ``start .. stop - 1`` of the ``num_frames``
+    that ``prefix``, ``suffix``, ``alpha`` and ``bounds`` describe (the reference's frame-tiled gather,
+    ``_gather_range``, ``vdn_h3/runtime.py:513-517``): ``q_raw``, ``gate`` / ``gate_hidden`` and the
+    ``[(stop - start)*T, H*D]`` result then hold that range's rows only.
     """
     if bridge not in ("alpha", "none"):
         raise ValueError("bridge must be 'alpha' or 'none'")
@@ -375,6 +379,9 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
     for frame, (lo, hi) in enumerate(bounds):
         if lo > frame or hi < frame or lo > hi:
             raise ValueError(f"bounds[{frame}] does not contain its query frame")
+    start, stop = (0, num_frames) if frame_range is None else (int(frame_range[0]), int(frame_range[1]))
+    if not 0 <= start < stop <= num_frames:
+        raise ValueError(f"frame_range ({start}, {stop}) is not a non-empty range of the {num_frames} frames")
     frames_state = (num_frames, heads, dim, dim)
     for name, t in (("prefix", prefix), ("suffix", suffix)):
         if t.dtype != torch.float32 or tuple(t.shape) != frames_state:
@@ -383,8 +390,9 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
         raise ValueError(f"alpha must be [{num_frames}, {heads}, {dim}]")
     if text_state is not None and tuple(text_state.shape) != (heads, dim, dim):
         raise ValueError(f"text_state must be [{heads}, {dim}, {dim}]")
-    if rows != num_frames * tokens_per_frame:
-        raise ValueError(f"q holds {rows} rows, not num_frames * tokens_per_frame = {num_frames * tokens_per_frame}")
+    if rows != (stop - start) * tokens_per_frame:
+        raise ValueError(f"q holds {rows} rows, not the range's frames * tokens_per_frame = "
+                         f"{(stop - start) * tokens_per_frame}")
     fused = gate is None
     if fused:
         if gate_hidden is None or gate_up_weight is None:
@@ -430,7 +438,8 @@ def readout_epilogue(q_raw, prefix, suffix, alpha, bounds, norm_weight, gate, *,
     common = (_lib.ptr(q_raw), q_raw.stride(0), q_raw.stride(1), int(bool(q_features)), _lib.ptr(prefix),
               _lib.ptr(suffix), _lib.ptr(logsum), _lib.ptr(text), _lib.ptr(bounds_t),
               int(bridge == "alpha"), _lib.ptr(norm_w))
-    tail = (_lib.ptr(out), out.stride(0), num_frames, tokens_per_frame, heads, dim, _lib.stream_handle(device))
+    tail = (_lib.ptr(out), out.stride(0), num_frames, start, stop - start, tokens_per_frame, heads, dim,
+            _lib.stream_handle(device))
     if fused:
         rc = _lib.lib().vdnh3_readout_fused_gate(*common, _lib.ptr(gate_hidden), gate_hidden.stride(0),
                                                  _lib.ptr(gate_up_weight), _lib.ptr(gate_up_bias), *tail)

@@ -78,7 +78,7 @@ class VDNState:
     def __init__(self, name: str, config: Mapping[str, Any], branches: Sequence[Any], num_heads: int,
                  head_dim: int, *, attention_backend: str = "hip", weight_maps=None, inference: bool = True,
                  projection_precision: str = "bf16", projection_info: Any = None, diagnostics: bool = False,
-                 block_fusion: bool = False, branch_execution: str = "serial", **_runtime):
+                 block_fusion: bool = False, branch_execution: str = "serial", tile_frames: int = 0, **_runtime):
         if attention_backend not in _window.ATTENTION_BACKENDS:
             raise ValueError(f"unsupported attention backend {attention_backend!r}")
         if projection_precision not in _projection.PROJECTION_PRECISIONS:
@@ -105,6 +105,14 @@ class VDNState:
         self.block_fusion = bool(block_fusion)
         self._maps = _block_weight_maps(self.branches, weight_maps)
         self._resident: dict[tuple[int, Any], dict[str, torch.Tensor]] = {}
+        # frame tiling of the branch (vdn_h3/hybrid.py:86, :136-148): handed to every branch that takes it
+        if isinstance(tile_frames, bool) or int(tile_frames) < 0:
+            raise ValueError("tile_frames must be a non-negative integer")
+        self.tile_frames = int(tile_frames)
+        for branch in self.branches:
+            set_runtime = getattr(branch, "set_runtime", None)
+            if set_runtime is not None:
+                set_runtime(tile_frames=self.tile_frames)
 
     # Weights are resident in HBM (a block's branch weights are ~55 MB at hidden 5120; all
     # 50 blocks fit many times over in 288 GB), so prefetch / consume are bookkeeping only.

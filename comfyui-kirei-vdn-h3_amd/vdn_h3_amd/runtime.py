@@ -67,6 +67,15 @@ class OptimizedLinearBranch:
         self.a_fp32 = bool(a_fp32)
         self.short_conv = targets
         self.enable_text_state = bool(enable_text_state)
+        self.tile_frames = 0
+
+    def set_runtime(self, *, tile_frames: int = 0, **_ignored):
+        """Runtime options a ``VDNState`` hands its branches (``vdn_h3/hybrid.py:136-148``): ``tile_frames``
+        > 0 runs ``projected_delta`` in frame tiles of that many frames (the reference picks 5 on GPUs of at
+        most 32 GB, ``vdn_h3/nodes.py:193-202``)."""
+        if isinstance(tile_frames, bool) or int(tile_frames) < 0:
+            raise ValueError("tile_frames must be a non-negative integer")
+        self.tile_frames = int(tile_frames)
 
     def _backend(self, tokens):
         return _b.DELTA_BACKENDS[self.delta_rule](tokens)
@@ -106,9 +115,9 @@ class OptimizedLinearBranch:
                                  num_frames, frame_size, name != "v")
         return feats, True
 
-    def _readout_flat(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, text_x,
-                      text_k_raw, text_v_raw, frame_size=None, out=None, proj_rows=None, text_proj_rows=None):
-        heads, dim = self.num_heads, self.head_dim
+    def _gate_rows(self, weights, xv, text_x, proj_rows, text_proj_rows):
+        """``(beta [rows, heads], gate_hidden [rows, rank], text_beta or None)`` of the video rows."""
+        heads = self.num_heads
         # beta = sigmoid(x W_beta^T) and the output-gate down-projection x W_down^T read the same rows:
         # one GEMM over [W_beta; W_down] with the sigmoid on the first `heads` columns (or rows the
         # caller computed with a wider GEMM over the same x)
@@ -124,7 +133,12 @@ class OptimizedLinearBranch:
             both = _linear.sigmoid_linear_split(rows_view, self._beta_down_weight(weights), heads)
             text_beta = both[:text_x.shape[0], :heads]
             both = both[gap:]
-        beta, gate_hidden = both[:, :heads], both[:, heads:]
+        return both[:, :heads], both[:, heads:], text_beta
+
+    def _readout_flat(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, text_x,
+                      text_k_raw, text_v_raw, frame_size=None, out=None, proj_rows=None, text_proj_rows=None):
+        heads, dim = self.num_heads, self.head_dim
+        beta, gate_hidden, text_beta = self._gate_rows(weights, xv, text_x, proj_rows, text_proj_rows)
         if "k" in self.short_conv and "v" in self.short_conv and frame_size is not None:
             # both convolutions in one launch (their workgroups share the launch's rounds)
             k_in, v_in = _b.conv_features_batch(
@@ -151,6 +165,71 @@ class OptimizedLinearBranch:
                                    tokens_per_frame=tokens_per_frame, out=out, q_features=q_feat,
                                    gate_hidden=gate_hidden, gate_up_weight=weights["output_gate.up.weight"],
                                    gate_up_bias=weights.get("output_gate.up.bias"))
+
+    def _tile_features(self, weights, raws, start, stop, num_frames, tokens_per_frame, frame_size):
+        """``{name: (rows, is_features)}`` for frames ``[start, stop)`` of each raw ``[F*T, H, D]`` tensor in
+        ``raws``: names without a short convolution give their raw rows (the feature map is fused into the
+        consumer); the others run the short convolution over the tile plus a halo of ``kt // 2`` frames on
+        each side, the frames its temporal taps read, so the tile's rows are those of the untiled call
+        (``vdn_h3/runtime.py:421-440``). Tensors with the same halo share one launch."""
+        t = tokens_per_frame
+        out = {n: (raw[start * t:stop * t], False) for n, raw in raws.items() if n not in self.short_conv}
+        conv = [n for n in raws if n in self.short_conv]
+        if not conv:
+            return out
+        if frame_size is None:
+            raise ValueError("short convolution requires frame_size")
+        groups = {}
+        for n in conv:
+            pad = int(weights[f"short_conv.{n}_tm.weight"].shape[-1]) // 2
+            groups.setdefault((max(0, start - pad), min(num_frames, stop + pad)), []).append(n)
+        for (hs, he), names in groups.items():
+            items = [(raws[n][hs * t:he * t], weights[f"short_conv.{n}_sp.weight"],
+                      weights[f"short_conv.{n}_tm.weight"], n != "v", None) for n in names]
+            feats = _b.conv_features_batch(items, he - hs, frame_size)
+            for n, f in zip(names, feats):
+                out[n] = (f[(start - hs) * t:(stop - hs) * t], True)
+        return out
+
+    def _projected_tiled(self, weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds, text_x,
+                         text_k_raw, text_v_raw, frame_size, tile, out, accumulate, proj, proj_rows=None,
+                         text_proj_rows=None):
+        """``to_out_linear`` of the branch readout into ``out`` (``[F*T, hidden]``), in frame tiles of ``tile``
+        frames (``vdn_h3/runtime.py:442-543``): the k / v features and frame statistics one tile at a time,
+        the recurrence over every frame, then the query features, gated readout and projection one tile at a
+        time, so the feature and readout buffers hold one tile. Each frame's statistics and readout and each
+        row's projection depend on that frame or row alone, so the result is the untiled one, bit for bit."""
+        heads, dim, t = self.num_heads, self.head_dim, tokens_per_frame
+        beta, gate_hidden, text_beta = self._gate_rows(weights, xv, text_x, proj_rows, text_proj_rows)
+        a = torch.empty((num_frames, heads, dim, dim), dtype=torch.float32, device=xv.device)
+        b = torch.empty_like(a)
+        for start in range(0, num_frames, tile):
+            stop = min(num_frames, start + tile)
+            rows = slice(start * t, stop * t)
+            feats = self._tile_features(weights, {"k": k_raw, "v": v_raw}, start, stop, num_frames, t, frame_size)
+            (k_in, k_feat), (v_in, v_feat) = feats["k"], feats["v"]
+            ta, tb = _b.frame_statistics_raw(k_in, v_in, beta[rows], stop - start, t, k_features=k_feat,
+                                             v_features=v_feat, a_fp32=self.a_fp32)
+            a[start:stop].copy_(ta)
+            b[start:stop].copy_(tb)
+            del feats, k_in, v_in, ta, tb
+        mean = _b.frame_mean(xv, num_frames, t)
+        alpha = _b.alpha_gate(mean, weights["alpha.down.weight"], weights["alpha.up.weight"],
+                              weights["alpha.dt_bias"], weights["alpha.A_log"], heads, dim)
+        text_state = self._text_state(weights, text_x, text_k_raw, text_v_raw, text_beta)
+        prefix, suffix = _b.run_scans_inference(self._backend(t), alpha, a, b, text_state)
+        del a, b
+        for start in range(0, num_frames, tile):
+            stop = min(num_frames, start + tile)
+            rows = slice(start * t, stop * t)
+            q_in, q_feat = self._tile_features(weights, {"q": q_raw}, start, stop, num_frames, t, frame_size)["q"]
+            flat = _b.readout_epilogue(q_in, prefix, suffix, alpha, bounds, weights["norm.weight"], None,
+                                       text_state=text_state, bridge=self.bridge, num_frames=num_frames,
+                                       tokens_per_frame=t, q_features=q_feat, gate_hidden=gate_hidden[rows],
+                                       gate_up_weight=weights["output_gate.up.weight"],
+                                       gate_up_bias=weights.get("output_gate.up.bias"), frame_range=(start, stop))
+            proj(flat, out=out[rows], accumulate=accumulate)
+            del q_in, flat
 
     def _check(self, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds):
         if torch.is_grad_enabled():
@@ -198,8 +277,13 @@ class OptimizedLinearBranch:
         ``proj_rows`` / ``text_proj_rows`` (optional, ``[rows, heads + rank]`` bf16): ``[beta | x W_down^T]``
         of the rows of ``xv`` / ``text_x``, already computed by the caller (the block computes them in the
         softmax gate's GEMM); without them the branch computes them itself.
+        ``tile_frames`` (default: the branch's runtime option, 0 = untiled) > 0 runs the branch in frame tiles
+        when ``inference`` (``vdn_h3/runtime.py:588-595``), with the same result.
         """
-        del inference, tile_frames
+        tile = self.tile_frames if tile_frames is None else tile_frames
+        if isinstance(tile, bool) or int(tile) < 0:
+            raise ValueError("tile_frames must be a non-negative integer")
+        tile = int(tile) if inference else 0
         self._check(xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds)
         proj = projector or (lambda rows, **kw: _projection.project(rows, weights, **kw))
         hidden = _projection.projection_out_features(weights)
@@ -210,6 +294,20 @@ class OptimizedLinearBranch:
             out = torch.empty((original_rows, hidden), dtype=torch.bfloat16, device=xv.device)
         elif out.shape != (original_rows, hidden):
             raise ValueError(f"out must be [{original_rows}, {hidden}]")
+        if tile > 0:
+            t = tokens_per_frame
+            if skip_ends and num_frames <= 2:
+                return out if accumulate else _b.fill_rows(out)
+            rows = slice(t, (num_frames - 1) * t) if skip_ends else slice(0, original_rows)
+            frames = num_frames - 2 if skip_ends else num_frames
+            inner_bounds = [(lo - 1, hi - 1) for lo, hi in bounds[1:-1]] if skip_ends else list(bounds)
+            if not accumulate and skip_ends:
+                _b.fill_rows(out[:rows.start])
+                _b.fill_rows(out[rows.stop:])
+            self._projected_tiled(weights, xv[rows], q_raw[rows], k_raw[rows], v_raw[rows], frames, t, inner_bounds,
+                                  text_x, text_k_raw, text_v_raw, frame_size, min(tile, frames), out[rows],
+                                  accumulate, proj, None if proj_rows is None else proj_rows[rows], text_proj_rows)
+            return out
         flat, rows = self.branch_rows(weights, xv, q_raw, k_raw, v_raw, num_frames, tokens_per_frame, bounds,
                                       frame_size=frame_size, text_x=text_x, text_k_raw=text_k_raw,
                                       text_v_raw=text_v_raw, skip_ends=skip_ends, proj_rows=proj_rows,

@@ -296,19 +296,24 @@ int vdnh3_alpha_logsum(const float *alpha, int frames, int heads, int head_dim, 
  *         and decay_a = exp(S[hi+1] - S[f]) with S = alpha_logsum)
  *   r = bf16(q~ L_f^T);  out[row][h*D + v] = bf16(RMSNorm(r)[v] * norm_w[v]) * gate[row][h*D + v]
  * alpha_logsum: [frames+1][heads][D] fp32 from vdnh3_alpha_logsum (may be NULL without use_alpha);
- * out and gate: [frames*tokens, heads*D] bf16 with 16-byte aligned rows; prefix, suffix and
+ * out and gate: [frame_count*tokens, heads*D] bf16 with 16-byte aligned rows; prefix, suffix and
  * text_state 16-byte aligned.
+ * Frame range (the reference's frame-tiled gather, vdn_h3/runtime.py:513-517, _gather_range over
+ * [start, stop)): the call reads out frames first_frame .. first_frame + frame_count - 1 of the
+ * `frames` frames that prefix, suffix, alpha_logsum and bounds describe; q, gate and out hold only
+ * that range's rows (row 0 = the first token of frame first_frame). first_frame = 0 and
+ * frame_count = frames read out every frame.
  */
 int vdnh3_readout(const uint16_t *q, int64_t q_row, int64_t q_head, int q_features, const float *prefix,
                   const float *suffix, const float *alpha_logsum, const float *text_state, const int32_t *bounds,
                   int use_alpha, const uint16_t *norm_w, const uint16_t *gate, int64_t gate_row,
-                  uint16_t *out, int64_t out_row, int frames, int tokens, int heads, int head_dim,
-                  void *stream);
+                  uint16_t *out, int64_t out_row, int frames, int first_frame, int frame_count, int tokens,
+                  int heads, int head_dim, void *stream);
 
 /*
  * vdnh3_readout with the output gate computed inside (vdn_h3/branch.py:754-758): for head h,
  *   gate[row][h*D + v] = bf16(sigmoid(bf16(sum_j gate_hidden[row][j] * gate_up_w[h*D + v][j] + gate_up_b[h*D + v])))
- * with gate_hidden = x W_down^T ([frames*tokens, D] bf16, row stride hidden_row, 16-byte aligned),
+ * with gate_hidden = x W_down^T ([frame_count*tokens, D] bf16, row stride hidden_row, 16-byte aligned),
  * gate_up_w [heads*D, D] bf16 and gate_up_b [heads*D] bf16 or NULL. The same values as
  * vdnh3_gemm's sigmoid epilogue followed by vdnh3_readout, without the [rows, heads*D] gate in
  * memory. out: 8-byte aligned rows.
@@ -317,8 +322,8 @@ int vdnh3_readout_fused_gate(const uint16_t *q, int64_t q_row, int64_t q_head, i
                              const float *suffix, const float *alpha_logsum, const float *text_state,
                              const int32_t *bounds, int use_alpha, const uint16_t *norm_w,
                              const uint16_t *gate_hidden, int64_t hidden_row, const uint16_t *gate_up_w,
-                             const uint16_t *gate_up_b, uint16_t *out, int64_t out_row, int frames, int tokens,
-                             int heads, int head_dim, void *stream);
+                             const uint16_t *gate_up_b, uint16_t *out, int64_t out_row, int frames,
+                             int first_frame, int frame_count, int tokens, int heads, int head_dim, void *stream);
 
 /* Per-frame mean over tokens in fp32: out[f][c] = mean_t x[(f*tokens + t)*x_row + c]
  * (vdn_h3/branch.py:743-745). */

@@ -136,3 +136,37 @@ def test_noalloc_fp8_quantisation_rejects_oversize_tensors_on_the_host(built_lib
     assert b"exceed" in built_lib.vdnh3_last_error()
     assert built_lib.vdnh3_quant_tensor_f8_noalloc(None, 8, p, p, None) == 1
     assert built_lib.vdnh3_quant_tensor_f8_noalloc(p, 12, p, p, None) == 1
+
+
+def test_tile_frames_option_checks():
+    from vdn_h3_amd.hybrid import VDNState
+    from vdn_h3_amd.runtime import OptimizedLinearBranch
+
+    br = OptimizedLinearBranch({}, 2, 64)
+    assert br.tile_frames == 0
+    br.set_runtime(tile_frames=5, kernel_backend="ignored")
+    assert br.tile_frames == 5
+    for bad in (-1, True):
+        with pytest.raises(ValueError, match="tile_frames"):
+            br.set_runtime(tile_frames=bad)
+    with pytest.raises(ValueError, match="tile_frames"):
+        VDNState("t", {}, [br], 2, 64, tile_frames=-2)
+    VDNState("t", {}, [br], 2, 64, tile_frames=3)
+    assert br.tile_frames == 3
+
+
+def test_readout_frame_range_checks():
+    from vdn_h3_amd import branch
+
+    frames, tokens, heads, dim = 4, 8, 1, 64
+    q = torch.zeros(2 * tokens, heads, dim, dtype=torch.bfloat16)
+    banks = torch.zeros(frames, heads, dim, dim)
+    alpha = torch.ones(frames, heads, dim)
+    kw = dict(num_frames=frames, tokens_per_frame=tokens, gate_hidden=torch.zeros(2 * tokens, dim),
+              gate_up_weight=torch.zeros(heads * dim, dim))
+    bounds = [(0, 1), (0, 2), (1, 3), (2, 3)]
+    for bad in ((3, 5), (2, 2), (-1, 1)):
+        with pytest.raises(ValueError, match="frame_range"):
+            branch.readout_epilogue(q, banks, banks, alpha, bounds, torch.ones(dim), None, frame_range=bad, **kw)
+    with pytest.raises(ValueError, match="range's frames"):
+        branch.readout_epilogue(q, banks, banks, alpha, bounds, torch.ones(dim), None, frame_range=(0, 3), **kw)
