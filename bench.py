@@ -692,13 +692,22 @@ def _median_seconds(fn, reps=3):
     return sorted(times)[len(times) // 2], times
 
 
+def _sample_rows(seq, n_rows, block=256):
+    """About ``n_rows`` query rows as evenly spaced blocks of ``block`` consecutive rows: rows of one block
+    share a key set, so the oracle evaluates them as one product, as it does for the whole sequence (single
+    scattered rows would time small products the full run never makes)."""
+    blocks = max(1, n_rows // block)
+    starts = [round(i * (seq - block) / max(1, blocks - 1)) for i in range(blocks)]
+    return [r for s in starts for r in range(s, min(seq, s + block))]
+
+
 def _cpu_window_sample(torch, w, lay, qkv_host, n_rows):
-    """``(FLOP, median s, times)`` of the window-attention oracle on ``n_rows`` evenly spaced query rows."""
+    """``(FLOP, median s, times)`` of the window-attention oracle on ``n_rows`` query rows (``_sample_rows``)."""
     from oracle import window_oracle as wo
     from vdn_h3_amd import synth
 
     hq, hk, hv = synth.split_qkv(qkv_host, w.heads, w.head_dim)
-    rows = torch.linspace(0, lay.seq_len - 1, n_rows).long().tolist()
+    rows = _sample_rows(lay.seq_len, n_rows)
     keys = sum(b - a for r in rows for a, b in wo.row_key_intervals(
         r, lay.seq_len, lay.video_start, lay.video_end, lay.num_frames, lay.tokens_per_frame, lay.bounds,
         lay.anchor_frames))
@@ -715,15 +724,16 @@ def cpu_baseline_window(torch, qkv, w, lay, n_rows):
     return {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port", "seconds_median": round(med, 3), "seconds_runs": [round(t, 3) for t in times],
             "cpu": model, "physical_cores": physical,
-            "sample": f"{n_rows} evenly spaced query rows x {w.heads} heads of the 40,688-row layout, fp32 oracle "
-                      "(oracle/window_oracle.py); 1 warm-up, median of 3"}
+            "sample": f"{n_rows} query rows (evenly spaced blocks of 256) x {w.heads} heads of the 40,688-row "
+                      "layout, fp32 oracle (oracle/window_oracle.py); 1 warm-up, median of 3"}
 
 
 def cpu_baseline_block(torch, device, lay, work, conv, n_rows):
     """CPU throughput of one hybrid block from bounded samples of its three parts, each the median of 3
     runs after a warm-up of the fp32 oracle on the host cores:
 
-    * window attention: ``n_rows`` evenly spaced query rows x 40 heads of the 40,688-row layout;
+    * window attention: ``n_rows`` query rows (evenly spaced blocks of 256 rows) x 40 heads of the 40,688-row
+      layout;
     * projections: ``oracle.branch_oracle.linear_bf16`` (fp32 GEMM, bf16 out) on 512 rows x K 5120 x N 15,360;
     * VDN branch: ``oracle.branch_oracle.projected_delta`` on 9 frames (7 inner) of 1296 tokens, 40 x 128,
       hidden 5120, text state and k/v short convolutions, scaled to the block's 29 inner frames.
@@ -768,7 +778,7 @@ def cpu_baseline_block(torch, device, lay, work, conv, n_rows):
             "parts": {
                 "window_attention": {"TFLOP/s": round(win_flop / win_s / 1e12, 5), "seconds_median": round(win_s, 3),
                                      "seconds_runs": [round(t, 3) for t in win_times],
-                                     "sample": f"{n_rows} query rows x {heads} heads"},
+                                     "sample": f"{n_rows} query rows (blocks of 256) x {heads} heads"},
                 "projections": {"TFLOP/s": round(proj_flop / proj_s / 1e12, 5), "seconds_median": round(proj_s, 3),
                                 "seconds_runs": [round(t, 3) for t in proj_times],
                                 "sample": "512 x 5120 x 15360 fp32 GEMM, bf16 out"},
