@@ -450,7 +450,7 @@ def bench_gdn(args, torch, device):
     import torch.nn.functional as F
 
     from vdn_h3_amd import _lib
-    from vdn_h3_amd.gdn import gdn_flops
+    from vdn_h3_amd.gdn import gdn_flops, gdn_forward_into
 
     tokens, heads, dim = 40688, 40, 128
     g = torch.Generator(device=device).manual_seed(50)
@@ -465,13 +465,9 @@ def bench_gdn(args, torch, device):
     ws_bytes = lib.vdnh3_gdn_workspace_bytes(tokens, heads, dim)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device)
-    sh = _lib.stream_handle(device)
 
-    def step():
-        _lib.check(lib.vdnh3_gdn_chunk_fwd(
-            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(v), v.stride(0),
-            v.stride(1), _lib.ptr(beta), beta.stride(0), _lib.ptr(lg), lg.stride(0), None, None, _lib.ptr(out),
-            out.stride(0), out.stride(1), tokens, heads, dim, _lib.ptr(ws), ws_bytes, sh), "gdn")
+    def step():  # the segments' preps on a second stream beside the scans (vdn_h3_amd.gdn)
+        gdn_forward_into(q, k, v, beta, lg, out, ws)
 
     ms = _time_steps(torch, stream, args.steps, args.warmup, step)
     flops = gdn_flops(tokens, heads, dim)

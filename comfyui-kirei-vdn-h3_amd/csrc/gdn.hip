@@ -12,16 +12,14 @@
 // inverse T = (I + A)^-1 in fp32 by 16 x 16 blocks, then W = T diag(b e^G) K and U~ = T diag(b) V
 // on bf16 MFMA (T's scaled columns rounded to bf16); writes W, U~, Q^ = e^G Q,
 // K^ = e^{G_C - G} K, P = Q K^T o D (bf16, each in the fragment order of the scan wavefront
-// that reads it) and G (fp32) for each chunk, as 16-byte stores. The prep of the next segment
-// runs beside the scan, whose four workgroups per head share each chunk's W, Q^, K^ and P
+// that reads it) and G (fp32) for each chunk, as 16-byte stores. When the host pipelines the
+// segments of a call (two streams), the prep of the next segment runs beside the scan, whose four workgroups per head share each chunk's W, Q^, K^ and P
 // through L2; the prep's q / k / v reads and its workspace writes carry the non-temporal hint,
 // so that they stream past L2 instead of displacing those lines (3% faster).
 // gdn_scan_kernel (grid heads x dv/32, sequential over chunks): one workgroup carries a 32-row
 // slice of the state in MFMA accumulators (fp32); per chunk U = U~ - W S^T, O = Q^ S^T + P U and
 // S = e^{G_C} S + U^T K^, each wavefront loading its operands into registers two chunks ahead.
 #include "common.h"
-
-#include <mutex>
 
 namespace vdnh3 {
 namespace {
@@ -486,53 +484,50 @@ int64_t gdn_segment_chunks(int64_t chunks, int heads, int head_dim) {
 // Workspace buffers: two when the sequence runs in more than one segment.
 int gdn_buffers(int64_t chunks, int64_t seg) { return seg < chunks ? 2 : 1; }
 
-// Per-device side stream (default priority) and events of the prep / scan pipeline, made on first
-// use with that device current. Every call re-records the same events, so calls on one device
-// hold the pipe's lock while they enqueue.
-struct GdnPipe {
-  hipStream_t side = nullptr;
-  hipEvent_t fork = nullptr, prep_done[2] = {}, scan_done[2] = {};
-  std::mutex lock;
+// The segment geometry of a call and the places of its workspace parts: buffer b holds
+// [W | U~ | Q^ | K^ | P | G] of the segments i with i % 2 == b; the fp32 state carried between
+// segments ([heads][D][D], 16-byte aligned) follows the buffers.
+struct GdnLayout {
+  int chunks = 0, seg = 0, segments = 0;
+  struct Buf {
+    uint16_t *W, *U, *Q, *K, *P;
+    float *G;
+  } buf[2] = {};
+  float *carry = nullptr;
 };
-int gdn_pipe(hipStream_t stream, GdnPipe **out) {
-  constexpr int kMaxDevices = 64;
-  static std::mutex table_lock;
-  static GdnPipe pipes[kMaxDevices];
-  int current = 0;
-  hipError_t err = hipGetDevice(&current);
-  if (err != hipSuccess) return set_error(VDNH3_ERR_RUNTIME, "no current HIP device: %s", hipGetErrorString(err));
-  hipDevice_t dev = current;
-  if (stream != nullptr && (err = hipStreamGetDevice(stream, &dev)) != hipSuccess)
-    return set_error(VDNH3_ERR_RUNTIME, "hipStreamGetDevice failed: %s", hipGetErrorString(err));
-  VDNH3_HOST_CHECK(dev >= 0 && dev < kMaxDevices, VDNH3_ERR_RUNTIME, "device %d is beyond the %d this library tracks",
-                   (int)dev, kMaxDevices);
-  std::lock_guard<std::mutex> guard(table_lock);
-  GdnPipe &p = pipes[dev];
-  if (p.side == nullptr) {
-    if (dev != current && (err = hipSetDevice(dev)) != hipSuccess)
-      return set_error(VDNH3_ERR_RUNTIME, "hipSetDevice(%d) failed: %s", (int)dev, hipGetErrorString(err));
-    hipStream_t side = nullptr;
-    hipEvent_t ev[5] = {};
-    err = hipStreamCreateWithFlags(&side, hipStreamNonBlocking);
-    for (int i = 0; i < 5 && err == hipSuccess; ++i) err = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
-    if (dev != current) (void)hipSetDevice(current);
-    if (err != hipSuccess) {
-      for (hipEvent_t e : ev)
-        if (e) (void)hipEventDestroy(e);
-      if (side) (void)hipStreamDestroy(side);
-      return set_error(VDNH3_ERR_RUNTIME, "gdn: side stream / events on device %d: %s", (int)dev,
-                       hipGetErrorString(err));
-    }
-    p.fork = ev[0];
-    p.prep_done[0] = ev[1];
-    p.prep_done[1] = ev[2];
-    p.scan_done[0] = ev[3];
-    p.scan_done[1] = ev[4];
-    p.side = side;
-  }
-  *out = &p;
-  return VDNH3_OK;
+void gdn_geometry(int tokens, int heads, int *chunks, int *seg, int *segments) {
+  *chunks = (tokens + kGdnC - 1) / kGdnC;
+  *seg = (int)gdn_segment_chunks(*chunks, heads, 128);
+  *segments = (*chunks + *seg - 1) / *seg;
 }
+GdnLayout gdn_layout(int tokens, int heads, void *workspace) {
+  constexpr int D = 128;
+  GdnLayout L;
+  gdn_geometry(tokens, heads, &L.chunks, &L.seg, &L.segments);
+  const int64_t n = (int64_t)L.seg * heads;
+  const int64_t buf_bytes = n * gdn_chunk_head_bytes(D);
+  for (int b = 0; b < gdn_buffers(L.chunks, L.seg); ++b) {
+    uint16_t *base = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + b * buf_bytes);
+    L.buf[b].W = base;
+    L.buf[b].U = L.buf[b].W + n * GdnWs<D>::W;
+    L.buf[b].Q = L.buf[b].U + n * GdnWs<D>::U;
+    L.buf[b].K = L.buf[b].Q + n * GdnWs<D>::Q;
+    L.buf[b].P = L.buf[b].K + n * GdnWs<D>::K;
+    L.buf[b].G = reinterpret_cast<float *>(L.buf[b].P + n * GdnWs<D>::P);
+  }
+  L.carry = reinterpret_cast<float *>(static_cast<char *>(workspace) + gdn_buffers(L.chunks, L.seg) * buf_bytes);
+  return L;
+}
+// Segment i covers chunks i seg ..: its tokens form an independent sequence whose initial state is the
+// state segment i - 1 ended with (the chunk form restarts exactly at a chunk boundary).
+void gdn_span(const GdnLayout &L, int tokens, int i, int64_t *t0, int *nc, int *nt) {
+  const int c0 = i * L.seg;
+  *nc = L.seg < L.chunks - c0 ? L.seg : L.chunks - c0;
+  *t0 = (int64_t)c0 * kGdnC;
+  *nt = (int)(tokens - *t0 < (int64_t)*nc * kGdnC ? tokens - *t0 : (int64_t)*nc * kGdnC);
+}
+
+int gdn_check_common(int tokens, int heads, int head_dim, const void *workspace, size_t workspace_bytes);
 }  // namespace
 }  // namespace vdnh3
 
@@ -545,112 +540,98 @@ extern "C" size_t vdnh3_gdn_workspace_bytes(int tokens, int heads, int head_dim)
                   (int64_t)heads * head_dim * head_dim * 4);
 }
 
+extern "C" int vdnh3_gdn_segments(int tokens, int heads, int head_dim) {
+  if (tokens <= 0 || heads <= 0 || head_dim != 128) return 0;
+  int chunks, seg, segments;
+  vdnh3::gdn_geometry(tokens, heads, &chunks, &seg, &segments);
+  return segments;
+}
+
+namespace vdnh3 {
+namespace {
+int gdn_check_common(int tokens, int heads, int head_dim, const void *workspace, size_t workspace_bytes) {
+  VDNH3_HOST_CHECK(head_dim == 128, VDNH3_ERR_INVALID, "gdn: head_dim must be 128, got %d", head_dim);
+  VDNH3_HOST_CHECK(tokens > 0 && heads > 0, VDNH3_ERR_INVALID, "gdn: tokens and heads must be positive");
+  VDNH3_HOST_CHECK(workspace != nullptr && reinterpret_cast<uintptr_t>(workspace) % 16 == 0, VDNH3_ERR_INVALID,
+                   "gdn: workspace must be non-null and 16-byte aligned");
+  VDNH3_HOST_CHECK(workspace_bytes >= vdnh3_gdn_workspace_bytes(tokens, heads, head_dim), VDNH3_ERR_INVALID,
+                   "gdn: workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+                   vdnh3_gdn_workspace_bytes(tokens, heads, head_dim));
+  return VDNH3_OK;
+}
+}  // namespace
+}  // namespace vdnh3
+
+extern "C" int vdnh3_gdn_prep(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
+                              int64_t k_head, const uint16_t *v, int64_t v_row, int64_t v_head, const float *beta,
+                              int64_t beta_row, const float *log_decay, int64_t decay_row, int tokens, int heads,
+                              int head_dim, int segment, void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace vdnh3;
+  int rc = gdn_check_common(tokens, heads, head_dim, workspace, workspace_bytes);
+  if (rc) return rc;
+  VDNH3_HOST_CHECK(q && k && v && beta && log_decay, VDNH3_ERR_INVALID, "gdn: null operand");
+  VDNH3_HOST_CHECK(q_row % 8 == 0 && q_head % 8 == 0 && k_row % 8 == 0 && k_head % 8 == 0 && v_row % 8 == 0 &&
+                       v_head % 8 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0,
+                   VDNH3_ERR_INVALID, "gdn: q/k/v must be 16-byte aligned with strides multiple of 8");
+  constexpr int D = 128;
+  const GdnLayout L = gdn_layout(tokens, heads, workspace);
+  VDNH3_HOST_CHECK(segment >= 0 && segment < L.segments, VDNH3_ERR_INVALID, "gdn: segment %d of %d", segment,
+                   L.segments);
+  int64_t t0;
+  int nc, nt;
+  gdn_span(L, tokens, segment, &t0, &nc, &nt);
+  const GdnLayout::Buf &b = L.buf[segment & 1];
+  hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(heads, nc), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     q + t0 * q_row, q_row, q_head, k + t0 * k_row, k_row, k_head, v + t0 * v_row, v_row, v_head,
+                     beta + t0 * beta_row, beta_row, log_decay + t0 * decay_row, decay_row, nt, heads, b.W, b.U,
+                     b.Q, b.K, b.P, b.G);
+  return check_launch("gdn_prep");
+}
+
+extern "C" int vdnh3_gdn_scan(const float *initial_state, float *final_state, uint16_t *out, int64_t o_row,
+                              int64_t o_head, int tokens, int heads, int head_dim, int segment, void *workspace,
+                              size_t workspace_bytes, void *stream) {
+  using namespace vdnh3;
+  int rc = gdn_check_common(tokens, heads, head_dim, workspace, workspace_bytes);
+  if (rc) return rc;
+  VDNH3_HOST_CHECK(out != nullptr && o_row % 8 == 0 && o_head % 8 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+                   VDNH3_ERR_INVALID, "gdn: out must be 16-byte aligned with strides multiple of 8");
+  constexpr int D = 128;
+  const GdnLayout L = gdn_layout(tokens, heads, workspace);
+  VDNH3_HOST_CHECK(segment >= 0 && segment < L.segments, VDNH3_ERR_INVALID, "gdn: segment %d of %d", segment,
+                   L.segments);
+  int64_t t0;
+  int nc, nt;
+  gdn_span(L, tokens, segment, &t0, &nc, &nt);
+  const GdnLayout::Buf &b = L.buf[segment & 1];
+  const auto pieces = [](const uint16_t *x) { return reinterpret_cast<const u32x4_t *>(x); };
+  // each scan workgroup reads its state slice before it writes the same slice, so the carry between
+  // segments is updated in place
+  hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(heads, D / 32), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     pieces(b.W), pieces(b.U), pieces(b.Q), pieces(b.K), pieces(b.P), b.G, nc, nt, heads,
+                     segment == 0 ? initial_state : L.carry, segment == L.segments - 1 ? final_state : L.carry,
+                     out + t0 * o_row, o_row, o_head);
+  return check_launch("gdn_scan");
+}
+
 extern "C" int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k,
                                    int64_t k_row, int64_t k_head, const uint16_t *v, int64_t v_row, int64_t v_head,
                                    const float *beta, int64_t beta_row, const float *log_decay, int64_t decay_row,
                                    const float *initial_state, float *final_state, uint16_t *out, int64_t o_row,
                                    int64_t o_head, int tokens, int heads, int head_dim, void *workspace,
                                    size_t workspace_bytes, void *stream) {
-  using namespace vdnh3;
-  VDNH3_HOST_CHECK(head_dim == 128, VDNH3_ERR_INVALID, "gdn: head_dim must be 128, got %d", head_dim);
-  VDNH3_HOST_CHECK(tokens > 0 && heads > 0, VDNH3_ERR_INVALID, "gdn: tokens and heads must be positive");
-  VDNH3_HOST_CHECK(q && k && v && beta && log_decay && out && workspace, VDNH3_ERR_INVALID, "gdn: null operand");
-  VDNH3_HOST_CHECK(workspace_bytes >= vdnh3_gdn_workspace_bytes(tokens, heads, head_dim), VDNH3_ERR_INVALID,
-                   "gdn: workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
-                   vdnh3_gdn_workspace_bytes(tokens, heads, head_dim));
-  VDNH3_HOST_CHECK(q_row % 8 == 0 && q_head % 8 == 0 && k_row % 8 == 0 && k_head % 8 == 0 && v_row % 8 == 0 &&
-                       v_head % 8 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
-                       reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
-                       reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
-                   VDNH3_ERR_INVALID, "gdn: q/k/v and workspace must be 16-byte aligned with strides multiple of 8");
-  VDNH3_HOST_CHECK(o_row % 8 == 0 && o_head % 8 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
-                   VDNH3_ERR_INVALID, "gdn: out must be 16-byte aligned with strides multiple of 8");
-  constexpr int D = 128;
-  const int chunks = (tokens + kGdnC - 1) / kGdnC;
-  const int seg = (int)gdn_segment_chunks(chunks, heads, D);
-  const int segments = (chunks + seg - 1) / seg;
-  const int64_t n = (int64_t)seg * heads;
-  // buffer b: [W | U~ | Q^ | K^ | P | G] of one segment
-  struct Buf {
-    uint16_t *W, *U, *Q, *K, *P;
-    float *G;
-  } buf[2];
-  const int64_t buf_bytes = n * gdn_chunk_head_bytes(D);
-  for (int b = 0; b < gdn_buffers(chunks, seg); ++b) {
-    uint16_t *base = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + b * buf_bytes);
-    buf[b].W = base;
-    buf[b].U = buf[b].W + n * GdnWs<D>::W;
-    buf[b].Q = buf[b].U + n * GdnWs<D>::U;
-    buf[b].K = buf[b].Q + n * GdnWs<D>::Q;
-    buf[b].P = buf[b].K + n * GdnWs<D>::K;
-    buf[b].G = reinterpret_cast<float *>(buf[b].P + n * GdnWs<D>::P);
-  }
-  // [heads][D][D] fp32 state between segments (16-byte aligned)
-  float *carry = reinterpret_cast<float *>(static_cast<char *>(workspace) + gdn_buffers(chunks, seg) * buf_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  // Segment i covers chunks i seg ..: its tokens form an independent sequence whose initial state is
-  // the state segment i - 1 ended with (the chunk form restarts exactly at a chunk boundary). Each scan
-  // workgroup reads its state slice before it writes the same slice, so the carry is updated in place.
-  auto span = [&](int i, int64_t *t0, int *nc, int *nt) {
-    const int c0 = i * seg;
-    *nc = seg < chunks - c0 ? seg : chunks - c0;
-    *t0 = (int64_t)c0 * kGdnC;
-    *nt = (int)(tokens - *t0 < (int64_t)*nc * kGdnC ? tokens - *t0 : (int64_t)*nc * kGdnC);
-  };
-  auto prep = [&](int i, hipStream_t st) -> int {
-    int64_t t0;
-    int nc, nt;
-    span(i, &t0, &nc, &nt);
-    const Buf &b = buf[i & 1];
-    hipLaunchKernelGGL(gdn_prep_kernel<D>, dim3(heads, nc), dim3(256), 0, st, q + t0 * q_row, q_row, q_head,
-                       k + t0 * k_row, k_row, k_head, v + t0 * v_row, v_row, v_head, beta + t0 * beta_row, beta_row,
-                       log_decay + t0 * decay_row, decay_row, nt, heads, b.W, b.U, b.Q, b.K, b.P, b.G);
-    return check_launch("gdn_prep");
-  };
-  auto scan = [&](int i, hipStream_t st) -> int {
-    int64_t t0;
-    int nc, nt;
-    span(i, &t0, &nc, &nt);
-    const Buf &b = buf[i & 1];
-    const auto pieces = [](const uint16_t *x) { return reinterpret_cast<const u32x4_t *>(x); };
-    hipLaunchKernelGGL(gdn_scan_kernel<D>, dim3(heads, D / 32), dim3(256), 0, st, pieces(b.W), pieces(b.U),
-                       pieces(b.Q), pieces(b.K), pieces(b.P), b.G, nc, nt, heads,
-                       i == 0 ? initial_state : carry, i == segments - 1 ? final_state : carry, out + t0 * o_row,
-                       o_row, o_head);
-    return check_launch("gdn_scan");
-  };
-  int rc = prep(0, s);
+  int rc = vdnh3::gdn_check_common(tokens, heads, head_dim, workspace, workspace_bytes);
   if (rc) return rc;
-  if (segments == 1) return scan(0, s);
-  // Two or more segments: the prep of segment i + 1 runs on the side stream while segment i scans
-  // on the caller's stream (a scan leaves most of each CU free). Buffer i % 2 holds segment i: the
-  // side stream waits for the scan that last read a buffer before its prep overwrites it, and the
-  // caller's stream waits for a segment's prep before scanning it. The last scan waits for the last
-  // prep, so every side-stream operation is joined back into the caller's stream.
-  GdnPipe *pp = nullptr;
-  if ((rc = gdn_pipe(s, &pp))) return rc;
-  std::lock_guard<std::mutex> guard(pp->lock);
-  auto ok = [](hipError_t e, const char *what) -> int {
-    return e == hipSuccess ? VDNH3_OK : set_error(VDNH3_ERR_RUNTIME, "gdn: %s: %s", what, hipGetErrorString(e));
-  };
-  if ((rc = ok(hipEventRecord(pp->fork, s), "fork record"))) return rc;
-  if ((rc = ok(hipStreamWaitEvent(pp->side, pp->fork, 0), "fork wait"))) return rc;
-  // on a failure after the fork, the caller's stream still waits for what the side stream holds
-  // (best effort), so that no side-stream work outlives the call's ordering on `stream`
-  auto fail = [&](int code) {
-    if (hipEventRecord(pp->fork, pp->side) == hipSuccess) (void)hipStreamWaitEvent(s, pp->fork, 0);
-    return code;
-  };
+  VDNH3_HOST_CHECK(out != nullptr, VDNH3_ERR_INVALID, "gdn: null operand");
+  const int segments = vdnh3_gdn_segments(tokens, heads, head_dim);
   for (int i = 0; i < segments; ++i) {
-    const int b = i & 1;
-    if (i + 1 < segments) {
-      if (i >= 1 && (rc = ok(hipStreamWaitEvent(pp->side, pp->scan_done[b ^ 1], 0), "scan wait"))) return fail(rc);
-      if ((rc = prep(i + 1, pp->side))) return fail(rc);
-      if ((rc = ok(hipEventRecord(pp->prep_done[b ^ 1], pp->side), "prep record"))) return fail(rc);
-    }
-    if (i >= 1 && (rc = ok(hipStreamWaitEvent(s, pp->prep_done[b], 0), "prep wait"))) return fail(rc);
-    if ((rc = scan(i, s))) return fail(rc);
-    if ((rc = ok(hipEventRecord(pp->scan_done[b], s), "scan record"))) return fail(rc);
+    if ((rc = vdnh3_gdn_prep(q, q_row, q_head, k, k_row, k_head, v, v_row, v_head, beta, beta_row, log_decay,
+                             decay_row, tokens, heads, head_dim, i, workspace, workspace_bytes, stream)))
+      return rc;
+    if ((rc = vdnh3_gdn_scan(initial_state, final_state, out, o_row, o_head, tokens, heads, head_dim, i, workspace,
+                             workspace_bytes, stream)))
+      return rc;
   }
   return VDNH3_OK;
 }

@@ -86,6 +86,10 @@ SIGNATURES = {
     "vdnh3_gdn_chunk_fwd": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64,
                                      _vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _vp,
                                      _c_size, _vp]),
+    "vdnh3_gdn_segments": (_c_int, [_c_int, _c_int, _c_int]),
+    "vdnh3_gdn_prep": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp,
+                                _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
+    "vdnh3_gdn_scan": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
     "vdnh3_rmsnorm_modulate": (_c_int, [_vp, _c_i64, _vp, _c_float, _vp, _vp, _c_i64, _c_int, _vp, _c_int, _vp,
                                         _c_i64, _c_int, _c_int, _vp]),
     "vdnh3_gated_residual": (_c_int, [_vp, _c_i64, _vp, _c_i64, _c_int, _vp, _c_int, _vp, _c_i64, _vp, _c_i64,

@@ -12,19 +12,114 @@ is the published Gated DeltaNet recurrence in chunk (WY) form, the workload a to
 
 from __future__ import annotations
 
+import ctypes
+import threading
+
 import torch
 
 from . import _lib
 
 
+class _Pipe:
+    """The second stream (default priority) and the events of the pipelined call on one device. Every call
+    re-records the same events (a wait enqueued earlier keeps the state of the record before it), so calls on
+    one device enqueue under ``lock``."""
+
+    def __init__(self, device):
+        self.side = torch.cuda.Stream(device=device)
+        self.prep_done = [torch.cuda.Event(), torch.cuda.Event()]
+        self.scan_done = [torch.cuda.Event(), torch.cuda.Event()]
+        self.lock = threading.Lock()
+
+
+_PIPES: dict = {}
+_PIPES_LOCK = threading.Lock()
+
+
+def _pipe(device: torch.device) -> _Pipe:
+    """The pipe of ``device``, made on first use. While one thread captures a graph that holds a pipelined
+    call, no other thread may make an eager pipelined call on the same device (its work would join that
+    capture through the shared side stream)."""
+    device = torch.device(device)
+    with _PIPES_LOCK:
+        pipe = _PIPES.get(device)
+        if pipe is None:
+            pipe = _PIPES[device] = _Pipe(device)
+    return pipe
+
+
+def side_stream(device: torch.device) -> torch.cuda.Stream:
+    """The second stream of the pipelined call on ``device``."""
+    return _pipe(device).side
+
+
+def gdn_forward_into(q, k, v, beta, g, out, workspace, *, initial_state=None, final_state=None,
+                     pipelined: bool = True) -> None:
+    """Enqueue one chunk-64 Gated DeltaNet call on the current stream: ``out`` ``[T, H, 128]`` bf16 from ``q``,
+    ``k``, ``v`` (bf16 views, 16-byte aligned, strides multiples of 8), fp32 ``beta`` / ``g`` ``[T, H]`` (row
+    stride ``H``) and ``workspace`` (``vdnh3_gdn_workspace_bytes`` bytes); the final state into ``final_state``
+    when given. A sequence of several segments runs with segment ``i + 1``'s prep on ``side_stream`` beside
+    segment ``i``'s scan on the current stream (``pipelined``), each prep after the scan that last read its
+    buffer, each scan after its prep; the current stream waits for every side-stream operation before its
+    last scan, so the call is ordered on the current stream and can be captured in a graph."""
+    tokens, heads, dim = q.shape
+    device = q.device
+    lib = _lib.lib()
+    ws_bytes = workspace.numel() * workspace.element_size()
+    segments = lib.vdnh3_gdn_segments(tokens, heads, dim)
+    if segments <= 0:
+        raise ValueError(f"gdn: no segment plan for tokens={tokens}, heads={heads}, head_dim={dim}")
+    cur = torch.cuda.current_stream(device)
+
+    def prep(i, stream):
+        rc = lib.vdnh3_gdn_prep(_lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
+                                _lib.ptr(v), v.stride(0), v.stride(1), _lib.ptr(beta), beta.stride(0), _lib.ptr(g),
+                                g.stride(0), tokens, heads, dim, i, _lib.ptr(workspace), ws_bytes,
+                                ctypes.c_void_p(stream.cuda_stream))
+        _lib.check(rc, "vdnh3_gdn_prep")
+
+    def scan(i):
+        rc = lib.vdnh3_gdn_scan(_lib.ptr(initial_state), _lib.ptr(final_state), _lib.ptr(out), out.stride(0),
+                                out.stride(1), tokens, heads, dim, i, _lib.ptr(workspace), ws_bytes,
+                                ctypes.c_void_p(cur.cuda_stream))
+        _lib.check(rc, "vdnh3_gdn_scan")
+
+    if segments == 1 or not pipelined:
+        for i in range(segments):
+            prep(i, cur)
+            scan(i)
+        return
+    pipe = _pipe(device)
+    side = pipe.side
+    with pipe.lock:
+        side.wait_stream(cur)  # the inputs and the workspace are ready on the current stream
+        try:
+            prep(0, cur)
+            for i in range(segments):
+                b = i & 1
+                if i + 1 < segments:  # segment i + 1 fills buffer b ^ 1, last read by scan i - 1
+                    if i >= 1:
+                        side.wait_event(pipe.scan_done[b ^ 1])
+                    prep(i + 1, side)
+                    pipe.prep_done[b ^ 1].record(side)
+                if i >= 1:
+                    cur.wait_event(pipe.prep_done[b])
+                scan(i)
+                pipe.scan_done[b].record(cur)
+        except BaseException:
+            cur.wait_stream(side)  # no side-stream work outlives the call's ordering on the current stream
+            raise
+
+
 def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
                            g: torch.Tensor, *, initial_state: torch.Tensor | None = None,
-                           output_final_state: bool = False, chunk_size: int = 64):
+                           output_final_state: bool = False, chunk_size: int = 64, pipelined: bool = True):
     """``(o [T, H, D] bf16, final state [H, D, D] fp32 or None)``.
 
     ``q``, ``k``, ``v``: ``[T, H, 128]`` bf16 (strided views are read in place); ``beta`` and ``g``
     (the log-decay, ``<= 0``): ``[T, H]``, computed in fp32; ``initial_state``: ``[H, D, D]``
     (dv rows, dk columns). Keys are used as given (the recurrence assumes unit-norm keys).
+    ``pipelined``: overlap the segments' preps and scans on two streams (``gdn_forward_into``).
     """
     if chunk_size != 64:
         raise ValueError("the HIP kernel is built for chunk_size 64")
@@ -52,15 +147,8 @@ def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, be
         init = initial_state.float().contiguous()
     final = torch.empty((heads, dim, dim), dtype=torch.float32, device=device) if output_final_state else None
     out = torch.empty((tokens, heads, dim), dtype=torch.bfloat16, device=device)
-    lib = _lib.lib()
-    ws_bytes = lib.vdnh3_gdn_workspace_bytes(tokens, heads, dim)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
-    rc = lib.vdnh3_gdn_chunk_fwd(_lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
-                                 _lib.ptr(v), v.stride(0), v.stride(1), _lib.ptr(beta), beta.stride(0), _lib.ptr(g),
-                                 g.stride(0), _lib.ptr(init), _lib.ptr(final), _lib.ptr(out), out.stride(0),
-                                 out.stride(1), tokens, heads, dim, _lib.ptr(ws), ws_bytes,
-                                 _lib.stream_handle(device))
-    _lib.check(rc, "vdnh3_gdn_chunk_fwd")
+    ws = torch.empty(_lib.lib().vdnh3_gdn_workspace_bytes(tokens, heads, dim), dtype=torch.uint8, device=device)
+    gdn_forward_into(q, k, v, beta, g, out, ws, initial_state=init, final_state=final, pipelined=pipelined)
     return out, final
 
 
@@ -74,4 +162,4 @@ def gdn_flops(tokens: int, heads: int, dim: int = 128, chunk: int = 64) -> float
     return chunks * heads * per
 
 
-__all__ = ["chunk_gated_delta_rule", "gdn_flops"]
+__all__ = ["chunk_gated_delta_rule", "gdn_flops", "gdn_forward_into", "side_stream"]

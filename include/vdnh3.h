@@ -389,16 +389,16 @@ int vdnh3_head_gate(const uint16_t *o, int64_t o_row, int64_t o_head, const uint
  * q, k, v: [tokens, heads, 128] bf16 views (element (t, h, d) at p[t*row + h*head + d]);
  * beta, log_decay: fp32 (element (t, h) at p[t*row + h]); out: bf16 like q; initial_state /
  * final_state: fp32 [heads][128][128] (dv rows, dk columns) or NULL (zero start / not written).
- * workspace: vdnh3_gdn_workspace_bytes(tokens, heads, 128) bytes, 16-byte aligned (two segment
- * buffers of at most ~1 GiB each, one for a sequence under 64 chunks, plus the fp32 state carried
- * between segments). A sequence of 64 chunks or more runs in segments whose prep overlaps the
- * previous segment's scan on a side stream the library owns (one per device, default priority,
- * created on the first such call): the call forks it from `stream` with an event and joins it back
- * before its last kernel, so all of its work is ordered on `stream` and it can be captured in a
- * graph, the call that creates the side stream included. Calls on one device serialise their
- * enqueue on a host lock. While a graph capture that holds such a call is open on one thread, no
- * other thread may make an eager pipelined call on the same device: the side stream stays in that
- * capture until it ends, and the eager call's work would join it.
+ * workspace: vdnh3_gdn_workspace_bytes(tokens, heads, 128) bytes, 16-byte aligned: one or two segment
+ * buffers of at most ~1 GiB each and the fp32 state carried between segments. A call runs in
+ * vdnh3_gdn_segments(tokens, heads, 128) segments (one below 64 chunks, else about 8 of at least 32
+ * chunks); segment i's prep (vdnh3_gdn_prep) fills buffer i % 2 from q, k, v, beta and the log-decay,
+ * and its scan (vdnh3_gdn_scan) reads that buffer and carries the state from segment i - 1 (the
+ * initial_state for i = 0) to segment i + 1 (final_state for the last one) while writing out.
+ * vdnh3_gdn_chunk_fwd runs prep 0, scan 0, prep 1, scan 1, ... on `stream`. A caller may instead
+ * overlap them on two streams (the faster path, vdn_h3_amd.gdn): prep i after scan i - 2 (its buffer's
+ * last reader), scan i after prep i and scan i - 1. The library holds no state: no streams, events
+ * or allocations of its own; all buffers are the caller's.
  * ------------------------------------------------------------------------------ */
 size_t vdnh3_gdn_workspace_bytes(int tokens, int heads, int head_dim);
 int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
@@ -406,6 +406,14 @@ int vdnh3_gdn_chunk_fwd(const uint16_t *q, int64_t q_row, int64_t q_head, const 
                         int64_t beta_row, const float *log_decay, int64_t decay_row, const float *initial_state,
                         float *final_state, uint16_t *out, int64_t o_row, int64_t o_head, int tokens, int heads,
                         int head_dim, void *workspace, size_t workspace_bytes, void *stream);
+int vdnh3_gdn_segments(int tokens, int heads, int head_dim);
+int vdnh3_gdn_prep(const uint16_t *q, int64_t q_row, int64_t q_head, const uint16_t *k, int64_t k_row,
+                   int64_t k_head, const uint16_t *v, int64_t v_row, int64_t v_head, const float *beta,
+                   int64_t beta_row, const float *log_decay, int64_t decay_row, int tokens, int heads, int head_dim,
+                   int segment, void *workspace, size_t workspace_bytes, void *stream);
+int vdnh3_gdn_scan(const float *initial_state, float *final_state, uint16_t *out, int64_t o_row, int64_t o_head,
+                   int tokens, int heads, int head_dim, int segment, void *workspace, size_t workspace_bytes,
+                   void *stream);
 
 /* ------------------------------------------------------------------------------
  * DiT block pointwise passes around attention and the MLP (reference vdn_h3/block_kernels.py)

@@ -91,7 +91,7 @@ def test_gdn_split_at_chunk_boundary_is_bit_identical(device):
 
 
 def test_gdn_pipelined_segments_match_chained_calls(device):
-    """A sequence long enough to run in pipelined segments (the prep of segment i + 1 on the library's
+    """A sequence long enough to run in pipelined segments (the prep of segment i + 1 on the host layer's
     side stream beside the scan of segment i, through two workspace buffers, so segment 2 reuses the
     buffer of segment 0) gives the same bits as the same segments run as separate one-segment calls
     chained through their final states."""
@@ -111,6 +111,40 @@ def test_gdn_pipelined_segments_match_chained_calls(device):
     torch.cuda.synchronize()
     assert torch.equal(torch.cat(parts).cpu(), whole.cpu())
     assert torch.equal(state.cpu(), s_whole.cpu())
+
+
+def test_gdn_serial_entry_points_match_the_pipelined_call(device):
+    """vdnh3_gdn_chunk_fwd (every segment's prep and scan in order on one stream) and the one-stream Python
+    path give the bits of the pipelined call (preps on the side stream)."""
+    from vdn_h3_amd import _lib
+    from vdn_h3_amd.gdn import chunk_gated_delta_rule
+
+    tokens, heads = 64 * 70 - 17, 3
+    print(f"case gdn serial vs pipelined T={tokens} H={heads}", flush=True)
+    q, k, v, beta, lg = (t.to(device) for t in _inputs(tokens, heads, 14, 0.05))
+    s0 = (torch.randn(heads, 128, 128, generator=torch.Generator().manual_seed(10)) * 0.1).to(device)
+    lib = _lib.lib()
+    assert lib.vdnh3_gdn_segments(tokens, heads, 128) == 3
+    piped, s_piped = chunk_gated_delta_rule(q, k, v, beta, lg, initial_state=s0, output_final_state=True)
+    one, s_one = chunk_gated_delta_rule(q, k, v, beta, lg, initial_state=s0, output_final_state=True,
+                                        pipelined=False)
+    out = torch.empty_like(piped)
+    s_out = torch.empty_like(s_piped)
+    ws_bytes = lib.vdnh3_gdn_workspace_bytes(tokens, heads, 128)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    qb, kb, vb = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
+    bf, gf = beta.float().contiguous(), lg.float().contiguous()
+    rc = lib.vdnh3_gdn_chunk_fwd(_lib.ptr(qb), qb.stride(0), qb.stride(1), _lib.ptr(kb), kb.stride(0), kb.stride(1),
+                                 _lib.ptr(vb), vb.stride(0), vb.stride(1), _lib.ptr(bf), bf.stride(0), _lib.ptr(gf),
+                                 gf.stride(0), _lib.ptr(s0), _lib.ptr(s_out), _lib.ptr(out), out.stride(0),
+                                 out.stride(1), tokens, heads, 128, _lib.ptr(ws), ws_bytes, _lib.stream_handle(device))
+    _lib.check(rc, "vdnh3_gdn_chunk_fwd")
+    torch.cuda.synchronize()
+    for got, s_got in ((one, s_one), (out, s_out)):
+        assert torch.equal(got, piped) and torch.equal(s_got, s_piped)
+    with pytest.raises(ValueError, match="segment 3 of 3"):
+        _lib.check(lib.vdnh3_gdn_scan(None, None, _lib.ptr(out), out.stride(0), out.stride(1), tokens, heads, 128,
+                                      3, _lib.ptr(ws), ws_bytes, _lib.stream_handle(device)), "vdnh3_gdn_scan")
 
 
 def test_gdn_pipelined_call_replays_in_a_graph(device):
