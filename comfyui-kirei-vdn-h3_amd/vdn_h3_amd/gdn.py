@@ -116,7 +116,8 @@ def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, be
                            output_final_state: bool = False, chunk_size: int = 64, pipelined: bool = True):
     """``(o [T, H, D] bf16, final state [H, D, D] fp32 or None)``.
 
-    ``q``, ``k``, ``v``: ``[T, H, 128]`` bf16 (strided views are read in place); ``beta`` and ``g``
+    ``q``, ``k``, ``v``: ``[T, H, D]`` bf16, D <= 128 (strided views are read in place; a head dim below 128
+    runs at 128 with zero channels added, which leaves the result exact); ``beta`` and ``g``
     (the log-decay, ``<= 0``): ``[T, H]``, computed in fp32; ``initial_state``: ``[H, D, D]``
     (dv rows, dk columns). Keys are used as given (the recurrence assumes unit-norm keys).
     ``pipelined``: overlap the segments' preps and scans on two streams (``gdn_forward_into``).
@@ -126,11 +127,24 @@ def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, be
     if q.ndim != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError("q, k and v must share shape [tokens, heads, dim]")
     tokens, heads, dim = q.shape
-    if dim != 128:
-        raise ValueError(f"head_dim must be 128, got {dim}")
+    if dim <= 0 or dim > 128:
+        raise ValueError(f"head_dim must be 1 to 128 (128 natively), got {dim}")
     if beta.shape != (tokens, heads) or g.shape != (tokens, heads):
         raise ValueError("beta and g must have shape [tokens, heads]")
     device = _lib.require_device(q, k, v, beta, g, initial_state)
+    if dim < 128:
+        # zero channels are exact: k's zero entries leave the state's added rows and columns zero (S_t keeps
+        # a_t S (I - b k k^T) there and b v k^T adds nothing), so the output's added channels are zero
+        if initial_state is not None and initial_state.shape != (heads, dim, dim):
+            raise ValueError(f"initial_state must have shape [{heads}, {dim}, {dim}]")
+        pad = lambda t: torch.nn.functional.pad(t.to(torch.bfloat16), (0, 128 - dim))  # noqa: E731
+        init = None
+        if initial_state is not None:
+            init = torch.zeros((heads, 128, 128), dtype=torch.float32, device=device)
+            init[:, :dim, :dim] = initial_state
+        o, s = chunk_gated_delta_rule(pad(q), pad(k), pad(v), beta, g, initial_state=init,
+                                      output_final_state=output_final_state, pipelined=pipelined)
+        return o[..., :dim].contiguous(), None if s is None else s[:, :dim, :dim].contiguous()
     ops = []
     for t in (q, k, v):
         t = t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)

@@ -212,6 +212,24 @@ def _check_qkv(query, key, value, name):
         raise TypeError(f"{name} computes in bf16; got {query.dtype}/{key.dtype}/{value.dtype}")
 
 
+KERNEL_HEAD_DIMS = (64, 128)
+
+
+def padded_head_dim(dim: int) -> int:
+    """The kernel head dim a ``dim``-channel head runs at: ``dim`` itself for 64 and 128, else the next of the
+    two (zero channels added); above 128 there is none."""
+    if dim <= 0 or dim > 128:
+        raise ValueError(f"window attention supports head dims 1 to 128 (64 and 128 natively), got {dim}")
+    return 64 if dim <= 64 else 128
+
+
+def zero_pad_channels(t: torch.Tensor, width: int) -> torch.Tensor:
+    """``[S, H, D]`` -> ``[S, H, width]`` bf16, the added channels zero."""
+    out = torch.zeros((t.shape[0], t.shape[1], width), dtype=torch.bfloat16, device=t.device)
+    out[..., :t.shape[2]] = t
+    return out
+
+
 def window_softmax_hip(query, key, value, video_start, video_end, num_frames, tokens_per_frame, bounds, scale,
                        anchor_frames="none", cache: WindowAttentionCache | None = None, *, gate=None,
                        out: torch.Tensor | None = None, plan: WindowPlan | None = None, diagnostics=None):
@@ -221,10 +239,25 @@ def window_softmax_hip(query, key, value, video_start, video_end, num_frames, to
     epilogue: the result is then ``bf16(bf16(O) * gate)``. Inputs are not modified.
     ``diagnostics`` (a ``DiagnosticsRecorder``) times the V^T pre-pass and the attention kernel
     as the stages ``attention.softmax.vt_prepass`` / ``attention.softmax.kernel``.
+    Head dims other than 64 and 128 (up to 128; the reference's op is shape-generic,
+    ``vdn_h3/window.py:277-313``) run at the next kernel head dim with zero channels added to q, k and v:
+    a zero channel adds nothing to a score and yields a zero output channel, and ``scale`` is the caller's.
     """
     _check_qkv(query, key, value, "window_softmax_hip")
     device = _lib.require_device(query, key, value, gate, out)
     seq, heads, dim = query.shape
+    if dim not in KERNEL_HEAD_DIMS:
+        width = padded_head_dim(dim)
+        if out is not None and (out.shape != (seq, heads, dim) or out.dtype != torch.bfloat16):
+            raise ValueError("out must be a bf16 [S, H, D] tensor")
+        res = window_softmax_hip(zero_pad_channels(query, width), zero_pad_channels(key, width),
+                                 zero_pad_channels(value, width), video_start, video_end, num_frames,
+                                 tokens_per_frame, bounds, scale, anchor_frames, cache, gate=gate, plan=plan,
+                                 diagnostics=diagnostics)
+        if out is None:
+            return res[..., :dim].contiguous()
+        out.copy_(res[..., :dim])
+        return out
     geometry = (seq, video_start, video_end, num_frames, tokens_per_frame, bounds, anchor_frames)
     plan, gate, g_row, out = _attention_operands(query.shape, device, plan, cache, geometry, gate, out)
     q, k, v = _kernel_operand(query), _kernel_operand(key), _kernel_operand(value)

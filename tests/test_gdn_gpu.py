@@ -242,3 +242,31 @@ def test_gdn_full_shape_sampled_heads(device):
     want, _ = go.chunked(q[:, sel].cpu(), k[:, sel].cpu(), v[:, sel].cpu(), beta[:, sel].cpu(), lg[:, sel].cpu())
     # 636 chunk steps, each through a bf16 S^T: the largest row error seen is 6.2 row-max ulps
     _check(out[:, sel], want, "gdn full shape heads 0, 39", row_ulps=8.0)
+
+
+@pytest.mark.parametrize("dim", [48, 96])
+def test_gdn_head_dims_below_128(device, dim):
+    """Head dims below 128 run at 128 with zero channels added (exact: the state's added rows and columns stay
+    zero), against the float64 recurrence at the true head dim, with an initial and a final state."""
+    from vdn_h3_amd.gdn import chunk_gated_delta_rule
+
+    tokens, heads = 300, 2
+    print(f"case gdn head_dim={dim}", flush=True)
+    g = torch.Generator().manual_seed(dim)
+    q = torch.randn(tokens, heads, dim, generator=g).to(torch.bfloat16)
+    k = F.normalize(torch.randn(tokens, heads, dim, generator=g), dim=-1).to(torch.bfloat16)
+    v = torch.randn(tokens, heads, dim, generator=g).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(tokens, heads, generator=g))
+    lg = -F.softplus(torch.randn(tokens, heads, generator=g)) * 0.05
+    s0 = torch.randn(heads, dim, dim, generator=g) * 0.1
+    want, s_want = go.recurrence(q, k, v, beta, lg, s0)
+    out, s_got = chunk_gated_delta_rule(q.to(device), k.to(device), v.to(device), beta.to(device), lg.to(device),
+                                        initial_state=s0.to(device), output_final_state=True)
+    torch.cuda.synchronize()
+    assert out.shape == (tokens, heads, dim) and s_got.shape == (heads, dim, dim)
+    _check(out, want, f"gdn output d={dim}")
+    s_err = (s_got.cpu().double() - s_want).abs().max().item()
+    assert s_err <= 1e-2 * s_want.abs().max().item(), s_err
+    with pytest.raises(ValueError, match="head_dim must be 1 to 128"):
+        big = torch.zeros(64, 1, 160, dtype=torch.bfloat16, device=device)
+        chunk_gated_delta_rule(big, big, big, torch.zeros(64, 1, device=device), torch.zeros(64, 1, device=device))

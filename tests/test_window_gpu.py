@@ -123,3 +123,33 @@ def test_full_shape_sampled_rows(device, input_scale):
     want = wo.window_attention_rows(hq, hk, hv, rows, lay.video_start, lay.video_end, lay.num_frames, T, lay.bounds,
                                     w.scale, lay.anchor_frames)
     assert_parity(out.cpu()[rows], want)
+
+
+@pytest.mark.parametrize("dim", [32, 80, 96])
+def test_head_dims_below_128_run_with_zero_channels(device, dim):
+    """Head dims other than 64 / 128 (the reference's window op is shape-generic, vdn_h3/window.py:277-313) run
+    at the next kernel head dim with zero channels added; the scale stays the caller's D^-1/2. The bar is the
+    kernel's own (max-abs 2e-2, cosine 0.9995 against the fp32 oracle at the true head dim), with the gate, and
+    into a caller's output."""
+    from vdn_h3_amd import window
+
+    frames, per_frame, vs, heads = 7, 24, 10, 3
+    ve = vs + frames * per_frame
+    seq = ve + 6
+    bounds = wo.window_bounds(frames, 1, 3)
+    print(f"case window head_dim={dim}", flush=True)
+    gate = torch.sigmoid(torch.randn(seq, heads, generator=torch.Generator().manual_seed(5))).to(torch.bfloat16)
+    got, want = _run(device, seq, vs, ve, frames, per_frame, heads, dim, bounds, "both", seed=dim, gate=gate)
+    assert got.shape == (seq, heads, dim)
+    assert_parity(got, want)
+    gen = torch.Generator().manual_seed(dim + 1)
+    q, k, v = [torch.randn(seq, heads, dim, generator=gen).to(torch.bfloat16).to(device) for _ in range(3)]
+    out = torch.empty(seq, heads, dim, dtype=torch.bfloat16, device=device)
+    res = window.window_softmax_hip(q, k, v, vs, ve, frames, per_frame, bounds, dim ** -0.5, "both", out=out)
+    torch.cuda.synchronize()
+    assert res is out
+    assert_parity(out, wo.window_attention_grouped(q.cpu(), k.cpu(), v.cpu(), vs, ve, frames, per_frame, bounds,
+                                                   dim ** -0.5, "both"))
+    with pytest.raises(ValueError, match="head dims 1 to 128"):
+        big = torch.zeros(seq, 1, 160, dtype=torch.bfloat16, device=device)
+        window.window_softmax_hip(big, big, big, vs, ve, frames, per_frame, bounds, 160 ** -0.5, "both")
