@@ -92,9 +92,11 @@ def gdn_forward_into(q, k, v, beta, g, out, workspace, *, initial_state=None, fi
     pipe = _pipe(device)
     side = pipe.side
     with pipe.lock:
-        side.wait_stream(cur)  # the inputs and the workspace are ready on the current stream
+        prep(0, cur)
+        # the fork follows prep 0: the side stream's first prep starts once segment 0 is prepared, so prep 0
+        # runs alone and scan 0, the head of the critical chain, starts as early as it can
+        side.wait_stream(cur)
         try:
-            prep(0, cur)
             for i in range(segments):
                 b = i & 1
                 if i + 1 < segments:  # segment i + 1 fills buffer b ^ 1, last read by scan i - 1
