@@ -441,7 +441,7 @@ def bench_branch(args, torch, device):
                    "flop_short_conv": conv_flops, "flop_to_out_linear": proj},
         "roofline": {"bound": "mfma", "kernel": "projected_delta (all kernels)", "achieved": round(tflops, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": _traffic(args.traffic_json, "projected_delta")},
     }
 
 
