@@ -688,10 +688,12 @@ def _median_seconds(fn, reps=3):
     return sorted(times)[len(times) // 2], times
 
 
-def _sample_rows(seq, n_rows, block=256):
-    """About ``n_rows`` query rows as evenly spaced blocks of ``block`` consecutive rows: rows of one block
-    share a key set, so the oracle evaluates them as one product, as it does for the whole sequence (single
-    scattered rows would time small products the full run never makes)."""
+def _sample_rows(seq, n_rows, block=768):
+    """About ``n_rows`` query rows as evenly spaced blocks of ``block`` consecutive rows (the first, middle
+    and last of the sequence for 2304 rows: text and anchor rows with every key, interior frames with their
+    window): rows of one block share a key set, so the oracle evaluates them as one product, as it does for
+    the whole sequence; its key gather is paid once per block (scattered rows, or small blocks, time gathers
+    and small products the full run amortises: 256-row blocks ran at 0.8x the 768-row rate)."""
     blocks = max(1, n_rows // block)
     starts = [round(i * (seq - block) / max(1, blocks - 1)) for i in range(blocks)]
     return [r for s in starts for r in range(s, min(seq, s + block))]
@@ -720,7 +722,7 @@ def cpu_baseline_window(torch, qkv, w, lay, n_rows):
     return {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port", "seconds_median": round(med, 3), "seconds_runs": [round(t, 3) for t in times],
             "cpu": model, "physical_cores": physical,
-            "sample": f"{n_rows} query rows (evenly spaced blocks of 256) x {w.heads} heads of the 40,688-row "
+            "sample": f"{n_rows} query rows (evenly spaced blocks of 768) x {w.heads} heads of the 40,688-row "
                       "layout, fp32 oracle (oracle/window_oracle.py); 1 warm-up, median of 3"}
 
 
@@ -728,7 +730,7 @@ def cpu_baseline_block(torch, device, lay, work, conv, n_rows):
     """CPU throughput of one hybrid block from bounded samples of its three parts, each the median of 3
     runs after a warm-up of the fp32 oracle on the host cores:
 
-    * window attention: ``n_rows`` query rows (evenly spaced blocks of 256 rows) x 40 heads of the 40,688-row
+    * window attention: ``n_rows`` query rows (evenly spaced blocks of 768 rows) x 40 heads of the 40,688-row
       layout;
     * projections: ``oracle.branch_oracle.linear_bf16`` (fp32 GEMM, bf16 out) on 512 rows x K 5120 x N 15,360;
     * VDN branch: ``oracle.branch_oracle.projected_delta`` on 9 frames (7 inner) of 1296 tokens, 40 x 128,
@@ -774,7 +776,7 @@ def cpu_baseline_block(torch, device, lay, work, conv, n_rows):
             "parts": {
                 "window_attention": {"TFLOP/s": round(win_flop / win_s / 1e12, 5), "seconds_median": round(win_s, 3),
                                      "seconds_runs": [round(t, 3) for t in win_times],
-                                     "sample": f"{n_rows} query rows (blocks of 256) x {heads} heads"},
+                                     "sample": f"{n_rows} query rows (blocks of 768) x {heads} heads"},
                 "projections": {"TFLOP/s": round(proj_flop / proj_s / 1e12, 5), "seconds_median": round(proj_s, 3),
                                 "seconds_runs": [round(t, 3) for t in proj_times],
                                 "sample": "512 x 5120 x 15360 fp32 GEMM, bf16 out"},

@@ -236,11 +236,12 @@ def window_attention_rows(query, key, value, rows, video_start, video_end, num_f
     for iv, positions in groups.items():
         sel = torch.cat([torch.arange(a, b) for a, b in iv])
         qrows = torch.tensor([rows[p] for p in positions])
+        q_all, k_all, v_all = query[qrows], key[sel], value[sel]  # one gather per key set, all heads
         for h0 in range(0, len(heads), head_chunk):
             hs = heads[h0:h0 + head_chunk]
-            q = query[qrows][:, hs].to(dtype).permute(1, 0, 2)      # [h, r, D]
-            k = key[sel][:, hs].to(dtype).permute(1, 0, 2)          # [h, n, D]
-            v = value[sel][:, hs].to(dtype).permute(1, 0, 2)
+            q = q_all[:, hs].to(dtype).permute(1, 0, 2)      # [h, r, D]
+            k = k_all[:, hs].to(dtype).permute(1, 0, 2)      # [h, n, D]
+            v = v_all[:, hs].to(dtype).permute(1, 0, 2)
             p = torch.softmax(torch.matmul(q, k.transpose(-1, -2)) * scale, dim=-1)
             res = torch.matmul(p, v).permute(1, 0, 2)               # [r, h, D]
             out[torch.tensor(positions)[:, None], torch.arange(h0, h0 + len(hs))[None, :]] = res
