@@ -96,13 +96,14 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
 
 def frame_statistics_raw(k_raw: torch.Tensor, v_raw: torch.Tensor, beta: torch.Tensor, num_frames: int,
                          tokens_per_frame: int, *, k_features: bool = False, v_features: bool = False,
-                         a_fp32: bool = True):
+                         a_fp32: bool = True, out=None):
     """``A, B`` ``[F, H, D, D]`` fp32 from ``k``/``v`` rows ``[F*T, H, D]`` and ``beta`` ``[F*T, H]``.
 
     ``k``/``v`` are raw projections (the feature map is applied on load) unless
     ``k_features``/``v_features`` say they already hold the features (short-convolution output).
     ``a_fp32=False`` forms ``A`` as the reference does for that flag (``vdn_h3/branch.py:238-240``):
     the bf16 product of ``bf16(k~ * beta)`` and ``k~``, rounded to bf16, then symmetrised.
+    ``out=(A, B)``: contiguous fp32 ``[F, H, D, D]`` tensors (e.g. frame slices of larger ones) to write into.
     """
     if k_raw.shape != v_raw.shape or k_raw.ndim != 3:
         raise ValueError("key and value must share shape [rows, heads, dim]")
@@ -117,8 +118,14 @@ def frame_statistics_raw(k_raw: torch.Tensor, v_raw: torch.Tensor, beta: torch.T
     beta = beta.to(torch.bfloat16)
     if beta.stride(1) != 1:
         beta = beta.contiguous()
-    a = torch.empty((num_frames, heads, dim, dim), dtype=torch.float32, device=device)
-    b = torch.empty_like(a)
+    if out is None:
+        a = torch.empty((num_frames, heads, dim, dim), dtype=torch.float32, device=device)
+        b = torch.empty_like(a)
+    else:
+        a, b = out
+        for t in (a, b):
+            if t.shape != (num_frames, heads, dim, dim) or t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError(f"out must hold two contiguous fp32 [{num_frames}, {heads}, {dim}, {dim}] tensors")
     flags = int(bool(k_features)) | (int(bool(v_features)) << 1) | (int(not a_fp32) << 2)
     rc = _lib.lib().vdnh3_frame_stats(_lib.ptr(k_raw), k_raw.stride(0), k_raw.stride(1), _lib.ptr(v_raw),
                                       v_raw.stride(0), v_raw.stride(1), flags, _lib.ptr(beta), beta.stride(0),

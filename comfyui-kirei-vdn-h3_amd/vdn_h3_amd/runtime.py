@@ -208,11 +208,9 @@ class OptimizedLinearBranch:
             rows = slice(start * t, stop * t)
             feats = self._tile_features(weights, {"k": k_raw, "v": v_raw}, start, stop, num_frames, t, frame_size)
             (k_in, k_feat), (v_in, v_feat) = feats["k"], feats["v"]
-            ta, tb = _b.frame_statistics_raw(k_in, v_in, beta[rows], stop - start, t, k_features=k_feat,
-                                             v_features=v_feat, a_fp32=self.a_fp32)
-            a[start:stop].copy_(ta)
-            b[start:stop].copy_(tb)
-            del feats, k_in, v_in, ta, tb
+            _b.frame_statistics_raw(k_in, v_in, beta[rows], stop - start, t, k_features=k_feat, v_features=v_feat,
+                                    a_fp32=self.a_fp32, out=(a[start:stop], b[start:stop]))
+            del feats, k_in, v_in
         mean = _b.frame_mean(xv, num_frames, t)
         alpha = _b.alpha_gate(mean, weights["alpha.down.weight"], weights["alpha.up.weight"],
                               weights["alpha.dt_bias"], weights["alpha.A_log"], heads, dim)
