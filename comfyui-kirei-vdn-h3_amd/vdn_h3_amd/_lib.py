@@ -159,6 +159,14 @@ def stream_handle(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def forward_only(what: str, *tensors) -> None:
+    """The HIP ops have no backward: in gradient mode an input that requires grad is an error, since the
+    result would silently carry no gradient."""
+    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors):
+        raise RuntimeError(f"{what} is forward-only (no backward) and an input requires grad; "
+                           "call it under torch.no_grad() or torch.inference_mode()")
+
+
 def require_device(*tensors) -> torch.device:
     """All tensors must live on one GPU; the HIP path has no CPU fallback."""
     device = None

@@ -133,6 +133,7 @@ def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, be
         raise ValueError(f"head_dim must be 1 to 128 (128 natively), got {dim}")
     if beta.shape != (tokens, heads) or g.shape != (tokens, heads):
         raise ValueError("beta and g must have shape [tokens, heads]")
+    _lib.forward_only("chunk_gated_delta_rule", q, k, v, beta, g, initial_state)
     device = _lib.require_device(q, k, v, beta, g, initial_state)
     if dim < 128:
         # zero channels are exact: k's zero entries leave the state's added rows and columns zero (S_t keeps

@@ -17,8 +17,10 @@ and the same exception types. Per call, on the caller's current stream:
 
 The branch runs after ``out_proj`` here (the reference computes it first and adds it last):
 the sum is the same bf16 addition, ``bf16(out + bf16(delta))``. A full-cover layout runs
-dense attention and no branch (``:422``, ``:495-499``). The path is inference-only
-(``torch.no_grad`` / ``inference_mode``). With ``rope_freqs`` the q/k pass also applies the
+dense attention and no branch (``:422``, ``:495-499``). The path is forward-only: with
+gradient mode on (the reference's deferred-branch case, ``:424``, ``:481-495``) a call whose input,
+rotary table and block weights need no gradient runs the same forward under ``torch.no_grad``, and
+one where any of them requires grad is a ``RuntimeError``. With ``rope_freqs`` the q/k pass also applies the
 split-half rotary embedding (``vdn_h3/hybrid.py:274-292``; ``rope_table`` gives the layout),
 with the q_norm epsilon for both, as the reference does. ``normalise_qk`` is the same q/k pass as a
 standalone op (the fused path gives the same bits).
@@ -187,6 +189,7 @@ def normalise_qk(q_raw: torch.Tensor, k_raw: torch.Tensor, q_weight: torch.Tenso
     """
     if q_raw.shape != k_raw.shape or q_raw.ndim != 3:
         raise ValueError("q and k must share shape [sequence, heads, dim]")
+    _lib.forward_only("normalise_qk", q_raw, k_raw, q_weight, k_weight, rope_freqs)
     device = _lib.require_device(q_raw, k_raw, q_weight, k_weight)
     seq, heads, dim = q_raw.shape
     q_raw, k_raw = _window._kernel_operand(q_raw), _window._kernel_operand(k_raw)
@@ -230,12 +233,27 @@ def _split_qkv(projected: torch.Tensor, heads: int, head_dim: int):
     return projected.unflatten(-1, (3, heads, head_dim)).unbind(-3)
 
 
+def _needs_grad(x, rope_freqs, attn, weight_map: Mapping) -> bool:
+    """Whether any tensor a block call reads requires grad: ``x``, the rotary table, the attention
+    module's parameters (or, for a plain object, the weights of its projections and norms) and the
+    block's branch / gate weights."""
+    tensors = [x, rope_freqs, *weight_map.values()]
+    params = getattr(attn, "parameters", None)
+    if callable(params):
+        tensors.extend(params())
+    else:
+        for name in ("qkv_proj", "out_proj", "q_norm", "k_norm"):
+            tensors.append(getattr(getattr(attn, name, None), "weight", None))
+    return any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
+
+
 class _VDNBlockForward:
     """The patched ``attn.forward`` of one block (``vdn_h3/hybrid.py:409-579``).
 
     Same call signature and contract as the reference's ``vdn_forward``: without a published
     layout the original forward runs; a layout whose length differs from ``x`` is a
-    ``RuntimeError``; the path is inference-only.
+    ``RuntimeError``; the path is forward-only (a call in gradient mode runs under ``no_grad``
+    when nothing it reads requires grad, else it is a ``RuntimeError``).
     """
 
     def __init__(self, attn: Any, state: VDNState, block_index: int):
@@ -253,8 +271,13 @@ class _VDNBlockForward:
         if rows != layout.seq_len:
             raise RuntimeError(f"attention got {rows} rows but the published VDN layout has {layout.seq_len}")
         if torch.is_grad_enabled():
-            raise RuntimeError("the MI355X VDN-H3 block is inference-only; run it under torch.no_grad()")
-        out = self._forward(x, layout, rope_freqs)
+            if _needs_grad(x, rope_freqs, self.attn, self.state._maps[self.index]):
+                raise RuntimeError("the MI355X VDN-H3 block is forward-only (no backward), and a tensor it reads "
+                                   "requires grad; run it under torch.no_grad() or inference_mode()")
+            with torch.no_grad():
+                out = self._forward(x, layout, rope_freqs)
+        else:
+            out = self._forward(x, layout, rope_freqs)
         self.state.forwards += 1
         self.state.last_layout = layout
         return out

@@ -34,6 +34,7 @@ def gemm(kind: int, a: torch.Tensor, b: torch.Tensor, *, a_scale=None, b_scale=N
     """
     if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[1]:
         raise ValueError(f"gemm operands must be [M, K] and [N, K]; got {tuple(a.shape)} and {tuple(b.shape)}")
+    _lib.forward_only("gemm", a, b, a_scale, b_scale, bias)
     device = _lib.require_device(a, b, a_scale, b_scale, bias, out)
     m, k = a.shape
     n = b.shape[0]
@@ -183,7 +184,7 @@ class HipLinear(torch.nn.Module):
         self.precision = precision
         self.per_tensor = bool(per_tensor)
         self.out_features, self.in_features = int(weight.shape[0]), int(weight.shape[1])
-        w = weight.to(torch.bfloat16).contiguous()
+        w = weight.detach().to(torch.bfloat16).contiguous()  # a constant of the forward-only op
         if precision == "bf16":
             self.register_buffer("weight", w)
             self.register_buffer("weight_scale", None)

@@ -21,6 +21,7 @@ def apply_softmax_gate(softmax_out: torch.Tensor, gate: torch.Tensor, state=None
     seq, heads, dim = softmax_out.shape
     if gate.numel() != seq * heads:
         raise ValueError(f"gate must hold one value per (row, head): {seq}x{heads}, got {tuple(gate.shape)}")
+    _lib.forward_only("apply_softmax_gate", softmax_out, gate)
     device = _lib.require_device(softmax_out, gate)
     o = softmax_out
     if o.dtype != torch.bfloat16:

@@ -244,6 +244,7 @@ def window_softmax_hip(query, key, value, video_start, video_end, num_frames, to
     a zero channel adds nothing to a score and yields a zero output channel, and ``scale`` is the caller's.
     """
     _check_qkv(query, key, value, "window_softmax_hip")
+    _lib.forward_only("window_softmax_hip", query, key, value, gate)
     device = _lib.require_device(query, key, value, gate, out)
     seq, heads, dim = query.shape
     if dim not in KERNEL_HEAD_DIMS:
@@ -302,6 +303,7 @@ def window_softmax_normed(q_raw, k_raw, value, q_weight, k_weight, q_eps, k_eps,
     ``diagnostics`` times the stages ``attention.softmax.qkv_prepass`` / ``attention.softmax.kernel``.
     """
     _check_qkv(q_raw, k_raw, value, "window_softmax_normed")
+    _lib.forward_only("window_softmax_normed", q_raw, k_raw, value, q_weight, k_weight, rope_freqs, gate)
     device = _lib.require_device(q_raw, k_raw, value, q_weight, k_weight, gate, out)
     seq, heads, dim = q_raw.shape
     wq = q_weight.to(torch.bfloat16).contiguous()

@@ -14,6 +14,35 @@ def test_window_op_rejects_cpu_tensors(built_lib):
         window.window_softmax_hip(q, q, q, 0, 8, 1, 8, [(0, 0)], 0.125)
 
 
+def test_ops_are_forward_only_in_gradient_mode(built_lib):
+    """An input that requires grad in gradient mode is an error before any device work (the HIP ops have no
+    backward, so their result would silently carry no gradient); under no_grad the same call reaches the
+    device check."""
+    from vdn_h3_amd import gdn, linear, softmax_kernels, window
+    from vdn_h3_amd.hybrid import normalise_qk
+
+    q = torch.zeros(8, 1, 64, dtype=torch.bfloat16, requires_grad=True)
+    w = torch.ones(64, dtype=torch.bfloat16)
+    beta = torch.zeros(8, 1)
+    calls = {
+        "window_softmax_hip": lambda: window.window_softmax_hip(q, q, q, 0, 8, 1, 8, [(0, 0)], 0.125),
+        "window_softmax_normed": lambda: window.window_softmax_normed(q, q, q, w, w, 1e-6, 1e-6, 0, 8, 1, 8,
+                                                                      [(0, 0)], 0.125),
+        "normalise_qk": lambda: normalise_qk(q, q, w, w),
+        "apply_softmax_gate": lambda: softmax_kernels.apply_softmax_gate(q, beta),
+        "gemm": lambda: linear.linear(q[:, 0], torch.zeros(16, 64, dtype=torch.bfloat16)),
+        "chunk_gated_delta_rule": lambda: gdn.chunk_gated_delta_rule(q, q, q, beta, beta),
+    }
+    for what, call in calls.items():
+        with pytest.raises(RuntimeError, match=f"{what} is forward-only"):
+            call()
+        with torch.no_grad(), pytest.raises(RuntimeError, match="no CPU fallback"):
+            call()
+    weight = torch.zeros(16, 64, requires_grad=True)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):  # the weight is a constant, not a grad input
+        linear.HipLinear(weight)
+
+
 def test_window_op_shape_errors(built_lib):
     from vdn_h3_amd import window
 

@@ -175,21 +175,33 @@ def test_gate_off_and_branch_off(device):
         _parity(out, ho.vdn_forward(t["x"], layout, aw, bw, heads, dim, **kw), f"block {cfg} vs oracle")
 
 
-def test_without_layout_calls_original_and_grad_is_rejected(device):
-    from vdn_h3_amd.hybrid import VDNState, make_vdn_forward
+def test_without_layout_calls_original_and_grad_mode_is_forward_only(device):
+    """No layout: the original forward. Gradient mode with nothing that requires grad (the reference's
+    deferred-branch case, ``vdn_h3/hybrid.py:424``): the no_grad block's bits and an output that needs
+    no grad. An input or a branch weight that requires grad: RuntimeError (the block has no backward)."""
+    from vdn_h3_amd.hybrid import VDNState, forward_scope, make_vdn_forward
     from vdn_h3_amd.runtime import OptimizedLinearBranch
 
     t, layout, aw, bw, heads, dim = _golden()
-    attn = _attn(aw, heads, dim, device)
-    attn.forward = lambda x, rope_freqs=None, transformer_options=None: "original"
-    state = VDNState("t", {}, [OptimizedLinearBranch({}, heads, dim)], heads, dim)
-    forward = make_vdn_forward(attn, state, 0)
+    original = lambda x, rope_freqs=None, transformer_options=None: "original"  # noqa: E731
+    dbw = {k: v.to(device) for k, v in bw.items()}
+    forward, _ = _block(aw, dbw, heads, dim, device)
+    forward._vdn_h3_original = original  # the forward it patched
     x = t["x"].to(device)
     assert forward(x) == "original"
-    from vdn_h3_amd.hybrid import forward_scope
-
-    with forward_scope(layout), pytest.raises(RuntimeError, match="inference-only"):
-        forward(x)
+    want = _run(forward, x, layout)
+    with forward_scope(layout):
+        got = forward(x)
+    torch.cuda.synchronize()
+    assert not got.requires_grad
+    assert torch.equal(got, want)
+    with forward_scope(layout), pytest.raises(RuntimeError, match="forward-only"):
+        forward(x.clone().requires_grad_(True))
+    grad_w = dict(dbw)
+    grad_w["to_out_linear.weight"] = grad_w["to_out_linear.weight"].clone().requires_grad_(True)
+    state = VDNState("t", {}, [OptimizedLinearBranch(grad_w, heads, dim)], heads, dim)
+    with forward_scope(layout), pytest.raises(RuntimeError, match="forward-only"):
+        make_vdn_forward(_attn(aw, heads, dim, device), state, 0)(x)
     with torch.no_grad(), forward_scope(layout), pytest.raises(RuntimeError, match="rows"):
         forward(x[:-1])
 
