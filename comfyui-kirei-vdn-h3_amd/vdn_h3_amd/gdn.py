@@ -123,6 +123,7 @@ def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, be
     (the log-decay, ``<= 0``): ``[T, H]``, computed in fp32; ``initial_state``: ``[H, D, D]``
     (dv rows, dk columns). Keys are used as given (the recurrence assumes unit-norm keys).
     ``pipelined``: overlap the segments' preps and scans on two streams (``gdn_forward_into``).
+    An empty sequence (``tokens == 0``) gives an empty output and the initial state (zeros without one).
     """
     if chunk_size != 64:
         raise ValueError("the HIP kernel is built for chunk_size 64")
@@ -135,11 +136,17 @@ def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, be
         raise ValueError("beta and g must have shape [tokens, heads]")
     _lib.forward_only("chunk_gated_delta_rule", q, k, v, beta, g, initial_state)
     device = _lib.require_device(q, k, v, beta, g, initial_state)
+    if initial_state is not None and initial_state.shape != (heads, dim, dim):
+        raise ValueError(f"initial_state must have shape [{heads}, {dim}, {dim}]")
+    if tokens == 0:  # no token: no output row, and the state is the initial one
+        final = None
+        if output_final_state:
+            final = (initial_state.float().clone() if initial_state is not None else
+                     torch.zeros((heads, dim, dim), dtype=torch.float32, device=device))
+        return torch.empty((0, heads, dim), dtype=torch.bfloat16, device=device), final
     if dim < 128:
         # zero channels are exact: k's zero entries leave the state's added rows and columns zero (S_t keeps
         # a_t S (I - b k k^T) there and b v k^T adds nothing), so the output's added channels are zero
-        if initial_state is not None and initial_state.shape != (heads, dim, dim):
-            raise ValueError(f"initial_state must have shape [{heads}, {dim}, {dim}]")
         pad = lambda t: torch.nn.functional.pad(t.to(torch.bfloat16), (0, 128 - dim))  # noqa: E731
         init = None
         if initial_state is not None:
@@ -159,8 +166,6 @@ def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, be
     g = g.float().contiguous()
     init = None
     if initial_state is not None:
-        if initial_state.shape != (heads, dim, dim):
-            raise ValueError(f"initial_state must have shape [{heads}, {dim}, {dim}]")
         init = initial_state.float().contiguous()
     final = torch.empty((heads, dim, dim), dtype=torch.float32, device=device) if output_final_state else None
     out = torch.empty((tokens, heads, dim), dtype=torch.bfloat16, device=device)

@@ -270,3 +270,18 @@ def test_gdn_head_dims_below_128(device, dim):
     with pytest.raises(ValueError, match="head_dim must be 1 to 128"):
         big = torch.zeros(64, 1, 160, dtype=torch.bfloat16, device=device)
         chunk_gated_delta_rule(big, big, big, torch.zeros(64, 1, device=device), torch.zeros(64, 1, device=device))
+
+
+def test_gdn_empty_sequence(device):
+    """No token: an empty output and the initial state as the final state (zeros without one)."""
+    from vdn_h3_amd.gdn import chunk_gated_delta_rule
+
+    print("case gdn empty sequence", flush=True)
+    for dim in (128, 48):
+        x = torch.zeros(0, 2, dim, dtype=torch.bfloat16, device=device)
+        z = torch.zeros(0, 2, device=device)
+        s0 = torch.randn(2, dim, dim, generator=torch.Generator().manual_seed(3)).to(device)
+        out, s = chunk_gated_delta_rule(x, x, x, z, z, initial_state=s0, output_final_state=True)
+        assert out.shape == (0, 2, dim) and torch.equal(s, s0) and s.data_ptr() != s0.data_ptr()
+        out, s = chunk_gated_delta_rule(x, x, x, z, z, output_final_state=True)
+        assert out.shape == (0, 2, dim) and s.shape == (2, dim, dim) and not s.any()
