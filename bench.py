@@ -27,7 +27,7 @@ Other workloads: ``stack`` (50 blocks x ``--steps`` denoising steps, ``x <- x + 
 (the DiT block pointwise passes), ``rope`` (q/k RMSNorm + RoPE),
 ``hbm_copy`` (counter calibration), ``mfma_peak`` (sustained MFMA rates, the ceiling calibration),
 ``cpu_configs`` (the fp32 CPU oracle timed per configuration at full size on the host cores, a few minutes).
-``cpu_baseline`` times the fp32 CPU oracle on the host cores (16 threads, the box's CPU share) on bounded
+``cpu_baseline`` times the fp32 CPU oracle on the host cores (16 threads, the host's CPU share for one GPU) on bounded
 samples (1 warm-up, median of 3): for ``block``, the window attention on sampled query rows, the projections
 on sampled rows and the VDN branch on 7 of its 29 inner frames, combined at the block's per-part work.
 """
@@ -382,7 +382,7 @@ def bench_gemm(args, torch, device):
 
 
 def library_gemm_rate(torch, device, stream, args, kind_name, xq, xs, wq, ws, ops):
-    """hipBLASLt on the same operands and box, timed like the kernel above (a comparison, not this library's
+    """hipBLASLt on the same operands and machine, timed like the kernel above (a comparison, not this library's
     path): torch._scaled_mm (fp8 per-tensor, bf16 out) or torch._int_mm (int8, int32 accumulators out, no
     scales applied)."""
     if kind_name == "i8":
@@ -576,7 +576,7 @@ def bench_rope(args, torch, device):
     }
 
 
-CPU_THREADS = 16   # the GPU box's CPU share for one GPU
+CPU_THREADS = 16   # host threads of the CPU baseline: the host's CPU share for one GPU on the benchmark machine
 
 
 MFMA_KINDS = {0: ("bf16_32x32x16", PEAK_BF16_TFLOPS), 1: ("int8_32x32x32", PEAK_I8_TOPS),

@@ -27,7 +27,7 @@
 //  - int8: stages of 128 bytes per row (whole 128-byte lines, half the barriers per MFMA) in two
 //    slots (128 KB); stage s issues the loads of stage s + 1 in its first three k-steps (of four),
 //    and the barrier sits before the last one. Against the ring at the projection shapes, bit-
-//    identical: -2.8 to -4.4% (qkv) and -4.0 to -4.7% (out) on two boxes. For fp8 (two k-steps per
+//    identical: -2.8 to -4.4% (qkv) and -4.0 to -4.7% (out) on two machines. For fp8 (two k-steps per
 //    stage, so the loads had one k-step to land) the same pipeline, and one with the loads spread
 //    over both k-steps and the barrier after the second, measured from -1.6% to +3.5%: not kept.
 // One barrier per stage frees a slot and publishes the next stage; fragments are double-buffered
