@@ -326,9 +326,11 @@ class _VDNBlockForward:
             gate, proj_rows = self._gate(x, weights, with_branch)
         plan = self._plan(layout, device)
         pending = None
-        if with_branch and state.branch_execution == "parallel" and hasattr(self.branch, "branch_rows"):
+        if (with_branch and state.branch_execution == "parallel" and hasattr(self.branch, "branch_rows")
+                and not getattr(self.branch, "tile_frames", 0)):
             # the branch reads only x, the raw q / k / v and its projections, none of which the attention
-            # below writes: it runs on a second stream and joins at the to_out_linear accumulation
+            # below writes: it runs on a second stream and joins at the to_out_linear accumulation (a
+            # frame-tiled branch, whose point is to hold one tile of rows, runs in order after out_proj)
             pending = self._start_branch(x, q_raw, k_raw, value, layout, weights, proj_rows)
         with scope("attention.softmax", device):
             # q_norm / k_norm (+ RoPE) run inside the attention: the keys in its pre-pass, each query

@@ -161,7 +161,8 @@ def test_tiled_branch_matches_reference_golden(device):
 
 
 def test_block_with_tile_frames_equals_untiled(device):
-    """VDNState(tile_frames=5) hands the option to its branches: the block output is the untiled block's."""
+    """VDNState(tile_frames=5) hands the option to its branches: the block output is the untiled block's, also
+    with branch_execution="parallel" (a tiled branch runs in order after out_proj)."""
     from vdn_h3_amd.hybrid import VDNState, forward_scope, make_vdn_forward
     from vdn_h3_amd.layout import text_first_layout
     from vdn_h3_amd.linear import HipLinear
@@ -182,12 +183,12 @@ def test_block_with_tile_frames_equals_untiled(device):
         k_norm=SimpleNamespace(weight=aw["k_norm.weight"].to(device), eps=1e-6))
     cfg = {"enable_softmax_gate": True, "linear_enabled": True, "enable_text_state": True}
     outs = []
-    for tile in (0, 5):
+    for tile, mode in ((0, "serial"), (5, "serial"), (5, "parallel")):
         branch = OptimizedLinearBranch(bw, heads, dim, enable_text_state=True)
-        state = VDNState("test", cfg, [branch], heads, dim, tile_frames=tile)
+        state = VDNState("test", cfg, [branch], heads, dim, tile_frames=tile, branch_execution=mode)
         assert branch.tile_frames == tile
         with torch.no_grad(), forward_scope(layout):
             outs.append(make_vdn_forward(attn, state, 0)(t["x"].to(device)))
     torch.cuda.synchronize()
-    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     _parity(outs[1], t["out"], "block with tile_frames=5 vs reference make_vdn_forward")
