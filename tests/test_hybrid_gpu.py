@@ -175,6 +175,58 @@ def test_gate_off_and_branch_off(device):
         _parity(out, ho.vdn_forward(t["x"], layout, aw, bw, heads, dim, **kw), f"block {cfg} vs oracle")
 
 
+@pytest.mark.parametrize("precision", ["bf16", "int8"])
+@pytest.mark.parametrize("full_cover", [False, True])
+def test_zero_softmax_gate_halves_the_block(device, precision, full_cover):
+    """A softmax gate with zero weights and bias is sigmoid(0) = 1/2 (the reference's
+    ``test_full_cover_gate_keeps_canonical_shape_and_loads_only_gate``, ``tests/test_hybrid.py``): with the
+    branch off the block is exactly half the ungated block, bit for bit, since halving commutes with every
+    rounding on the path (bf16 attention output, the gate product, the per-token int8 scale, the projection)."""
+    from vdn_h3_amd import projection
+    from vdn_h3_amd.layout import text_first_layout
+
+    print(f"case zero softmax gate precision={precision} full_cover={full_cover}", flush=True)
+    t, layout, aw, bw, heads, dim = _golden()
+    if full_cover:
+        layout = text_first_layout(16, 5, (8, 8))
+        assert layout.full_cover
+    x = t["x"][:layout.seq_len].to(device)
+    dbw = {k: v.to(device) for k, v in bw.items()}
+    dbw["softmax_gate.up.weight"] = torch.zeros_like(dbw["softmax_gate.up.weight"])
+    dbw["softmax_gate.up.bias"] = torch.zeros_like(dbw["softmax_gate.up.bias"])
+    if precision == "int8":
+        (dbw,), _ = projection.prepare_projection_maps([dbw], device, "int8")
+    outs = []
+    for gate in (True, False):
+        forward, _ = _block(aw, dbw, heads, dim, device, precision=precision,
+                            config={"enable_softmax_gate": gate, "linear_enabled": False})
+        outs.append(_run(forward, x, layout))
+    gated, plain = outs
+    assert torch.count_nonzero(plain) > 0
+    assert torch.equal(gated, plain * 0.5)
+
+
+def test_branch_changes_only_inner_video_rows(device):
+    """The branch adds to the video rows only (the reference's ``test_linear_delta_changes_only_target_video_rows``):
+    against the block with ``linear_enabled=False`` the text rows and the two anchor frames (``anchor_frames="both"``)
+    keep their bits, and every inner frame changes."""
+    print("case branch rows", flush=True)
+    t, layout, aw, bw, heads, dim = _golden()
+    assert layout.anchor_frames == "both"
+    dbw = {k: v.to(device) for k, v in bw.items()}
+    outs = []
+    for linear in (True, False):
+        forward, _ = _block(aw, dbw, heads, dim, device, config={"linear_enabled": linear})
+        outs.append(_run(forward, t["x"].to(device), layout))
+    on, off = outs
+    tpf, vs, ve = layout.tokens_per_frame, layout.video_start, layout.video_end
+    same = torch.ones(layout.seq_len, dtype=torch.bool)
+    same[vs + tpf:ve - tpf] = False
+    assert torch.equal(on[same.to(device)], off[same.to(device)])
+    inner = (on[vs + tpf:ve - tpf] != off[vs + tpf:ve - tpf]).view(layout.num_frames - 2, tpf, -1)
+    assert bool(inner.any(dim=2).any(dim=1).all()), "every inner frame carries a branch delta"
+
+
 def test_without_layout_calls_original_and_grad_mode_is_forward_only(device):
     """No layout: the original forward. Gradient mode with nothing that requires grad (the reference's
     deferred-branch case, ``vdn_h3/hybrid.py:424``): the no_grad block's bits and an output that needs
