@@ -142,3 +142,22 @@ def test_full_shape_key_counts_and_pairs():
     assert pairs == 512 * 40688 + 2 * 1296 * 40688 + 1296 * (4 * 14768 + 5 * 21248 + 15 * 22544 + 5 * 16064)
     assert abs(pairs - 8.829e8) / 8.829e8 < 1e-3
     assert abs(4 * 128 * 40 * pairs - 1.8082e13) / 1.8082e13 < 1e-3
+
+
+def test_a_wrong_anchor_mode_fails_parity():
+    """With distinct q / k / v every anchor mode gives a different result, far outside the GPU tests' bar
+    (the reference's autotune check, ``tests/test_autotune.py:11-41``: a backend with the wrong anchors must fail
+    parity), so a kernel or plan that mixed up the modes could not pass them."""
+    gen = torch.Generator().manual_seed(77)
+    frames, per_frame, heads, dim = 11, 4, 2, 16
+    vs = 6
+    ve = vs + frames * per_frame
+    seq = ve + 3
+    q, k, v = (torch.randn(seq, heads, dim, generator=gen) for _ in range(3))
+    bounds = wo.window_bounds(frames, 1, 5)
+    outs = {m: wo.window_attention_grouped(q, k, v, vs, ve, frames, per_frame, bounds, dim ** -0.5, m)
+            for m in wo.ANCHOR_FRAME_MODES}
+    modes = list(outs)
+    for i, a in enumerate(modes):
+        for b in modes[i + 1:]:
+            assert (outs[a] - outs[b]).abs().max().item() > 0.1, (a, b)
