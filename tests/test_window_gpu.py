@@ -153,3 +153,30 @@ def test_head_dims_below_128_run_with_zero_channels(device, dim):
     with pytest.raises(ValueError, match="head dims 1 to 128"):
         big = torch.zeros(seq, 1, 160, dtype=torch.bfloat16, device=device)
         window.window_softmax_hip(big, big, big, vs, ve, frames, per_frame, bounds, 160 ** -0.5, "both")
+
+
+def test_calls_hold_no_memory_beyond_their_output(device):
+    """The op keeps nothing between calls but the cached tile plan (the reference releases its per-group buffers,
+    ``tests/test_window.py:14-38``): after a warm call, further calls whose outputs are dropped leave the
+    allocated device memory where it was, and a kept output adds exactly its own size."""
+    from vdn_h3_amd import window
+
+    frames, per_frame, text, heads, dim = 13, 64, 16, 2, 128
+    seq = text + frames * per_frame
+    print("case window memory", flush=True)
+    qkv = torch.randn(seq, 3 * heads * dim, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).to(device)
+    q, k, v = [t.view(seq, heads, dim) for t in qkv.split(heads * dim, dim=-1)]
+    cache = window.WindowAttentionCache(limit=4)
+    args = (text, seq, frames, per_frame, wo.window_bounds(frames, 1, 5), dim ** -0.5, "both", cache)
+    first = window.window_softmax_hip(q, k, v, *args)
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(device)
+    for _ in range(3):
+        window.window_softmax_hip(q, k, v, *args)
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated(device) == base
+    kept = window.window_softmax_hip(q, k, v, *args)
+    torch.cuda.synchronize()
+    grown = torch.cuda.memory_allocated(device) - base
+    assert grown == kept.untyped_storage().nbytes() or grown == -(-kept.untyped_storage().nbytes() // 512) * 512
+    assert torch.equal(kept, first)
