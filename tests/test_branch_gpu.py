@@ -110,6 +110,35 @@ def test_factor_and_status(device):
             branch.VdnDelta().factor_apply(alpha.to(device), bad.to(device), b.to(device))
 
 
+def test_factor_status_scopes_nest_and_validate_outside_a_scope(device):
+    """Outside a scope a bad factor raises at once; an inner scope's failure leaves the outer scope's recorded
+    statuses in place, and the outer scope validates them on exit (the reference's
+    ``tests/test_cholesky.py`` nesting and immediate-check cases)."""
+    from vdn_h3_amd import branch
+
+    print("case factor status scopes", flush=True)
+    frames, heads, dim, tokens = 2, 1, 64, 200
+    kf = torch.nn.functional.normalize(_rand((frames, heads, tokens, dim), 14), dim=-1)
+    a = (kf * 0.5).transpose(-1, -2) @ kf
+    b = _rand((frames, heads, dim, dim), 15)
+    alpha = torch.rand(frames, heads, dim, generator=torch.Generator().manual_seed(16))
+    bad = a.clone()
+    bad[0, 0] = -2.0 * torch.eye(dim)
+    good = (alpha.to(device), a.to(device), b.to(device))
+    invalid = (alpha.to(device), bad.to(device), b.to(device))
+    with pytest.raises(torch.linalg.LinAlgError, match="leading minor of order 1"):
+        branch.VdnDelta().factor_apply(*invalid)
+    assert branch._CHOLESKY_CHECKS.get() is None
+    with branch.cholesky_runtime_scope() as outer:
+        branch.VdnDelta().factor_apply(*good)
+        with pytest.raises(torch.linalg.LinAlgError):
+            with branch.cholesky_runtime_scope() as inner:
+                branch.VdnDelta().factor_apply(*invalid)
+        assert branch._CHOLESKY_CHECKS.get() is outer
+        assert len(outer.statuses) == 1 and outer.factor_calls == 1 and not inner.statuses
+    assert branch._CHOLESKY_CHECKS.get() is None
+
+
 @pytest.mark.parametrize("text", [False, True])
 def test_scans(device, text):
     from vdn_h3_amd import branch
