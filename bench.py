@@ -570,7 +570,7 @@ def bench_rope(args, torch, device):
         "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(t_rope, 4), "dtype": "bf16",
         "config": {"workload": "qk_rmsnorm_rope_s40688_h40_d128", "seq_len": seq, "heads": heads, "head_dim": dim,
                    "rot_dim": dim, "bytes_per_step": io + table, "note": "rope table built in the timed call"},
-        "roofline": {"bound": "hbm", "kernel": "qk_rmsnorm_kernel<128, rope>", "achieved": round(gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "qk_rmsnorm_rope_kernel<128>", "achieved": round(gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
         "plain_qk_rmsnorm_ms": round(t_norm, 4),
     }
